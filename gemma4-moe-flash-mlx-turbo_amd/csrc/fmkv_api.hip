@@ -1,0 +1,620 @@
+// C ABI of the MI355X quantized KV cache (include/fmkv.h).
+//
+// Host-side state mirrors KVCache (src/cache.rs:166-172): the monotonic
+// `offset` (RoPE position), the optional sliding `window`, and the stored
+// K/V -- here a preallocated device arena of 16-token head-blocks instead of
+// MLX arrays re-concatenated on every append (src/cache.rs:132-148).
+// Errors never cross the boundary as exceptions: every entry point returns a
+// status and records a message for fmkv_last_error().
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/fmkv.h"
+#include "fmkv_internal.h"
+
+using fmkv::BlockLayout;
+
+namespace {
+
+thread_local std::string g_err;
+int32_t g_bps_override = 0;
+
+// Kernel-timing records (fmkv_profile_enable / fmkv_profile_collect).
+struct Profiler {
+  std::vector<hipEvent_t> ev;  // pairs
+  int32_t max_records = 0;
+  int32_t used = 0;
+  void clear_events() {
+    for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+    ev.clear();
+    used = 0;
+  }
+} g_prof;
+
+// Next event pair for a decode launch, or {null, null} when not profiling.
+void next_events(hipEvent_t* e0, hipEvent_t* e1) {
+  *e0 = *e1 = nullptr;
+  if (g_prof.max_records <= 0 || g_prof.used >= g_prof.max_records) return;
+  const size_t i = 2 * (size_t)g_prof.used;
+  *e0 = g_prof.ev[i];
+  *e1 = g_prof.ev[i + 1];
+  g_prof.used++;
+}
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(FMKV_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// src/cache.rs:29-43: MMIX LCG stepped before each draw, +1 iff bit 63 == 0.
+std::vector<float> lcg_signs(int n, uint64_t seed) {
+  std::vector<float> s(n);
+  uint64_t state = seed;
+  for (int i = 0; i < n; i++) {
+    state = state * 6364136223846793005ull + 1442695040888963407ull;
+    s[i] = ((state >> 63) & 1ull) == 0 ? 1.0f : -1.0f;
+  }
+  return s;
+}
+
+int check_desc(const fmkv_cache_desc* d) {
+  if (!d) return fail(FMKV_ERR_INVALID_ARG, "descriptor is null");
+  if (d->n_kv_heads < 1 || d->n_kv_heads > 256)
+    return fail(FMKV_ERR_INVALID_ARG, "n_kv_heads must be in [1, 256]");
+  if (d->head_dim != 128 && d->head_dim != 256 && d->head_dim != 512)
+    return fail(FMKV_ERR_UNSUPPORTED, "head_dim must be 128, 256 or 512");
+  if (d->group_size != 64) return fail(FMKV_ERR_UNSUPPORTED, "group_size must be 64");
+  if (d->mode == FMKV_MODE_AFFINE) {
+    if (d->bits != 4 && d->bits != 8)
+      return fail(FMKV_ERR_UNSUPPORTED, "affine mode supports 4 or 8 bits");
+  } else if (d->mode == FMKV_MODE_CODEBOOK) {
+    if (d->bits < 2 || d->bits > 4)
+      return fail(FMKV_ERR_UNSUPPORTED, "codebook mode supports 2, 3 or 4 bits");
+  } else {
+    return fail(FMKV_ERR_UNSUPPORTED, "unknown mode");
+  }
+  if (d->window < 0) return fail(FMKV_ERR_INVALID_ARG, "window must be >= 0");
+  if (d->window > 0) {
+    if (d->window % fmkv::kBlockTokens != 0)
+      return fail(FMKV_ERR_UNSUPPORTED, "window must be a multiple of 16");
+  } else {
+    if (d->capacity < 1) return fail(FMKV_ERR_INVALID_ARG, "capacity must be >= 1 for a global cache");
+    if (d->capacity > ((int64_t)1 << 31) - 64)
+      return fail(FMKV_ERR_INVALID_ARG, "capacity must be < 2^31 - 64");
+  }
+  return FMKV_OK;
+}
+
+int64_t n_slots_of(const fmkv_cache_desc& d) {
+  return d.window > 0 ? (int64_t)d.window : fmkv::round_up(d.capacity, fmkv::kBlockTokens);
+}
+
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 256;
+  return cus;
+}
+
+// Split-K plan: about two work-groups per CU, at least 2 blocks each.
+int32_t choose_bps(int64_t total_head_blocks, int cus) {
+  if (g_bps_override > 0) return g_bps_override;
+  const int64_t target = 2 * (int64_t)cus;
+  int64_t bps = (total_head_blocks + target - 1) / target;
+  if (bps < 2) bps = 2;
+  return (int32_t)bps;
+}
+
+struct Workspace {
+  float* ptr = nullptr;
+  size_t bytes = 0;
+  int ensure(size_t need) {
+    if (need <= bytes) return FMKV_OK;
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+    hipError_t e = hipMalloc(&ptr, need);
+    if (e != hipSuccess) return fail(FMKV_ERR_OOM, "split workspace allocation failed");
+    bytes = need;
+    return FMKV_OK;
+  }
+  void release() {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+  }
+};
+
+}  // namespace
+
+struct fmkv_cache {
+  fmkv_cache_desc desc;
+  BlockLayout layout;
+  uint8_t* arena;
+  int64_t n_blocks;
+  float* d_signs;
+  float c, sqrt_d;
+  int64_t offset;
+  int64_t vis_begin;
+  Workspace ws;
+  int cus;
+};
+
+struct fmkv_pool {
+  fmkv_cache_desc desc;
+  BlockLayout layout;
+  uint8_t* arena;
+  int64_t n_blocks;
+  float* d_signs;
+  float c, sqrt_d;
+  Workspace ws;
+  int cus;
+};
+
+namespace {
+
+fmkv::Store cache_store(const fmkv_cache* c) {
+  fmkv::Store s;
+  s.base = c->arena;
+  s.block_stride = c->layout.block_bytes;
+  s.head_stride = c->n_blocks * c->layout.block_bytes;
+  s.block_table = nullptr;
+  s.table_stride = 0;
+  s.n_blocks = c->n_blocks;
+  s.n_kv_heads = c->desc.n_kv_heads;
+  s.layout = c->layout;
+  return s;
+}
+
+fmkv::Store pool_store(const fmkv_pool* p, const int32_t* table, int32_t stride) {
+  fmkv::Store s;
+  s.base = p->arena;
+  s.block_stride = p->layout.block_bytes * p->desc.n_kv_heads;
+  s.head_stride = p->layout.block_bytes;
+  s.block_table = table;
+  s.table_stride = stride;
+  s.n_blocks = p->n_blocks;
+  s.n_kv_heads = p->desc.n_kv_heads;
+  s.layout = p->layout;
+  return s;
+}
+
+int64_t visible_begin(const fmkv_cache* c) {
+  int64_t b = c->vis_begin;
+  if (c->desc.window > 0 && c->offset - c->desc.window > b) b = c->offset - c->desc.window;
+  return b < 0 ? 0 : b;
+}
+
+int make_signs(const fmkv_cache_desc& d, float** out) {
+  std::vector<float> s = lcg_signs(d.head_dim, d.sign_seed);
+  hipError_t e = hipMalloc(out, sizeof(float) * d.head_dim);
+  if (e != hipSuccess) return fail(FMKV_ERR_OOM, "sign vector allocation failed");
+  e = hipMemcpy(*out, s.data(), sizeof(float) * d.head_dim, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpy(signs)");
+  return FMKV_OK;
+}
+
+int check_attn_args(const fmkv_cache_desc& d, const void* q, int32_t n_q_heads, float tau,
+                    const void* out, int32_t out_dtype) {
+  if (!q || !out) return fail(FMKV_ERR_INVALID_ARG, "q/out must be device pointers");
+  if (d.mode != FMKV_MODE_AFFINE)
+    return fail(FMKV_ERR_UNSUPPORTED, "decode attention reads affine-mode caches");
+  if (n_q_heads < d.n_kv_heads || n_q_heads % d.n_kv_heads != 0)
+    return fail(FMKV_ERR_INVALID_ARG, "n_q_heads must be a multiple of n_kv_heads");
+  if (n_q_heads / d.n_kv_heads > 8)
+    return fail(FMKV_ERR_UNSUPPORTED, "at most 8 query heads per KV head");
+  if (tau != 0.0f) return fail(FMKV_ERR_UNSUPPORTED, "sparse-V threshold is not implemented");
+  if (out_dtype != FMKV_DTYPE_BF16 && out_dtype != FMKV_DTYPE_F32)
+    return fail(FMKV_ERR_INVALID_ARG, "out_dtype must be FMKV_DTYPE_BF16 or FMKV_DTYPE_F32");
+  return FMKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fmkv_last_error(void) { return g_err.c_str(); }
+
+int fmkv_validate_desc(const fmkv_cache_desc* desc) { return check_desc(desc); }
+
+int fmkv_layout_bytes(const fmkv_cache_desc* desc, int64_t* block_bytes, int64_t* arena_bytes) {
+  int rc = check_desc(desc);
+  if (rc) return rc;
+  const BlockLayout L = fmkv::make_layout(desc->head_dim, desc->bits, desc->mode);
+  if (block_bytes) *block_bytes = L.block_bytes;
+  if (arena_bytes)
+    *arena_bytes = L.block_bytes * desc->n_kv_heads * (n_slots_of(*desc) / fmkv::kBlockTokens);
+  return FMKV_OK;
+}
+
+int fmkv_cache_create(const fmkv_cache_desc* desc, fmkv_cache** out) {
+  int rc = check_desc(desc);
+  if (rc) return rc;
+  if (!out) return fail(FMKV_ERR_INVALID_ARG, "out is null");
+  *out = nullptr;
+  fmkv_cache* c = new fmkv_cache();
+  c->desc = *desc;
+  c->layout = fmkv::make_layout(desc->head_dim, desc->bits, desc->mode);
+  c->n_blocks = n_slots_of(*desc) / fmkv::kBlockTokens;
+  c->c = 1.0f / std::sqrt((float)desc->head_dim);
+  c->sqrt_d = std::sqrt((float)desc->head_dim);
+  c->offset = 0;
+  c->vis_begin = 0;
+  c->arena = nullptr;
+  c->d_signs = nullptr;
+  const int64_t bytes = c->layout.block_bytes * c->n_blocks * desc->n_kv_heads;
+  hipError_t e = hipMalloc(&c->arena, bytes);
+  if (e != hipSuccess) {
+    delete c;
+    return fail(FMKV_ERR_OOM, "cache arena allocation failed (" + std::to_string(bytes) + " bytes)");
+  }
+  e = hipMemset(c->arena, 0, bytes);
+  if (e != hipSuccess) {
+    (void)hipFree(c->arena);
+    delete c;
+    return hip_fail(e, "hipMemset(arena)");
+  }
+  rc = make_signs(*desc, &c->d_signs);
+  if (rc) {
+    (void)hipFree(c->arena);
+    delete c;
+    return rc;
+  }
+  c->cus = device_cus();
+  *out = c;
+  return FMKV_OK;
+}
+
+int fmkv_cache_destroy(fmkv_cache* c) {
+  if (!c) return FMKV_OK;
+  if (c->arena) (void)hipFree(c->arena);
+  if (c->d_signs) (void)hipFree(c->d_signs);
+  c->ws.release();
+  delete c;
+  return FMKV_OK;
+}
+
+int fmkv_cache_offset(const fmkv_cache* c, int64_t* out) {
+  if (!c || !out) return fail(FMKV_ERR_INVALID_ARG, "null argument");
+  *out = c->offset;
+  return FMKV_OK;
+}
+
+int fmkv_cache_stored_len(const fmkv_cache* c, int64_t* out) {
+  if (!c || !out) return fail(FMKV_ERR_INVALID_ARG, "null argument");
+  *out = c->offset - visible_begin(c);
+  return FMKV_OK;
+}
+
+int fmkv_cache_append(fmkv_cache* c, const void* k, const void* v, int64_t n, void* stream) {
+  if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
+  if (n < 0) return fail(FMKV_ERR_INVALID_ARG, "n_tokens must be >= 0");
+  if (n == 0) return FMKV_OK;
+  if (!k || !v) return fail(FMKV_ERR_INVALID_ARG, "k/v must be device pointers");
+  if (n > ((int64_t)1 << 30)) return fail(FMKV_ERR_INVALID_ARG, "n_tokens too large");
+  const int64_t W = c->desc.window;
+  if (W == 0 && c->offset + n > c->desc.capacity)
+    return fail(FMKV_ERR_CAPACITY, "append of " + std::to_string(n) + " tokens at offset " +
+                                       std::to_string(c->offset) + " exceeds capacity " +
+                                       std::to_string(c->desc.capacity));
+  if (c->offset + n > ((int64_t)1 << 31) - 64)
+    return fail(FMKV_ERR_CAPACITY, "position counter would exceed 2^31");
+  fmkv::AppendArgs a;
+  a.st = cache_store(c);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.start_pos = nullptr;
+  a.start_scalar = c->offset;
+  a.n_new = (int32_t)n;
+  a.window = (int32_t)W;
+  a.signs = c->d_signs;
+  a.c = c->c;
+  a.sqrt_d = c->sqrt_d;
+  a.cb_bits = c->desc.bits;
+  int64_t tasks;
+  if (W > 0) {
+    const int64_t n_eff = n < W ? n : W;
+    tasks = (n_eff + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens + 1;
+    if (tasks > W / fmkv::kBlockTokens) tasks = W / fmkv::kBlockTokens;
+  } else {
+    tasks = (c->offset + n - 1) / fmkv::kBlockTokens - c->offset / fmkv::kBlockTokens + 1;
+  }
+  hipError_t e = fmkv::launch_append(a, 1, (int)tasks, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "append launch");
+  c->offset += n;
+  return FMKV_OK;
+}
+
+int fmkv_cache_trim(fmkv_cache* c, int64_t keep_last) {
+  if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
+  if (keep_last < 0) return fail(FMKV_ERR_INVALID_ARG, "keep_last must be >= 0");
+  const int64_t b = c->offset - keep_last;
+  if (b > c->vis_begin) c->vis_begin = b;
+  return FMKV_OK;
+}
+
+int fmkv_decode_attention(fmkv_cache* c, const void* q, int32_t n_q_heads, float scale, float tau,
+                          void* out, int32_t out_dtype, void* stream) {
+  if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
+  int rc = check_attn_args(c->desc, q, n_q_heads, tau, out, out_dtype);
+  if (rc) return rc;
+  const int H = c->desc.n_kv_heads, D = c->desc.head_dim;
+  fmkv::AttnArgs a;
+  a.st = cache_store(c);
+  a.seq_lens = nullptr;
+  a.seq_len = c->offset;
+  a.window = c->desc.window;
+  a.vis_begin = c->vis_begin;
+  a.group = n_q_heads / H;
+  a.n_q_heads = n_q_heads;
+  a.q = static_cast<const uint16_t*>(q);
+  a.qscale = scale * 1.4426950408889634f;
+  a.signs = c->d_signs;
+  a.c = c->c;
+  int64_t filled = c->desc.window > 0 ? std::min<int64_t>(c->offset, c->desc.window) : c->offset;
+  int64_t vb = c->desc.window > 0 ? 0 : c->vis_begin;
+  int64_t nblk = (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
+  if (nblk < 1) nblk = 1;
+  a.bps = choose_bps(nblk * H, c->cus);
+  a.max_splits = (int32_t)((nblk + a.bps - 1) / a.bps);
+  a.direct = a.max_splits == 1;
+  a.out = out;
+  a.out_f32 = out_dtype == FMKV_DTYPE_F32;
+  a.part_o = nullptr;
+  a.part_ml = nullptr;
+  if (!a.direct) {
+    const size_t n_rows = (size_t)a.max_splits * n_q_heads;
+    rc = c->ws.ensure(n_rows * (D + 2) * sizeof(float));
+    if (rc) return rc;
+    a.part_o = c->ws.ptr;
+    a.part_ml = c->ws.ptr + n_rows * D;
+  }
+  hipEvent_t e0, e1;
+  next_events(&e0, &e1);
+  hipError_t e = fmkv::launch_decode_attention(a, 1, H, static_cast<hipStream_t>(stream), e0, e1);
+  if (e != hipSuccess) return hip_fail(e, "decode attention launch");
+  return FMKV_OK;
+}
+
+int fmkv_cache_decode_splits(const fmkv_cache* c, int32_t* n_splits) {
+  if (!c || !n_splits) return fail(FMKV_ERR_INVALID_ARG, "null argument");
+  int64_t filled = c->desc.window > 0 ? std::min<int64_t>(c->offset, c->desc.window) : c->offset;
+  int64_t vb = c->desc.window > 0 ? 0 : c->vis_begin;
+  int64_t nblk = (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
+  if (nblk < 1) nblk = 1;
+  const int32_t bps = choose_bps(nblk * c->desc.n_kv_heads, c->cus);
+  *n_splits = (int32_t)((nblk + bps - 1) / bps);
+  return FMKV_OK;
+}
+
+int fmkv_cache_fetch(const fmkv_cache* c, void* k_out, void* v_out, int32_t out_dtype, void* stream) {
+  if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
+  if (!k_out || !v_out) return fail(FMKV_ERR_INVALID_ARG, "k_out/v_out must be device pointers");
+  if (out_dtype != FMKV_DTYPE_BF16 && out_dtype != FMKV_DTYPE_F32)
+    return fail(FMKV_ERR_INVALID_ARG, "bad out_dtype");
+  fmkv::FetchArgs a;
+  a.st = cache_store(c);
+  a.offset = c->offset;
+  a.window = c->desc.window;
+  a.first_pos = visible_begin(c);
+  a.n_pos = c->offset - a.first_pos;
+  a.signs = c->d_signs;
+  a.c = c->c;
+  a.k_out = k_out;
+  a.v_out = v_out;
+  a.out_f32 = out_dtype == FMKV_DTYPE_F32;
+  hipError_t e = fmkv::launch_fetch(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "fetch launch");
+  return FMKV_OK;
+}
+
+int fmkv_cache_read_codes(const fmkv_cache* c, void* codes, void* meta, void* stream) {
+  if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
+  if (!codes || !meta) return fail(FMKV_ERR_INVALID_ARG, "codes/meta must be device pointers");
+  fmkv::ReadArgs a;
+  a.st = cache_store(c);
+  a.n_slots = c->desc.window > 0 ? c->desc.window : c->desc.capacity;
+  a.codes = static_cast<uint32_t*>(codes);
+  a.meta = static_cast<uint16_t*>(meta);
+  hipError_t e = fmkv::launch_read_codes(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "read_codes launch");
+  return FMKV_OK;
+}
+
+int fmkv_pool_create(const fmkv_cache_desc* desc, int64_t n_blocks, fmkv_pool** out) {
+  if (!desc) return fail(FMKV_ERR_INVALID_ARG, "descriptor is null");
+  fmkv_cache_desc d = *desc;
+  d.window = 0;
+  d.capacity = 1;
+  int rc = check_desc(&d);
+  if (rc) return rc;
+  if (desc->window != 0) return fail(FMKV_ERR_UNSUPPORTED, "paged pools hold global (linear) sequences");
+  if (!out) return fail(FMKV_ERR_INVALID_ARG, "out is null");
+  if (n_blocks < 1 || n_blocks > ((int64_t)1 << 31) - 1)
+    return fail(FMKV_ERR_INVALID_ARG, "n_blocks must be in [1, 2^31)");
+  *out = nullptr;
+  fmkv_pool* p = new fmkv_pool();
+  p->desc = *desc;
+  p->layout = fmkv::make_layout(desc->head_dim, desc->bits, desc->mode);
+  p->n_blocks = n_blocks;
+  p->c = 1.0f / std::sqrt((float)desc->head_dim);
+  p->sqrt_d = std::sqrt((float)desc->head_dim);
+  p->arena = nullptr;
+  p->d_signs = nullptr;
+  const int64_t bytes = p->layout.block_bytes * desc->n_kv_heads * n_blocks;
+  hipError_t e = hipMalloc(&p->arena, bytes);
+  if (e != hipSuccess) {
+    delete p;
+    return fail(FMKV_ERR_OOM, "pool allocation failed (" + std::to_string(bytes) + " bytes)");
+  }
+  e = hipMemset(p->arena, 0, bytes);
+  if (e != hipSuccess) {
+    (void)hipFree(p->arena);
+    delete p;
+    return hip_fail(e, "hipMemset(pool)");
+  }
+  rc = make_signs(*desc, &p->d_signs);
+  if (rc) {
+    (void)hipFree(p->arena);
+    delete p;
+    return rc;
+  }
+  p->cus = device_cus();
+  *out = p;
+  return FMKV_OK;
+}
+
+int fmkv_pool_destroy(fmkv_pool* p) {
+  if (!p) return FMKV_OK;
+  if (p->arena) (void)hipFree(p->arena);
+  if (p->d_signs) (void)hipFree(p->d_signs);
+  p->ws.release();
+  delete p;
+  return FMKV_OK;
+}
+
+int fmkv_paged_append(fmkv_pool* p, const void* k, const void* v, const int32_t* block_tables,
+                      int32_t max_blocks, const int32_t* start_pos, int32_t n_seqs, int32_t n_new,
+                      void* stream) {
+  if (!p) return fail(FMKV_ERR_INVALID_ARG, "pool is null");
+  if (n_seqs < 0 || n_new < 0 || max_blocks < 1)
+    return fail(FMKV_ERR_INVALID_ARG, "n_seqs/n_new must be >= 0 and max_blocks >= 1");
+  if (n_seqs == 0 || n_new == 0) return FMKV_OK;
+  if (!k || !v || !block_tables || !start_pos)
+    return fail(FMKV_ERR_INVALID_ARG, "k/v/block_tables/start_pos must be device pointers");
+  if (n_seqs > 65535) return fail(FMKV_ERR_INVALID_ARG, "at most 65535 sequences per call");
+  fmkv::AppendArgs a;
+  a.st = pool_store(p, block_tables, max_blocks);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.start_pos = start_pos;
+  a.start_scalar = 0;
+  a.n_new = n_new;
+  a.window = 0;
+  a.signs = p->d_signs;
+  a.c = p->c;
+  a.sqrt_d = p->sqrt_d;
+  a.cb_bits = p->desc.bits;
+  const int tasks = (n_new + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens + 1;
+  hipError_t e = fmkv::launch_append(a, n_seqs, tasks, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "paged append launch");
+  return FMKV_OK;
+}
+
+int fmkv_paged_decode_attention(fmkv_pool* p, const void* q, const int32_t* block_tables,
+                                int32_t max_blocks, const int32_t* seq_lens, int32_t n_seqs,
+                                int32_t max_seq_len, int32_t n_q_heads, float scale, float tau,
+                                void* out, int32_t out_dtype, void* stream) {
+  if (!p) return fail(FMKV_ERR_INVALID_ARG, "pool is null");
+  int rc = check_attn_args(p->desc, q, n_q_heads, tau, out, out_dtype);
+  if (rc) return rc;
+  if (n_seqs < 0 || max_seq_len < 0 || max_blocks < 1)
+    return fail(FMKV_ERR_INVALID_ARG, "bad n_seqs / max_seq_len / max_blocks");
+  if (n_seqs == 0) return FMKV_OK;
+  if (!block_tables || !seq_lens) return fail(FMKV_ERR_INVALID_ARG, "block_tables/seq_lens are null");
+  if ((int64_t)max_seq_len > (int64_t)max_blocks * fmkv::kBlockTokens)
+    return fail(FMKV_ERR_INVALID_ARG, "max_seq_len exceeds max_blocks * 16");
+  if (n_seqs > 65535) return fail(FMKV_ERR_INVALID_ARG, "at most 65535 sequences per call");
+  const int H = p->desc.n_kv_heads, D = p->desc.head_dim;
+  fmkv::AttnArgs a;
+  a.st = pool_store(p, block_tables, max_blocks);
+  a.seq_lens = seq_lens;
+  a.seq_len = 0;
+  a.window = 0;
+  a.vis_begin = 0;
+  a.group = n_q_heads / H;
+  a.n_q_heads = n_q_heads;
+  a.q = static_cast<const uint16_t*>(q);
+  a.qscale = scale * 1.4426950408889634f;
+  a.signs = p->d_signs;
+  a.c = p->c;
+  int64_t nblk = (max_seq_len + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens;
+  if (nblk < 1) nblk = 1;
+  a.bps = choose_bps(nblk * H * n_seqs, p->cus);
+  a.max_splits = (int32_t)((nblk + a.bps - 1) / a.bps);
+  a.direct = a.max_splits == 1;
+  a.out = out;
+  a.out_f32 = out_dtype == FMKV_DTYPE_F32;
+  a.part_o = nullptr;
+  a.part_ml = nullptr;
+  if (!a.direct) {
+    const size_t n_rows = (size_t)n_seqs * a.max_splits * n_q_heads;
+    rc = p->ws.ensure(n_rows * (D + 2) * sizeof(float));
+    if (rc) return rc;
+    a.part_o = p->ws.ptr;
+    a.part_ml = p->ws.ptr + n_rows * D;
+  }
+  hipEvent_t e0, e1;
+  next_events(&e0, &e1);
+  hipError_t e =
+      fmkv::launch_decode_attention(a, n_seqs, H, static_cast<hipStream_t>(stream), e0, e1);
+  if (e != hipSuccess) return hip_fail(e, "paged decode attention launch");
+  return FMKV_OK;
+}
+
+int fmkv_pool_read_codes(const fmkv_pool* p, void* codes, void* meta, void* stream) {
+  if (!p) return fail(FMKV_ERR_INVALID_ARG, "pool is null");
+  if (!codes || !meta) return fail(FMKV_ERR_INVALID_ARG, "codes/meta must be device pointers");
+  fmkv::ReadArgs a;
+  a.st = pool_store(p, nullptr, 0);
+  a.n_slots = p->n_blocks * fmkv::kBlockTokens;
+  a.codes = static_cast<uint32_t*>(codes);
+  a.meta = static_cast<uint16_t*>(meta);
+  hipError_t e = fmkv::launch_read_codes(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "pool read_codes launch");
+  return FMKV_OK;
+}
+
+int fmkv_set_blocks_per_split(int32_t bps) {
+  if (bps < 0) return fail(FMKV_ERR_INVALID_ARG, "blocks_per_split must be >= 0");
+  g_bps_override = bps;
+  return FMKV_OK;
+}
+
+int fmkv_profile_enable(int32_t max_records) {
+  if (max_records < 0 || max_records > (1 << 20))
+    return fail(FMKV_ERR_INVALID_ARG, "max_records must be in [0, 2^20]");
+  g_prof.clear_events();
+  g_prof.max_records = 0;
+  if (max_records == 0) return FMKV_OK;
+  g_prof.ev.resize(2 * (size_t)max_records, nullptr);
+  for (size_t i = 0; i < g_prof.ev.size(); i++) {
+    hipError_t e = hipEventCreate(&g_prof.ev[i]);
+    if (e != hipSuccess) {
+      g_prof.ev.resize(i);
+      g_prof.clear_events();
+      return hip_fail(e, "hipEventCreate");
+    }
+  }
+  g_prof.max_records = max_records;
+  return FMKV_OK;
+}
+
+int fmkv_profile_collect(double* total_ms, int32_t* n_records) {
+  if (!total_ms || !n_records) return fail(FMKV_ERR_INVALID_ARG, "null argument");
+  double sum = 0.0;
+  for (int32_t i = 0; i < g_prof.used; i++) {
+    hipError_t e = hipEventSynchronize(g_prof.ev[2 * (size_t)i + 1]);
+    if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+    float ms = 0.0f;
+    e = hipEventElapsedTime(&ms, g_prof.ev[2 * (size_t)i], g_prof.ev[2 * (size_t)i + 1]);
+    if (e != hipSuccess) return hip_fail(e, "hipEventElapsedTime");
+    sum += ms;
+  }
+  *total_ms = sum;
+  *n_records = g_prof.used;
+  g_prof.used = 0;
+  return FMKV_OK;
+}
+
+}  // extern "C"

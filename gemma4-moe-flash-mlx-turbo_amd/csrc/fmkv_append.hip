@@ -1,0 +1,335 @@
+// Append kernel: rotate -> quantize -> slot write, one work-group per
+// (touched head-block, KV head, sequence).
+//
+// Replaces the store half of KVCache::update_and_fetch (src/cache.rs:266-310)
+// and its quantizer turbo_round_trip_kv (src/cache.rs:94-129):
+//  - rotation x.R (R from build_rht, src/cache.rs:47-62) as an in-wave fast
+//    Walsh-Hadamard transform, stages h = 1, 2, ..., D/2 (registers first,
+//    then lane exchanges), then * (1/sqrt D) and the LCG sign;
+//  - affine mode: MLX group-64 affine quantization (4/8-bit, f16 scale/bias);
+//  - codebook mode: the reference's own TurboQuant Lloyd-Max binning;
+//  - slot write: ring slot pos % W for sliding layers, pos for global layers,
+//    block table for paged pools.
+// Every float op is written out in the oracle's order and the file is built
+// with -ffp-contract=off, so codes and scales are bit-identical to it.
+#include "fmkv_device.h"
+#include "fmkv_internal.h"
+
+namespace fmkv {
+namespace {
+
+constexpr int kAppendThreads = 256;
+
+__constant__ float kCbBounds2[3] = {-0.982f, 0.0f, 0.982f};
+__constant__ float kCbBounds3[7] = {-1.748f, -1.050f, -0.501f, 0.0f, 0.501f, 1.050f, 1.748f};
+__constant__ float kCbBounds4[15] = {-2.401f, -1.844f, -1.437f, -1.099f, -0.800f,
+                                     -0.522f, -0.258f, 0.0f,    0.258f,  0.522f,
+                                     0.800f,  1.099f,  1.437f,  1.844f,  2.401f};
+
+// Canonical unnormalised FWHT of a row held as E contiguous values per lane.
+template <int E>
+__device__ inline void wave_fwht(float (&x)[E], int lane) {
+#pragma unroll
+  for (int h = 1; h < E; h <<= 1)
+#pragma unroll
+    for (int i = 0; i < E; i += 2 * h)
+#pragma unroll
+      for (int jj = i; jj < i + h; jj++) {
+        float a = x[jj], b = x[jj + h];
+        x[jj] = a + b;
+        x[jj + h] = a - b;
+      }
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const bool upper = (lane & m) != 0;
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      float p = __shfl_xor(x[i], m);
+      x[i] = upper ? (p - x[i]) : (x[i] + p);
+    }
+  }
+}
+
+template <int E>
+__device__ inline void load_row(const uint16_t* src, float (&x)[E]) {
+  if constexpr (E == 8) {
+    uint4 u = *reinterpret_cast<const uint4*>(src);
+    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      x[2 * i] = __uint_as_float(w[i] << 16);
+      x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  } else if constexpr (E == 4) {
+    uint2 u = *reinterpret_cast<const uint2*>(src);
+    x[0] = __uint_as_float(u.x << 16);
+    x[1] = __uint_as_float(u.x & 0xffff0000u);
+    x[2] = __uint_as_float(u.y << 16);
+    x[3] = __uint_as_float(u.y & 0xffff0000u);
+  } else {
+    uint32_t u = *reinterpret_cast<const uint32_t*>(src);
+    x[0] = __uint_as_float(u << 16);
+    x[1] = __uint_as_float(u & 0xffff0000u);
+  }
+}
+
+// MLX affine_quantize for the group spanning 64/E lanes (see oracle).
+template <int E, int BITS>
+__device__ inline void affine_quant(const float (&y)[E], uint32_t (&code)[E], float& scale_o,
+                                    float& bias_o) {
+  constexpr int kLanesPerGroup = 64 / E;
+  float mx = y[0], mn = y[0];
+#pragma unroll
+  for (int i = 1; i < E; i++) {
+    mx = fmaxf(mx, y[i]);
+    mn = fminf(mn, y[i]);
+  }
+#pragma unroll
+  for (int m = 1; m < kLanesPerGroup; m <<= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, m));
+    mn = fminf(mn, __shfl_xor(mn, m));
+  }
+  const float n_bins = (float)((1 << BITS) - 1);
+  float scale = fmaxf((mx - mn) / n_bins, 1e-7f);
+  const bool side = fabsf(mn) > fabsf(mx);
+  scale = side ? scale : -scale;
+  const float edge = side ? mn : mx;
+  const float q0 = rintf(edge / scale);
+  float bias = 0.0f;
+  if (q0 != 0.0f) {
+    scale = edge / q0;
+    bias = edge;
+  }
+#pragma unroll
+  for (int i = 0; i < E; i++) {
+    float q = rintf((y[i] - bias) / scale);
+    q = fminf(fmaxf(q, 0.0f), n_bins);
+    code[i] = (uint32_t)q;
+  }
+  scale_o = scale;
+  bias_o = bias;
+}
+
+// Sum of squares in the oracle's order: per-lane left to right, then a
+// xor-butterfly over all 64 lanes.
+template <int E>
+__device__ inline float canonical_sumsq(const float (&x)[E]) {
+  float acc = x[0] * x[0];
+#pragma unroll
+  for (int i = 1; i < E; i++) {
+    float sq = x[i] * x[i];
+    acc = acc + sq;
+  }
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) acc = acc + __shfl_xor(acc, m);
+  return acc;
+}
+
+__device__ inline int cb_index(float z, int bits) {
+  int idx = 0;
+  if (bits == 2) {
+#pragma unroll
+    for (int b = 0; b < 3; b++) idx += (z >= kCbBounds2[b]) ? 1 : 0;
+  } else if (bits == 3) {
+#pragma unroll
+    for (int b = 0; b < 7; b++) idx += (z >= kCbBounds3[b]) ? 1 : 0;
+  } else {
+#pragma unroll
+    for (int b = 0; b < 15; b++) idx += (z >= kCbBounds4[b]) ? 1 : 0;
+  }
+  return idx;
+}
+
+// Token owning 32-bit word w of an affine V-code region, for byte/nibble k.
+template <int BITS>
+__device__ inline uint32_t v_clear_mask(int w, const int* cov) {
+  const int q = ((w & 255) >> 2) >> 4;
+  uint32_t m = 0;
+  if constexpr (BITS == 8) {
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      if (cov[4 * q + r] >= 0) m |= 0xffu << (8 * r);
+  } else {
+#pragma unroll
+    for (int p = 0; p < 8; p++)
+      if (cov[4 * q + 2 * (p & 1) + (p >> 2)] >= 0) m |= 0xfu << (4 * p);
+  }
+  return m;
+}
+
+template <int D, int BITS, int MODE>
+__global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
+  constexpr int E = D / 64;
+  constexpr BlockLayout L = make_layout(D, BITS, MODE);
+  constexpr int kWords = (int)(L.code_bytes / 4);
+  __shared__ uint32_t kst[kWords];
+  __shared__ uint32_t vst[kWords];
+  __shared__ int cov_row[kBlockTokens];
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int h = blockIdx.y, seq = blockIdx.z, bx = blockIdx.x;
+  const int64_t pos0 = a.start_pos ? (int64_t)a.start_pos[seq] : a.start_scalar;
+  const int64_t end = pos0 + a.n_new;
+  const int64_t W = a.window;
+  if (a.n_new <= 0) return;
+
+  int64_t lb, e0 = pos0, s0 = 0;
+  if (W > 0) {
+    e0 = end - W > pos0 ? end - W : pos0;
+    const int64_t n_eff = end - e0;
+    s0 = e0 % W;
+    const int64_t nb_ring = W / kBlockTokens;
+    const int64_t first = s0 / kBlockTokens, last = (s0 + n_eff - 1) / kBlockTokens;
+    int64_t count = last - first + 1;
+    if (count > nb_ring) count = nb_ring;
+    if (bx >= count) return;
+    lb = (first + bx) % nb_ring;
+  } else {
+    const int64_t first = pos0 / kBlockTokens, last = (end - 1) / kBlockTokens;
+    if (bx > last - first) return;
+    lb = first + bx;
+  }
+
+  if (tid < kBlockTokens) {
+    const int64_t slot = lb * kBlockTokens + tid;
+    int64_t p = (W > 0) ? e0 + ((slot - s0) % W + W) % W : slot;
+    const bool covered = p >= e0 && p < end;
+    cov_row[tid] = covered ? (int)(p - pos0) : -1;
+  }
+  int64_t phys = lb;
+  if (a.st.block_table) {
+    // caller-owned table: positions past its width or entries outside the
+    // pool are not written (no out-of-bounds access on bad input)
+    if (lb >= a.st.table_stride) return;
+    phys = (int64_t)a.st.block_table[(int64_t)seq * a.st.table_stride + lb];
+  }
+  if (phys < 0 || phys >= a.st.n_blocks) return;
+  uint8_t* blk = a.st.base + phys * a.st.block_stride + (int64_t)h * a.st.head_stride;
+  __syncthreads();
+
+  bool all_cov = true;
+#pragma unroll
+  for (int t = 0; t < kBlockTokens; t++) all_cov = all_cov && (cov_row[t] >= 0);
+
+  for (int w = tid; w < kWords; w += kAppendThreads) {
+    kst[w] = 0u;
+    if constexpr (MODE == kAffine) {
+      const uint32_t old =
+          all_cov ? 0u : reinterpret_cast<const uint32_t*>(blk + L.v_codes)[w];
+      vst[w] = old & ~v_clear_mask<BITS>(w, cov_row);
+    } else {
+      vst[w] = 0u;
+    }
+  }
+  __syncthreads();
+
+  const int H = a.st.n_kv_heads;
+  for (int r = wv; r < 2 * kBlockTokens; r += kAppendThreads / 64) {
+    const int t = r >> 1, isv = r & 1;
+    const int row = cov_row[t];
+    if (row < 0) continue;
+    const uint16_t* src =
+        (isv ? a.v : a.k) + (((int64_t)seq * a.n_new + row) * H + h) * D + lane * E;
+    float x[E];
+    load_row<E>(src, x);
+    uint32_t* stage = isv ? vst : kst;
+    if constexpr (MODE == kAffine) {
+      wave_fwht<E>(x, lane);
+#pragma unroll
+      for (int i = 0; i < E; i++) x[i] = (x[i] * a.c) * a.signs[lane * E + i];
+      uint32_t code[E];
+      float scale, bias;
+      affine_quant<E, BITS>(x, code, scale, bias);
+#pragma unroll
+      for (int i = 0; i < E; i++) {
+        int64_t off;
+        int sh;
+        if (isv)
+          v_code_pos(BITS, t, lane * E + i, &off, &sh);
+        else
+          k_code_pos(BITS, t, lane * E + i, &off, &sh);
+        atomicOr(&stage[off >> 2], code[i] << sh);
+      }
+      if ((lane % (64 / E)) == 0) {
+        const int g = lane / (64 / E);
+        const uint32_t sb = (uint32_t)f32_to_f16_bits(scale) |
+                            ((uint32_t)f32_to_f16_bits(bias) << 16);
+        *reinterpret_cast<uint32_t*>(blk + (isv ? L.v_meta : L.k_meta) + scale_pos(g, t)) = sb;
+      }
+    } else {
+      constexpr int bits = BITS;
+      const float norm = sqrtf(canonical_sumsq<E>(x));
+      const float den = norm + 1e-8f;
+#pragma unroll
+      for (int i = 0; i < E; i++) x[i] = x[i] / den;
+      wave_fwht<E>(x, lane);
+      const int64_t row_bits = (int64_t)D * bits;
+#pragma unroll
+      for (int i = 0; i < E; i++) {
+        const float z = ((x[i] * a.c) * a.signs[lane * E + i]) * a.sqrt_d;
+        const uint32_t idx = (uint32_t)cb_index(z, bits);
+        const int64_t bit = t * row_bits + (int64_t)(lane * E + i) * bits;
+        const int wi = (int)(bit >> 5), off = (int)(bit & 31);
+        atomicOr(&stage[wi], idx << off);
+        if (off + bits > 32) atomicOr(&stage[wi + 1], idx >> (32 - off));
+      }
+      if (lane == 0)
+        *reinterpret_cast<uint16_t*>(blk + (isv ? L.v_meta : L.k_meta) + t * 2) =
+            f32_to_f16_bits(norm);
+    }
+  }
+  __syncthreads();
+
+  uint32_t* kdst = reinterpret_cast<uint32_t*>(blk + L.k_codes);
+  uint32_t* vdst = reinterpret_cast<uint32_t*>(blk + L.v_codes);
+  for (int w = tid; w < kWords; w += kAppendThreads) {
+    int tk;
+    if constexpr (MODE == kAffine) {
+      tk = ((w & 255) >> 2) & 15;
+      vdst[w] = vst[w];
+    } else {
+      tk = (int)((int64_t)w * 4 / (L.code_bytes / kBlockTokens));
+      if (cov_row[tk] >= 0) vdst[w] = vst[w];
+    }
+    if (cov_row[tk] >= 0) kdst[w] = kst[w];
+  }
+}
+
+template <int D, int BITS, int MODE>
+hipError_t launch_t(const AppendArgs& a, int n_seqs, int max_tasks, hipStream_t s) {
+  dim3 grid(max_tasks, a.st.n_kv_heads, n_seqs);
+  hipLaunchKernelGGL((append_kernel<D, BITS, MODE>), grid, dim3(kAppendThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_append(const AppendArgs& a, int n_seqs, int max_tasks, hipStream_t s) {
+  const BlockLayout& L = a.st.layout;
+  if (max_tasks <= 0 || n_seqs <= 0) return hipSuccess;
+  if (L.mode == kAffine) {
+    switch (L.head_dim * 16 + L.bits) {
+      case 128 * 16 + 4: return launch_t<128, 4, kAffine>(a, n_seqs, max_tasks, s);
+      case 128 * 16 + 8: return launch_t<128, 8, kAffine>(a, n_seqs, max_tasks, s);
+      case 256 * 16 + 4: return launch_t<256, 4, kAffine>(a, n_seqs, max_tasks, s);
+      case 256 * 16 + 8: return launch_t<256, 8, kAffine>(a, n_seqs, max_tasks, s);
+      case 512 * 16 + 4: return launch_t<512, 4, kAffine>(a, n_seqs, max_tasks, s);
+      case 512 * 16 + 8: return launch_t<512, 8, kAffine>(a, n_seqs, max_tasks, s);
+    }
+  } else {
+    switch (L.head_dim * 16 + L.bits) {
+      case 128 * 16 + 2: return launch_t<128, 2, kCodebook>(a, n_seqs, max_tasks, s);
+      case 128 * 16 + 3: return launch_t<128, 3, kCodebook>(a, n_seqs, max_tasks, s);
+      case 128 * 16 + 4: return launch_t<128, 4, kCodebook>(a, n_seqs, max_tasks, s);
+      case 256 * 16 + 2: return launch_t<256, 2, kCodebook>(a, n_seqs, max_tasks, s);
+      case 256 * 16 + 3: return launch_t<256, 3, kCodebook>(a, n_seqs, max_tasks, s);
+      case 256 * 16 + 4: return launch_t<256, 4, kCodebook>(a, n_seqs, max_tasks, s);
+      case 512 * 16 + 2: return launch_t<512, 2, kCodebook>(a, n_seqs, max_tasks, s);
+      case 512 * 16 + 3: return launch_t<512, 3, kCodebook>(a, n_seqs, max_tasks, s);
+      case 512 * 16 + 4: return launch_t<512, 4, kCodebook>(a, n_seqs, max_tasks, s);
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace fmkv

@@ -1,0 +1,119 @@
+// Device helpers shared by the fmkv kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fmkv_layout.h"
+
+namespace fmkv {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+__device__ inline float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// Round-to-nearest-even f32 -> bf16 (NaN kept quiet).
+__device__ inline uint16_t f32_to_bf16(float f) {
+  uint32_t x = __float_as_uint(f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+  x += 0x7fffu + ((x >> 16) & 1u);
+  return (uint16_t)(x >> 16);
+}
+
+__device__ inline uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;  // v_cvt_f16_f32, round to nearest even
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ inline float f16_bits_to_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xffffu));
+}
+
+// Lane l receives the value of lane (l & ~15) | ((l + 8) & 15): the other
+// half of its 16-lane row (DPP row_ror:8).
+__device__ inline float row_ror8(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+}
+
+// Sum / max with the lane 16 (resp. 32) apart: permlane swaps return the
+// pair {own, partner} in some order, so a commutative op gives both lanes the
+// same bits.
+__device__ inline float xor16_sum(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float xor32_sum(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float xor16_max(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float xor32_max(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Two 8-bit codes -> two exact f16 values: v_perm builds {c, 0x64} halves,
+// i.e. 1024 + c, and the packed subtract removes the 1024 exactly.
+// sel 0x04010400 takes bytes (0, 1) of w, 0x04030402 bytes (2, 3).
+__device__ inline half2_t u8x2_to_h2(uint32_t w, uint32_t sel) {
+  uint32_t x = __builtin_amdgcn_perm(0x64646464u, w, sel);
+  return __builtin_bit_cast(half2_t, x) - (half2_t){(_Float16)1024.0f, (_Float16)1024.0f};
+}
+
+// Nibbles k and k + 4 of w -> two exact f16 values (same 1024 trick).
+__device__ inline half2_t u4x2_to_h2(uint32_t w, int k) {
+  uint32_t x = ((w >> (4 * k)) & 0x000F000Fu) | 0x64006400u;
+  return __builtin_bit_cast(half2_t, x) - (half2_t){(_Float16)1024.0f, (_Float16)1024.0f};
+}
+
+__device__ inline half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t d) {
+  return (half8_t){a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+__device__ inline half4_t cat4(half2_t a, half2_t b) { return (half4_t){a[0], a[1], b[0], b[1]}; }
+
+// Visible-position test shared by the attention and combine kernels.
+struct SeqGeom {
+  int64_t blk_lo, blk_hi;  // logical blocks to scan
+};
+
+__device__ inline SeqGeom seq_geometry(int64_t T, int64_t window, int64_t vis_begin) {
+  SeqGeom g;
+  if (window > 0) {
+    int64_t filled = T < window ? T : window;
+    g.blk_lo = 0;
+    g.blk_hi = (filled + kBlockTokens - 1) / kBlockTokens;
+  } else {
+    int64_t vb = vis_begin > 0 ? vis_begin : 0;
+    g.blk_lo = vb / kBlockTokens;
+    g.blk_hi = (T + kBlockTokens - 1) / kBlockTokens;
+    if (g.blk_hi < g.blk_lo) g.blk_hi = g.blk_lo;
+  }
+  return g;
+}
+
+// Blocks to scan for one sequence; paged tables bound it by their width.
+__device__ inline SeqGeom seq_geometry(int64_t T, int64_t window, int64_t vis_begin,
+                                       int32_t table_stride, bool paged) {
+  SeqGeom g = seq_geometry(T, window, vis_begin);
+  if (paged && g.blk_hi > table_stride) g.blk_hi = table_stride;
+  if (g.blk_hi < g.blk_lo) g.blk_hi = g.blk_lo;
+  return g;
+}
+
+// Split count of a sequence (>= 1, so split 0 always writes a result),
+// never more than the grid provides.
+__device__ inline int n_splits_for(const SeqGeom& g, int bps, int max_splits) {
+  int64_t nb = g.blk_hi - g.blk_lo;
+  int64_t ns = (nb + bps - 1) / bps;
+  if (ns < 1) ns = 1;
+  if (ns > max_splits) ns = max_splits;
+  return (int)ns;
+}
+
+}  // namespace fmkv

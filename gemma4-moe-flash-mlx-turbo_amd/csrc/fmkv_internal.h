@@ -1,0 +1,84 @@
+// Kernel argument structs and launchers shared by the fmkv translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fmkv_layout.h"
+
+namespace fmkv {
+
+// Where the head-blocks of one cache / pool live.
+struct Store {
+  uint8_t* base;
+  int64_t head_stride;   // bytes between heads of one logical block
+  int64_t block_stride;  // bytes between physical blocks
+  const int32_t* block_table;  // paged: [n_seqs][table_stride]; null otherwise
+  int32_t table_stride;
+  int64_t n_blocks;            // physical blocks (bounds for table entries)
+  int32_t n_kv_heads;
+  BlockLayout layout;
+};
+
+struct AppendArgs {
+  Store st;
+  const uint16_t* k;  // bf16 [n_seqs][n_new][n_kv_heads][D]
+  const uint16_t* v;
+  const int32_t* start_pos;  // per sequence, or null -> start_scalar
+  int64_t start_scalar;
+  int32_t n_new;
+  int32_t window;   // ring slots, 0 = linear
+  const float* signs;  // [D] +-1
+  float c;             // 1/sqrt(D) (f32)
+  float sqrt_d;        // sqrt(D) (f32), codebook mode
+  int32_t cb_bits;     // codebook bits
+};
+
+struct AttnArgs {
+  Store st;
+  const int32_t* seq_lens;  // per sequence, or null -> seq_len
+  int64_t seq_len;
+  int64_t window;
+  int64_t vis_begin;
+  int32_t group;      // q heads per kv head
+  int32_t n_q_heads;
+  const uint16_t* q;  // bf16 [n_seqs][n_q_heads][D]
+  float qscale;       // softmax scale * log2(e)
+  const float* signs;
+  float c;
+  int32_t bps;        // blocks per split
+  int32_t max_splits;
+  float* part_o;      // [n_seqs][max_splits][n_q_heads][D]
+  float* part_ml;     // [n_seqs][max_splits][n_q_heads][2]
+  void* out;          // [n_seqs][n_q_heads][D]
+  int32_t out_f32;
+  int32_t direct;     // 1: no combine, write out
+};
+
+struct ReadArgs {
+  Store st;
+  int64_t n_slots;    // slots to convert (ring: W; linear: capacity; pool: n_blocks*16)
+  uint32_t* codes;    // [n_slots][2][H][words]
+  uint16_t* meta;     // [n_slots][2][H][n_meta]
+};
+
+struct FetchArgs {
+  Store st;
+  int64_t offset;
+  int64_t window;
+  int64_t first_pos;  // first visible position
+  int64_t n_pos;      // visible positions
+  const float* signs;
+  float c;
+  void* k_out;        // [n_pos][H][D]
+  void* v_out;
+  int32_t out_f32;
+};
+
+hipError_t launch_append(const AppendArgs& a, int n_seqs, int max_tasks, hipStream_t s);
+// ev_begin / ev_end (optional) are recorded around the split-K kernel only.
+hipError_t launch_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
+                                   hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr);
+hipError_t launch_read_codes(const ReadArgs& a, hipStream_t s);
+hipError_t launch_fetch(const FetchArgs& a, hipStream_t s);
+
+}  // namespace fmkv

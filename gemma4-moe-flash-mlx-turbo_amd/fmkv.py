@@ -1,0 +1,346 @@
+"""Python host binding of the fmkv C ABI (include/fmkv.h).
+
+Mirrors the reference's Rust cache API (src/cache.rs:186-310) so callers and
+tests read like the reference:
+
+    cache = KVCache.new_quantized_with_window(head_dim=256, bits=4, window=1024,
+                                              n_kv_heads=8)
+    cache.update_and_fetch(k, v)          # append (store half); returns a view
+    out = cache.attention(q, scale=1.0)   # decode read (SDPA replacement)
+    cache.offset(), cache.stored_len(), cache.peek_kv()
+
+Device memory and streams come from PyTorch (plumbing only): tensors are
+passed to the library as raw device pointers. The HIP library is required;
+nothing here computes on the CPU, and loading fails loudly when libfmkv.so is
+missing.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch  # imported before libfmkv.so so both share torch's HIP runtime
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "libfmkv.so"
+
+FMKV_OK = 0
+FMKV_ERR_INVALID_ARG = 1
+FMKV_ERR_UNSUPPORTED = 2
+FMKV_ERR_OOM = 3
+FMKV_ERR_HIP = 4
+FMKV_ERR_CAPACITY = 5
+MODE_AFFINE = 0
+MODE_CODEBOOK = 1
+DTYPE_BF16 = 0
+DTYPE_F32 = 1
+BLOCK_TOKENS = 16
+
+EXPORTED = (
+    "fmkv_last_error", "fmkv_validate_desc", "fmkv_layout_bytes", "fmkv_cache_create",
+    "fmkv_cache_destroy", "fmkv_cache_offset", "fmkv_cache_stored_len", "fmkv_cache_append",
+    "fmkv_cache_trim", "fmkv_decode_attention", "fmkv_cache_fetch", "fmkv_cache_read_codes",
+    "fmkv_pool_create", "fmkv_pool_destroy", "fmkv_paged_append", "fmkv_paged_decode_attention",
+    "fmkv_pool_read_codes", "fmkv_set_blocks_per_split", "fmkv_cache_decode_splits",
+    "fmkv_profile_enable", "fmkv_profile_collect",
+)
+
+
+class Exception_(RuntimeError):
+    """Error raised for a non-zero fmkv status (mirrors mlx_rs::error::Exception)."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"fmkv error {code}: {msg}")
+        self.code = code
+
+
+class CacheDesc(ctypes.Structure):
+    _fields_ = [
+        ("n_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("bits", ctypes.c_int32),
+        ("group_size", ctypes.c_int32),
+        ("mode", ctypes.c_int32),
+        ("window", ctypes.c_int32),
+        ("capacity", ctypes.c_int64),
+        ("sign_seed", ctypes.c_uint64),
+    ]
+
+
+_lib = None
+
+
+def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
+    """Load libfmkv.so (built by build.py); raises if it is missing."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(
+            f"{p} not found: build the HIP library first (python {PKG_DIR / 'build.py'})")
+    lib = ctypes.CDLL(str(p))
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    P = ctypes.POINTER
+    sig = {
+        "fmkv_last_error": ([], ctypes.c_char_p),
+        "fmkv_validate_desc": ([P(CacheDesc)], ctypes.c_int),
+        "fmkv_layout_bytes": ([P(CacheDesc), P(i64), P(i64)], ctypes.c_int),
+        "fmkv_cache_create": ([P(CacheDesc), P(vp)], ctypes.c_int),
+        "fmkv_cache_destroy": ([vp], ctypes.c_int),
+        "fmkv_cache_offset": ([vp, P(i64)], ctypes.c_int),
+        "fmkv_cache_stored_len": ([vp, P(i64)], ctypes.c_int),
+        "fmkv_cache_append": ([vp, vp, vp, i64, vp], ctypes.c_int),
+        "fmkv_cache_trim": ([vp, i64], ctypes.c_int),
+        "fmkv_decode_attention": ([vp, vp, i32, ctypes.c_float, ctypes.c_float, vp, i32, vp], ctypes.c_int),
+        "fmkv_cache_fetch": ([vp, vp, vp, i32, vp], ctypes.c_int),
+        "fmkv_cache_read_codes": ([vp, vp, vp, vp], ctypes.c_int),
+        "fmkv_pool_create": ([P(CacheDesc), i64, P(vp)], ctypes.c_int),
+        "fmkv_pool_destroy": ([vp], ctypes.c_int),
+        "fmkv_paged_append": ([vp, vp, vp, vp, i32, vp, i32, i32, vp], ctypes.c_int),
+        "fmkv_paged_decode_attention": ([vp, vp, vp, i32, vp, i32, i32, i32, ctypes.c_float,
+                                         ctypes.c_float, vp, i32, vp], ctypes.c_int),
+        "fmkv_pool_read_codes": ([vp, vp, vp, vp], ctypes.c_int),
+        "fmkv_set_blocks_per_split": ([i32], ctypes.c_int),
+        "fmkv_cache_decode_splits": ([vp, P(i32)], ctypes.c_int),
+        "fmkv_profile_enable": ([i32], ctypes.c_int),
+        "fmkv_profile_collect": ([P(ctypes.c_double), P(i32)], ctypes.c_int),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _check(rc: int) -> None:
+    if rc != FMKV_OK:
+        raise Exception_(rc, load_library().fmkv_last_error().decode())
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("fmkv needs device tensors")
+    if not t.is_contiguous():
+        raise ValueError("fmkv needs contiguous tensors")
+    return t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
+def make_desc(n_kv_heads: int, head_dim: int, bits: int, window: int = 0, capacity: int = 0,
+              mode: int = MODE_AFFINE, group_size: int = 64, sign_seed: int = 42) -> CacheDesc:
+    return CacheDesc(n_kv_heads, head_dim, bits, group_size, mode, window, capacity, sign_seed)
+
+
+def validate(desc: CacheDesc) -> None:
+    _check(load_library().fmkv_validate_desc(ctypes.byref(desc)))
+
+
+def layout_bytes(desc: CacheDesc) -> tuple[int, int]:
+    b, a = ctypes.c_int64(), ctypes.c_int64()
+    _check(load_library().fmkv_layout_bytes(ctypes.byref(desc), ctypes.byref(b), ctypes.byref(a)))
+    return b.value, a.value
+
+
+def set_blocks_per_split(bps: int) -> None:
+    _check(load_library().fmkv_set_blocks_per_split(bps))
+
+
+def profile_enable(max_records: int) -> None:
+    """Record HIP events around the next max_records split-K kernels."""
+    _check(load_library().fmkv_profile_enable(max_records))
+
+
+def profile_collect() -> tuple[float, int]:
+    """(summed kernel milliseconds, launches timed) since the last collect."""
+    ms, n = ctypes.c_double(), ctypes.c_int32()
+    _check(load_library().fmkv_profile_collect(ctypes.byref(ms), ctypes.byref(n)))
+    return ms.value, n.value
+
+
+class KVCache:
+    """Quantized KV cache of one attention layer (src/cache.rs:166-172)."""
+
+    def __init__(self, desc: CacheDesc):
+        self.desc = desc
+        self._lib = load_library()
+        h = ctypes.c_void_p()
+        _check(self._lib.fmkv_cache_create(ctypes.byref(desc), ctypes.byref(h)))
+        self._h = h
+
+    # --- constructors mirroring src/cache.rs:202-227 --------------------------
+    @classmethod
+    def new_quantized_with_window(cls, head_dim: int, bits: int, window: int | None,
+                                  n_kv_heads: int, capacity: int = 0,
+                                  mode: int = MODE_AFFINE, sign_seed: int = 42) -> "KVCache":
+        return cls(make_desc(n_kv_heads, head_dim, bits, window or 0, capacity, mode,
+                             sign_seed=sign_seed))
+
+    @classmethod
+    def new_quantized(cls, head_dim: int, bits: int, n_kv_heads: int, capacity: int,
+                      mode: int = MODE_AFFINE) -> "KVCache":
+        return cls.new_quantized_with_window(head_dim, bits, None, n_kv_heads, capacity, mode)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.fmkv_cache_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # --- state (src/cache.rs:229-242) ------------------------------------------
+    def offset(self) -> int:
+        v = ctypes.c_int64()
+        _check(self._lib.fmkv_cache_offset(self._h, ctypes.byref(v)))
+        return v.value
+
+    def stored_len(self) -> int:
+        v = ctypes.c_int64()
+        _check(self._lib.fmkv_cache_stored_len(self._h, ctypes.byref(v)))
+        return v.value
+
+    # --- append / fetch (src/cache.rs:247-310) ---------------------------------
+    def append(self, keys: torch.Tensor, values: torch.Tensor, stream=None) -> None:
+        """keys/values: bf16 [n_tokens, n_kv_heads, head_dim] on the device."""
+        self._check_kv(keys, values)
+        _check(self._lib.fmkv_cache_append(self._h, _ptr(keys), _ptr(values), keys.shape[0],
+                                           _stream(stream)))
+
+    def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor, stream=None,
+                         fetch: bool = False):
+        """Store new positions; with fetch=True also return the visible
+        dequantized K/V like the reference's return value."""
+        self.append(keys, values, stream)
+        return self.peek_kv(stream=stream) if fetch else None
+
+    def peek_kv(self, dtype=torch.bfloat16, stream=None):
+        n = self.stored_len()
+        if n == 0:
+            return None
+        shape = (n, self.desc.n_kv_heads, self.desc.head_dim)
+        k = torch.empty(shape, dtype=dtype, device="cuda")
+        v = torch.empty(shape, dtype=dtype, device="cuda")
+        _check(self._lib.fmkv_cache_fetch(self._h, _ptr(k), _ptr(v), _dtype_code(dtype),
+                                          _stream(stream)))
+        return k, v
+
+    def trim(self, keep_last: int) -> None:
+        _check(self._lib.fmkv_cache_trim(self._h, keep_last))
+
+    # --- attention read (src/model/gemma4_attention.rs:94-103) -----------------
+    def attention(self, q: torch.Tensor, scale: float = 1.0, sparse_v_tau: float = 0.0,
+                  out: torch.Tensor | None = None, dtype=torch.bfloat16, stream=None) -> torch.Tensor:
+        """q: bf16 [n_q_heads, head_dim] -> out [n_q_heads, head_dim]."""
+        if q.dtype != torch.bfloat16 or q.dim() != 2 or q.shape[1] != self.desc.head_dim:
+            raise ValueError("q must be bf16 [n_q_heads, head_dim]")
+        if out is None:
+            out = torch.empty(q.shape, dtype=dtype, device=q.device)
+        _check(self._lib.fmkv_decode_attention(self._h, _ptr(q), q.shape[0], scale, sparse_v_tau,
+                                               _ptr(out), _dtype_code(out.dtype), _stream(stream)))
+        return out
+
+    def decode_splits(self) -> int:
+        v = ctypes.c_int32()
+        _check(self._lib.fmkv_cache_decode_splits(self._h, ctypes.byref(v)))
+        return v.value
+
+    # --- raw contents for bit-exact checks -------------------------------------
+    def n_slots(self) -> int:
+        return self.desc.window if self.desc.window > 0 else self.desc.capacity
+
+    def read_codes(self, stream=None):
+        """(codes uint32 [n_slots, 2, H, words], meta uint16 [n_slots, 2, H, n_meta])."""
+        return _read_codes(self._lib.fmkv_cache_read_codes, self._h, self.desc, self.n_slots(), stream)
+
+    def _check_kv(self, keys, values):
+        d = self.desc
+        for t in (keys, values):
+            if t.dtype != torch.bfloat16 or t.dim() != 3 or t.shape[1:] != (d.n_kv_heads, d.head_dim):
+                raise ValueError(f"K/V must be bf16 [n, {d.n_kv_heads}, {d.head_dim}], got "
+                                 f"{tuple(t.shape)} {t.dtype}")
+        if keys.shape != values.shape:
+            raise ValueError("keys and values differ in shape")
+
+
+class PagedPool:
+    """Pool of 16-token blocks shared by many sequences (batched decode)."""
+
+    def __init__(self, desc: CacheDesc, n_blocks: int):
+        self.desc = desc
+        self.n_blocks = n_blocks
+        self._lib = load_library()
+        h = ctypes.c_void_p()
+        _check(self._lib.fmkv_pool_create(ctypes.byref(desc), n_blocks, ctypes.byref(h)))
+        self._h = h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.fmkv_pool_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def append(self, keys, values, block_tables, start_pos, stream=None) -> None:
+        """keys/values bf16 [n_seqs, n_new, H, D]; block_tables int32 [n_seqs, max_blocks];
+        start_pos int32 [n_seqs]."""
+        n_seqs, n_new = keys.shape[0], keys.shape[1]
+        _check(self._lib.fmkv_paged_append(self._h, _ptr(keys), _ptr(values), _ptr(block_tables),
+                                           block_tables.shape[1], _ptr(start_pos), n_seqs, n_new,
+                                           _stream(stream)))
+
+    def attention(self, q, block_tables, seq_lens, max_seq_len: int, scale: float = 1.0,
+                  out=None, dtype=torch.bfloat16, stream=None):
+        """q bf16 [n_seqs, n_q_heads, D]; seq_lens int32 [n_seqs]."""
+        if out is None:
+            out = torch.empty(q.shape, dtype=dtype, device=q.device)
+        _check(self._lib.fmkv_paged_decode_attention(
+            self._h, _ptr(q), _ptr(block_tables), block_tables.shape[1], _ptr(seq_lens),
+            q.shape[0], max_seq_len, q.shape[1], scale, 0.0, _ptr(out), _dtype_code(out.dtype),
+            _stream(stream)))
+        return out
+
+    def read_codes(self, stream=None):
+        return _read_codes(self._lib.fmkv_pool_read_codes, self._h, self.desc,
+                           self.n_blocks * BLOCK_TOKENS, stream)
+
+
+def _dtype_code(dtype) -> int:
+    if dtype == torch.bfloat16:
+        return DTYPE_BF16
+    if dtype == torch.float32:
+        return DTYPE_F32
+    raise ValueError(f"unsupported output dtype {dtype}")
+
+
+def words_per_row(desc: CacheDesc) -> int:
+    return (desc.head_dim * desc.bits + 31) // 32
+
+
+def meta_per_row(desc: CacheDesc) -> int:
+    return 2 * (desc.head_dim // 64) if desc.mode == MODE_AFFINE else 1
+
+
+def _read_codes(fn, handle, desc, n_slots, stream):
+    H = desc.n_kv_heads
+    codes = torch.zeros((n_slots, 2, H, words_per_row(desc)), dtype=torch.int32, device="cuda")
+    meta = torch.zeros((n_slots, 2, H, meta_per_row(desc)), dtype=torch.int16, device="cuda")
+    _check(fn(handle, _ptr(codes), _ptr(meta), _stream(stream)))
+    return codes, meta

@@ -1,0 +1,174 @@
+/*
+ * fmkv -- MI355X quantized KV cache for Gemma-4 attention layers (C ABI).
+ *
+ * Drop-in boundary for flash-moe's KV-cache path. The reference keeps the
+ * cache in Rust (`KVCache`, src/cache.rs:166-310) and computes with MLX
+ * through mlx-rs; its one hand-written FFI is `mlx_array_from_mmap`
+ * (src/ffi.rs:5-14). This header is the C surface that replaces the MLX calls
+ * on that path: plain integers, sizes and device pointers, no exceptions, an
+ * int status on every call and a thread-local error string.
+ *
+ * Conventions
+ *  - Device buffers are HIP device pointers owned by the caller.
+ *  - K/V input rows are bf16, contiguous [n_tokens][n_kv_heads][head_dim]
+ *    (post-RoPE K and post-v_norm V, src/model/gemma4_attention.rs:62-81).
+ *  - q is bf16 [n_q_heads][head_dim]; out is [n_q_heads][head_dim] in bf16
+ *    or f32 (FMKV_DTYPE_*). q head h reads KV head h / (n_q_heads/n_kv_heads).
+ *  - `stream` is a hipStream_t (NULL = default stream). Every call is
+ *    stream-ordered and asynchronous unless stated; nothing synchronises.
+ *  - A handle is used by one host thread at a time (no internal locks).
+ *  - Descriptor validation runs before any HIP call, so invalid input is
+ *    reported on machines without a GPU too.
+ */
+#ifndef FMKV_H
+#define FMKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define FMKV_OK 0
+#define FMKV_ERR_INVALID_ARG 1 /* null pointer, negative size, bad dtype */
+#define FMKV_ERR_UNSUPPORTED 2 /* head_dim / bits / group / mode not supported */
+#define FMKV_ERR_OOM 3         /* device allocation failed */
+#define FMKV_ERR_HIP 4         /* a HIP call or launch failed */
+#define FMKV_ERR_CAPACITY 5    /* append would exceed a linear cache's capacity */
+
+/* cache modes */
+#define FMKV_MODE_AFFINE 0   /* rotated, group-64 affine 4/8-bit codes + f16 scale/bias */
+#define FMKV_MODE_CODEBOOK 1 /* rotated TurboQuant Lloyd-Max 2/3/4-bit indices + f16 norm */
+
+/* output dtypes */
+#define FMKV_DTYPE_BF16 0
+#define FMKV_DTYPE_F32 1
+
+/* Cache descriptor. Mirrors the arguments of
+ * KVCache::new_quantized_with_window(head_dim, bits, window)
+ * (src/cache.rs:206-227) plus what a preallocated device arena needs. */
+typedef struct fmkv_cache_desc {
+  int32_t n_kv_heads; /* >= 1 */
+  int32_t head_dim;   /* 128, 256 or 512 */
+  int32_t bits;       /* affine: 4 or 8; codebook: 2, 3 or 4 (src/cache.rs:67-89) */
+  int32_t group_size; /* 64 */
+  int32_t mode;       /* FMKV_MODE_* */
+  int32_t window;     /* 0: global layer, linear growth; W > 0: ring of W slots (W % 16 == 0) */
+  int64_t capacity;   /* linear caches: max positions; ignored for rings */
+  uint64_t sign_seed; /* seed of the RHT sign vector; the reference uses 42 (src/cache.rs:49) */
+} fmkv_cache_desc;
+
+typedef struct fmkv_cache fmkv_cache;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* fmkv_last_error(void);
+
+/* Validate a descriptor without touching HIP (src/cache.rs:87 panics on bad
+ * bits; here it is FMKV_ERR_UNSUPPORTED). */
+int fmkv_validate_desc(const fmkv_cache_desc* desc);
+
+/* Bytes of one 16-token head-block and of the whole arena for `desc`. */
+int fmkv_layout_bytes(const fmkv_cache_desc* desc, int64_t* block_bytes, int64_t* arena_bytes);
+
+/* Create / destroy. Replaces KVCache::new_quantized_with_window
+ * (src/cache.rs:206-227) and its drop; Model::make_cache (src/model/mod.rs:375-396)
+ * calls it once per layer. The handle owns all device storage. */
+int fmkv_cache_create(const fmkv_cache_desc* desc, fmkv_cache** out);
+int fmkv_cache_destroy(fmkv_cache* cache);
+
+/* KVCache::offset (src/cache.rs:230-232): positions appended so far. */
+int fmkv_cache_offset(const fmkv_cache* cache, int64_t* out);
+/* KVCache::stored_len (src/cache.rs:236-242): positions currently visible
+ * (min(offset, window) for rings, minus anything trimmed). */
+int fmkv_cache_stored_len(const fmkv_cache* cache, int64_t* out);
+
+/* The store half of KVCache::update_and_fetch (src/cache.rs:266-310):
+ * rotate, quantize and write n_tokens new positions (offset .. offset+n-1);
+ * rings overwrite slot pos % W, so afterwards exactly the last W positions
+ * are stored (tail_along_time, src/cache.rs:140-148). Advances offset by n. */
+int fmkv_cache_append(fmkv_cache* cache, const void* k_bf16, const void* v_bf16,
+                      int64_t n_tokens, void* stream);
+
+/* Hide all but the last `keep_last` stored positions (the explicit form of
+ * tail_along_time, src/cache.rs:140-148). offset is unchanged. */
+int fmkv_cache_trim(fmkv_cache* cache, int64_t keep_last);
+
+/* Decode-step attention read over the cache, replacing
+ * mlx_rs::fast::scaled_dot_product_attention(q, k_all, v_all, scale, None)
+ * at src/model/gemma4_attention.rs:94-103 for L == 1 (Gemma-4: scale 1.0).
+ * The current position attends to its own quantized K/V, as in the
+ * reference where the round trip precedes the concat (src/cache.rs:295-298).
+ * sparse_v_tau must be 0 (the tau gate of gemma4_attention.rs:196-234 is not
+ * implemented; nonzero returns FMKV_ERR_UNSUPPORTED). */
+int fmkv_decode_attention(fmkv_cache* cache, const void* q_bf16, int32_t n_q_heads, float scale,
+                          float sparse_v_tau, void* out, int32_t out_dtype, void* stream);
+
+/* The fetch half of update_and_fetch and KVCache::peek_kv (src/cache.rs:247-257):
+ * dequantized, un-rotated K and V of the visible positions in chronological
+ * order, [stored_len][n_kv_heads][head_dim] in out_dtype. */
+int fmkv_cache_fetch(const fmkv_cache* cache, void* k_out, void* v_out, int32_t out_dtype,
+                     void* stream);
+
+/* Raw stored codes in a canonical layout, indexed by slot (slot = pos % W for
+ * rings, pos for linear caches), for bit-exact checks:
+ *   codes  uint32 [n_slots][2][n_kv_heads][words]   (K = 0, V = 1; LE bit stream)
+ *   meta   uint16 [n_slots][2][n_kv_heads][n_meta]  (affine: scale g, bias g
+ *          interleaved, n_meta = 2*head_dim/64; codebook: norm, n_meta = 1)
+ * n_slots = window for rings, capacity for linear caches. */
+int fmkv_cache_read_codes(const fmkv_cache* cache, void* codes, void* meta, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Paged pool for batched, ragged decode (block tables of 16-token blocks). */
+/* The reference has no paged cache (one Vec<Cache> per request,            */
+/* src/engine.rs:70); this is the batched form of the same append/read.     */
+/* ---------------------------------------------------------------------- */
+
+typedef struct fmkv_pool fmkv_pool;
+
+/* Pool of n_blocks physical 16-token blocks, each holding all KV heads. */
+int fmkv_pool_create(const fmkv_cache_desc* desc, int64_t n_blocks, fmkv_pool** out);
+int fmkv_pool_destroy(fmkv_pool* pool);
+
+/* Append n_new tokens to each of n_seqs sequences. k/v: bf16
+ * [n_seqs][n_new][n_kv_heads][head_dim]. block_tables: int32 device
+ * [n_seqs][max_blocks]; start_pos: int32 device [n_seqs], the position of
+ * each sequence's first new token. */
+int fmkv_paged_append(fmkv_pool* pool, const void* k_bf16, const void* v_bf16,
+                      const int32_t* block_tables, int32_t max_blocks, const int32_t* start_pos,
+                      int32_t n_seqs, int32_t n_new, void* stream);
+
+/* Decode attention for n_seqs sequences; seq_lens: int32 device [n_seqs]
+ * (positions visible, current token included); max_seq_len bounds them.
+ * q: bf16 [n_seqs][n_q_heads][head_dim]; out: [n_seqs][n_q_heads][head_dim]. */
+int fmkv_paged_decode_attention(fmkv_pool* pool, const void* q_bf16, const int32_t* block_tables,
+                                int32_t max_blocks, const int32_t* seq_lens, int32_t n_seqs,
+                                int32_t max_seq_len, int32_t n_q_heads, float scale,
+                                float sparse_v_tau, void* out, int32_t out_dtype, void* stream);
+
+/* Canonical codes of every pool block, indexed by (physical block * 16 + t). */
+int fmkv_pool_read_codes(const fmkv_pool* pool, void* codes, void* meta, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Tuning and introspection                                                 */
+/* ---------------------------------------------------------------------- */
+
+/* Blocks per split-K work-group for decode attention (0 = automatic). */
+int fmkv_set_blocks_per_split(int32_t blocks_per_split);
+
+/* Kernel timing (profiling aid, no reference counterpart): while enabled,
+ * each decode attention call records a pair of HIP events around its split-K
+ * kernel on the caller's stream, up to max_records pairs (0 disables and
+ * frees them). fmkv_profile_collect waits for the recorded pairs, returns the
+ * summed kernel time in milliseconds and the number of launches timed, and
+ * clears the records. */
+int fmkv_profile_enable(int32_t max_records);
+int fmkv_profile_collect(double* total_ms, int32_t* n_records);
+/* Split count the next decode call on `cache` will use (for profiling). */
+int fmkv_cache_decode_splits(const fmkv_cache* cache, int32_t* n_splits);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FMKV_H */

@@ -1,0 +1,402 @@
+"""Pins of the CPU oracle (no GPU).
+
+The reference ships no tests or golden vectors for its KV path, so every
+oracle function is pinned here by something outside its own formula: known
+answers copied from src/cache.rs, closed forms (Sylvester entries, Lloyd-Max
+conditional means), invariants (orthogonality, involution), brute force on
+tiny inputs, and independent numpy restatements in IEEE single precision.
+"""
+import math
+
+import numpy as np
+import pytest
+from scipy.special import erf, logsumexp
+
+import synth
+
+
+# --------------------------------------------------------------------------
+# scalar conversions
+# --------------------------------------------------------------------------
+def test_f16_conversion_matches_numpy(ora):
+    rng = np.random.default_rng(1)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 20000),
+        np.array([0.0, -0.0, 65504, 65519.99, 65520, -65520, 6.1035156e-05, 5.9604645e-08,
+                  2.9802322e-08, 2.9802326e-08, 8.940697e-08, 1e-7, -1e-7, np.inf, -np.inf],
+                 dtype=np.float32),
+    ]).astype(np.float32)
+    got = ora.f32_to_f16(x)
+    want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    back = ora.f16_to_f32(want)
+    assert np.array_equal(back, want.view(np.float16).astype(np.float32))
+
+
+def test_bf16_conversion_matches_torch(ora):
+    import torch
+
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal(50000) * 10.0 ** rng.integers(-30, 30, 50000)).astype(np.float32)
+    got = ora.f32_to_bf16(x)
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+    assert np.array_equal(synth.f32_to_bf16_bits(x), want)
+
+
+# --------------------------------------------------------------------------
+# src/cache.rs:6-62 -- Hadamard, LCG signs, RHT
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("n", [2, 8, 64, 256, 512])
+def test_hadamard_closed_form(ora, n):
+    h = ora.hadamard(n)
+    i = np.arange(n)
+    pop = np.vectorize(lambda v: bin(v).count("1"))(i[:, None] & i[None, :])
+    want = np.where(pop % 2 == 0, 1.0, -1.0) * np.float32(1.0 / math.sqrt(n))
+    assert np.array_equal(h, want.astype(np.float32))
+    assert np.allclose(h.astype(np.float64) @ h.T.astype(np.float64), np.eye(n), atol=1e-6)
+
+
+def test_signs_known_answer(ora):
+    # first 32 signs for seed 42 (SplitMix-free MMIX LCG of src/cache.rs:29-43)
+    s = ora.signs(512, 42)
+    text = "".join("+" if v > 0 else "-" for v in s[:32])
+    assert text == "-++--++++++--+-+-++-+++++--++---"
+    assert int(s[:256].sum()) == -20
+    assert int(s.sum()) == -24
+    # independent big-integer evaluation of the LCG
+    st, ref = 42, []
+    for _ in range(512):
+        st = (st * 6364136223846793005 + 1442695040888963407) % (1 << 64)
+        ref.append(1.0 if (st >> 63) == 0 else -1.0)
+    assert np.array_equal(s, np.array(ref, np.float32))
+
+
+@pytest.mark.parametrize("d", [128, 256, 512])
+def test_rht_orthogonal_and_transpose(ora, d):
+    r, rt = ora.build_rht(d, 42)
+    assert np.array_equal(rt, r.T)
+    assert np.allclose(r.astype(np.float64) @ rt.astype(np.float64), np.eye(d), atol=1e-6)
+
+
+# --------------------------------------------------------------------------
+# src/cache.rs:67-89 -- Lloyd-Max tables
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_lloyd_max_tables_are_lloyd_max(ora, bits):
+    c, b = ora.codebook(bits)
+    assert len(c) == 1 << bits and len(b) == (1 << bits) - 1
+    assert np.allclose(c, -c[::-1]) and np.allclose(b, -b[::-1])
+    # boundaries are midpoints of neighbouring centroids (nearest-neighbour rule)
+    assert np.max(np.abs(b - (c[:-1] + c[1:]) / 2)) <= 1.5e-3
+    # centroids are N(0,1) conditional means of their cells (centroid rule)
+    edges = np.concatenate([[-np.inf], b.astype(np.float64), [np.inf]])
+    phi = lambda x: np.exp(-0.5 * x * x) / math.sqrt(2 * math.pi)
+    Phi = lambda x: 0.5 * (1 + erf(x / math.sqrt(2)))
+    cm = (phi(edges[:-1]) - phi(edges[1:])) / (Phi(edges[1:]) - Phi(edges[:-1]))
+    assert np.max(np.abs(cm - c)) <= 6e-3
+
+
+def test_codebook_rejects_other_bits(ora):
+    with pytest.raises(ValueError):
+        ora.codebook(5)
+
+
+# --------------------------------------------------------------------------
+# canonical FWHT rotation vs the reference's dense x.R
+# --------------------------------------------------------------------------
+def np_fwht_f32(x):
+    """Independent numpy FWHT in the canonical stage order (f32 per op)."""
+    y = np.array(x, dtype=np.float32).copy()
+    n = y.shape[-1]
+    h = 1
+    while h < n:
+        y = y.reshape(y.shape[:-1] + (n // (2 * h), 2, h))
+        a, b = y[..., 0, :].copy(), y[..., 1, :].copy()
+        y[..., 0, :] = a + b
+        y[..., 1, :] = a - b
+        y = y.reshape(y.shape[:-3] + (n,))
+        h *= 2
+    return y
+
+
+@pytest.mark.parametrize("d", [128, 256, 512])
+def test_fwht_matches_dense_and_numpy(ora, d):
+    rng = np.random.default_rng(d)
+    x = rng.standard_normal(d).astype(np.float32)
+    got = ora.fwht(x)
+    assert np.array_equal(got, np_fwht_f32(x))
+    h = ora.hadamard(d).astype(np.float64) * math.sqrt(d)
+    assert np.allclose(got, x.astype(np.float64) @ h, rtol=0, atol=1e-4 * math.sqrt(d))
+    # one-hot rows map to Hadamard rows exactly; FWHT twice is d * identity
+    e = np.zeros(d, np.float32)
+    e[d // 3] = 1.0
+    assert np.array_equal(ora.fwht(e), np.round(h[d // 3]).astype(np.float32))
+    assert np.allclose(ora.fwht(ora.fwht(x)), d * x, atol=1e-3)
+
+
+@pytest.mark.parametrize("d", [256, 512])
+def test_rotate_rows_is_x_times_r(ora, d):
+    rng = np.random.default_rng(7 + d)
+    xb = synth.f32_to_bf16_bits(rng.standard_normal((8, d)).astype(np.float32) * 3)
+    s = ora.signs(d, 42)
+    y = ora.rotate_rows(xb, s)
+    r, _ = ora.build_rht(d, 42)
+    x = ora.bf16_to_f32(xb).astype(np.float64)
+    assert np.allclose(y, x @ r.astype(np.float64), atol=2e-5 * np.abs(x).max() * math.sqrt(d))
+    # canonical order, restated with numpy f32 ops
+    c = np.float32(1.0) / np.sqrt(np.float32(d))
+    want = (np_fwht_f32(ora.bf16_to_f32(xb)) * c) * s
+    assert np.array_equal(y, want.astype(np.float32))
+    # inverse rotation (f64) recovers x
+    assert np.allclose(ora.unrotate_rows_f64(y.astype(np.float64), s), x, atol=1e-4)
+
+
+# --------------------------------------------------------------------------
+# MLX affine quantizer (A16)
+# --------------------------------------------------------------------------
+def np_affine(y, bits):
+    """numpy f32 restatement of MLX affine_quantize for groups of 64."""
+    y = np.asarray(y, np.float32).reshape(-1, 64)
+    nb = np.float32((1 << bits) - 1)
+    mx, mn = y.max(1), y.min(1)
+    scale = np.maximum((mx - mn) / nb, np.float32(1e-7))
+    side = np.abs(mn) > np.abs(mx)
+    scale = np.where(side, scale, -scale).astype(np.float32)
+    edge = np.where(side, mn, mx).astype(np.float32)
+    q0 = np.rint(edge / scale).astype(np.float32)
+    nz = q0 != 0
+    scale = np.where(nz, edge / np.where(nz, q0, 1), scale).astype(np.float32)
+    bias = np.where(nz, edge, 0).astype(np.float32)
+    q = np.clip(np.rint((y - bias[:, None]) / scale[:, None]), 0, nb).astype(np.int64)
+    return q, scale, bias
+
+
+def test_affine_known_answers(ora):
+    # 4-bit, values 0..15 (+ pad with 0..15 repeated): scale -1, bias 15, code 15 - w
+    w = np.tile(np.arange(16, dtype=np.float32), 4)
+    p, sc, bi = ora.affine_quantize(w[None, :], 4)
+    codes = ora.unpack_codes(p, 64, 4)[0]
+    assert np.array_equal(codes, 15 - w.astype(np.int64))
+    assert ora.f16_to_f32(sc)[0, 0] == -1.0 and ora.f16_to_f32(bi)[0, 0] == 15.0
+    # 4-bit, values -8..7: scale 1, bias -8, code w + 8
+    w = np.tile(np.arange(-8, 8, dtype=np.float32), 4)
+    p, sc, bi = ora.affine_quantize(w[None, :], 4)
+    assert np.array_equal(ora.unpack_codes(p, 64, 4)[0], (w + 8).astype(np.int64))
+    # half-way cases round to even: (2.5-15)/-1 = 12.5 -> 12 ; (3.5-15)/-1 = 11.5 -> 12
+    w = np.zeros(64, np.float32)
+    w[1], w[2], w[3] = 15.0, 2.5, 3.5
+    codes = ora.unpack_codes(ora.affine_quantize(w[None, :], 4)[0], 64, 4)[0]
+    assert codes[2] == 12 and codes[3] == 12 and codes[1] == 0 and codes[0] == 15
+    # constant group -> code 0, bias = the constant
+    w = np.full(64, 3.0, np.float32)
+    p, sc, bi = ora.affine_quantize(w[None, :], 8)
+    assert not ora.unpack_codes(p, 64, 8).any() and ora.f16_to_f32(bi)[0, 0] == 3.0
+    # packing: element k of a word at bits [4k, 4k+4)
+    w = np.tile(np.arange(-8, 8, dtype=np.float32), 4)
+    p, _, _ = ora.affine_quantize(w[None, :], 4)  # -8..7 -> code k at element k
+    assert p[0, 0] == 0x76543210 and p[0, 1] == 0xFEDCBA98
+    p, _, _ = ora.affine_quantize(np.tile(np.arange(-128, 128, 4, dtype=np.float32), 1)[None, :], 8)
+    # 8-bit, -128..124 step 4: q0 = rint(-128 / (252/255)) = -130, scale = 128/130,
+    # code_k = rint(4k * 130/128) = 0, 4, 8, 12 -> byte k of the word is element k
+    assert p[0, 0] == 0x0C080400
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_affine_matches_numpy_and_error_bound(ora, bits):
+    rng = np.random.default_rng(bits)
+    y = (rng.standard_normal((300, 256)) * rng.uniform(0.01, 30, (300, 1))).astype(np.float32)
+    y[5] = 0.0
+    y[6, :64] = -2.0
+    p, sc, bi = ora.affine_quantize(y, bits)
+    codes = ora.unpack_codes(p, 256, bits).reshape(-1, 64)
+    q, scale, bias = np_affine(y, bits)
+    assert np.array_equal(codes, q)
+    assert np.array_equal(sc.reshape(-1), scale.astype(np.float16).view(np.uint16))
+    assert np.array_equal(bi.reshape(-1), bias.astype(np.float16).view(np.uint16))
+    assert codes.min() >= 0 and codes.max() <= (1 << bits) - 1
+    # unclipped codes: |dequant - w| <= |scale|/2 (+ f16 storage of scale and
+    # bias). MLX's edge rule (scale = edge / q0) can shrink |scale| so the far
+    # end of the range clips; those codes sit at 0 or n_bins.
+    yg = y.reshape(-1, 64).astype(np.float64)
+    raw = np.rint((y.reshape(-1, 64) - bias[:, None]) / scale[:, None])
+    clipped = (raw < 0) | (raw > (1 << bits) - 1)
+    assert np.all(np.isin(codes[clipped], [0, (1 << bits) - 1]))
+    deq = ora.affine_dequantize(p, sc, bi, 256, bits).reshape(-1, 64)
+    s16 = ora.f16_to_f32(sc).reshape(-1).astype(np.float64)
+    b16 = ora.f16_to_f32(bi).reshape(-1).astype(np.float64)
+    bound = (np.abs(scale) / 2 + q.max(1) * np.abs(s16 - scale) + np.abs(b16 - bias)) * (1 + 1e-6) + 1e-12
+    ok = np.abs(deq - yg) <= bound[:, None]
+    assert np.all(ok | clipped)
+    assert clipped.mean() < 0.02
+
+
+# --------------------------------------------------------------------------
+# TurboQuant round trip (A7), dense reference order and canonical order
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_turbo_round_trip_known_answers(ora, bits):
+    d = 256
+    c, _ = ora.codebook(bits)
+    x = np.zeros((3, d), np.float32)
+    x[1, 17] = 1.0  # one-hot: z = +-1 in every coordinate -> +-centroid for +-1
+    x[2, 200] = -4.0
+    xb = synth.f32_to_bf16_bits(x)
+    out = ora.bf16_to_f32(ora.turbo_round_trip_dense(xb, bits))
+    assert not out[0].any()  # zero row: norm 0, output 0
+    top = c[np.searchsorted(ora.codebook(bits)[1], 1.0 - 1e-6, side="right")]
+    want1 = np.zeros(d)
+    want1[17] = top
+    want2 = np.zeros(d)
+    want2[200] = -4.0 * top
+    assert np.allclose(out[1], want1, atol=2e-2 * top)
+    assert np.allclose(out[2], want2, atol=8e-2 * top)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("d", [256, 512])
+def test_codebook_canonical_vs_dense_reference(ora, bits, d):
+    rng = np.random.default_rng(bits * d)
+    x = rng.standard_normal((64, d)).astype(np.float32)
+    x[:, :4] *= 20
+    xb = synth.f32_to_bf16_bits(x)
+    s = ora.signs(d, 42)
+    packed, norms = ora.codebook_quantize(xb, bits, s)
+    # indices vs exact math: bins of (x/|x|).R.sqrt(d) computed in f64
+    xf = ora.bf16_to_f32(xb).astype(np.float64)
+    r, _ = ora.build_rht(d, 42)
+    z = (xf / np.linalg.norm(xf, axis=1, keepdims=True)) @ r.astype(np.float64) * math.sqrt(d)
+    idx_exact = np.searchsorted(ora.codebook(bits)[1].astype(np.float64), z, side="right")
+    idx = ora.unpack_codes(packed, d, bits)
+    assert np.mean(idx != idx_exact) < 1e-3
+    assert np.allclose(ora.f16_to_f32(norms), np.linalg.norm(xf, axis=1), rtol=1e-3)
+    # canonical round trip stays close to the reference-order dense round trip
+    rt = ora.bf16_to_f32(ora.codebook_round_trip(packed, norms, d, bits, s))
+    dense = ora.bf16_to_f32(ora.turbo_round_trip_dense(xb, bits))
+    err = np.abs(rt - dense)
+    assert np.mean(err) <= 2e-3 * np.abs(dense).mean() + 1e-3
+
+
+# --------------------------------------------------------------------------
+# cache index semantics (A8, A9, A14)
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("window", [4, 16, 48])
+def test_ring_equals_concat_then_tail(ora, window):
+    """Brute force: the reference keeps tail_along_time(concat(...), W); a ring
+    that overwrites slot p % W holds exactly those positions."""
+    stored = []  # positions, chronological (reference model)
+    rng = np.random.default_rng(window)
+    offset = 0
+    for _ in range(40):
+        n = int(rng.integers(1, 2 * window))
+        stored = (stored + list(range(offset, offset + n)))[-window:]
+        offset += n
+        held = sorted(p for p in (ora.slot_position(s, offset, window) for s in range(window)) if p >= 0)
+        assert held == stored
+        assert all(ora.ring_slot(p, window) == p % window for p in stored)
+
+
+def test_sliding_mask_decode_sees_last_w(ora):
+    W = 8
+    for stored in range(0, 3 * W):
+        st = min(stored, W)
+        m = ora.sliding_mask(st, 1, W)
+        vis = np.flatnonzero(m[0] == 0)
+        # columns are [stored cache ..., current]; visible = last min(st+1, W)
+        assert list(vis) == list(range(st + 1 - min(st + 1, W), st + 1))
+    # prefill rows: causal band
+    m = ora.sliding_mask(3, 5, 4)
+    for i in range(5):
+        row = 3 + i
+        want = [j for j in range(8) if j <= row and row - j < 4]
+        assert list(np.flatnonzero(m[i] == 0)) == want
+    cm = ora.causal_mask(2, 3)
+    assert [list(np.flatnonzero(r == 0)) for r in cm] == [[0, 1, 2], [0, 1, 2, 3], [0, 1, 2, 3, 4]]
+
+
+def test_paged_address(ora):
+    table = np.array([7, 2, 9], np.int32)
+    assert [ora.paged_address(table, p, 16) for p in (0, 15, 16, 40)] == [112, 127, 32, 152]
+
+
+# --------------------------------------------------------------------------
+# attention (A12, A13) and the split merge (A17)
+# --------------------------------------------------------------------------
+def np_attention(q, k, v, scale=1.0, tau=0.0):
+    hq, d = q.shape
+    hkv = k.shape[1]
+    rep = hq // hkv
+    out = np.zeros((hq, d))
+    for h in range(hq):
+        s = k[:, h // rep] @ q[h] * scale
+        w = np.exp(s - logsumexp(s))
+        if tau > 0:
+            w = np.where(w >= tau, w, 0)
+        out[h] = w @ v[:, h // rep]
+    return out
+
+
+def test_attention_special_cases(ora):
+    rng = np.random.default_rng(3)
+    d = 64
+    q = rng.standard_normal((4, d))
+    v = rng.standard_normal((1, 2, d))
+    k = rng.standard_normal((1, 2, d))
+    assert np.allclose(ora.attention_f64(q, k, v), v[0][[0, 0, 1, 1]])  # T = 1 -> v
+    k = np.repeat(rng.standard_normal((1, 2, d)), 9, axis=0)
+    v = rng.standard_normal((9, 2, d))
+    assert np.allclose(ora.attention_f64(q, k, v), v.mean(0)[[0, 0, 1, 1]])  # equal keys -> mean
+    valid = np.zeros(9, np.uint8)
+    valid[4] = 1
+    assert np.allclose(ora.attention_f64(q, k, v, valid), v[4][[0, 0, 1, 1]])
+
+
+@pytest.mark.parametrize("tau", [0.0, 1e-3, 5e-2])
+def test_attention_matches_numpy(ora, tau):
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal((8, 32)) * 0.5
+    k = rng.standard_normal((50, 2, 32))
+    v = rng.standard_normal((50, 2, 32))
+    assert np.allclose(ora.attention_f64(q, k, v, None, 0.7, tau), np_attention(q, k, v, 0.7, tau),
+                       atol=1e-12)
+
+
+def test_lse_merge_equals_full_softmax(ora):
+    rng = np.random.default_rng(5)
+    s = rng.standard_normal(40) * 5
+    v = rng.standard_normal((40, 16))
+    parts = np.split(np.arange(40), [7, 20, 21])
+    m = np.array([s[p].max() for p in parts])
+    l = np.array([np.exp(s[p] - s[p].max()).sum() for p in parts])
+    o = np.stack([np.exp(s[p] - s[p].max()) @ v[p] for p in parts])
+    w = np.exp(s - logsumexp(s))
+    assert np.allclose(ora.lse_merge(m, l, o), w @ v, atol=1e-12)
+
+
+def test_sdpa_bf16_baseline_close_to_exact(ora):
+    rng = np.random.default_rng(6)
+    q = synth.f32_to_bf16_bits(rng.standard_normal((4, 64)).astype(np.float32) * 0.2)
+    k = synth.f32_to_bf16_bits(rng.standard_normal((100, 2, 64)).astype(np.float32))
+    v = synth.f32_to_bf16_bits(rng.standard_normal((100, 2, 64)).astype(np.float32))
+    got = ora.bf16_to_f32(ora.sdpa_bf16_decode(q, k, v, 1.0, 2))
+    want = ora.attention_f64(ora.bf16_to_f32(q), ora.bf16_to_f32(k), ora.bf16_to_f32(v))
+    assert np.max(np.abs(got - want)) < 2e-2
+
+
+# --------------------------------------------------------------------------
+# cache model: append with ring semantics, trim, stored_len
+# --------------------------------------------------------------------------
+def test_oracle_cache_ring_and_trim(ora):
+    c = ora.OracleCache(2, 128, 4, window=32)
+    rng = np.random.default_rng(9)
+    total = 0
+    for n in (5, 30, 1, 40, 16):
+        k = synth.f32_to_bf16_bits(rng.standard_normal((n, 2, 128)).astype(np.float32))
+        c.append(k, k)
+        total += n
+        assert c.offset == total and c.stored_len() == min(total, 32)
+    c.trim(10)
+    assert c.stored_len() == 10
+    assert list(c.visible_positions()) == list(range(total - 10, total))
+    k, v = c.dequant_kv()
+    assert k.shape == (10, 2, 128) and np.allclose(k, v)
