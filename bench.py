@@ -83,17 +83,26 @@ def run_c3(args) -> dict:
     log(f"prefill {T0} tokens in {prefill_ms:.2f} ms ({append_prefill_tps/1e6:.2f} M tokens/s)")
     del dk, dv
 
-    # ---- decode inputs resident on the device ----
+    # ---- decode inputs resident on the device; raw pointers per step ----
     kd = dev_bf16(synth.kv_rows(41, n_dec, Hkv, D, None, dist="t3"))
     vd = dev_bf16(synth.kv_rows(42, n_dec, Hkv, D, None))
     qd = dev_bf16(synth.q_rows(43, Hq, Hkv, D, None, batch=n_dec))
     out = torch.empty((Hq, D), dtype=torch.bfloat16, device="cuda")
+    lib, h = fmkv.load_library(), cache._h
+    stream = torch.cuda.current_stream().cuda_stream
+    row = Hkv * D * 2
+    kp = [kd.data_ptr() + t * row for t in range(n_dec)]
+    vp = [vd.data_ptr() + t * row for t in range(n_dec)]
+    qp = [qd.data_ptr() + t * Hq * D * 2 for t in range(n_dec)]
+    outp = out.data_ptr()
     i = 0
 
     def step():
         nonlocal i
-        cache.append(kd[i:i + 1], vd[i:i + 1])
-        cache.attention(qd[i], 1.0, out=out)
+        rc = lib.fmkv_cache_append(h, kp[i], vp[i], 1, stream)
+        rc |= lib.fmkv_decode_attention(h, qp[i], Hq, 1.0, 0.0, outp, fmkv.DTYPE_BF16, stream)
+        if rc:
+            raise RuntimeError(lib.fmkv_last_error().decode())
         i += 1
 
     for _ in range(args.warmup):
@@ -209,6 +218,7 @@ def main(argv=None) -> int:
     ap.add_argument("--context", type=int, default=32768)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--bps", type=int, default=0, help="blocks per split-K work-group (0: auto)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the KV path is "
@@ -219,6 +229,10 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
+    if args.bps:
+        import fmkv
+
+        fmkv.set_blocks_per_split(args.bps)
     res = run_c3(args)
     print(json.dumps(res), flush=True)
     return 0

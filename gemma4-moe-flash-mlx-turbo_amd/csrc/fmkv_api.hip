@@ -106,11 +106,13 @@ int device_cus() {
   return cus;
 }
 
-// Split-K plan: about two work-groups per CU, at least 2 blocks each.
+// Split-K plan: about two work-groups per CU, an even number of blocks each
+// (the kernel walks blocks in pairs).
 int32_t choose_bps(int64_t total_head_blocks, int cus) {
   if (g_bps_override > 0) return g_bps_override;
   const int64_t target = 2 * (int64_t)cus;
   int64_t bps = (total_head_blocks + target - 1) / target;
+  bps += bps & 1;
   if (bps < 2) bps = 2;
   return (int32_t)bps;
 }

@@ -26,53 +26,6 @@ __constant__ float kCbBounds4[15] = {-2.401f, -1.844f, -1.437f, -1.099f, -0.800f
                                      -0.522f, -0.258f, 0.0f,    0.258f,  0.522f,
                                      0.800f,  1.099f,  1.437f,  1.844f,  2.401f};
 
-// Canonical unnormalised FWHT of a row held as E contiguous values per lane.
-template <int E>
-__device__ inline void wave_fwht(float (&x)[E], int lane) {
-#pragma unroll
-  for (int h = 1; h < E; h <<= 1)
-#pragma unroll
-    for (int i = 0; i < E; i += 2 * h)
-#pragma unroll
-      for (int jj = i; jj < i + h; jj++) {
-        float a = x[jj], b = x[jj + h];
-        x[jj] = a + b;
-        x[jj + h] = a - b;
-      }
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const bool upper = (lane & m) != 0;
-#pragma unroll
-    for (int i = 0; i < E; i++) {
-      float p = __shfl_xor(x[i], m);
-      x[i] = upper ? (p - x[i]) : (x[i] + p);
-    }
-  }
-}
-
-template <int E>
-__device__ inline void load_row(const uint16_t* src, float (&x)[E]) {
-  if constexpr (E == 8) {
-    uint4 u = *reinterpret_cast<const uint4*>(src);
-    uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      x[2 * i] = __uint_as_float(w[i] << 16);
-      x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-    }
-  } else if constexpr (E == 4) {
-    uint2 u = *reinterpret_cast<const uint2*>(src);
-    x[0] = __uint_as_float(u.x << 16);
-    x[1] = __uint_as_float(u.x & 0xffff0000u);
-    x[2] = __uint_as_float(u.y << 16);
-    x[3] = __uint_as_float(u.y & 0xffff0000u);
-  } else {
-    uint32_t u = *reinterpret_cast<const uint32_t*>(src);
-    x[0] = __uint_as_float(u << 16);
-    x[1] = __uint_as_float(u & 0xffff0000u);
-  }
-}
-
 // MLX affine_quantize for the group spanning 64/E lanes (see oracle).
 template <int E, int BITS>
 __device__ inline void affine_quant(const float (&y)[E], uint32_t (&code)[E], float& scale_o,

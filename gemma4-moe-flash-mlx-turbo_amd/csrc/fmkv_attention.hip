@@ -39,32 +39,49 @@ __device__ inline int qk_dim(int g, int s, int j, int i) {
     return g * 64 + s * 32 + j * 8 + i;
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 template <int BITS, int GW>
 struct BlockRegs {
   static constexpr int kCodeLoads = (BITS == 8) ? GW : GW / 2;
-  uint4 k[kCodeLoads];
-  uint4 v[kCodeLoads];
-  uint4 ks[GW];
-  uint4 vs[GW];
+  u32x4 k[kCodeLoads];
+  u32x4 v[kCodeLoads];
+  u32x4 ks[GW];
+  u32x4 vs[GW];
 };
 
+// One head-block's slice for this wave via buffer loads: the block base is a
+// scalar resource (bounded by the block size; out-of-range reads return 0),
+// lanes differ only in a 32-bit offset.
+// `valid` false gives a zero-size resource: the loads are dropped by the
+// hardware (no memory traffic) and return zeros, so callers can issue them
+// unconditionally.
 template <int D, int BITS, int GW>
-__device__ inline void load_block(BlockRegs<BITS, GW>& r, const uint8_t* blk, int wave, int lane) {
+__device__ inline void load_block(BlockRegs<BITS, GW>& r, const uint8_t* blk, bool valid, int wave,
+                                  int lane) {
   constexpr BlockLayout L = make_layout(D, BITS, kAffine);
   constexpr int kLoads = BlockRegs<BITS, GW>::kCodeLoads;
-  const int j = lane >> 4;
-  // chunk index of this wave's first code chunk
-  const int c0 = wave * kLoads;
+  // the block base is the same for the whole wave; say so, so that the
+  // resource lives in SGPRs
+  const uint64_t addr = reinterpret_cast<uint64_t>(blk);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)addr);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(addr >> 32));
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), 0,
+                                        valid ? (int)L.block_bytes : 0, 0x00020000);
+  const int vo = lane * 16;          // 16 bytes per lane of a 1 KiB chunk
+  const int so = (lane >> 4) * 16;   // 4 tokens' {scale, bias} of a group
+  const int c0 = wave * kLoads;      // this wave's first code chunk
 #pragma unroll
   for (int i = 0; i < kLoads; i++) {
-    r.k[i] = *reinterpret_cast<const uint4*>(blk + L.k_codes + (c0 + i) * 1024 + lane * 16);
-    r.v[i] = *reinterpret_cast<const uint4*>(blk + L.v_codes + (c0 + i) * 1024 + lane * 16);
+    r.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, vo, (int)L.k_codes + (c0 + i) * 1024, 0);
+    r.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, vo, (int)L.v_codes + (c0 + i) * 1024, 0);
   }
 #pragma unroll
   for (int gi = 0; gi < GW; gi++) {
     const int g = wave * GW + gi;
-    r.ks[gi] = *reinterpret_cast<const uint4*>(blk + L.k_meta + g * 64 + j * 16);
-    r.vs[gi] = *reinterpret_cast<const uint4*>(blk + L.v_meta + g * 64 + j * 16);
+    r.ks[gi] = __builtin_amdgcn_raw_buffer_load_b128(rs, so, (int)L.k_meta + g * 64, 0);
+    r.vs[gi] = __builtin_amdgcn_raw_buffer_load_b128(rs, so, (int)L.v_meta + g * 64, 0);
   }
 }
 
@@ -72,14 +89,12 @@ __device__ inline void load_block(BlockRegs<BITS, GW>& r, const uint8_t* blk, in
 template <int BITS, int GW>
 __device__ inline half8_t k_operand(const BlockRegs<BITS, GW>& r, int gi, int s) {
   if constexpr (BITS == 8) {
-    const uint4 u = r.k[gi];
-    const uint32_t w0 = s ? u.z : u.x, w1 = s ? u.w : u.y;
+    const u32x4 u = r.k[gi];
+    const uint32_t w0 = u[2 * s], w1 = u[2 * s + 1];
     return cat8(u8x2_to_h2(w0, 0x04010400u), u8x2_to_h2(w0, 0x04030402u),
                 u8x2_to_h2(w1, 0x04010400u), u8x2_to_h2(w1, 0x04030402u));
   } else {
-    const uint4 u = r.k[gi >> 1];
-    const int wi = (gi & 1) * 2 + s;
-    const uint32_t w = wi == 0 ? u.x : wi == 1 ? u.y : wi == 2 ? u.z : u.w;
+    const uint32_t w = r.k[gi >> 1][(gi & 1) * 2 + s];
     return cat8(u4x2_to_h2(w, 0), u4x2_to_h2(w, 1), u4x2_to_h2(w, 2), u4x2_to_h2(w, 3));
   }
 }
@@ -88,14 +103,11 @@ __device__ inline half8_t k_operand(const BlockRegs<BITS, GW>& r, int gi, int s)
 template <int BITS, int GW>
 __device__ inline half4_t v_operand(const BlockRegs<BITS, GW>& r, int gi, int ct) {
   if constexpr (BITS == 8) {
-    const uint4 u = r.v[gi];
-    const uint32_t w = ct == 0 ? u.x : ct == 1 ? u.y : ct == 2 ? u.z : u.w;
+    const uint32_t w = r.v[gi][ct];
     return cat4(u8x2_to_h2(w, 0x04010400u), u8x2_to_h2(w, 0x04030402u));
   } else {
-    const uint4 u = r.v[gi >> 1];
     const int ctc = (gi & 1) * 4 + ct;  // column tile inside the 128-dim chunk
-    const int wi = ctc >> 1;
-    const uint32_t w = wi == 0 ? u.x : wi == 1 ? u.y : wi == 2 ? u.z : u.w;
+    const uint32_t w = r.v[gi >> 1][ctc >> 1];
     const int k0 = (ctc & 1) * 2;
     return cat4(u4x2_to_h2(w, k0), u4x2_to_h2(w, k0 + 1));
   }
@@ -104,35 +116,25 @@ __device__ inline half4_t v_operand(const BlockRegs<BITS, GW>& r, int gi, int ct
 __device__ inline float lo16(uint32_t w) { return f16_bits_to_f32(w); }
 __device__ inline float hi16(uint32_t w) { return f16_bits_to_f32(w >> 16); }
 
-// Cooperative FWHT over `heads` rows of D floats in LDS (NT threads).
-template <int D, int NT>
-__device__ inline void lds_fwht(float* buf, int heads) {
-  const int n_pairs = heads * D / 2;
-  for (int h = 1; h < D; h <<= 1) {
-    for (int idx = threadIdx.x; idx < n_pairs; idx += NT) {
-      const int i = (idx / h) * 2 * h + (idx % h);
-      const float a = buf[i], b = buf[i + h];
-      buf[i] = a + b;
-      buf[i + h] = a - b;
-    }
-    __syncthreads();
-  }
-}
-
+// Three waves per SIMD (register budget <= 168): enough resident waves to hide
+// the MFMA / LDS latencies of a block while two blocks per wave are in flight.
 template <int D, int BITS, int DW>
-__global__ __launch_bounds__((D / DW) * 64) void decode_attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__((D / DW) * 64) __attribute__((amdgpu_waves_per_eu(3, 8)))
+void decode_attn_kernel(AttnArgs a) {
   constexpr int NW = D / DW;
   constexpr int GW = DW / 64;
-  constexpr int NT = NW * 64;
   constexpr int NG = D / 64;
   static_assert(BITS == 8 || GW % 2 == 0, "4-bit needs 128-dim wave slices");
 
-  __shared__ float qo[8 * D];                 // q_rot, then the split's O
+  constexpr int QS = D + 4;                   // padded row stride (LDS banks)
+  __shared__ float qo[8 * QS];                // q_rot, then the split's O
   __shared__ float4_t sx[2][NW > 1 ? NW : 1][64];  // partial S exchange
   __shared__ float qsum_s[8][NG];
   __shared__ float ml_s[8][2];
+  __shared__ float sgn_s[D];                  // RHT signs, for the epilogue
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int j = lane >> 4, c = lane & 15;
   const int head = c & 7;
   const bool hi = c < 8;
@@ -159,21 +161,66 @@ __global__ __launch_bounds__((D / DW) * 64) void decode_attn_kernel(AttnArgs a) 
     return hbase + phys * a.st.block_stride;
   };
 
-  BlockRegs<BITS, GW> nxt;
-  if (b_begin < b_end) load_block<D, BITS, GW>(nxt, blk_ptr(b_begin), wave, lane);
-
-  // ---- q prologue: q_rot = (FWHT(q * qscale) * c) o s, per GQA head ----
+  // ---- first in the memory queue: this wave's q rows and the sign vector
+  // (kept in registers for the epilogue too), so they do not wait behind the
+  // block stream ----
+  constexpr int E = D / 64;
+  constexpr int LPG = 64 / E;          // lanes per 64-dim group
+  constexpr int kHPW = (8 + NW - 1) / NW;  // GQA heads per wave, at most
   const uint16_t* qg = a.q + ((int64_t)seq * a.n_q_heads + (int64_t)kvh * G) * D;
-  for (int idx = tid; idx < G * D; idx += NT) qo[idx] = bf16_to_f32(qg[idx]) * a.qscale;
-  __syncthreads();
-  lds_fwht<D, NT>(qo, G);
-  for (int idx = tid; idx < G * D; idx += NT) qo[idx] = (qo[idx] * a.c) * a.signs[idx % D];
-  __syncthreads();
-  for (int idx = tid; idx < G * NG; idx += NT) {
-    const int hh = idx / NG, g = idx % NG;
-    float s = 0.0f;
-    for (int d = 0; d < 64; d++) s += qo[hh * D + g * 64 + d];
-    qsum_s[hh][g] = s;
+  float qx[kHPW][E];
+#pragma unroll
+  for (int k = 0; k < kHPW; k++) {
+    const int hh = wave + k * NW;
+    if (hh < G) load_row<E>(qg + hh * D + lane * E, qx[k]);
+  }
+  float sg[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) sg[i] = a.signs[lane * E + i];
+
+  // Loads are issued unconditionally: a block past the split gets a zero-size
+  // resource (no traffic) and its tokens are masked, so the loaded registers
+  // never merge with stale ones across the loop and no copy forces a wait.
+  const int64_t b_last = b_end > b_begin ? b_end - 1 : b_begin;
+  auto fetch = [&](BlockRegs<BITS, GW>& r, int64_t lb) {
+    const bool valid = lb < b_end;
+    load_block<D, BITS, GW>(r, blk_ptr(valid ? lb : b_last), valid, wave, lane);
+  };
+  // two blocks in flight per wave while the prologue runs
+  BlockRegs<BITS, GW> nx1, nx2;
+  fetch(nx1, b_begin);
+  fetch(nx2, b_begin + 1);
+
+  // ---- q prologue: q_rot = (FWHT(q * qscale) * c) o s ----
+#pragma unroll
+  for (int k = 0; k < kHPW; k++) {
+    const int hh = wave + k * NW;
+    if (hh >= G) continue;
+    float x[E];
+#pragma unroll
+    for (int i = 0; i < E; i++) x[i] = qx[k][i] * a.qscale;
+    wave_fwht<E>(x, lane);
+    float gsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      x[i] = (x[i] * a.c) * sg[i];
+      gsum += x[i];
+    }
+#pragma unroll
+    for (int i = 0; i < E; i += (E >= 4 ? 4 : E)) {
+      if constexpr (E >= 4)
+        *reinterpret_cast<float4_t*>(&qo[hh * QS + lane * E + i]) =
+            (float4_t){x[i], x[i + 1], x[i + 2], x[i + 3]};
+      else
+        for (int t = 0; t < E; t++) qo[hh * QS + lane * E + t] = x[t];
+    }
+#pragma unroll
+    for (int m = 1; m < LPG; m <<= 1) gsum += __shfl_xor(gsum, m);
+    if ((lane & (LPG - 1)) == 0) qsum_s[hh][lane / LPG] = gsum;
+  }
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < E; i++) sgn_s[lane * E + i] = sg[i];
   }
   __syncthreads();
 
@@ -186,7 +233,7 @@ __global__ __launch_bounds__((D / DW) * 64) void decode_attn_kernel(AttnArgs a) 
     for (int s = 0; s < 2; s++) {
 #pragma unroll
       for (int i = 0; i < 8; i++) {
-        const float v = col_valid ? qo[head * D + qk_dim<BITS>(g, s, j, i)] : 0.0f;
+        const float v = col_valid ? qo[head * QS + qk_dim<BITS>(g, s, j, i)] : 0.0f;
         const _Float16 vh = (_Float16)v;
         bq[gi][s][i] = hi ? vh : (_Float16)(v - (float)vh);
       }
@@ -201,13 +248,21 @@ __global__ __launch_bounds__((D / DW) * 64) void decode_attn_kernel(AttnArgs a) 
   float bacc[GW];
 #pragma unroll
   for (int gi = 0; gi < GW; gi++) bacc[gi] = 0.0f;
-  float m_run = -INFINITY, l_run = 0.0f;
+  // m_run starts finite (-1e30): exp2(-inf - m) is 0 for masked tokens and
+  // exp2(m_old - m_new) underflows to 0 at the first visible token, so the
+  // softmax needs no special cases.
+  float m_run = -1e30f, l_run = 0.0f;
   int par = 0;
+  const float lo_sel = hi ? 0.0f : 1.0f;  // 1 on the residual columns
 
-  for (int64_t b = b_begin; b < b_end; b++) {
-    const BlockRegs<BITS, GW> cur = nxt;
-    if (b + 1 < b_end) load_block<D, BITS, GW>(nxt, blk_ptr(b + 1), wave, lane);
+  // visible slots: linear [vis_lo, vis_hi); ring [0, min(T, W)), unless a trim
+  // hides older positions (then each slot's position is computed)
+  const int64_t vis_lo = a.window > 0 ? 0 : a.vis_begin;
+  const int64_t vis_hi = a.window > 0 ? (T < a.window ? T : a.window) : T;
+  const bool ring_trim = a.window > 0 && a.vis_begin > T - a.window;
 
+  auto process = [&](const BlockRegs<BITS, GW>& cur, int64_t b) {
+    // S^T = K . q_rot^T per 64-dim group, then * scale + bias * sum(q)
     float4_t sv = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int gi = 0; gi < GW; gi++) {
@@ -216,8 +271,7 @@ __global__ __launch_bounds__((D / DW) * 64) void decode_attn_kernel(AttnArgs a) 
                                                    acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand<BITS, GW>(cur, gi, 1), bq[gi][1],
                                                    acc, 0, 0, 0);
-      const uint4 ks = cur.ks[gi];
-      const uint32_t kw[4] = {ks.x, ks.y, ks.z, ks.w};
+      const u32x4 kw = cur.ks[gi];
 #pragma unroll
       for (int i = 0; i < 4; i++) sv[i] = fmaf(lo16(kw[i]), acc[i], fmaf(hi16(kw[i]), qs[gi], sv[i]));
     }
@@ -233,19 +287,25 @@ __global__ __launch_bounds__((D / DW) * 64) void decode_attn_kernel(AttnArgs a) 
 #pragma unroll
     for (int i = 0; i < 4; i++) s[i] = sv[i] + row_ror8(sv[i]);
 
-    // visibility of tokens 4j..4j+3 of this block
+    // visibility: whole block in the common case (uniform test), per token
+    // only at the edges of the visible range
+    const int64_t t0 = b * kBlockTokens;
+    const bool full = b < b_end && t0 >= vis_lo && t0 + kBlockTokens <= vis_hi && !ring_trim;
+    if (!full) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int64_t slot = b * kBlockTokens + 4 * j + i;
-      const int64_t p = slot_position(slot, T, a.window);
-      if (p < 0 || p < a.vis_begin) s[i] = -INFINITY;
+      for (int i = 0; i < 4; i++) {
+        const int64_t slot = t0 + 4 * j + i;
+        bool vis = b < b_end && slot >= vis_lo && slot < vis_hi;
+        if (ring_trim) vis = vis && slot_position(slot, T, a.window) >= a.vis_begin;
+        if (!vis) s[i] = -INFINITY;
+      }
     }
     float mb = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     mb = xor16_max(mb);
     mb = xor32_max(mb);
     const float m_new = fmaxf(m_run, mb);
-    if (__builtin_amdgcn_read_exec() && __any(m_new > m_run)) {
-      const float alpha = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - m_new);
+    if (__any(m_new > m_run)) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
 #pragma unroll
       for (int i = 0; i < GW * 4; i++) o[i] *= alpha;
 #pragma unroll
@@ -255,26 +315,41 @@ __global__ __launch_bounds__((D / DW) * 64) void decode_attn_kernel(AttnArgs a) 
     }
     float p[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) p[i] = (s[i] == -INFINITY) ? 0.0f : exp2f(s[i] - m_run);
+    for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(s[i] - m_run);
     l_run += (p[0] + p[1]) + (p[2] + p[3]);
 
+    // O^T += V^T . P'^T with P' = p * v_scale as f16 hi (c < 8) / residual (c >= 8)
 #pragma unroll
     for (int gi = 0; gi < GW; gi++) {
-      const uint4 vsr = cur.vs[gi];
-      const uint32_t vw[4] = {vsr.x, vsr.y, vsr.z, vsr.w};
-      half4_t bp;
+      const u32x4 vw = cur.vs[gi];
+      float x[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float x = p[i] * lo16(vw[i]);
-        const _Float16 xh = (_Float16)x;
-        bp[i] = hi ? xh : (_Float16)(x - (float)xh);
+        x[i] = p[i] * lo16(vw[i]);
         bacc[gi] = fmaf(p[i], hi16(vw[i]), bacc[gi]);
       }
+      const half2_t h01 = pkrtz(x[0], x[1]);
+      const half2_t h23 = pkrtz(x[2], x[3]);
+      const half4_t bp = cat4(
+          pkrtz(fmaf(-lo_sel, (float)h01[0], x[0]),
+                                     fmaf(-lo_sel, (float)h01[1], x[1])),
+          pkrtz(fmaf(-lo_sel, (float)h23[0], x[2]),
+                                     fmaf(-lo_sel, (float)h23[1], x[3])));
 #pragma unroll
       for (int ct = 0; ct < 4; ct++)
         o[gi * 4 + ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(v_operand<BITS, GW>(cur, gi, ct),
                                                                bp, o[gi * 4 + ct], 0, 0, 0);
     }
+  };
+
+  // ping-pong over two register sets: while one block is processed the other
+  // is in flight; a set is reloaded as soon as it has been consumed (no
+  // register copies, which would force a wait on every outstanding load)
+  for (int64_t b = b_begin; b < b_end; b += 2) {
+    process(nx1, b);
+    fetch(nx1, b + 2);
+    process(nx2, b + 1);  // fully masked when b + 1 == b_end
+    fetch(nx2, b + 3);
   }
 
   // ---- epilogue ----
@@ -290,75 +365,123 @@ __global__ __launch_bounds__((D / DW) * 64) void decode_attn_kernel(AttnArgs a) 
 #pragma unroll
     for (int i = 0; i < 4; i++) o[k][i] = o[k][i] + row_ror8(o[k][i]);
 
-  __syncthreads();  // everyone is done reading q_rot out of qo
+  __syncthreads();  // all waves are done reading q_rot out of qo
   if (hi && col_valid) {
 #pragma unroll
     for (int gi = 0; gi < GW; gi++)
 #pragma unroll
-      for (int ct = 0; ct < 4; ct++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int d = (wave * GW + gi) * 64 + ct * 16 + 4 * j + i;
-          qo[head * D + d] = (o[gi * 4 + ct][i] + bacc[gi]) * a.signs[d];
-        }
+      for (int ct = 0; ct < 4; ct++) {
+        const int d = (wave * GW + gi) * 64 + ct * 16 + 4 * j;
+        *reinterpret_cast<float4_t*>(&qo[head * QS + d]) = o[gi * 4 + ct] + bacc[gi];
+      }
     if (wave == 0 && j == 0) {
       ml_s[head][0] = m_run;
       ml_s[head][1] = l_run;
     }
   }
   __syncthreads();
-  lds_fwht<D, NT>(qo, G);
 
+  // inverse rotation o . R^T = c * FWHT(o o s), one head per wave, then store
   const int64_t qh0 = (int64_t)seq * a.n_q_heads + (int64_t)kvh * G;
-  if (a.direct) {
-    for (int idx = tid; idx < G * D; idx += NT) {
-      const int hh = idx / D;
+  const int64_t pbase = ((int64_t)seq * a.max_splits + split) * a.n_q_heads + (int64_t)kvh * G;
+  for (int hh = wave; hh < G; hh += NW) {
+    float x[E];
+#pragma unroll
+    for (int i = 0; i < E; i++) x[i] = qo[hh * QS + lane * E + i] * sgn_s[lane * E + i];
+    wave_fwht<E>(x, lane);
+    if (a.direct) {
       const float l = ml_s[hh][1];
-      const float v = l > 0.0f ? (qo[idx] * a.c) / l : 0.0f;
-      const int64_t o_idx = qh0 * D + idx;
-      if (a.out_f32)
-        reinterpret_cast<float*>(a.out)[o_idx] = v;
-      else
-        reinterpret_cast<uint16_t*>(a.out)[o_idx] = f32_to_bf16(v);
-    }
-  } else {
-    const int64_t base = ((int64_t)seq * a.max_splits + split) * a.n_q_heads + (int64_t)kvh * G;
-    for (int idx = tid; idx < G * D; idx += NT) a.part_o[base * D + idx] = qo[idx] * a.c;
-    if (tid < G) {
-      a.part_ml[(base + tid) * 2 + 0] = ml_s[tid][0];
-      a.part_ml[(base + tid) * 2 + 1] = ml_s[tid][1];
+      const int64_t o_idx = (qh0 + hh) * D + lane * E;
+#pragma unroll
+      for (int i = 0; i < E; i++) {
+        const float v = l > 0.0f ? (x[i] * a.c) / l : 0.0f;
+        if (a.out_f32)
+          reinterpret_cast<float*>(a.out)[o_idx + i] = v;
+        else
+          reinterpret_cast<uint16_t*>(a.out)[o_idx + i] = f32_to_bf16(v);
+      }
+    } else {
+      float* dst = a.part_o + (pbase + hh) * D + lane * E;
+      if constexpr (E % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < E; i += 4)
+          *reinterpret_cast<float4_t*>(dst + i) =
+              (float4_t){x[i] * a.c, x[i + 1] * a.c, x[i + 2] * a.c, x[i + 3] * a.c};
+      } else {
+#pragma unroll
+        for (int i = 0; i < E; i++) dst[i] = x[i] * a.c;
+      }
+      if (lane == 0) {
+        a.part_ml[(pbase + hh) * 2 + 0] = ml_s[hh][0];
+        a.part_ml[(pbase + hh) * 2 + 1] = ml_s[hh][1];
+      }
     }
   }
 }
 
 // out[seq][h][d] = sum_s 2^(m_s - M) O_s[d] / sum_s 2^(m_s - M) l_s.
+// One work-group per (64 dims, q head, sequence); thread (sl, dq) owns dims
+// d0 + 4*dq .. +3 and splits sl, sl + 16, ...; partial sums meet in LDS.
 template <int D>
-__global__ __launch_bounds__(64) void combine_kernel(AttnArgs a) {
-  const int seq = blockIdx.z, h = blockIdx.y;
-  const int d = blockIdx.x * 64 + threadIdx.x;
+__global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
+  __shared__ float red_m[256];
+  __shared__ float4_t red_o[16][16];
+  __shared__ float red_l[16];
+  const int seq = blockIdx.z, h = blockIdx.y, tid = threadIdx.x;
+  const int dq = tid & 15, sl = tid >> 4;
+  const int d0 = blockIdx.x * 64 + dq * 4;
   const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
   const int n_splits = n_splits_for(geo, a.bps, a.max_splits);
   const int64_t stride = (int64_t)a.n_q_heads;
   const int64_t base = (int64_t)seq * a.max_splits * stride + h;
+
   float M = -INFINITY;
-  for (int s = 0; s < n_splits; s++) M = fmaxf(M, a.part_ml[(base + s * stride) * 2]);
-  float num = 0.0f, den = 0.0f;
+  for (int s = tid; s < n_splits; s += 256) M = fmaxf(M, a.part_ml[(base + s * stride) * 2]);
+  red_m[tid] = M;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (tid < w) red_m[tid] = fmaxf(red_m[tid], red_m[tid + w]);
+    __syncthreads();
+  }
+  M = red_m[0];
+
+  float4_t acc = (float4_t){0.f, 0.f, 0.f, 0.f};
+  float den = 0.0f;
   if (M != -INFINITY) {
-    for (int s = 0; s < n_splits; s++) {
+#pragma unroll 4
+    for (int s = sl; s < n_splits; s += 16) {
       const int64_t r = base + s * stride;
-      const float w = exp2f(a.part_ml[r * 2] - M);
-      den = fmaf(w, a.part_ml[r * 2 + 1], den);
-      num = fmaf(w, a.part_o[r * D + d], num);
+      const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + r * 2);
+      const float w = exp2f(ml.x - M);
+      den = fmaf(w, ml.y, den);
+      const float4_t ov = *reinterpret_cast<const float4_t*>(a.part_o + r * D + d0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) acc[i] = fmaf(w, ov[i], acc[i]);
     }
   }
-  const float v = den > 0.0f ? num / den : 0.0f;
-  const int64_t o_idx = ((int64_t)seq * a.n_q_heads + h) * D + d;
-  if (a.out_f32)
-    reinterpret_cast<float*>(a.out)[o_idx] = v;
-  else
-    reinterpret_cast<uint16_t*>(a.out)[o_idx] = f32_to_bf16(v);
+  red_o[sl][dq] = acc;
+  if (dq == 0) red_l[sl] = den;
+  __syncthreads();
+  if (tid < 16) {
+    float4_t s = red_o[0][tid];
+    float L = red_l[0];
+#pragma unroll
+    for (int k = 1; k < 16; k++) {
+      s += red_o[k][tid];
+      L += red_l[k];
+    }
+    const int64_t o_idx = ((int64_t)seq * a.n_q_heads + h) * D + blockIdx.x * 64 + tid * 4;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float v = L > 0.0f ? s[i] / L : 0.0f;
+      if (a.out_f32)
+        reinterpret_cast<float*>(a.out)[o_idx + i] = v;
+      else
+        reinterpret_cast<uint16_t*>(a.out)[o_idx + i] = f32_to_bf16(v);
+    }
+  }
 }
 
 template <int D, int BITS>
@@ -373,7 +496,7 @@ hipError_t launch_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s
   if (ev1) (void)hipEventRecord(ev1, s);
   if (e != hipSuccess || a.direct) return e;
   dim3 cgrid(D / 64, a.n_q_heads, n_seqs);
-  hipLaunchKernelGGL((combine_kernel<D>), cgrid, dim3(64), 0, s, a);
+  hipLaunchKernelGGL((combine_kernel<D>), cgrid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -72,10 +72,65 @@ __device__ inline half2_t u4x2_to_h2(uint32_t w, int k) {
   return __builtin_bit_cast(half2_t, x) - (half2_t){(_Float16)1024.0f, (_Float16)1024.0f};
 }
 
+// Two f32 -> packed f16, round toward zero (v_cvt_pkrtz_f16_f32).
+__device__ inline half2_t pkrtz(float a, float b) {
+  return __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+
 __device__ inline half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t d) {
   return (half8_t){a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 __device__ inline half4_t cat4(half2_t a, half2_t b) { return (half4_t){a[0], a[1], b[0], b[1]}; }
+
+// E contiguous bf16 values -> f32 (one 32/64/128-bit load).
+template <int E>
+__device__ inline void load_row(const uint16_t* src, float (&x)[E]) {
+  if constexpr (E == 8) {
+    const uint4 u = *reinterpret_cast<const uint4*>(src);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      x[2 * i] = __uint_as_float(w[i] << 16);
+      x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  } else if constexpr (E == 4) {
+    const uint2 u = *reinterpret_cast<const uint2*>(src);
+    x[0] = __uint_as_float(u.x << 16);
+    x[1] = __uint_as_float(u.x & 0xffff0000u);
+    x[2] = __uint_as_float(u.y << 16);
+    x[3] = __uint_as_float(u.y & 0xffff0000u);
+  } else {
+    const uint32_t u = *reinterpret_cast<const uint32_t*>(src);
+    x[0] = __uint_as_float(u << 16);
+    x[1] = __uint_as_float(u & 0xffff0000u);
+  }
+}
+
+// Canonical unnormalised FWHT of a D = 64*E row held as E contiguous values
+// per lane: stages h = 1 .. E/2 in registers, then h = E .. D/2 across lanes
+// (lane xor h/E); (a, b) -> (a + b, a - b) exactly as the oracle.
+template <int E>
+__device__ inline void wave_fwht(float (&x)[E], int lane) {
+#pragma unroll
+  for (int h = 1; h < E; h <<= 1)
+#pragma unroll
+    for (int i = 0; i < E; i += 2 * h)
+#pragma unroll
+      for (int jj = i; jj < i + h; jj++) {
+        const float a = x[jj], b = x[jj + h];
+        x[jj] = a + b;
+        x[jj + h] = a - b;
+      }
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const bool upper = (lane & m) != 0;
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      const float p = __shfl_xor(x[i], m);
+      x[i] = upper ? (p - x[i]) : (x[i] + p);
+    }
+  }
+}
 
 // Visible-position test shared by the attention and combine kernels.
 struct SeqGeom {
