@@ -29,7 +29,7 @@ __constant__ float kCbBounds4[15] = {-2.401f, -1.844f, -1.437f, -1.099f, -0.800f
 // MLX affine_quantize for the group spanning 64/E lanes (see oracle).
 template <int E, int BITS>
 __device__ inline void affine_quant(const float (&y)[E], uint32_t (&code)[E], float& scale_o,
-                                    float& bias_o) {
+                                    float& bias_o, int lane) {
   constexpr int kLanesPerGroup = 64 / E;
   float mx = y[0], mn = y[0];
 #pragma unroll
@@ -37,11 +37,8 @@ __device__ inline void affine_quant(const float (&y)[E], uint32_t (&code)[E], fl
     mx = fmaxf(mx, y[i]);
     mn = fminf(mn, y[i]);
   }
-#pragma unroll
-  for (int m = 1; m < kLanesPerGroup; m <<= 1) {
-    mx = fmaxf(mx, __shfl_xor(mx, m));
-    mn = fminf(mn, __shfl_xor(mn, m));
-  }
+  mx = group_max<kLanesPerGroup>(mx, lane);
+  mn = group_min<kLanesPerGroup>(mn, lane);
   const float n_bins = (float)((1 << BITS) - 1);
   float scale = fmaxf((mx - mn) / n_bins, 1e-7f);
   const bool side = fabsf(mn) > fabsf(mx);
@@ -66,16 +63,14 @@ __device__ inline void affine_quant(const float (&y)[E], uint32_t (&code)[E], fl
 // Sum of squares in the oracle's order: per-lane left to right, then a
 // xor-butterfly over all 64 lanes.
 template <int E>
-__device__ inline float canonical_sumsq(const float (&x)[E]) {
+__device__ inline float canonical_sumsq(const float (&x)[E], int lane) {
   float acc = x[0] * x[0];
 #pragma unroll
   for (int i = 1; i < E; i++) {
     float sq = x[i] * x[i];
     acc = acc + sq;
   }
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) acc = acc + __shfl_xor(acc, m);
-  return acc;
+  return group_sum<64>(acc, lane);
 }
 
 __device__ inline int cb_index(float z, int bits) {
@@ -192,7 +187,7 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
       for (int i = 0; i < E; i++) x[i] = (x[i] * a.c) * a.signs[lane * E + i];
       uint32_t code[E];
       float scale, bias;
-      affine_quant<E, BITS>(x, code, scale, bias);
+      affine_quant<E, BITS>(x, code, scale, bias, lane);
 #pragma unroll
       for (int i = 0; i < E; i++) {
         int64_t off;
@@ -211,7 +206,7 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
       }
     } else {
       constexpr int bits = BITS;
-      const float norm = sqrtf(canonical_sumsq<E>(x));
+      const float norm = sqrtf(canonical_sumsq<E>(x, lane));
       const float den = norm + 1e-8f;
 #pragma unroll
       for (int i = 0; i < E; i++) x[i] = x[i] / den;

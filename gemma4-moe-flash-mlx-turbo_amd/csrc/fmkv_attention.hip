@@ -214,8 +214,7 @@ void decode_attn_kernel(AttnArgs a) {
       else
         for (int t = 0; t < E; t++) qo[hh * QS + lane * E + t] = x[t];
     }
-#pragma unroll
-    for (int m = 1; m < LPG; m <<= 1) gsum += __shfl_xor(gsum, m);
+    gsum = group_sum<LPG>(gsum, lane);
     if ((lane & (LPG - 1)) == 0) qsum_s[hh][lane / LPG] = gsum;
   }
   if (wave == 0) {

@@ -106,6 +106,76 @@ __device__ inline void load_row(const uint16_t* src, float (&x)[E]) {
   }
 }
 
+// Value of lane (lane ^ M), in registers: DPP quad_perm (M = 1, 2), row
+// shifts (M = 4: lanes with bit 2 clear read lane + 4, the others lane - 4),
+// row_ror:8 (M = 8) and the permlane swaps (M = 16, 32).
+template <int M>
+__device__ inline float xor_partner(float v, int lane) {
+  const int iv = __builtin_bit_cast(int, v);
+  if constexpr (M == 1) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xf, 0xf, false));
+  } else if constexpr (M == 2) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xf, 0xf, false));
+  } else if constexpr (M == 4) {
+    const int up = __builtin_amdgcn_update_dpp(0, iv, 0x104, 0xf, 0xf, false);  // lane + 4
+    const int dn = __builtin_amdgcn_update_dpp(0, iv, 0x114, 0xf, 0xf, false);  // lane - 4
+    return __builtin_bit_cast(float, (lane & 4) ? dn : up);
+  } else if constexpr (M == 8) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xf, 0xf, false));
+  } else if constexpr (M == 16) {
+    auto r = __builtin_amdgcn_permlane16_swap((uint32_t)iv, (uint32_t)iv, false, false);
+    return __uint_as_float((lane & 16) ? r[0] : r[1]);
+  } else {
+    auto r = __builtin_amdgcn_permlane32_swap((uint32_t)iv, (uint32_t)iv, false, false);
+    return __uint_as_float((lane & 32) ? r[0] : r[1]);
+  }
+}
+
+// Butterfly reductions over aligned groups of LANES lanes (strides 1, 2, ...,
+// LANES/2, own value first): every lane of a group ends with the same bits.
+template <int LANES>
+__device__ inline float group_sum(float v, int lane) {
+  if constexpr (LANES > 1) v = v + xor_partner<1>(v, lane);
+  if constexpr (LANES > 2) v = v + xor_partner<2>(v, lane);
+  if constexpr (LANES > 4) v = v + xor_partner<4>(v, lane);
+  if constexpr (LANES > 8) v = v + xor_partner<8>(v, lane);
+  if constexpr (LANES > 16) v = v + xor_partner<16>(v, lane);
+  if constexpr (LANES > 32) v = v + xor_partner<32>(v, lane);
+  return v;
+}
+template <int LANES>
+__device__ inline float group_max(float v, int lane) {
+  if constexpr (LANES > 1) v = fmaxf(v, xor_partner<1>(v, lane));
+  if constexpr (LANES > 2) v = fmaxf(v, xor_partner<2>(v, lane));
+  if constexpr (LANES > 4) v = fmaxf(v, xor_partner<4>(v, lane));
+  if constexpr (LANES > 8) v = fmaxf(v, xor_partner<8>(v, lane));
+  if constexpr (LANES > 16) v = fmaxf(v, xor_partner<16>(v, lane));
+  if constexpr (LANES > 32) v = fmaxf(v, xor_partner<32>(v, lane));
+  return v;
+}
+template <int LANES>
+__device__ inline float group_min(float v, int lane) {
+  if constexpr (LANES > 1) v = fminf(v, xor_partner<1>(v, lane));
+  if constexpr (LANES > 2) v = fminf(v, xor_partner<2>(v, lane));
+  if constexpr (LANES > 4) v = fminf(v, xor_partner<4>(v, lane));
+  if constexpr (LANES > 8) v = fminf(v, xor_partner<8>(v, lane));
+  if constexpr (LANES > 16) v = fminf(v, xor_partner<16>(v, lane));
+  if constexpr (LANES > 32) v = fminf(v, xor_partner<32>(v, lane));
+  return v;
+}
+
+// One cross-lane FWHT stage at lane stride M: (a, b) -> (a + b, a - b), the
+// upper lane of each pair computing partner - own.
+template <int M, int E>
+__device__ inline void fwht_lane_stage(float (&x)[E], int lane) {
+  const bool upper = (lane & M) != 0;
+#pragma unroll
+  for (int i = 0; i < E; i++) {
+    const float p = xor_partner<M>(x[i], lane);
+    x[i] = upper ? (p - x[i]) : (x[i] + p);
+  }
+}
+
 // Canonical unnormalised FWHT of a D = 64*E row held as E contiguous values
 // per lane: stages h = 1 .. E/2 in registers, then h = E .. D/2 across lanes
 // (lane xor h/E); (a, b) -> (a + b, a - b) exactly as the oracle.
@@ -121,15 +191,12 @@ __device__ inline void wave_fwht(float (&x)[E], int lane) {
         x[jj] = a + b;
         x[jj + h] = a - b;
       }
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const bool upper = (lane & m) != 0;
-#pragma unroll
-    for (int i = 0; i < E; i++) {
-      const float p = __shfl_xor(x[i], m);
-      x[i] = upper ? (p - x[i]) : (x[i] + p);
-    }
-  }
+  fwht_lane_stage<1>(x, lane);
+  fwht_lane_stage<2>(x, lane);
+  fwht_lane_stage<4>(x, lane);
+  fwht_lane_stage<8>(x, lane);
+  fwht_lane_stage<16>(x, lane);
+  fwht_lane_stage<32>(x, lane);
 }
 
 // Visible-position test shared by the attention and combine kernels.

@@ -52,7 +52,15 @@ struct AttnArgs {
   void* out;          // [n_seqs][n_q_heads][D]
   int32_t out_f32;
   int32_t direct;     // 1: no combine, write out
+  // rotated q in MFMA operand layout, written by the q-prep kernel:
+  // [n_seqs][n_kv_heads][waves][64 lanes][kQPrepVecs x 16 B]
+  uint32_t* qprep;
+  uint32_t sign_bits[16];  // RHT signs of dims 0..511, bit set = -1
 };
+
+// 16-byte vectors per lane of the q-prep table (<= 2 groups x 2 MFMA
+// operands, plus the group sums).
+constexpr int kQPrepVecs = 5;
 
 struct ReadArgs {
   Store st;

@@ -131,26 +131,7 @@ __global__ __launch_bounds__(64) void fetch_kernel(FetchArgs a) {
       x[e] = w * a.signs[d];
     }
   }
-  // canonical FWHT (registers, then lanes)
-#pragma unroll
-  for (int hh = 1; hh < E; hh <<= 1)
-#pragma unroll
-    for (int b = 0; b < E; b += 2 * hh)
-#pragma unroll
-      for (int jj = b; jj < b + hh; jj++) {
-        const float p = x[jj], q = x[jj + hh];
-        x[jj] = p + q;
-        x[jj + hh] = p - q;
-      }
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const bool upper = (lane & m) != 0;
-#pragma unroll
-    for (int e = 0; e < E; e++) {
-      const float p = __shfl_xor(x[e], m);
-      x[e] = upper ? (p - x[e]) : (x[e] + p);
-    }
-  }
+  wave_fwht<E>(x, lane);
   void* dst = isv ? a.v_out : a.k_out;
   const int64_t base = (i * H + h) * D + lane * E;
 #pragma unroll
