@@ -99,8 +99,12 @@ def run_c3(args) -> dict:
 
     def step():
         nonlocal i
-        rc = lib.fmkv_cache_append(h, kp[i], vp[i], 1, stream)
-        rc |= lib.fmkv_decode_attention(h, qp[i], Hq, 1.0, 0.0, outp, fmkv.DTYPE_BF16, stream)
+        if args.unfused:
+            rc = lib.fmkv_cache_append(h, kp[i], vp[i], 1, stream)
+            rc |= lib.fmkv_decode_attention(h, qp[i], Hq, 1.0, 0.0, outp, fmkv.DTYPE_BF16, stream)
+        else:
+            rc = lib.fmkv_decode_step(h, kp[i], vp[i], 1, qp[i], Hq, 1.0, 0.0, outp,
+                                      fmkv.DTYPE_BF16, stream)
         if rc:
             raise RuntimeError(lib.fmkv_last_error().decode())
         i += 1
@@ -219,6 +223,8 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--bps", type=int, default=0, help="blocks per split-K work-group (0: auto)")
+    ap.add_argument("--unfused", action="store_true",
+                    help="time fmkv_cache_append + fmkv_decode_attention instead of fmkv_decode_step")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the KV path is "

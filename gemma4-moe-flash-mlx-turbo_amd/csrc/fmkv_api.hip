@@ -106,15 +106,24 @@ int device_cus() {
   return cus;
 }
 
-// Split-K plan: about two work-groups per CU, an even number of blocks each
-// (the kernel walks blocks in pairs).
-int32_t choose_bps(int64_t total_head_blocks, int cus) {
+// Split-K plan: blocks per split such that the grid has about `wg_per_cu`
+// work-groups per CU (each keeps several blocks in flight, so one per CU
+// already saturates HBM; more would only add split partials).
+int32_t choose_bps(int64_t total_head_blocks, int cus, int wg_per_cu) {
   if (g_bps_override > 0) return g_bps_override;
-  const int64_t target = 2 * (int64_t)cus;
+  const int64_t target = (int64_t)wg_per_cu * cus;
   int64_t bps = (total_head_blocks + target - 1) / target;
-  bps += bps & 1;
-  if (bps < 2) bps = 2;
+  if (bps < 1) bps = 1;
   return (int32_t)bps;
+}
+
+// src/cache.rs:29-43 signs as a bit mask (bit d set = -1), the form the
+// decode kernel takes them in as a kernel argument.
+void sign_bits_of(const fmkv_cache_desc& d, uint32_t out[16]) {
+  std::vector<float> s = lcg_signs(d.head_dim, d.sign_seed);
+  for (int w = 0; w < 16; w++) out[w] = 0;
+  for (int i = 0; i < d.head_dim; i++)
+    if (s[i] < 0.0f) out[i >> 5] |= 1u << (i & 31);
 }
 
 struct Workspace {
@@ -145,6 +154,7 @@ struct fmkv_cache {
   uint8_t* arena;
   int64_t n_blocks;
   float* d_signs;
+  uint32_t sign_bits[16];
   float c, sqrt_d;
   int64_t offset;
   int64_t vis_begin;
@@ -158,6 +168,7 @@ struct fmkv_pool {
   uint8_t* arena;
   int64_t n_blocks;
   float* d_signs;
+  uint32_t sign_bits[16];
   float c, sqrt_d;
   Workspace ws;
   int cus;
@@ -221,6 +232,149 @@ int check_attn_args(const fmkv_cache_desc& d, const void* q, int32_t n_q_heads, 
   return FMKV_OK;
 }
 
+// Validation and launch arguments of an append of n tokens at the cache's
+// offset (no state change).
+int prepare_append(const fmkv_cache* c, const void* k, const void* v, int64_t n,
+                   fmkv::AppendArgs* a, int64_t* tasks) {
+  if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
+  if (n < 0) return fail(FMKV_ERR_INVALID_ARG, "n_tokens must be >= 0");
+  if (n == 0) return FMKV_OK;
+  if (!k || !v) return fail(FMKV_ERR_INVALID_ARG, "k/v must be device pointers");
+  if (n > ((int64_t)1 << 30)) return fail(FMKV_ERR_INVALID_ARG, "n_tokens too large");
+  const int64_t W = c->desc.window;
+  if (W == 0 && c->offset + n > c->desc.capacity)
+    return fail(FMKV_ERR_CAPACITY, "append of " + std::to_string(n) + " tokens at offset " +
+                                       std::to_string(c->offset) + " exceeds capacity " +
+                                       std::to_string(c->desc.capacity));
+  if (c->offset + n > ((int64_t)1 << 31) - 64)
+    return fail(FMKV_ERR_CAPACITY, "position counter would exceed 2^31");
+  a->st = cache_store(c);
+  a->k = static_cast<const uint16_t*>(k);
+  a->v = static_cast<const uint16_t*>(v);
+  a->start_pos = nullptr;
+  a->start_scalar = c->offset;
+  a->n_new = (int32_t)n;
+  a->window = (int32_t)W;
+  std::memcpy(a->sign_bits, c->sign_bits, sizeof(a->sign_bits));
+  a->c = c->c;
+  a->sqrt_d = c->sqrt_d;
+  a->cb_bits = c->desc.bits;
+  a->qp.out = nullptr;
+  if (W > 0) {
+    const int64_t n_eff = n < W ? n : W;
+    *tasks = (n_eff + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens + 1;
+    if (*tasks > W / fmkv::kBlockTokens) *tasks = W / fmkv::kBlockTokens;
+  } else {
+    *tasks = (c->offset + n - 1) / fmkv::kBlockTokens - c->offset / fmkv::kBlockTokens + 1;
+  }
+  return FMKV_OK;
+}
+
+// Split-K plan, workspace ([part_o | part_ml | q-prep table]) and launch
+// arguments of decode attention over the first T positions; qp receives the
+// q-prep arguments (launched alone, or inside the append of a decode step).
+template <typename Owner>
+int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, int64_t nblk,
+                             const void* q, int32_t n_q_heads, float scale, float tau, void* out,
+                             int32_t out_dtype, int wg_per_cu, fmkv::AttnArgs* a,
+                             fmkv::QPrepArgs* qp) {
+  int rc = check_attn_args(o->desc, q, n_q_heads, tau, out, out_dtype);
+  if (rc) return rc;
+  const int H = o->desc.n_kv_heads, D = o->desc.head_dim;
+  a->st = st;
+  a->group = n_q_heads / H;
+  a->n_q_heads = n_q_heads;
+  a->c = o->c;
+  if (nblk < 1) nblk = 1;
+  a->bps = choose_bps(nblk * H * n_seqs, o->cus, wg_per_cu);
+  a->max_splits = (int32_t)((nblk + a->bps - 1) / a->bps);
+  a->direct = a->max_splits == 1;
+  a->out = out;
+  a->out_f32 = out_dtype == FMKV_DTYPE_F32;
+  const size_t n_rows = a->direct ? 0 : (size_t)n_seqs * a->max_splits * n_q_heads;
+  const size_t q_off = (n_rows * (D + 2) + 63) / 64 * 64;  // floats; 256-byte aligned table
+  const size_t q_words = (size_t)fmkv::qprep_words(n_seqs, H, D);
+  rc = o->ws.ensure((q_off + q_words) * sizeof(float));
+  if (rc) return rc;
+  a->part_o = n_rows ? o->ws.ptr : nullptr;
+  a->part_ml = n_rows ? o->ws.ptr + n_rows * D : nullptr;
+  uint32_t* table = reinterpret_cast<uint32_t*>(o->ws.ptr + q_off);
+  a->qprep = table;
+  qp->q = static_cast<const uint16_t*>(q);
+  qp->n_q_heads = n_q_heads;
+  qp->group = n_q_heads / H;
+  qp->qscale = scale * 1.4426950408889634f;
+  qp->c = o->c;
+  std::memcpy(qp->sign_bits, o->sign_bits, sizeof(qp->sign_bits));
+  qp->out = table;
+  return FMKV_OK;
+}
+
+int prepare_attention(fmkv_cache* c, int64_t T, const void* q, int32_t n_q_heads, float scale,
+                      float tau, void* out, int32_t out_dtype, fmkv::AttnArgs* a,
+                      fmkv::QPrepArgs* qp) {
+  const int64_t W = c->desc.window;
+  a->seq_lens = nullptr;
+  a->seq_len = T;
+  a->window = W;
+  a->vis_begin = c->vis_begin;
+  const int64_t filled = W > 0 ? std::min<int64_t>(T, W) : T;
+  const int64_t vb = W > 0 ? 0 : c->vis_begin;
+  const int64_t nblk =
+      (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
+  return prepare_attention_common(c, cache_store(c), 1, nblk, q, n_q_heads, scale, tau, out,
+                                  out_dtype, fmkv::kAttnWgPerCu, a, qp);
+}
+
+int prepare_paged_append(const fmkv_pool* p, const void* k, const void* v,
+                         const int32_t* block_tables, int32_t max_blocks, const int32_t* start_pos,
+                         int32_t n_seqs, int32_t n_new, fmkv::AppendArgs* a, int* tasks) {
+  if (!p) return fail(FMKV_ERR_INVALID_ARG, "pool is null");
+  if (n_seqs < 0 || n_new < 0 || max_blocks < 1)
+    return fail(FMKV_ERR_INVALID_ARG, "n_seqs/n_new must be >= 0 and max_blocks >= 1");
+  if (n_seqs == 0 || n_new == 0) return FMKV_OK;
+  if (!k || !v || !block_tables || !start_pos)
+    return fail(FMKV_ERR_INVALID_ARG, "k/v/block_tables/start_pos must be device pointers");
+  if (n_seqs > 65535) return fail(FMKV_ERR_INVALID_ARG, "at most 65535 sequences per call");
+  a->st = pool_store(p, block_tables, max_blocks);
+  a->k = static_cast<const uint16_t*>(k);
+  a->v = static_cast<const uint16_t*>(v);
+  a->start_pos = start_pos;
+  a->start_scalar = 0;
+  a->n_new = n_new;
+  a->window = 0;
+  std::memcpy(a->sign_bits, p->sign_bits, sizeof(a->sign_bits));
+  a->c = p->c;
+  a->sqrt_d = p->sqrt_d;
+  a->cb_bits = p->desc.bits;
+  a->qp.out = nullptr;
+  *tasks = (n_new + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens + 1;
+  return FMKV_OK;
+}
+
+int prepare_paged_attention(fmkv_pool* p, const void* q, const int32_t* block_tables,
+                            int32_t max_blocks, const int32_t* seq_lens, int32_t n_seqs,
+                            int32_t max_seq_len, int32_t n_q_heads, float scale, float tau,
+                            void* out, int32_t out_dtype, fmkv::AttnArgs* a, fmkv::QPrepArgs* qp) {
+  if (n_seqs < 0 || max_seq_len < 0 || max_blocks < 1)
+    return fail(FMKV_ERR_INVALID_ARG, "bad n_seqs / max_seq_len / max_blocks");
+  if (n_seqs > 0 && (!block_tables || !seq_lens))
+    return fail(FMKV_ERR_INVALID_ARG, "block_tables/seq_lens are null");
+  if ((int64_t)max_seq_len > (int64_t)max_blocks * fmkv::kBlockTokens)
+    return fail(FMKV_ERR_INVALID_ARG, "max_seq_len exceeds max_blocks * 16");
+  if (n_seqs > 65535) return fail(FMKV_ERR_INVALID_ARG, "at most 65535 sequences per call");
+  a->seq_lens = seq_lens;
+  a->seq_len = 0;
+  a->window = 0;
+  a->vis_begin = 0;
+  const int64_t nblk = (max_seq_len + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens;
+  // ragged lengths: the bound counts every sequence at max_seq_len, so aim at
+  // more work-groups than for one sequence
+  return prepare_attention_common(p, pool_store(p, block_tables, max_blocks),
+                                  n_seqs > 0 ? n_seqs : 1, nblk, q, n_q_heads, scale, tau, out,
+                                  out_dtype, 4 * fmkv::kAttnWgPerCu, a, qp);
+}
+
 }  // namespace
 
 extern "C" {
@@ -272,6 +426,7 @@ int fmkv_cache_create(const fmkv_cache_desc* desc, fmkv_cache** out) {
     delete c;
     return rc;
   }
+  sign_bits_of(*desc, c->sign_bits);
   c->cus = device_cus();
   *out = c;
   return FMKV_OK;
@@ -299,41 +454,36 @@ int fmkv_cache_stored_len(const fmkv_cache* c, int64_t* out) {
 }
 
 int fmkv_cache_append(fmkv_cache* c, const void* k, const void* v, int64_t n, void* stream) {
-  if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
-  if (n < 0) return fail(FMKV_ERR_INVALID_ARG, "n_tokens must be >= 0");
-  if (n == 0) return FMKV_OK;
-  if (!k || !v) return fail(FMKV_ERR_INVALID_ARG, "k/v must be device pointers");
-  if (n > ((int64_t)1 << 30)) return fail(FMKV_ERR_INVALID_ARG, "n_tokens too large");
-  const int64_t W = c->desc.window;
-  if (W == 0 && c->offset + n > c->desc.capacity)
-    return fail(FMKV_ERR_CAPACITY, "append of " + std::to_string(n) + " tokens at offset " +
-                                       std::to_string(c->offset) + " exceeds capacity " +
-                                       std::to_string(c->desc.capacity));
-  if (c->offset + n > ((int64_t)1 << 31) - 64)
-    return fail(FMKV_ERR_CAPACITY, "position counter would exceed 2^31");
   fmkv::AppendArgs a;
-  a.st = cache_store(c);
-  a.k = static_cast<const uint16_t*>(k);
-  a.v = static_cast<const uint16_t*>(v);
-  a.start_pos = nullptr;
-  a.start_scalar = c->offset;
-  a.n_new = (int32_t)n;
-  a.window = (int32_t)W;
-  a.signs = c->d_signs;
-  a.c = c->c;
-  a.sqrt_d = c->sqrt_d;
-  a.cb_bits = c->desc.bits;
-  int64_t tasks;
-  if (W > 0) {
-    const int64_t n_eff = n < W ? n : W;
-    tasks = (n_eff + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens + 1;
-    if (tasks > W / fmkv::kBlockTokens) tasks = W / fmkv::kBlockTokens;
-  } else {
-    tasks = (c->offset + n - 1) / fmkv::kBlockTokens - c->offset / fmkv::kBlockTokens + 1;
-  }
+  int64_t tasks = 0;
+  int rc = prepare_append(c, k, v, n, &a, &tasks);
+  if (rc || n == 0) return rc;
   hipError_t e = fmkv::launch_append(a, 1, (int)tasks, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "append launch");
   c->offset += n;
+  return FMKV_OK;
+}
+
+int fmkv_decode_step(fmkv_cache* c, const void* k, const void* v, int64_t n, const void* q,
+                     int32_t n_q_heads, float scale, float tau, void* out, int32_t out_dtype,
+                     void* stream) {
+  if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
+  if (n < 1) return fail(FMKV_ERR_INVALID_ARG, "a decode step appends at least one token");
+  fmkv::AppendArgs ap;
+  int64_t tasks = 0;
+  int rc = prepare_append(c, k, v, n, &ap, &tasks);
+  if (rc) return rc;
+  fmkv::AttnArgs at;
+  rc = prepare_attention(c, c->offset + n, q, n_q_heads, scale, tau, out, out_dtype, &at, &ap.qp);
+  if (rc) return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = fmkv::launch_append(ap, 1, (int)tasks, s);
+  if (e != hipSuccess) return hip_fail(e, "append launch");
+  c->offset += n;
+  hipEvent_t e0, e1;
+  next_events(&e0, &e1);
+  e = fmkv::launch_decode_attention(at, 1, c->desc.n_kv_heads, s, e0, e1);
+  if (e != hipSuccess) return hip_fail(e, "decode attention launch");
   return FMKV_OK;
 }
 
@@ -348,42 +498,17 @@ int fmkv_cache_trim(fmkv_cache* c, int64_t keep_last) {
 int fmkv_decode_attention(fmkv_cache* c, const void* q, int32_t n_q_heads, float scale, float tau,
                           void* out, int32_t out_dtype, void* stream) {
   if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
-  int rc = check_attn_args(c->desc, q, n_q_heads, tau, out, out_dtype);
-  if (rc) return rc;
-  const int H = c->desc.n_kv_heads, D = c->desc.head_dim;
   fmkv::AttnArgs a;
-  a.st = cache_store(c);
-  a.seq_lens = nullptr;
-  a.seq_len = c->offset;
-  a.window = c->desc.window;
-  a.vis_begin = c->vis_begin;
-  a.group = n_q_heads / H;
-  a.n_q_heads = n_q_heads;
-  a.q = static_cast<const uint16_t*>(q);
-  a.qscale = scale * 1.4426950408889634f;
-  a.signs = c->d_signs;
-  a.c = c->c;
-  int64_t filled = c->desc.window > 0 ? std::min<int64_t>(c->offset, c->desc.window) : c->offset;
-  int64_t vb = c->desc.window > 0 ? 0 : c->vis_begin;
-  int64_t nblk = (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
-  if (nblk < 1) nblk = 1;
-  a.bps = choose_bps(nblk * H, c->cus);
-  a.max_splits = (int32_t)((nblk + a.bps - 1) / a.bps);
-  a.direct = a.max_splits == 1;
-  a.out = out;
-  a.out_f32 = out_dtype == FMKV_DTYPE_F32;
-  a.part_o = nullptr;
-  a.part_ml = nullptr;
-  if (!a.direct) {
-    const size_t n_rows = (size_t)a.max_splits * n_q_heads;
-    rc = c->ws.ensure(n_rows * (D + 2) * sizeof(float));
-    if (rc) return rc;
-    a.part_o = c->ws.ptr;
-    a.part_ml = c->ws.ptr + n_rows * D;
-  }
+  fmkv::QPrepArgs qp;
+  int rc = prepare_attention(c, c->offset, q, n_q_heads, scale, tau, out, out_dtype, &a, &qp);
+  if (rc) return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e =
+      fmkv::launch_qprep(qp, c->desc.head_dim, c->desc.bits, c->desc.n_kv_heads, 1, s);
+  if (e != hipSuccess) return hip_fail(e, "q preparation launch");
   hipEvent_t e0, e1;
   next_events(&e0, &e1);
-  hipError_t e = fmkv::launch_decode_attention(a, 1, H, static_cast<hipStream_t>(stream), e0, e1);
+  e = fmkv::launch_decode_attention(a, 1, c->desc.n_kv_heads, s, e0, e1);
   if (e != hipSuccess) return hip_fail(e, "decode attention launch");
   return FMKV_OK;
 }
@@ -394,7 +519,7 @@ int fmkv_cache_decode_splits(const fmkv_cache* c, int32_t* n_splits) {
   int64_t vb = c->desc.window > 0 ? 0 : c->vis_begin;
   int64_t nblk = (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
   if (nblk < 1) nblk = 1;
-  const int32_t bps = choose_bps(nblk * c->desc.n_kv_heads, c->cus);
+  const int32_t bps = choose_bps(nblk * c->desc.n_kv_heads, c->cus, fmkv::kAttnWgPerCu);
   *n_splits = (int32_t)((nblk + bps - 1) / bps);
   return FMKV_OK;
 }
@@ -471,6 +596,7 @@ int fmkv_pool_create(const fmkv_cache_desc* desc, int64_t n_blocks, fmkv_pool** 
     delete p;
     return rc;
   }
+  sign_bits_of(*desc, p->sign_bits);
   p->cus = device_cus();
   *out = p;
   return FMKV_OK;
@@ -488,26 +614,11 @@ int fmkv_pool_destroy(fmkv_pool* p) {
 int fmkv_paged_append(fmkv_pool* p, const void* k, const void* v, const int32_t* block_tables,
                       int32_t max_blocks, const int32_t* start_pos, int32_t n_seqs, int32_t n_new,
                       void* stream) {
-  if (!p) return fail(FMKV_ERR_INVALID_ARG, "pool is null");
-  if (n_seqs < 0 || n_new < 0 || max_blocks < 1)
-    return fail(FMKV_ERR_INVALID_ARG, "n_seqs/n_new must be >= 0 and max_blocks >= 1");
-  if (n_seqs == 0 || n_new == 0) return FMKV_OK;
-  if (!k || !v || !block_tables || !start_pos)
-    return fail(FMKV_ERR_INVALID_ARG, "k/v/block_tables/start_pos must be device pointers");
-  if (n_seqs > 65535) return fail(FMKV_ERR_INVALID_ARG, "at most 65535 sequences per call");
   fmkv::AppendArgs a;
-  a.st = pool_store(p, block_tables, max_blocks);
-  a.k = static_cast<const uint16_t*>(k);
-  a.v = static_cast<const uint16_t*>(v);
-  a.start_pos = start_pos;
-  a.start_scalar = 0;
-  a.n_new = n_new;
-  a.window = 0;
-  a.signs = p->d_signs;
-  a.c = p->c;
-  a.sqrt_d = p->sqrt_d;
-  a.cb_bits = p->desc.bits;
-  const int tasks = (n_new + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens + 1;
+  int tasks = 0;
+  int rc = prepare_paged_append(p, k, v, block_tables, max_blocks, start_pos, n_seqs, n_new, &a,
+                                &tasks);
+  if (rc || n_seqs == 0 || n_new == 0) return rc;
   hipError_t e = fmkv::launch_append(a, n_seqs, tasks, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "paged append launch");
   return FMKV_OK;
@@ -518,48 +629,44 @@ int fmkv_paged_decode_attention(fmkv_pool* p, const void* q, const int32_t* bloc
                                 int32_t max_seq_len, int32_t n_q_heads, float scale, float tau,
                                 void* out, int32_t out_dtype, void* stream) {
   if (!p) return fail(FMKV_ERR_INVALID_ARG, "pool is null");
-  int rc = check_attn_args(p->desc, q, n_q_heads, tau, out, out_dtype);
-  if (rc) return rc;
-  if (n_seqs < 0 || max_seq_len < 0 || max_blocks < 1)
-    return fail(FMKV_ERR_INVALID_ARG, "bad n_seqs / max_seq_len / max_blocks");
-  if (n_seqs == 0) return FMKV_OK;
-  if (!block_tables || !seq_lens) return fail(FMKV_ERR_INVALID_ARG, "block_tables/seq_lens are null");
-  if ((int64_t)max_seq_len > (int64_t)max_blocks * fmkv::kBlockTokens)
-    return fail(FMKV_ERR_INVALID_ARG, "max_seq_len exceeds max_blocks * 16");
-  if (n_seqs > 65535) return fail(FMKV_ERR_INVALID_ARG, "at most 65535 sequences per call");
-  const int H = p->desc.n_kv_heads, D = p->desc.head_dim;
   fmkv::AttnArgs a;
-  a.st = pool_store(p, block_tables, max_blocks);
-  a.seq_lens = seq_lens;
-  a.seq_len = 0;
-  a.window = 0;
-  a.vis_begin = 0;
-  a.group = n_q_heads / H;
-  a.n_q_heads = n_q_heads;
-  a.q = static_cast<const uint16_t*>(q);
-  a.qscale = scale * 1.4426950408889634f;
-  a.signs = p->d_signs;
-  a.c = p->c;
-  int64_t nblk = (max_seq_len + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens;
-  if (nblk < 1) nblk = 1;
-  a.bps = choose_bps(nblk * H * n_seqs, p->cus);
-  a.max_splits = (int32_t)((nblk + a.bps - 1) / a.bps);
-  a.direct = a.max_splits == 1;
-  a.out = out;
-  a.out_f32 = out_dtype == FMKV_DTYPE_F32;
-  a.part_o = nullptr;
-  a.part_ml = nullptr;
-  if (!a.direct) {
-    const size_t n_rows = (size_t)n_seqs * a.max_splits * n_q_heads;
-    rc = p->ws.ensure(n_rows * (D + 2) * sizeof(float));
-    if (rc) return rc;
-    a.part_o = p->ws.ptr;
-    a.part_ml = p->ws.ptr + n_rows * D;
-  }
+  fmkv::QPrepArgs qp;
+  int rc = prepare_paged_attention(p, q, block_tables, max_blocks, seq_lens, n_seqs, max_seq_len,
+                                   n_q_heads, scale, tau, out, out_dtype, &a, &qp);
+  if (rc || n_seqs == 0) return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e =
+      fmkv::launch_qprep(qp, p->desc.head_dim, p->desc.bits, p->desc.n_kv_heads, n_seqs, s);
+  if (e != hipSuccess) return hip_fail(e, "q preparation launch");
   hipEvent_t e0, e1;
   next_events(&e0, &e1);
-  hipError_t e =
-      fmkv::launch_decode_attention(a, n_seqs, H, static_cast<hipStream_t>(stream), e0, e1);
+  e = fmkv::launch_decode_attention(a, n_seqs, p->desc.n_kv_heads, s, e0, e1);
+  if (e != hipSuccess) return hip_fail(e, "paged decode attention launch");
+  return FMKV_OK;
+}
+
+int fmkv_paged_decode_step(fmkv_pool* p, const void* k, const void* v,
+                           const int32_t* block_tables, int32_t max_blocks,
+                           const int32_t* start_pos, const int32_t* seq_lens, int32_t n_seqs,
+                           int32_t n_new, int32_t max_seq_len, const void* q, int32_t n_q_heads,
+                           float scale, float tau, void* out, int32_t out_dtype, void* stream) {
+  if (!p) return fail(FMKV_ERR_INVALID_ARG, "pool is null");
+  if (n_new < 1) return fail(FMKV_ERR_INVALID_ARG, "a decode step appends at least one token");
+  fmkv::AppendArgs ap;
+  int tasks = 0;
+  int rc = prepare_paged_append(p, k, v, block_tables, max_blocks, start_pos, n_seqs, n_new, &ap,
+                                &tasks);
+  if (rc) return rc;
+  fmkv::AttnArgs at;
+  rc = prepare_paged_attention(p, q, block_tables, max_blocks, seq_lens, n_seqs, max_seq_len,
+                               n_q_heads, scale, tau, out, out_dtype, &at, &ap.qp);
+  if (rc || n_seqs == 0) return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = fmkv::launch_append(ap, n_seqs, tasks, s);
+  if (e != hipSuccess) return hip_fail(e, "paged append launch");
+  hipEvent_t e0, e1;
+  next_events(&e0, &e1);
+  e = fmkv::launch_decode_attention(at, n_seqs, p->desc.n_kv_heads, s, e0, e1);
   if (e != hipSuccess) return hip_fail(e, "paged decode attention launch");
   return FMKV_OK;
 }

@@ -14,6 +14,7 @@
 // with -ffp-contract=off, so codes and scales are bit-identical to it.
 #include "fmkv_device.h"
 #include "fmkv_internal.h"
+#include "fmkv_qprep.h"
 
 namespace fmkv {
 namespace {
@@ -110,12 +111,23 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
   constexpr int E = D / 64;
   constexpr BlockLayout L = make_layout(D, BITS, MODE);
   constexpr int kWords = (int)(L.code_bytes / 4);
+  constexpr int kWaves = kAppendThreads / 64;
+  constexpr int kRowsPerWave = 2 * kBlockTokens / kWaves;  // K and V rows of 16 slots
   __shared__ uint32_t kst[kWords];
   __shared__ uint32_t vst[kWords];
   __shared__ int cov_row[kBlockTokens];
 
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = blockIdx.y, seq = blockIdx.z, bx = blockIdx.x;
+  if constexpr (MODE == kAffine) {
+    // decode step: the last column of work-groups prepares q for the
+    // attention launch that follows, in the shadow of the append's loads
+    if (a.qp.out && bx == (int)gridDim.x - 1) {
+      qprep_workgroup<D, BITS>(a.qp, a.st.n_kv_heads, h, seq, tid);
+      return;
+    }
+  }
   const int64_t pos0 = a.start_pos ? (int64_t)a.start_pos[seq] : a.start_scalar;
   const int64_t end = pos0 + a.n_new;
   const int64_t W = a.window;
@@ -138,12 +150,17 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
     lb = first + bx;
   }
 
-  if (tid < kBlockTokens) {
-    const int64_t slot = lb * kBlockTokens + tid;
-    int64_t p = (W > 0) ? e0 + ((slot - s0) % W + W) % W : slot;
-    const bool covered = p >= e0 && p < end;
-    cov_row[tid] = covered ? (int)(p - pos0) : -1;
-  }
+  // input row written to slot t of this block, or -1 (ring: slot - s0 lies
+  // in (-W, W), so one conditional add replaces the modulo)
+  auto row_of = [&](int t) -> int {
+    const int64_t slot = lb * kBlockTokens + t;
+    int64_t p = slot;
+    if (W > 0) {
+      const int64_t d = slot - s0;
+      p = e0 + (d < 0 ? d + W : d);
+    }
+    return (p >= e0 && p < end) ? (int)(p - pos0) : -1;
+  };
   int64_t phys = lb;
   if (a.st.block_table) {
     // caller-owned table: positions past its width or entries outside the
@@ -153,6 +170,23 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
   }
   if (phys < 0 || phys >= a.st.n_blocks) return;
   uint8_t* blk = a.st.base + phys * a.st.block_stride + (int64_t)h * a.st.head_stride;
+
+  // this wave's input rows (r = wave + k * waves: slot r / 2, K or V by
+  // r & 1) are loaded first, so that they share one memory round trip with
+  // the V-word read below; rows not written here re-read row 0 unused
+  const int H = a.st.n_kv_heads;
+  float x[kRowsPerWave][E];
+  int rows[kRowsPerWave];
+#pragma unroll
+  for (int k = 0; k < kRowsPerWave; k++) {
+    const int r = wv + k * kWaves;
+    rows[k] = row_of(r >> 1);
+    const int row = rows[k] < 0 ? 0 : rows[k];
+    const uint16_t* src =
+        ((r & 1) ? a.v : a.k) + (((int64_t)seq * a.n_new + row) * H + h) * D + lane * E;
+    load_row<E>(src, x[k]);
+  }
+  if (tid < kBlockTokens) cov_row[tid] = row_of(tid);
   __syncthreads();
 
   bool all_cov = true;
@@ -171,23 +205,20 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
   }
   __syncthreads();
 
-  const int H = a.st.n_kv_heads;
-  for (int r = wv; r < 2 * kBlockTokens; r += kAppendThreads / 64) {
+  const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
+#pragma unroll
+  for (int k = 0; k < kRowsPerWave; k++) {
+    const int r = wv + k * kWaves;
     const int t = r >> 1, isv = r & 1;
-    const int row = cov_row[t];
-    if (row < 0) continue;
-    const uint16_t* src =
-        (isv ? a.v : a.k) + (((int64_t)seq * a.n_new + row) * H + h) * D + lane * E;
-    float x[E];
-    load_row<E>(src, x);
+    if (rows[k] < 0) continue;
     uint32_t* stage = isv ? vst : kst;
     if constexpr (MODE == kAffine) {
-      wave_fwht<E>(x, lane);
+      wave_fwht<E>(x[k], lane);
 #pragma unroll
-      for (int i = 0; i < E; i++) x[i] = (x[i] * a.c) * a.signs[lane * E + i];
+      for (int i = 0; i < E; i++) x[k][i] = apply_sign(x[k][i] * a.c, sbits, i);
       uint32_t code[E];
       float scale, bias;
-      affine_quant<E, BITS>(x, code, scale, bias, lane);
+      affine_quant<E, BITS>(x[k], code, scale, bias, lane);
 #pragma unroll
       for (int i = 0; i < E; i++) {
         int64_t off;
@@ -206,15 +237,15 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
       }
     } else {
       constexpr int bits = BITS;
-      const float norm = sqrtf(canonical_sumsq<E>(x, lane));
+      const float norm = sqrtf(canonical_sumsq<E>(x[k], lane));
       const float den = norm + 1e-8f;
 #pragma unroll
-      for (int i = 0; i < E; i++) x[i] = x[i] / den;
-      wave_fwht<E>(x, lane);
+      for (int i = 0; i < E; i++) x[k][i] = x[k][i] / den;
+      wave_fwht<E>(x[k], lane);
       const int64_t row_bits = (int64_t)D * bits;
 #pragma unroll
       for (int i = 0; i < E; i++) {
-        const float z = ((x[i] * a.c) * a.signs[lane * E + i]) * a.sqrt_d;
+        const float z = apply_sign(x[k][i] * a.c, sbits, i) * a.sqrt_d;
         const uint32_t idx = (uint32_t)cb_index(z, bits);
         const int64_t bit = t * row_bits + (int64_t)(lane * E + i) * bits;
         const int wi = (int)(bit >> 5), off = (int)(bit & 31);
@@ -245,7 +276,8 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
 
 template <int D, int BITS, int MODE>
 hipError_t launch_t(const AppendArgs& a, int n_seqs, int max_tasks, hipStream_t s) {
-  dim3 grid(max_tasks, a.st.n_kv_heads, n_seqs);
+  const int qcol = (MODE == kAffine && a.qp.out) ? 1 : 0;
+  dim3 grid(max_tasks + qcol, a.st.n_kv_heads, n_seqs);
   hipLaunchKernelGGL((append_kernel<D, BITS, MODE>), grid, dim3(kAppendThreads), 0, s, a);
   return hipGetLastError();
 }
@@ -254,7 +286,10 @@ hipError_t launch_t(const AppendArgs& a, int n_seqs, int max_tasks, hipStream_t 
 
 hipError_t launch_append(const AppendArgs& a, int n_seqs, int max_tasks, hipStream_t s) {
   const BlockLayout& L = a.st.layout;
-  if (max_tasks <= 0 || n_seqs <= 0) return hipSuccess;
+  if (n_seqs <= 0) return hipSuccess;
+  if (max_tasks <= 0 && !a.qp.out) return hipSuccess;
+  if (a.qp.out && L.mode != kAffine) return hipErrorInvalidValue;
+  if (max_tasks < 0) max_tasks = 0;
   if (L.mode == kAffine) {
     switch (L.head_dim * 16 + L.bits) {
       case 128 * 16 + 4: return launch_t<128, 4, kAffine>(a, n_seqs, max_tasks, s);

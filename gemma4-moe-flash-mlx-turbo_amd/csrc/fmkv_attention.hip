@@ -9,7 +9,10 @@
 //   QK^T  S^T[16 tok x 16 col] += K[16 x 32] . Q^T[32 x 16] on MFMA
 //         (v_mfma_f32_16x16x32_f16), K codes converted exactly to f16
 //         integers; per 64-dim group the f16 scale/bias are applied after the
-//         MFMA: s += scale * acc + bias * sum(q_group).
+//         MFMA: s += scale * acc + bias * sum(q_group). (Codes stay
+//         unbiased: an f16 1024 + code operand with the offset cancelled in
+//         the accumulator is cheaper but inflates the fp32 partial sums ~64x
+//         at 4 bits, which outlier channels turn into visible error.)
 //         Column c = q head (c & 7) of the GQA group, c < 8 carrying the f16
 //         high part of q_rot and c >= 8 the residual, so S keeps ~22 bits of
 //         q precision; DPP row_ror:8 folds the two halves.
@@ -20,24 +23,20 @@
 //         same columns; bias terms are summed on the side.
 // The QK output lane layout equals the PV B-operand layout (lane (j, c) holds
 // tokens 4j..4j+3 of column c), so no register shuffles are needed.
+//
+// q arrives pre-rotated in the MFMA operand layout (fmkv_qprep.h), so the
+// prologue is one load per operand, issued ahead of the first blocks. Each
+// wave then keeps DEPTH blocks in flight in as many register sets, refilling
+// a set as soon as it has been consumed.
 // Epilogue: O is written to LDS, inverse-rotated (o . R^T = c * FWHT(o o s))
 // and stored either as the final output (single split) or as a split partial
-// (m, l, O) for fmkv_combine.
+// (m, l, O) for the combine kernel.
 #include "fmkv_device.h"
 #include "fmkv_internal.h"
+#include "fmkv_qprep.h"
 
 namespace fmkv {
 namespace {
-
-// Dim of head_dim fed to lane k-group j, element i, of the QK MFMA s (0/1)
-// of group g (matches the K-code placement in fmkv_layout.h).
-template <int BITS>
-__device__ inline int qk_dim(int g, int s, int j, int i) {
-  if constexpr (BITS == 8)
-    return g * 64 + j * 16 + s * 8 + i;
-  else
-    return g * 64 + s * 32 + j * 8 + i;
-}
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -116,22 +115,20 @@ __device__ inline half4_t v_operand(const BlockRegs<BITS, GW>& r, int gi, int ct
 __device__ inline float lo16(uint32_t w) { return f16_bits_to_f32(w); }
 __device__ inline float hi16(uint32_t w) { return f16_bits_to_f32(w >> 16); }
 
-// Three waves per SIMD (register budget <= 168): enough resident waves to hide
-// the MFMA / LDS latencies of a block while two blocks per wave are in flight.
-template <int D, int BITS, int DW>
-__global__ __launch_bounds__((D / DW) * 64) __attribute__((amdgpu_waves_per_eu(3, 8)))
+// Waves per SIMD: three with two blocks in flight per wave (register budget
+// <= 168), two with three or four (<= 256), one beyond (<= 512 with AGPRs).
+template <int D, int BITS, int DW, int DEPTH>
+__global__ __launch_bounds__((D / DW) * 64)
+__attribute__((amdgpu_waves_per_eu(DEPTH >= 5 ? 1 : (DEPTH >= 3 ? 2 : 3), 8)))
 void decode_attn_kernel(AttnArgs a) {
   constexpr int NW = D / DW;
   constexpr int GW = DW / 64;
-  constexpr int NG = D / 64;
   static_assert(BITS == 8 || GW % 2 == 0, "4-bit needs 128-dim wave slices");
 
   constexpr int QS = D + 4;                   // padded row stride (LDS banks)
-  __shared__ float qo[8 * QS];                // q_rot, then the split's O
+  __shared__ float qo[8 * QS];                // the split's O, for the epilogue
   __shared__ float4_t sx[2][NW > 1 ? NW : 1][64];  // partial S exchange
-  __shared__ float qsum_s[8][NG];
   __shared__ float ml_s[8][2];
-  __shared__ float sgn_s[D];                  // RHT signs, for the epilogue
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -151,8 +148,15 @@ void decode_attn_kernel(AttnArgs a) {
   int64_t b_end = b_begin + a.bps;
   if (b_end > geo.blk_hi) b_end = geo.blk_hi;
 
-  const int32_t* table =
-      a.st.block_table ? a.st.block_table + (int64_t)seq * a.st.table_stride : nullptr;
+  // Table entries are read through the constant address space: a uniform
+  // index then becomes a scalar load, counted apart from the vector loads of
+  // the block stream, so resolving the next block never waits for the
+  // blocks in flight.
+  typedef const int32_t __attribute__((address_space(4)))* table_ptr;
+  const table_ptr table =
+      a.st.block_table
+          ? (table_ptr)(uintptr_t)(a.st.block_table + (int64_t)seq * a.st.table_stride)
+          : nullptr;
   const uint8_t* hbase = a.st.base + (int64_t)kvh * a.st.head_stride;
   auto blk_ptr = [&](int64_t lb) -> const uint8_t* {
     int64_t phys = table ? (int64_t)table[lb] : lb;
@@ -161,84 +165,35 @@ void decode_attn_kernel(AttnArgs a) {
     return hbase + phys * a.st.block_stride;
   };
 
-  // ---- first in the memory queue: this wave's q rows and the sign vector
-  // (kept in registers for the epilogue too), so they do not wait behind the
-  // block stream ----
+  // ---- prologue: this wave's q operands first, then the first blocks ----
   constexpr int E = D / 64;
-  constexpr int LPG = 64 / E;          // lanes per 64-dim group
-  constexpr int kHPW = (8 + NW - 1) / NW;  // GQA heads per wave, at most
-  const uint16_t* qg = a.q + ((int64_t)seq * a.n_q_heads + (int64_t)kvh * G) * D;
-  float qx[kHPW][E];
+  static_assert(DW == kAttnDW, "q-prep table is laid out for 128-dim wave slices");
+  const uint32_t* qp = qprep_entry(a.qprep, seq, (int)gridDim.y, kvh, NW, wave, lane);
+  u32x4 qv[kQPrepVecs];
 #pragma unroll
-  for (int k = 0; k < kHPW; k++) {
-    const int hh = wave + k * NW;
-    if (hh < G) load_row<E>(qg + hh * D + lane * E, qx[k]);
-  }
-  float sg[E];
-#pragma unroll
-  for (int i = 0; i < E; i++) sg[i] = a.signs[lane * E + i];
+  for (int i = 0; i < kQPrepVecs; i++) qv[i] = *reinterpret_cast<const u32x4*>(qp + 4 * i);
 
   // Loads are issued unconditionally: a block past the split gets a zero-size
-  // resource (no traffic) and its tokens are masked, so the loaded registers
-  // never merge with stale ones across the loop and no copy forces a wait.
+  // resource (no traffic), so the loaded registers never merge with stale
+  // ones across the loop and no copy forces a wait.
   const int64_t b_last = b_end > b_begin ? b_end - 1 : b_begin;
   auto fetch = [&](BlockRegs<BITS, GW>& r, int64_t lb) {
     const bool valid = lb < b_end;
     load_block<D, BITS, GW>(r, blk_ptr(valid ? lb : b_last), valid, wave, lane);
   };
-  // two blocks in flight per wave while the prologue runs
-  BlockRegs<BITS, GW> nx1, nx2;
-  fetch(nx1, b_begin);
-  fetch(nx2, b_begin + 1);
-
-  // ---- q prologue: q_rot = (FWHT(q * qscale) * c) o s ----
+  BlockRegs<BITS, GW> rs[DEPTH];
 #pragma unroll
-  for (int k = 0; k < kHPW; k++) {
-    const int hh = wave + k * NW;
-    if (hh >= G) continue;
-    float x[E];
-#pragma unroll
-    for (int i = 0; i < E; i++) x[i] = qx[k][i] * a.qscale;
-    wave_fwht<E>(x, lane);
-    float gsum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < E; i++) {
-      x[i] = (x[i] * a.c) * sg[i];
-      gsum += x[i];
-    }
-#pragma unroll
-    for (int i = 0; i < E; i += (E >= 4 ? 4 : E)) {
-      if constexpr (E >= 4)
-        *reinterpret_cast<float4_t*>(&qo[hh * QS + lane * E + i]) =
-            (float4_t){x[i], x[i + 1], x[i + 2], x[i + 3]};
-      else
-        for (int t = 0; t < E; t++) qo[hh * QS + lane * E + t] = x[t];
-    }
-    gsum = group_sum<LPG>(gsum, lane);
-    if ((lane & (LPG - 1)) == 0) qsum_s[hh][lane / LPG] = gsum;
-  }
-  if (wave == 0) {
-#pragma unroll
-    for (int i = 0; i < E; i++) sgn_s[lane * E + i] = sg[i];
-  }
-  __syncthreads();
+  for (int s = 0; s < DEPTH; s++) fetch(rs[s], b_begin + s);
 
   half8_t bq[GW][2];
   float qs[GW];
 #pragma unroll
   for (int gi = 0; gi < GW; gi++) {
-    const int g = wave * GW + gi;
 #pragma unroll
-    for (int s = 0; s < 2; s++) {
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float v = col_valid ? qo[head * QS + qk_dim<BITS>(g, s, j, i)] : 0.0f;
-        const _Float16 vh = (_Float16)v;
-        bq[gi][s][i] = hi ? vh : (_Float16)(v - (float)vh);
-      }
-    }
-    qs[gi] = (hi && col_valid) ? qsum_s[head][g] : 0.0f;
+    for (int s = 0; s < 2; s++) bq[gi][s] = __builtin_bit_cast(half8_t, qv[gi * 2 + s]);
+    qs[gi] = __uint_as_float(qv[2 * GW][gi]);
   }
+  const uint32_t sbits = qv[2 * GW][2];
 
   // ---- main loop ----
   float4_t o[GW * 4];
@@ -317,7 +272,8 @@ void decode_attn_kernel(AttnArgs a) {
     for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(s[i] - m_run);
     l_run += (p[0] + p[1]) + (p[2] + p[3]);
 
-    // O^T += V^T . P'^T with P' = p * v_scale as f16 hi (c < 8) / residual (c >= 8)
+    // O^T += V^T . P'^T with P' = p * v_scale as f16 hi (c < 8) / residual
+    // (c >= 8)
 #pragma unroll
     for (int gi = 0; gi < GW; gi++) {
       const u32x4 vw = cur.vs[gi];
@@ -330,10 +286,8 @@ void decode_attn_kernel(AttnArgs a) {
       const half2_t h01 = pkrtz(x[0], x[1]);
       const half2_t h23 = pkrtz(x[2], x[3]);
       const half4_t bp = cat4(
-          pkrtz(fmaf(-lo_sel, (float)h01[0], x[0]),
-                                     fmaf(-lo_sel, (float)h01[1], x[1])),
-          pkrtz(fmaf(-lo_sel, (float)h23[0], x[2]),
-                                     fmaf(-lo_sel, (float)h23[1], x[3])));
+          pkrtz(fmaf(-lo_sel, (float)h01[0], x[0]), fmaf(-lo_sel, (float)h01[1], x[1])),
+          pkrtz(fmaf(-lo_sel, (float)h23[0], x[2]), fmaf(-lo_sel, (float)h23[1], x[3])));
 #pragma unroll
       for (int ct = 0; ct < 4; ct++)
         o[gi * 4 + ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(v_operand<BITS, GW>(cur, gi, ct),
@@ -341,14 +295,17 @@ void decode_attn_kernel(AttnArgs a) {
     }
   };
 
-  // ping-pong over two register sets: while one block is processed the other
-  // is in flight; a set is reloaded as soon as it has been consumed (no
-  // register copies, which would force a wait on every outstanding load)
-  for (int64_t b = b_begin; b < b_end; b += 2) {
-    process(nx1, b);
-    fetch(nx1, b + 2);
-    process(nx2, b + 1);  // fully masked when b + 1 == b_end
-    fetch(nx2, b + 3);
+  // DEPTH register sets in rotation: while one block is processed the others
+  // are in flight; a set is reloaded as soon as it has been consumed (no
+  // register copies, which would force a wait on every outstanding load).
+  // Blocks past the split are skipped (a uniform branch) but still fetched
+  // as dropped loads, so every set sees the same load sequence.
+  for (int64_t b = b_begin; b < b_end; b += DEPTH) {
+#pragma unroll
+    for (int s = 0; s < DEPTH; s++) {
+      if (b + s < b_end) process(rs[s], b + s);
+      fetch(rs[s], b + s + DEPTH);
+    }
   }
 
   // ---- epilogue ----
@@ -386,7 +343,7 @@ void decode_attn_kernel(AttnArgs a) {
   for (int hh = wave; hh < G; hh += NW) {
     float x[E];
 #pragma unroll
-    for (int i = 0; i < E; i++) x[i] = qo[hh * QS + lane * E + i] * sgn_s[lane * E + i];
+    for (int i = 0; i < E; i++) x[i] = apply_sign(qo[hh * QS + lane * E + i], sbits, i);
     wave_fwht<E>(x, lane);
     if (a.direct) {
       const float l = ml_s[hh][1];
@@ -420,12 +377,13 @@ void decode_attn_kernel(AttnArgs a) {
 
 // out[seq][h][d] = sum_s 2^(m_s - M) O_s[d] / sum_s 2^(m_s - M) l_s.
 // One work-group per (64 dims, q head, sequence); thread (sl, dq) owns dims
-// d0 + 4*dq .. +3 and splits sl, sl + 16, ...; partial sums meet in LDS.
+// d0 + 4*dq .. +3 and splits sl, sl + 16, ..., merged in one pass with a
+// running maximum; the 16 partial merges meet in LDS.
 template <int D>
 __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
-  __shared__ float red_m[256];
   __shared__ float4_t red_o[16][16];
-  __shared__ float red_l[16];
+  __shared__ float red_m[16][16];
+  __shared__ float red_l[16][16];
   const int seq = blockIdx.z, h = blockIdx.y, tid = threadIdx.x;
   const int dq = tid & 15, sl = tid >> 4;
   const int d0 = blockIdx.x * 64 + dq * 4;
@@ -436,40 +394,40 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
   const int64_t stride = (int64_t)a.n_q_heads;
   const int64_t base = (int64_t)seq * a.max_splits * stride + h;
 
-  float M = -INFINITY;
-  for (int s = tid; s < n_splits; s += 256) M = fmaxf(M, a.part_ml[(base + s * stride) * 2]);
-  red_m[tid] = M;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (tid < w) red_m[tid] = fmaxf(red_m[tid], red_m[tid + w]);
-    __syncthreads();
-  }
-  M = red_m[0];
-
+  // split maxima are finite (the split kernel starts from -1e30): the first
+  // merge scales the empty state by exp2(-inf) = 0
+  float M = -INFINITY, den = 0.0f;
   float4_t acc = (float4_t){0.f, 0.f, 0.f, 0.f};
-  float den = 0.0f;
-  if (M != -INFINITY) {
 #pragma unroll 4
-    for (int s = sl; s < n_splits; s += 16) {
-      const int64_t r = base + s * stride;
-      const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + r * 2);
-      const float w = exp2f(ml.x - M);
-      den = fmaf(w, ml.y, den);
-      const float4_t ov = *reinterpret_cast<const float4_t*>(a.part_o + r * D + d0);
+  for (int s = sl; s < n_splits; s += 16) {
+    const int64_t r = base + s * stride;
+    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + r * 2);
+    const float4_t ov = *reinterpret_cast<const float4_t*>(a.part_o + r * D + d0);
+    const float mn = fmaxf(M, ml.x);
+    const float alpha = exp2f(M - mn);
+    const float w = exp2f(ml.x - mn);
+    den = fmaf(w, ml.y, den * alpha);
 #pragma unroll
-      for (int i = 0; i < 4; i++) acc[i] = fmaf(w, ov[i], acc[i]);
-    }
+    for (int i = 0; i < 4; i++) acc[i] = fmaf(w, ov[i], acc[i] * alpha);
+    M = mn;
   }
   red_o[sl][dq] = acc;
-  if (dq == 0) red_l[sl] = den;
+  red_m[sl][dq] = M;
+  red_l[sl][dq] = den;
   __syncthreads();
   if (tid < 16) {
-    float4_t s = red_o[0][tid];
-    float L = red_l[0];
+    float Mx = red_m[0][tid];
 #pragma unroll
-    for (int k = 1; k < 16; k++) {
-      s += red_o[k][tid];
-      L += red_l[k];
+    for (int k = 1; k < 16; k++) Mx = fmaxf(Mx, red_m[k][tid]);
+    float4_t s = (float4_t){0.f, 0.f, 0.f, 0.f};
+    float L = 0.0f;
+    if (Mx != -INFINITY) {
+#pragma unroll
+      for (int k = 0; k < 16; k++) {
+        const float w = exp2f(red_m[k][tid] - Mx);  // 0 for slots without splits (-inf)
+        s += w * red_o[k][tid];
+        L = fmaf(w, red_l[k][tid], L);
+      }
     }
     const int64_t o_idx = ((int64_t)seq * a.n_q_heads + h) * D + blockIdx.x * 64 + tid * 4;
 #pragma unroll
@@ -483,14 +441,27 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
   }
 }
 
+// One work-group per (KV head, sequence).
+template <int D, int BITS>
+__global__ __launch_bounds__((D / kAttnDW) * 64) void qprep_kernel(QPrepArgs a) {
+  qprep_workgroup<D, BITS>(a, (int)gridDim.x, blockIdx.x, blockIdx.y, threadIdx.x);
+}
+
+template <int D, int BITS>
+hipError_t launch_qprep_t(const QPrepArgs& a, int n_kv_heads, int n_seqs, hipStream_t s) {
+  hipLaunchKernelGGL((qprep_kernel<D, BITS>), dim3(n_kv_heads, n_seqs), dim3((D / kAttnDW) * 64),
+                     0, s, a);
+  return hipGetLastError();
+}
+
 template <int D, int BITS>
 hipError_t launch_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                     hipEvent_t ev0, hipEvent_t ev1) {
-  constexpr int DW = 128;
+  constexpr int DW = kAttnDW;
   constexpr int NT = (D / DW) * 64;
   dim3 grid(a.max_splits, n_kv_heads, n_seqs);
   if (ev0) (void)hipEventRecord(ev0, s);
-  hipLaunchKernelGGL((decode_attn_kernel<D, BITS, DW>), grid, dim3(NT), 0, s, a);
+  hipLaunchKernelGGL((decode_attn_kernel<D, BITS, DW, kAttnDepth>), grid, dim3(NT), 0, s, a);
   hipError_t e = hipGetLastError();
   if (ev1) (void)hipEventRecord(ev1, s);
   if (e != hipSuccess || a.direct) return e;
@@ -510,6 +481,20 @@ hipError_t launch_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads
     case 256 * 16 + 8: return launch_t<256, 8>(a, n_seqs, n_kv_heads, s, e0, e1);
     case 512 * 16 + 4: return launch_t<512, 4>(a, n_seqs, n_kv_heads, s, e0, e1);
     case 512 * 16 + 8: return launch_t<512, 8>(a, n_seqs, n_kv_heads, s, e0, e1);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_qprep(const QPrepArgs& a, int head_dim, int bits, int n_kv_heads, int n_seqs,
+                        hipStream_t s) {
+  if (n_seqs <= 0) return hipSuccess;
+  switch (head_dim * 16 + bits) {
+    case 128 * 16 + 4: return launch_qprep_t<128, 4>(a, n_kv_heads, n_seqs, s);
+    case 128 * 16 + 8: return launch_qprep_t<128, 8>(a, n_kv_heads, n_seqs, s);
+    case 256 * 16 + 4: return launch_qprep_t<256, 4>(a, n_kv_heads, n_seqs, s);
+    case 256 * 16 + 8: return launch_qprep_t<256, 8>(a, n_kv_heads, n_seqs, s);
+    case 512 * 16 + 4: return launch_qprep_t<512, 4>(a, n_kv_heads, n_seqs, s);
+    case 512 * 16 + 8: return launch_qprep_t<512, 8>(a, n_kv_heads, n_seqs, s);
   }
   return hipErrorInvalidValue;
 }

@@ -19,6 +19,38 @@ struct Store {
   BlockLayout layout;
 };
 
+// Decode split-K plan shared by the host and the kernels: head dims per wave,
+// blocks in flight per wave (register sets of the load pipeline) and
+// work-groups per CU the split count aims at.
+#ifndef FMKV_ATTN_DEPTH
+#define FMKV_ATTN_DEPTH 2
+#endif
+#ifndef FMKV_ATTN_WG_PER_CU
+#define FMKV_ATTN_WG_PER_CU 2
+#endif
+constexpr int kAttnDW = 128;
+constexpr int kAttnDepth = FMKV_ATTN_DEPTH;
+constexpr int kAttnWgPerCu = FMKV_ATTN_WG_PER_CU;
+
+// 16-byte vectors per lane of the q-prep table (two groups x two MFMA B
+// operands, plus the group sums and sign bits).
+constexpr int kQPrepVecs = 5;
+
+// Rotated q for the decode kernel (layout in fmkv_qprep.h).
+struct QPrepArgs {
+  const uint16_t* q;   // bf16 [n_seqs][n_q_heads][D]
+  int32_t n_q_heads;
+  int32_t group;       // q heads per KV head
+  float qscale;        // softmax scale * log2(e)
+  float c;             // 1/sqrt(D)
+  uint32_t sign_bits[16];  // RHT signs of dims 0..D-1, bit d set = -1
+  uint32_t* out;       // table, [n_seqs][n_kv_heads][D/128][64][kQPrepVecs x 4]
+};
+
+__host__ __device__ constexpr int64_t qprep_words(int64_t n_seqs, int n_kv_heads, int head_dim) {
+  return n_seqs * n_kv_heads * (head_dim / kAttnDW) * 64 * kQPrepVecs * 4;
+}
+
 struct AppendArgs {
   Store st;
   const uint16_t* k;  // bf16 [n_seqs][n_new][n_kv_heads][D]
@@ -27,10 +59,11 @@ struct AppendArgs {
   int64_t start_scalar;
   int32_t n_new;
   int32_t window;   // ring slots, 0 = linear
-  const float* signs;  // [D] +-1
+  uint32_t sign_bits[16];  // RHT signs of dims 0..D-1, bit d set = -1
   float c;             // 1/sqrt(D) (f32)
   float sqrt_d;        // sqrt(D) (f32), codebook mode
   int32_t cb_bits;     // codebook bits
+  QPrepArgs qp;        // qp.out != null: the launch also prepares q (decode step)
 };
 
 struct AttnArgs {
@@ -41,9 +74,7 @@ struct AttnArgs {
   int64_t vis_begin;
   int32_t group;      // q heads per kv head
   int32_t n_q_heads;
-  const uint16_t* q;  // bf16 [n_seqs][n_q_heads][D]
-  float qscale;       // softmax scale * log2(e)
-  const float* signs;
+  const uint32_t* qprep;  // q-prep table of this call
   float c;
   int32_t bps;        // blocks per split
   int32_t max_splits;
@@ -52,15 +83,7 @@ struct AttnArgs {
   void* out;          // [n_seqs][n_q_heads][D]
   int32_t out_f32;
   int32_t direct;     // 1: no combine, write out
-  // rotated q in MFMA operand layout, written by the q-prep kernel:
-  // [n_seqs][n_kv_heads][waves][64 lanes][kQPrepVecs x 16 B]
-  uint32_t* qprep;
-  uint32_t sign_bits[16];  // RHT signs of dims 0..511, bit set = -1
 };
-
-// 16-byte vectors per lane of the q-prep table (<= 2 groups x 2 MFMA
-// operands, plus the group sums).
-constexpr int kQPrepVecs = 5;
 
 struct ReadArgs {
   Store st;
@@ -82,7 +105,12 @@ struct FetchArgs {
   int32_t out_f32;
 };
 
+// With a.qp.out set the launch carries one more column of work-groups that
+// fill the q-prep table (n_seqs x n_kv_heads rows); max_tasks may then be 0.
 hipError_t launch_append(const AppendArgs& a, int n_seqs, int max_tasks, hipStream_t s);
+// The q-prep table on its own (attention without a fused append).
+hipError_t launch_qprep(const QPrepArgs& a, int head_dim, int bits, int n_kv_heads, int n_seqs,
+                        hipStream_t s);
 // ev_begin / ev_end (optional) are recorded around the split-K kernel only.
 hipError_t launch_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                                    hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr);

@@ -43,7 +43,7 @@ EXPORTED = (
     "fmkv_cache_trim", "fmkv_decode_attention", "fmkv_cache_fetch", "fmkv_cache_read_codes",
     "fmkv_pool_create", "fmkv_pool_destroy", "fmkv_paged_append", "fmkv_paged_decode_attention",
     "fmkv_pool_read_codes", "fmkv_set_blocks_per_split", "fmkv_cache_decode_splits",
-    "fmkv_profile_enable", "fmkv_profile_collect",
+    "fmkv_profile_enable", "fmkv_profile_collect", "fmkv_decode_step", "fmkv_paged_decode_step",
 )
 
 
@@ -106,6 +106,10 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         "fmkv_cache_decode_splits": ([vp, P(i32)], ctypes.c_int),
         "fmkv_profile_enable": ([i32], ctypes.c_int),
         "fmkv_profile_collect": ([P(ctypes.c_double), P(i32)], ctypes.c_int),
+        "fmkv_decode_step": ([vp, vp, vp, i64, vp, i32, ctypes.c_float, ctypes.c_float, vp, i32,
+                              vp], ctypes.c_int),
+        "fmkv_paged_decode_step": ([vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, vp, i32,
+                                    ctypes.c_float, ctypes.c_float, vp, i32, vp], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -253,6 +257,21 @@ class KVCache:
                                                _ptr(out), _dtype_code(out.dtype), _stream(stream)))
         return out
 
+    def decode_step(self, keys: torch.Tensor, values: torch.Tensor, q: torch.Tensor,
+                    scale: float = 1.0, sparse_v_tau: float = 0.0, out: torch.Tensor | None = None,
+                    dtype=torch.bfloat16, stream=None) -> torch.Tensor:
+        """update_and_fetch(keys, values) then attention(q) in one call
+        (src/model/gemma4_attention.rs:84-103); shapes as append / attention."""
+        self._check_kv(keys, values)
+        if q.dtype != torch.bfloat16 or q.dim() != 2 or q.shape[1] != self.desc.head_dim:
+            raise ValueError("q must be bf16 [n_q_heads, head_dim]")
+        if out is None:
+            out = torch.empty(q.shape, dtype=dtype, device=q.device)
+        _check(self._lib.fmkv_decode_step(self._h, _ptr(keys), _ptr(values), keys.shape[0],
+                                          _ptr(q), q.shape[0], scale, sparse_v_tau, _ptr(out),
+                                          _dtype_code(out.dtype), _stream(stream)))
+        return out
+
     def decode_splits(self) -> int:
         v = ctypes.c_int32()
         _check(self._lib.fmkv_cache_decode_splits(self._h, ctypes.byref(v)))
@@ -315,6 +334,18 @@ class PagedPool:
             self._h, _ptr(q), _ptr(block_tables), block_tables.shape[1], _ptr(seq_lens),
             q.shape[0], max_seq_len, q.shape[1], scale, 0.0, _ptr(out), _dtype_code(out.dtype),
             _stream(stream)))
+        return out
+
+    def decode_step(self, keys, values, block_tables, start_pos, seq_lens, max_seq_len: int, q,
+                    scale: float = 1.0, out=None, dtype=torch.bfloat16, stream=None):
+        """append(keys, values, ...) at start_pos, then attention over seq_lens
+        (= start_pos + n_new) in one call."""
+        if out is None:
+            out = torch.empty(q.shape, dtype=dtype, device=q.device)
+        _check(self._lib.fmkv_paged_decode_step(
+            self._h, _ptr(keys), _ptr(values), _ptr(block_tables), block_tables.shape[1],
+            _ptr(start_pos), _ptr(seq_lens), keys.shape[0], keys.shape[1], max_seq_len, _ptr(q),
+            q.shape[1], scale, 0.0, _ptr(out), _dtype_code(out.dtype), _stream(stream)))
         return out
 
     def read_codes(self, stream=None):

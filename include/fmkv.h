@@ -105,6 +105,16 @@ int fmkv_cache_trim(fmkv_cache* cache, int64_t keep_last);
 int fmkv_decode_attention(fmkv_cache* cache, const void* q_bf16, int32_t n_q_heads, float scale,
                           float sparse_v_tau, void* out, int32_t out_dtype, void* stream);
 
+/* One decode step of an attention layer, as Gemma4Attention::forward runs it
+ * (src/model/gemma4_attention.rs:84-103): cache.update_and_fetch(k, v) for
+ * n_tokens new positions, then attention of q over every visible position --
+ * fmkv_cache_append followed by fmkv_decode_attention, with the q rotation
+ * done inside the append launch. Arguments and errors as those two calls;
+ * nothing is launched or changed when validation fails. */
+int fmkv_decode_step(fmkv_cache* cache, const void* k_bf16, const void* v_bf16, int64_t n_tokens,
+                     const void* q_bf16, int32_t n_q_heads, float scale, float sparse_v_tau,
+                     void* out, int32_t out_dtype, void* stream);
+
 /* The fetch half of update_and_fetch and KVCache::peek_kv (src/cache.rs:247-257):
  * dequantized, un-rotated K and V of the visible positions in chronological
  * order, [stored_len][n_kv_heads][head_dim] in out_dtype. */
@@ -146,6 +156,18 @@ int fmkv_paged_decode_attention(fmkv_pool* pool, const void* q_bf16, const int32
                                 int32_t max_blocks, const int32_t* seq_lens, int32_t n_seqs,
                                 int32_t max_seq_len, int32_t n_q_heads, float scale,
                                 float sparse_v_tau, void* out, int32_t out_dtype, void* stream);
+
+/* Batched decode step: fmkv_paged_append of n_new tokens per sequence at
+ * start_pos, then fmkv_paged_decode_attention with seq_lens (which the
+ * caller sets to start_pos + n_new), the q rotation riding in the append
+ * launch (the per-layer sequence of src/model/gemma4_attention.rs:84-103 for
+ * a batch of requests). */
+int fmkv_paged_decode_step(fmkv_pool* pool, const void* k_bf16, const void* v_bf16,
+                           const int32_t* block_tables, int32_t max_blocks,
+                           const int32_t* start_pos, const int32_t* seq_lens, int32_t n_seqs,
+                           int32_t n_new, int32_t max_seq_len, const void* q_bf16,
+                           int32_t n_q_heads, float scale, float sparse_v_tau, void* out,
+                           int32_t out_dtype, void* stream);
 
 /* Canonical codes of every pool block, indexed by (physical block * 16 + t). */
 int fmkv_pool_read_codes(const fmkv_pool* pool, void* codes, void* meta, void* stream);
