@@ -6,7 +6,8 @@ Every .hip file under csrc/ is compiled by hipcc for gfx950 and linked into
 one shared library next to this file. Compile flags:
   -ffp-contract=off          the append kernel reproduces the oracle's rounding
                              op by op, so no implicit FMA contraction anywhere;
-  -packed-fp32-ops disabled  no packed FP32 instructions are generated.
+  -packed-fp32-ops disabled  no packed FP32 instructions are generated;
+  -amdgpu-mfma-vgpr-form=1   MFMA accumulators in VGPRs (see HIP_FLAGS).
 """
 from __future__ import annotations
 
@@ -33,6 +34,10 @@ HIP_FLAGS = [
     "-fPIC",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: the decode kernel rescales them
+    # with VALU ops, and accumulators kept in AGPRs were copied back and
+    # forth on every loop iteration
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall",
     "-Wno-unused-result",
     f"-I{INCLUDE}",

@@ -270,9 +270,9 @@ int prepare_append(const fmkv_cache* c, const void* k, const void* v, int64_t n,
   return FMKV_OK;
 }
 
-// Split-K plan, workspace ([part_o | part_ml | q-prep table]) and launch
-// arguments of decode attention over the first T positions; qp receives the
-// q-prep arguments (launched alone, or inside the append of a decode step).
+// Split-K plan, workspace ([part_o | part_ml | q-prep tables]) and launch
+// arguments of decode attention; qp receives the q-prep arguments (launched
+// alone, or inside the append of a decode step).
 template <typename Owner>
 int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, int64_t nblk,
                              const void* q, int32_t n_q_heads, float scale, float tau, void* out,
@@ -284,6 +284,7 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   a->st = st;
   a->group = n_q_heads / H;
   a->n_q_heads = n_q_heads;
+  std::memcpy(a->sign_bits, o->sign_bits, sizeof(a->sign_bits));
   a->c = o->c;
   if (nblk < 1) nblk = 1;
   a->bps = choose_bps(nblk * H * n_seqs, o->cus, wg_per_cu);
@@ -292,24 +293,25 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   a->out = out;
   a->out_f32 = out_dtype == FMKV_DTYPE_F32;
   const size_t n_rows = a->direct ? 0 : (size_t)n_seqs * a->max_splits * n_q_heads;
-  const size_t q_off = (n_rows * (D + 2) + 63) / 64 * 64;  // floats; 256-byte aligned table
-  const size_t q_words = (size_t)fmkv::qprep_words(n_seqs, H, D);
-  rc = o->ws.ensure((q_off + q_words) * sizeof(float));
+  const size_t tab_off = (n_rows * (D + 2) * sizeof(float) + 255) / 256 * 256;
+  const size_t tab_bytes = (size_t)n_seqs * H * fmkv::qprep_bytes(D);
+  rc = o->ws.ensure(tab_off + tab_bytes);
   if (rc) return rc;
   a->part_o = n_rows ? o->ws.ptr : nullptr;
   a->part_ml = n_rows ? o->ws.ptr + n_rows * D : nullptr;
-  uint32_t* table = reinterpret_cast<uint32_t*>(o->ws.ptr + q_off);
-  a->qprep = table;
+  uint8_t* tab = reinterpret_cast<uint8_t*>(o->ws.ptr) + tab_off;
+  a->qprep = tab;
   qp->q = static_cast<const uint16_t*>(q);
   qp->n_q_heads = n_q_heads;
   qp->group = n_q_heads / H;
   qp->qscale = scale * 1.4426950408889634f;
   qp->c = o->c;
   std::memcpy(qp->sign_bits, o->sign_bits, sizeof(qp->sign_bits));
-  qp->out = table;
+  qp->out = tab;
   return FMKV_OK;
 }
 
+// Decode attention over the first T positions of a cache.
 int prepare_attention(fmkv_cache* c, int64_t T, const void* q, int32_t n_q_heads, float scale,
                       float tau, void* out, int32_t out_dtype, fmkv::AttnArgs* a,
                       fmkv::QPrepArgs* qp) {
@@ -355,7 +357,8 @@ int prepare_paged_append(const fmkv_pool* p, const void* k, const void* v,
 int prepare_paged_attention(fmkv_pool* p, const void* q, const int32_t* block_tables,
                             int32_t max_blocks, const int32_t* seq_lens, int32_t n_seqs,
                             int32_t max_seq_len, int32_t n_q_heads, float scale, float tau,
-                            void* out, int32_t out_dtype, fmkv::AttnArgs* a, fmkv::QPrepArgs* qp) {
+                            void* out, int32_t out_dtype, fmkv::AttnArgs* a,
+                            fmkv::QPrepArgs* qp) {
   if (n_seqs < 0 || max_seq_len < 0 || max_blocks < 1)
     return fail(FMKV_ERR_INVALID_ARG, "bad n_seqs / max_seq_len / max_blocks");
   if (n_seqs > 0 && (!block_tables || !seq_lens))
@@ -503,8 +506,7 @@ int fmkv_decode_attention(fmkv_cache* c, const void* q, int32_t n_q_heads, float
   int rc = prepare_attention(c, c->offset, q, n_q_heads, scale, tau, out, out_dtype, &a, &qp);
   if (rc) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e =
-      fmkv::launch_qprep(qp, c->desc.head_dim, c->desc.bits, c->desc.n_kv_heads, 1, s);
+  hipError_t e = fmkv::launch_qprep(qp, c->desc.head_dim, c->desc.bits, c->desc.n_kv_heads, 1, s);
   if (e != hipSuccess) return hip_fail(e, "q preparation launch");
   hipEvent_t e0, e1;
   next_events(&e0, &e1);

@@ -124,6 +124,7 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
     // decode step: the last column of work-groups prepares q for the
     // attention launch that follows, in the shadow of the append's loads
     if (a.qp.out && bx == (int)gridDim.x - 1) {
+      static_assert(kAppendThreads == kQPrepThreads, "q-prep work-group size");
       qprep_workgroup<D, BITS>(a.qp, a.st.n_kv_heads, h, seq, tid);
       return;
     }

@@ -3,34 +3,47 @@
 // Replaces mlx_rs::fast::scaled_dot_product_attention at decode (L == 1,
 // src/model/gemma4_attention.rs:94-103) reading the cache written by
 // fmkv_append. One work-group = one (split of consecutive 16-token blocks,
-// KV head, sequence); its NW = D/DW waves each own DW dims of head_dim.
+// KV head, sequence) with four wave pairs. Pair p streams whole head-blocks
+// b_begin + p, b_begin + p + 4, ...; its two waves each own one half of
+// head_dim (half the 64-dim groups), exchange their partial scores once per
+// block through LDS (a flag handshake inside the pair, no work-group
+// barrier) and then run identical online-softmax bookkeeping. Two waves per
+// SIMD hide each other's latencies. The pairs' (m, l, O) meet once, in LDS,
+// at the end.
 //
-// Per block (16 tokens):
+// Memory path: each wave copies its half of its pair's next blocks
+// HBM -> LDS with buffer_load_dwordx4 ... lds (16 bytes per lane, no VGPRs
+// held while in flight), several stages deep, and waits for a stage with an
+// explicit vmcnt. The copies are issued from inline asm, so the compiler
+// neither tracks them nor inserts waits of its own on LDS reads; every stage
+// read is preceded by the vmcnt wait covering it, computed from the number
+// of copies issued after that stage. The compiler issues no vector-memory
+// loads of its own in this kernel (the one candidate, the sign-bit lookup,
+// is written so that it cannot become one).
+//
+// Per block (16 tokens), per 64-dim group g of the wave's half:
 //   QK^T  S^T[16 tok x 16 col] += K[16 x 32] . Q^T[32 x 16] on MFMA
 //         (v_mfma_f32_16x16x32_f16), K codes converted exactly to f16
-//         integers; per 64-dim group the f16 scale/bias are applied after the
-//         MFMA: s += scale * acc + bias * sum(q_group). (Codes stay
-//         unbiased: an f16 1024 + code operand with the offset cancelled in
-//         the accumulator is cheaper but inflates the fp32 partial sums ~64x
-//         at 4 bits, which outlier channels turn into visible error.)
+//         integers; the f16 scale/bias apply after the MFMA:
+//         s += scale * acc + bias * sum(q_group).
 //         Column c = q head (c & 7) of the GQA group, c < 8 carrying the f16
 //         high part of q_rot and c >= 8 the residual, so S keeps ~22 bits of
 //         q precision; DPP row_ror:8 folds the two halves.
-//   Waves exchange their partial S through LDS (one barrier per block) and
-//   run identical online-softmax bookkeeping (base-2, eager rescale).
 //   PV    O^T[16 dim x 16 col] += V^T[16 dim x 16 tok] . P'^T[16 tok x 16 col]
 //         (v_mfma_f32_16x16x16f16) with P' = p * v_scale split hi/lo in the
 //         same columns; bias terms are summed on the side.
 // The QK output lane layout equals the PV B-operand layout (lane (j, c) holds
 // tokens 4j..4j+3 of column c), so no register shuffles are needed.
+// (Codes stay unbiased: an f16 1024 + code operand with the offset cancelled
+// in the accumulator is cheaper but inflates the fp32 partial sums ~64x at 4
+// bits, which outlier channels turn into visible error.)
 //
-// q arrives pre-rotated in the MFMA operand layout (fmkv_qprep.h), so the
-// prologue is one load per operand, issued ahead of the first blocks. Each
-// wave then keeps DEPTH blocks in flight in as many register sets, refilling
-// a set as soon as it has been consumed.
-// Epilogue: O is written to LDS, inverse-rotated (o . R^T = c * FWHT(o o s))
-// and stored either as the final output (single split) or as a split partial
-// (m, l, O) for the combine kernel.
+// q_rot = (FWHT(q * scale * log2 e) * c) o s arrives as a table of MFMA B
+// operands (fmkv_qprep.h), written once per step by the append launch of a
+// decode step or by qprep_kernel, and copied to LDS ahead of the first
+// blocks. Epilogue: the pairs' results merge in LDS, the inverse rotation
+// o . R^T = c * FWHT(o o s) follows, and the result is the final output (one
+// split) or a split partial for combine_kernel.
 #include "fmkv_device.h"
 #include "fmkv_internal.h"
 #include "fmkv_qprep.h"
@@ -40,104 +53,145 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-template <int BITS, int GW>
-struct BlockRegs {
-  static constexpr int kCodeLoads = (BITS == 8) ? GW : GW / 2;
-  u32x4 k[kCodeLoads];
-  u32x4 v[kCodeLoads];
-  u32x4 ks[GW];
-  u32x4 vs[GW];
+constexpr int kChunk = 1024;  // bytes per full LDS copy instruction (64 lanes x 16 B)
+
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+
+// Staging plan of one (head_dim, bits). A stage holds one head-block as
+//   [K codes][V codes][wave 0: K meta, V meta of its groups][wave 1: ...];
+// each wave copies its groups' code chunks and, with one partial
+// instruction, its groups' scale/bias. Stages per pair: about 136 KiB of
+// staging per work-group, at least two, and the largest wait (stages x
+// copies per block) within the 6-bit vmcnt field.
+template <int D, int BITS>
+struct AttnPlan {
+  static constexpr BlockLayout L = make_layout(D, BITS, kAffine);
+  static constexpr int NG = D / 64;
+  static constexpr int GH = NG / 2;  // groups per wave
+  static constexpr int kCodeChunks = (int)(L.code_bytes / kChunk);  // per K or V region
+  // code chunks a wave copies per region: its groups' chunks (at 4 bits one
+  // chunk holds two groups; at head_dim 128 both waves copy the one chunk)
+  static constexpr int kWaveChunks = BITS == 8 ? GH : (GH >= 2 ? GH / 2 : 1);
+  static constexpr int kMetaHalf = GH * 64;  // one wave's K (or V) scale/bias bytes
+  static constexpr int kMetaOff = 2 * kCodeChunks * kChunk;
+  static constexpr int kStageBytes = kMetaOff + 4 * kMetaHalf;
+  static constexpr int kCopies = 2 * kWaveChunks + 1;  // copy instructions per wave per block
+  static constexpr int kFit = (136 * 1024) / (kAttnPairs * kStageBytes);
+  static constexpr int kStagesA = kFit < 2 ? 2 : (kFit > 8 ? 8 : kFit);
+  static constexpr int kStages = kStagesA * kCopies <= 63 ? kStagesA : 63 / kCopies;
+  static constexpr int kQS = D + 4;  // padded row stride (LDS banks)
+  static constexpr int kMergeBytes = kAttnPairs * 8 * kQS * 4;
+  static constexpr int kStageRegion = cmax(kAttnPairs * kStages * kStageBytes, kMergeBytes);
+  // prologue: the q-prep table; loop: the score exchange
+  static constexpr int kXBytes = kAttnWaves * 2 * 64 * 16;
+  static constexpr int kScratch = cmax((int)qprep_bytes(D), kXBytes);
+  static_assert(NG % 2 == 0 && kCodeChunks >= 1, "layout");
+  static_assert(kStages * kCopies <= 63, "vmcnt immediates");
+  static_assert(8 * GH <= 64, "one partial instruction copies a wave's scale/bias");
 };
 
-// One head-block's slice for this wave via buffer loads: the block base is a
-// scalar resource (bounded by the block size; out-of-range reads return 0),
-// lanes differ only in a 32-bit offset.
-// `valid` false gives a zero-size resource: the loads are dropped by the
-// hardware (no memory traffic) and return zeros, so callers can issue them
-// unconditionally.
-template <int D, int BITS, int GW>
-__device__ inline void load_block(BlockRegs<BITS, GW>& r, const uint8_t* blk, bool valid, int wave,
-                                  int lane) {
-  constexpr BlockLayout L = make_layout(D, BITS, kAffine);
-  constexpr int kLoads = BlockRegs<BITS, GW>::kCodeLoads;
-  // the block base is the same for the whole wave; say so, so that the
-  // resource lives in SGPRs
-  const uint64_t addr = reinterpret_cast<uint64_t>(blk);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)addr);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(addr >> 32));
-  const __amdgpu_buffer_rsrc_t rs =
-      __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), 0,
-                                        valid ? (int)L.block_bytes : 0, 0x00020000);
-  const int vo = lane * 16;          // 16 bytes per lane of a 1 KiB chunk
-  const int so = (lane >> 4) * 16;   // 4 tokens' {scale, bias} of a group
-  const int c0 = wave * kLoads;      // this wave's first code chunk
-#pragma unroll
-  for (int i = 0; i < kLoads; i++) {
-    r.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, vo, (int)L.k_codes + (c0 + i) * 1024, 0);
-    r.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, vo, (int)L.v_codes + (c0 + i) * 1024, 0);
-  }
-#pragma unroll
-  for (int gi = 0; gi < GW; gi++) {
-    const int g = wave * GW + gi;
-    r.ks[gi] = __builtin_amdgcn_raw_buffer_load_b128(rs, so, (int)L.k_meta + g * 64, 0);
-    r.vs[gi] = __builtin_amdgcn_raw_buffer_load_b128(rs, so, (int)L.v_meta + g * 64, 0);
+__device__ inline uint32_t lds_addr(const void* p) {
+  return (uint32_t)reinterpret_cast<uintptr_t>(p);  // low half of the flat LDS address
+}
+
+// Raw buffer resource over [base, base + bytes); reads past the end return 0.
+__device__ inline u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  u32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) & 0xffffu;  // stride 0
+  r[2] = bytes;
+  r[3] = 0x00020000u;
+  return r;
+}
+
+// One copy instruction: each active lane moves 16 bytes from rsrc + voff to
+// LDS at lds + 16 * lane.
+__device__ inline void dma16(uint32_t lds, int voff, const u32x4 rs) {
+  asm volatile("buffer_load_dwordx4 %1, %2, 0 offen lds" :: "{m0}"(lds), "v"(voff), "s"(rs)
+               : "memory");
+}
+
+template <int N>
+__device__ inline void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
+// Wait until at most `pending` (wave-uniform) blocks' copies, CP
+// instructions each, are outstanding; P bounds pending.
+template <int CP, int P>
+__device__ inline void wait_copies(int pending) {
+  if constexpr (P > 0) {
+    if (pending >= P) {
+      wait_vmcnt<P * CP>();
+      return;
+    }
+    wait_copies<CP, P - 1>(pending);
+  } else {
+    wait_vmcnt<0>();
   }
 }
 
-// K codes of group gi (wave-local) for MFMA s in {0, 1}: 8 exact f16 values.
-template <int BITS, int GW>
-__device__ inline half8_t k_operand(const BlockRegs<BITS, GW>& r, int gi, int s) {
+__device__ inline u32x4 lds16(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// K operand (8 codes as exact f16) of MFMA s of group g; `w` is the lane's
+// 16 bytes of the group's chunk (8-bit) or of the two groups' chunk (4-bit).
+template <int BITS>
+__device__ inline half8_t k_operand(const u32x4 w, int g, int s) {
   if constexpr (BITS == 8) {
-    const u32x4 u = r.k[gi];
-    const uint32_t w0 = u[2 * s], w1 = u[2 * s + 1];
+    const uint32_t w0 = w[2 * s], w1 = w[2 * s + 1];
     return cat8(u8x2_to_h2(w0, 0x04010400u), u8x2_to_h2(w0, 0x04030402u),
                 u8x2_to_h2(w1, 0x04010400u), u8x2_to_h2(w1, 0x04030402u));
   } else {
-    const uint32_t w = r.k[gi >> 1][(gi & 1) * 2 + s];
-    return cat8(u4x2_to_h2(w, 0), u4x2_to_h2(w, 1), u4x2_to_h2(w, 2), u4x2_to_h2(w, 3));
+    const uint32_t x = w[(g & 1) * 2 + s];
+    return cat8(u4x2_to_h2(x, 0), u4x2_to_h2(x, 1), u4x2_to_h2(x, 2), u4x2_to_h2(x, 3));
   }
 }
 
-// V codes of column tile ct (0..3) of group gi: tokens 4j..4j+3 of one dim.
-template <int BITS, int GW>
-__device__ inline half4_t v_operand(const BlockRegs<BITS, GW>& r, int gi, int ct) {
+// V codes of column tile ct (0..3) of group g: tokens 4j..4j+3 of one dim.
+template <int BITS>
+__device__ inline half4_t v_operand(const u32x4 w, int g, int ct) {
   if constexpr (BITS == 8) {
-    const uint32_t w = r.v[gi][ct];
-    return cat4(u8x2_to_h2(w, 0x04010400u), u8x2_to_h2(w, 0x04030402u));
+    const uint32_t x = w[ct];
+    return cat4(u8x2_to_h2(x, 0x04010400u), u8x2_to_h2(x, 0x04030402u));
   } else {
-    const int ctc = (gi & 1) * 4 + ct;  // column tile inside the 128-dim chunk
-    const uint32_t w = r.v[gi >> 1][ctc >> 1];
+    const int ctc = (g & 1) * 4 + ct;  // column tile inside the 128-dim chunk
+    const uint32_t x = w[ctc >> 1];
     const int k0 = (ctc & 1) * 2;
-    return cat4(u4x2_to_h2(w, k0), u4x2_to_h2(w, k0 + 1));
+    return cat4(u4x2_to_h2(x, k0), u4x2_to_h2(x, k0 + 1));
   }
 }
 
 __device__ inline float lo16(uint32_t w) { return f16_bits_to_f32(w); }
 __device__ inline float hi16(uint32_t w) { return f16_bits_to_f32(w >> 16); }
 
-// Waves per SIMD: three with two blocks in flight per wave (register budget
-// <= 168), two with three or four (<= 256), one beyond (<= 512 with AGPRs).
-template <int D, int BITS, int DW, int DEPTH>
-__global__ __launch_bounds__((D / DW) * 64)
-__attribute__((amdgpu_waves_per_eu(DEPTH >= 5 ? 1 : (DEPTH >= 3 ? 2 : 3), 8)))
+// Two waves per SIMD (register budget <= 256 each).
+template <int D, int BITS>
+__global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void decode_attn_kernel(AttnArgs a) {
-  constexpr int NW = D / DW;
-  constexpr int GW = DW / 64;
-  static_assert(BITS == 8 || GW % 2 == 0, "4-bit needs 128-dim wave slices");
+  using P = AttnPlan<D, BITS>;
+  constexpr BlockLayout L = P::L;
+  constexpr int NG = P::NG, GH = P::GH;
+  constexpr int E = D / 64;
+  constexpr int QS = P::kQS;
+  constexpr int CP = P::kCopies, NST = P::kStages, SB = P::kStageBytes;
+  constexpr int MH = P::kMetaHalf;
 
-  constexpr int QS = D + 4;                   // padded row stride (LDS banks)
-  __shared__ float qo[8 * QS];                // the split's O, for the epilogue
-  __shared__ float4_t sx[2][NW > 1 ? NW : 1][64];  // partial S exchange
-  __shared__ float ml_s[8][2];
+  __shared__ __align__(16) uint8_t stage[P::kStageRegion];
+  __shared__ __align__(16) uint8_t scratch[P::kScratch];  // q-prep table, then score exchange
+  __shared__ float ml_s[kAttnPairs][8][2];
+  __shared__ int xflag[kAttnWaves];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int pair = wave >> 1, half = wave & 1;
   const int j = lane >> 4, c = lane & 15;
   const int head = c & 7;
   const bool hi = c < 8;
   const int G = a.group;
   const bool col_valid = head < G;
   const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  const int g0 = half * GH;  // this wave's first group
 
   const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
   const SeqGeom geo =
@@ -149,9 +203,8 @@ void decode_attn_kernel(AttnArgs a) {
   if (b_end > geo.blk_hi) b_end = geo.blk_hi;
 
   // Table entries are read through the constant address space: a uniform
-  // index then becomes a scalar load, counted apart from the vector loads of
-  // the block stream, so resolving the next block never waits for the
-  // blocks in flight.
+  // index then becomes a scalar load, which never waits for the copies in
+  // flight.
   typedef const int32_t __attribute__((address_space(4)))* table_ptr;
   const table_ptr table =
       a.st.block_table
@@ -165,48 +218,73 @@ void decode_attn_kernel(AttnArgs a) {
     return hbase + phys * a.st.block_stride;
   };
 
-  // ---- prologue: this wave's q operands first, then the first blocks ----
-  constexpr int E = D / 64;
-  static_assert(DW == kAttnDW, "q-prep table is laid out for 128-dim wave slices");
-  const uint32_t* qp = qprep_entry(a.qprep, seq, (int)gridDim.y, kvh, NW, wave, lane);
-  u32x4 qv[kQPrepVecs];
-#pragma unroll
-  for (int i = 0; i < kQPrepVecs; i++) qv[i] = *reinterpret_cast<const u32x4*>(qp + 4 * i);
+  // this pair's blocks: pb0 + 4 i, i < nb
+  const int64_t pb0 = b_begin + pair;
+  const int nb = pb0 < b_end ? (int)((b_end - pb0 + kAttnPairs - 1) / kAttnPairs) : 0;
+  uint8_t* const pstage = stage + pair * NST * SB;
+  const uint32_t pstage_lds = lds_addr(pstage);
 
-  // Loads are issued unconditionally: a block past the split gets a zero-size
-  // resource (no traffic), so the loaded registers never merge with stale
-  // ones across the loop and no copy forces a wait.
-  const int64_t b_last = b_end > b_begin ? b_end - 1 : b_begin;
-  auto fetch = [&](BlockRegs<BITS, GW>& r, int64_t lb) {
-    const bool valid = lb < b_end;
-    load_block<D, BITS, GW>(r, blk_ptr(valid ? lb : b_last), valid, wave, lane);
+  // This wave's part of block lb into stage st: its groups' K and V code
+  // chunks, then one partial instruction moving its groups' K and V
+  // scale/bias (lanes < 4 GH: K, the next 4 GH: V) to its meta area.
+  const int kc0 = BITS == 8 ? g0 : (GH >= 2 ? g0 / 2 : 0);  // first code chunk
+  const int mlane = lane < 4 * GH ? lane : lane - 4 * GH;
+  const int meta_voff = (lane < 4 * GH ? (int)L.k_meta : (int)L.v_meta) + g0 * 64 + mlane * 16;
+  auto copy_block = [&](int st, int64_t lb) {
+    const u32x4 rs = buffer_rsrc(blk_ptr(lb), (uint32_t)L.block_bytes);
+    const uint32_t sl = pstage_lds + st * SB;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of this stage are done
+#pragma unroll
+    for (int k = 0; k < P::kWaveChunks; k++) {
+      const int ch = kc0 + k;
+      dma16(sl + (int)L.k_codes + ch * kChunk, (int)L.k_codes + ch * kChunk + lane * 16, rs);
+      dma16(sl + (int)L.v_codes + ch * kChunk, (int)L.v_codes + ch * kChunk + lane * 16, rs);
+    }
+    if (lane < 8 * GH) dma16(sl + P::kMetaOff + half * 2 * MH, meta_voff, rs);
   };
-  BlockRegs<BITS, GW> rs[DEPTH];
-#pragma unroll
-  for (int s = 0; s < DEPTH; s++) fetch(rs[s], b_begin + s);
 
-  half8_t bq[GW][2];
-  float qs[GW];
-#pragma unroll
-  for (int gi = 0; gi < GW; gi++) {
-#pragma unroll
-    for (int s = 0; s < 2; s++) bq[gi][s] = __builtin_bit_cast(half8_t, qv[gi * 2 + s]);
-    qs[gi] = __uint_as_float(qv[2 * GW][gi]);
+  // ---- copies: the q-prep table of (seq, kvh) (wave w: its KiB entries w,
+  // w + 8, ...), then the first stages; the table is waited for alone ----
+  constexpr int NE = 2 * NG;  // B-operand entries; the group sums follow
+  if (lane == 0) xflag[wave] = 0;
+  {
+    const uint8_t* tab = a.qprep + ((int64_t)seq * gridDim.y + kvh) * qprep_bytes(D);
+    const u32x4 rt = buffer_rsrc(tab, (uint32_t)qprep_bytes(D));
+    for (int e = wave; e <= NE; e += kAttnWaves)
+      dma16(lds_addr(scratch + e * kChunk), e * kChunk + lane * 16, rt);
   }
-  const uint32_t sbits = qv[2 * GW][2];
+#pragma unroll
+  for (int s = 0; s < NST; s++)
+    if (s < nb) copy_block(s, pb0 + (int64_t)kAttnPairs * s);
+  wait_copies<CP, NST>(nb < NST ? nb : NST);  // the table copies preceded every block
+  __syncthreads();
+
+  // B operands of this wave's groups (hi / residual halves of q_rot, see
+  // fmkv_qprep.h) and their q sums for the bias term
+  half8_t bq[GH][2];
+  float qs[GH];
+  const float* qsum = reinterpret_cast<const float*>(scratch + NE * kChunk);  // [head][NG]
+#pragma unroll
+  for (int gi = 0; gi < GH; gi++) {
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+      bq[gi][s] = *reinterpret_cast<const half8_t*>(scratch + ((g0 + gi) * 2 + s) * kChunk + lane * 16);
+    qs[gi] = (hi && col_valid) ? qsum[head * NG + g0 + gi] : 0.0f;
+  }
+  __syncthreads();  // the table is consumed: the region becomes the score exchange
+  float4_t* const xs = reinterpret_cast<float4_t*>(scratch);  // [wave][parity][lane]
 
   // ---- main loop ----
-  float4_t o[GW * 4];
+  float4_t o[GH * 4];
 #pragma unroll
-  for (int i = 0; i < GW * 4; i++) o[i] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  float bacc[GW];
+  for (int i = 0; i < GH * 4; i++) o[i] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  float bacc[GH];
 #pragma unroll
-  for (int gi = 0; gi < GW; gi++) bacc[gi] = 0.0f;
+  for (int gi = 0; gi < GH; gi++) bacc[gi] = 0.0f;
   // m_run starts finite (-1e30): exp2(-inf - m) is 0 for masked tokens and
   // exp2(m_old - m_new) underflows to 0 at the first visible token, so the
   // softmax needs no special cases.
   float m_run = -1e30f, l_run = 0.0f;
-  int par = 0;
   const float lo_sel = hi ? 0.0f : 1.0f;  // 1 on the residual columns
 
   // visible slots: linear [vis_lo, vis_hi); ring [0, min(T, W)), unless a trim
@@ -215,41 +293,69 @@ void decode_attn_kernel(AttnArgs a) {
   const int64_t vis_hi = a.window > 0 ? (T < a.window ? T : a.window) : T;
   const bool ring_trim = a.window > 0 && a.vis_begin > T - a.window;
 
-  auto process = [&](const BlockRegs<BITS, GW>& cur, int64_t b) {
-    // S^T = K . q_rot^T per 64-dim group, then * scale + bias * sum(q)
+  // LDS operands, read one group ahead of their use so that the read
+  // latency overlaps the previous group's MFMAs
+  auto codes = [&](const uint8_t* sp, int region, int gi) {
+    const int g = g0 + gi;
+    return lds16(sp + region + (BITS == 8 ? g : g / 2) * kChunk + lane * 16);
+  };
+  auto kmeta = [&](const uint8_t* sp, int gi) {
+    return lds16(sp + P::kMetaOff + half * 2 * MH + gi * 64 + j * 16);
+  };
+  auto vmeta = [&](const uint8_t* sp, int gi) {
+    return lds16(sp + P::kMetaOff + half * 2 * MH + MH + gi * 64 + j * 16);
+  };
+
+  auto process = [&](const uint8_t* sp, int64_t b, int it) {
+    // this half's S^T = K . q_rot^T, * scale + bias * sum(q), per group
     float4_t sv = (float4_t){0.f, 0.f, 0.f, 0.f};
+    u32x4 kw = codes(sp, (int)L.k_codes, 0), km = kmeta(sp, 0);
 #pragma unroll
-    for (int gi = 0; gi < GW; gi++) {
+    for (int gi = 0; gi < GH; gi++) {
+      const u32x4 kw_g = kw, km_g = km;
+      if (gi + 1 < GH) {
+        if (BITS == 8 || ((g0 + gi + 1) & 1) == 0) kw = codes(sp, (int)L.k_codes, gi + 1);
+        km = kmeta(sp, gi + 1);
+      }
+      const int g = g0 + gi;
       float4_t acc = (float4_t){0.f, 0.f, 0.f, 0.f};
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand<BITS, GW>(cur, gi, 0), bq[gi][0],
-                                                   acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand<BITS, GW>(cur, gi, 1), bq[gi][1],
-                                                   acc, 0, 0, 0);
-      const u32x4 kw = cur.ks[gi];
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand<BITS>(kw_g, g, 0), bq[gi][0], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand<BITS>(kw_g, g, 1), bq[gi][1], acc, 0, 0, 0);
 #pragma unroll
-      for (int i = 0; i < 4; i++) sv[i] = fmaf(lo16(kw[i]), acc[i], fmaf(hi16(kw[i]), qs[gi], sv[i]));
+      for (int i = 0; i < 4; i++)
+        sv[i] = fmaf(lo16(km_g[i]), acc[i], fmaf(hi16(km_g[i]), qs[gi], sv[i]));
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if constexpr (NW > 1) {
-      sx[par][wave][lane] = sv;
-      __syncthreads();
-      sv = sx[par][0][lane];
-#pragma unroll
-      for (int w2 = 1; w2 < NW; w2++) sv += sx[par][w2][lane];
-      par ^= 1;
-    }
+    u32x4 vw = codes(sp, (int)L.v_codes, 0), vm = vmeta(sp, 0);  // in flight during the softmax
+
+    // exchange the half scores with the partner wave: publish (the release
+    // orders the data before the flag), then wait for the partner's; both
+    // waves add the halves in the same order, so they hold identical scores
+    const int par = it & 1;
+    xs[(wave * 2 + par) * 64 + lane] = sv;
+    __hip_atomic_store(&xflag[wave], it + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    while (__hip_atomic_load(&xflag[wave ^ 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+           it + 1)
+      __builtin_amdgcn_s_sleep(1);
+    const float4_t sp_other = xs[((wave ^ 1) * 2 + par) * 64 + lane];
+    const float4_t s0 = half == 0 ? sv : sp_other;
+    const float4_t s1 = half == 0 ? sp_other : sv;
     float s[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) s[i] = sv[i] + row_ror8(sv[i]);
+    for (int i = 0; i < 4; i++) {
+      const float t = s0[i] + s1[i];
+      s[i] = t + row_ror8(t);
+    }
 
     // visibility: whole block in the common case (uniform test), per token
     // only at the edges of the visible range
     const int64_t t0 = b * kBlockTokens;
-    const bool full = b < b_end && t0 >= vis_lo && t0 + kBlockTokens <= vis_hi && !ring_trim;
+    const bool full = t0 >= vis_lo && t0 + kBlockTokens <= vis_hi && !ring_trim;
     if (!full) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int64_t slot = t0 + 4 * j + i;
-        bool vis = b < b_end && slot >= vis_lo && slot < vis_hi;
+        bool vis = slot >= vis_lo && slot < vis_hi;
         if (ring_trim) vis = vis && slot_position(slot, T, a.window) >= a.vis_begin;
         if (!vis) s[i] = -INFINITY;
       }
@@ -260,10 +366,14 @@ void decode_attn_kernel(AttnArgs a) {
     const float m_new = fmaxf(m_run, mb);
     if (__any(m_new > m_run)) {
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      // until something has been accumulated, O and the bias sums are zero
+      // and need no rescaling (the common case of the first block)
+      if (__any(l_run > 0.0f)) {
 #pragma unroll
-      for (int i = 0; i < GW * 4; i++) o[i] *= alpha;
+        for (int i = 0; i < GH * 4; i++) o[i] *= alpha;
 #pragma unroll
-      for (int gi = 0; gi < GW; gi++) bacc[gi] *= alpha;
+        for (int gi = 0; gi < GH; gi++) bacc[gi] *= alpha;
+      }
       l_run *= alpha;
       m_run = m_new;
     }
@@ -275,88 +385,110 @@ void decode_attn_kernel(AttnArgs a) {
     // O^T += V^T . P'^T with P' = p * v_scale as f16 hi (c < 8) / residual
     // (c >= 8)
 #pragma unroll
-    for (int gi = 0; gi < GW; gi++) {
-      const u32x4 vw = cur.vs[gi];
+    for (int gi = 0; gi < GH; gi++) {
+      const u32x4 vw_g = vw, vm_g = vm;
+      if (gi + 1 < GH) {
+        if (BITS == 8 || ((g0 + gi + 1) & 1) == 0) vw = codes(sp, (int)L.v_codes, gi + 1);
+        vm = vmeta(sp, gi + 1);
+      }
       float x[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        x[i] = p[i] * lo16(vw[i]);
-        bacc[gi] = fmaf(p[i], hi16(vw[i]), bacc[gi]);
+        x[i] = p[i] * lo16(vm_g[i]);
+        bacc[gi] = fmaf(p[i], hi16(vm_g[i]), bacc[gi]);
       }
       const half2_t h01 = pkrtz(x[0], x[1]);
       const half2_t h23 = pkrtz(x[2], x[3]);
       const half4_t bp = cat4(
           pkrtz(fmaf(-lo_sel, (float)h01[0], x[0]), fmaf(-lo_sel, (float)h01[1], x[1])),
           pkrtz(fmaf(-lo_sel, (float)h23[0], x[2]), fmaf(-lo_sel, (float)h23[1], x[3])));
+      const int g = g0 + gi;
 #pragma unroll
       for (int ct = 0; ct < 4; ct++)
-        o[gi * 4 + ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(v_operand<BITS, GW>(cur, gi, ct),
-                                                               bp, o[gi * 4 + ct], 0, 0, 0);
+        o[gi * 4 + ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(v_operand<BITS>(vw_g, g, ct), bp,
+                                                               o[gi * 4 + ct], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // DEPTH register sets in rotation: while one block is processed the others
-  // are in flight; a set is reloaded as soon as it has been consumed (no
-  // register copies, which would force a wait on every outstanding load).
-  // Blocks past the split are skipped (a uniform branch) but still fetched
-  // as dropped loads, so every set sees the same load sequence.
-  for (int64_t b = b_begin; b < b_end; b += DEPTH) {
-#pragma unroll
-    for (int s = 0; s < DEPTH; s++) {
-      if (b + s < b_end) process(rs[s], b + s);
-      fetch(rs[s], b + s + DEPTH);
-    }
+  // stage st holds block i; before reading it, wait until only the copies
+  // issued after it (the next min(NST - 1, nb - 1 - i) blocks) are pending;
+  // once read, the stage is refilled with block i + NST
+  int st = 0;
+  for (int i = 0; i < nb; i++) {
+    const int rest = nb - 1 - i;
+    wait_copies<CP, NST - 1>(rest < NST - 1 ? rest : NST - 1);
+    process(pstage + st * SB, pb0 + (int64_t)kAttnPairs * i, i);
+    if (i + NST < nb) copy_block(st, pb0 + (int64_t)kAttnPairs * (i + NST));
+    st = st + 1 == NST ? 0 : st + 1;
   }
 
-  // ---- epilogue ----
+  // ---- epilogue: merge the four pairs, inverse rotation, store ----
   l_run = xor16_sum(l_run);
   l_run = xor32_sum(l_run);
 #pragma unroll
-  for (int gi = 0; gi < GW; gi++) {
+  for (int gi = 0; gi < GH; gi++) {
     bacc[gi] = xor16_sum(bacc[gi]);
     bacc[gi] = xor32_sum(bacc[gi]);
   }
 #pragma unroll
-  for (int k = 0; k < GW * 4; k++)
+  for (int k = 0; k < GH * 4; k++)
 #pragma unroll
     for (int i = 0; i < 4; i++) o[k][i] = o[k][i] + row_ror8(o[k][i]);
 
-  __syncthreads();  // all waves are done reading q_rot out of qo
+  __syncthreads();  // every wave is done with its stages (all copies waited for)
+  float* R = reinterpret_cast<float*>(stage);  // [pair][head][QS]
   if (hi && col_valid) {
 #pragma unroll
-    for (int gi = 0; gi < GW; gi++)
+    for (int gi = 0; gi < GH; gi++)
 #pragma unroll
       for (int ct = 0; ct < 4; ct++) {
-        const int d = (wave * GW + gi) * 64 + ct * 16 + 4 * j;
-        *reinterpret_cast<float4_t*>(&qo[head * QS + d]) = o[gi * 4 + ct] + bacc[gi];
+        const int d = (g0 + gi) * 64 + ct * 16 + 4 * j;
+        *reinterpret_cast<float4_t*>(&R[(pair * 8 + head) * QS + d]) = o[gi * 4 + ct] + bacc[gi];
       }
-    if (wave == 0 && j == 0) {
-      ml_s[head][0] = m_run;
-      ml_s[head][1] = l_run;
+    if (half == 0 && j == 0) {
+      ml_s[pair][head][0] = m_run;
+      ml_s[pair][head][1] = l_run;
     }
   }
   __syncthreads();
 
-  // inverse rotation o . R^T = c * FWHT(o o s), one head per wave, then store
-  const int64_t qh0 = (int64_t)seq * a.n_q_heads + (int64_t)kvh * G;
-  const int64_t pbase = ((int64_t)seq * a.max_splits + split) * a.n_q_heads + (int64_t)kvh * G;
-  for (int hh = wave; hh < G; hh += NW) {
+  // head w on wave w
+  if (wave < G) {
+    const int hh = wave;
+    const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
+    float M = ml_s[0][hh][0];
+#pragma unroll
+    for (int q = 1; q < kAttnPairs; q++) M = fmaxf(M, ml_s[q][hh][0]);
+    float wgt[kAttnPairs], Lsum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kAttnPairs; q++) {
+      wgt[q] = __builtin_amdgcn_exp2f(ml_s[q][hh][0] - M);
+      Lsum = fmaf(wgt[q], ml_s[q][hh][1], Lsum);
+    }
     float x[E];
 #pragma unroll
-    for (int i = 0; i < E; i++) x[i] = apply_sign(qo[hh * QS + lane * E + i], sbits, i);
+    for (int i = 0; i < E; i++) {
+      float v = 0.0f;
+#pragma unroll
+      for (int q = 0; q < kAttnPairs; q++) v = fmaf(wgt[q], R[(q * 8 + hh) * QS + lane * E + i], v);
+      x[i] = apply_sign(v, sbits, i);
+    }
     wave_fwht<E>(x, lane);
+    const int64_t qh0 = (int64_t)seq * a.n_q_heads + (int64_t)kvh * G;
     if (a.direct) {
-      const float l = ml_s[hh][1];
       const int64_t o_idx = (qh0 + hh) * D + lane * E;
 #pragma unroll
       for (int i = 0; i < E; i++) {
-        const float v = l > 0.0f ? (x[i] * a.c) / l : 0.0f;
+        const float v = Lsum > 0.0f ? (x[i] * a.c) / Lsum : 0.0f;
         if (a.out_f32)
           reinterpret_cast<float*>(a.out)[o_idx + i] = v;
         else
           reinterpret_cast<uint16_t*>(a.out)[o_idx + i] = f32_to_bf16(v);
       }
     } else {
+      const int64_t pbase =
+          ((int64_t)seq * a.max_splits + split) * a.n_q_heads + (int64_t)kvh * G;
       float* dst = a.part_o + (pbase + hh) * D + lane * E;
       if constexpr (E % 4 == 0) {
 #pragma unroll
@@ -368,8 +500,8 @@ void decode_attn_kernel(AttnArgs a) {
         for (int i = 0; i < E; i++) dst[i] = x[i] * a.c;
       }
       if (lane == 0) {
-        a.part_ml[(pbase + hh) * 2 + 0] = ml_s[hh][0];
-        a.part_ml[(pbase + hh) * 2 + 1] = ml_s[hh][1];
+        a.part_ml[(pbase + hh) * 2 + 0] = M;
+        a.part_ml[(pbase + hh) * 2 + 1] = Lsum;
       }
     }
   }
@@ -443,25 +575,23 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
 
 // One work-group per (KV head, sequence).
 template <int D, int BITS>
-__global__ __launch_bounds__((D / kAttnDW) * 64) void qprep_kernel(QPrepArgs a) {
+__global__ __launch_bounds__(kQPrepThreads) void qprep_kernel(QPrepArgs a) {
   qprep_workgroup<D, BITS>(a, (int)gridDim.x, blockIdx.x, blockIdx.y, threadIdx.x);
 }
 
 template <int D, int BITS>
 hipError_t launch_qprep_t(const QPrepArgs& a, int n_kv_heads, int n_seqs, hipStream_t s) {
-  hipLaunchKernelGGL((qprep_kernel<D, BITS>), dim3(n_kv_heads, n_seqs), dim3((D / kAttnDW) * 64),
-                     0, s, a);
+  hipLaunchKernelGGL((qprep_kernel<D, BITS>), dim3(n_kv_heads, n_seqs), dim3(kQPrepThreads), 0, s,
+                     a);
   return hipGetLastError();
 }
 
 template <int D, int BITS>
 hipError_t launch_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                     hipEvent_t ev0, hipEvent_t ev1) {
-  constexpr int DW = kAttnDW;
-  constexpr int NT = (D / DW) * 64;
   dim3 grid(a.max_splits, n_kv_heads, n_seqs);
   if (ev0) (void)hipEventRecord(ev0, s);
-  hipLaunchKernelGGL((decode_attn_kernel<D, BITS, DW, kAttnDepth>), grid, dim3(NT), 0, s, a);
+  hipLaunchKernelGGL((decode_attn_kernel<D, BITS>), grid, dim3(kAttnWaves * 64), 0, s, a);
   hipError_t e = hipGetLastError();
   if (ev1) (void)hipEventRecord(ev1, s);
   if (e != hipSuccess || a.direct) return e;

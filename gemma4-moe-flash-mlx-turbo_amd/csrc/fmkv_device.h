@@ -72,6 +72,29 @@ __device__ inline half2_t u4x2_to_h2(uint32_t w, int k) {
   return __builtin_bit_cast(half2_t, x) - (half2_t){(_Float16)1024.0f, (_Float16)1024.0f};
 }
 
+// RHT sign bits of this lane's E = D/64 dims (bit i = dim lane * E + i)
+// from the argument words (bit d of the mask = sign of dim d is -1): the
+// words are written into lanes 0..D/32-1 of one register and each lane
+// fetches its word with a bpermute. (A select chain over the words would be
+// turned into a vector load of the argument segment, and kernels that track
+// their own vector-memory counts must not get one.)
+template <int D>
+__device__ inline uint32_t lane_sign_bits(const uint32_t (&bits)[16], int lane) {
+  constexpr int E = D / 64;
+  int words = 0;
+#pragma unroll
+  for (int k = 0; k < D / 32; k++)
+    asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(words) : "s"(bits[k]), "n"(k));
+  const uint32_t word = (uint32_t)__builtin_amdgcn_ds_bpermute(((lane * E) >> 5) * 4, words);
+  return (word >> ((lane * E) & 31)) & ((1u << E) - 1u);
+}
+
+// x * s with s = -1 where bit i is set, else +1: a sign flip, bit-identical
+// to the multiplication.
+__device__ inline float apply_sign(float x, uint32_t bits, int i) {
+  return __uint_as_float(__float_as_uint(x) ^ (((bits >> i) & 1u) << 31));
+}
+
 // Two f32 -> packed f16, round toward zero (v_cvt_pkrtz_f16_f32).
 __device__ inline half2_t pkrtz(float a, float b) {
   return __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(a, b));

@@ -19,24 +19,20 @@ struct Store {
   BlockLayout layout;
 };
 
-// Decode split-K plan shared by the host and the kernels: head dims per wave,
-// blocks in flight per wave (register sets of the load pipeline) and
-// work-groups per CU the split count aims at.
-#ifndef FMKV_ATTN_DEPTH
-#define FMKV_ATTN_DEPTH 2
-#endif
-#ifndef FMKV_ATTN_WG_PER_CU
-#define FMKV_ATTN_WG_PER_CU 2
-#endif
-constexpr int kAttnDW = 128;
-constexpr int kAttnDepth = FMKV_ATTN_DEPTH;
-constexpr int kAttnWgPerCu = FMKV_ATTN_WG_PER_CU;
+// Decode split-K plan shared by the host and the kernels: wave pairs per
+// work-group (each pair streams whole head-blocks, one half of head_dim per
+// wave) and work-groups per CU the split count aims at (one: a work-group's
+// LDS staging fills the CU).
+constexpr int kAttnPairs = 4;
+constexpr int kAttnWaves = 2 * kAttnPairs;
 
-// 16-byte vectors per lane of the q-prep table (two groups x two MFMA B
-// operands, plus the group sums and sign bits).
-constexpr int kQPrepVecs = 5;
+// q preparation (fmkv_qprep.h): per (sequence, KV head) a table of the
+// decode kernel's MFMA B operands and group sums, (2 D/64 + 1) KiB.
+constexpr int kQPrepThreads = 256;
+__host__ __device__ constexpr int64_t qprep_bytes(int head_dim) {
+  return (2 * (head_dim / 64) + 1) * 1024;
+}
 
-// Rotated q for the decode kernel (layout in fmkv_qprep.h).
 struct QPrepArgs {
   const uint16_t* q;   // bf16 [n_seqs][n_q_heads][D]
   int32_t n_q_heads;
@@ -44,12 +40,12 @@ struct QPrepArgs {
   float qscale;        // softmax scale * log2(e)
   float c;             // 1/sqrt(D)
   uint32_t sign_bits[16];  // RHT signs of dims 0..D-1, bit d set = -1
-  uint32_t* out;       // table, [n_seqs][n_kv_heads][D/128][64][kQPrepVecs x 4]
+  uint8_t* out;        // tables, [n_seqs][n_kv_heads][qprep_bytes(D)]
 };
-
-__host__ __device__ constexpr int64_t qprep_words(int64_t n_seqs, int n_kv_heads, int head_dim) {
-  return n_seqs * n_kv_heads * (head_dim / kAttnDW) * 64 * kQPrepVecs * 4;
-}
+#ifndef FMKV_ATTN_WG_PER_CU
+#define FMKV_ATTN_WG_PER_CU 1
+#endif
+constexpr int kAttnWgPerCu = FMKV_ATTN_WG_PER_CU;
 
 struct AppendArgs {
   Store st;
@@ -74,7 +70,8 @@ struct AttnArgs {
   int64_t vis_begin;
   int32_t group;      // q heads per kv head
   int32_t n_q_heads;
-  const uint32_t* qprep;  // q-prep table of this call
+  const uint8_t* qprep;    // q-prep tables of this call
+  uint32_t sign_bits[16];  // RHT signs of dims 0..D-1, bit d set = -1
   float c;
   int32_t bps;        // blocks per split
   int32_t max_splits;
@@ -106,9 +103,9 @@ struct FetchArgs {
 };
 
 // With a.qp.out set the launch carries one more column of work-groups that
-// fill the q-prep table (n_seqs x n_kv_heads rows); max_tasks may then be 0.
+// fill the q-prep tables (n_seqs x n_kv_heads); max_tasks may then be 0.
 hipError_t launch_append(const AppendArgs& a, int n_seqs, int max_tasks, hipStream_t s);
-// The q-prep table on its own (attention without a fused append).
+// The q-prep tables on their own (attention without a fused append).
 hipError_t launch_qprep(const QPrepArgs& a, int head_dim, int bits, int n_kv_heads, int n_seqs,
                         hipStream_t s);
 // ev_begin / ev_end (optional) are recorded around the split-K kernel only.
