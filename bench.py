@@ -31,6 +31,12 @@ PKG = ROOT / "gemma4-moe-flash-mlx-turbo_amd"
 sys.path.insert(0, str(PKG))
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per decode_attn_kernel launch at this workload, from rocprofv3
+# FETCH_SIZE / WRITE_SIZE passes scaled by a plain copy's readings
+# (profiles/decode_attn_c3_hbm_traffic.md holds the runs and the commands);
+# counters cannot be read inside the timed run itself.
+TRAFFIC_BYTES_PER_LAUNCH = 75_860_000
+TRAFFIC_SOURCE = "profiles/decode_attn_c3_hbm_traffic.md"
 
 
 def log(msg: str) -> None:
@@ -170,8 +176,9 @@ def run_c3(args) -> dict:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "decode_attn_kernel<512,8,128>",
+            "traffic": TRAFFIC_BYTES_PER_LAUNCH,
+            "traffic_source": TRAFFIC_SOURCE,
+            "kernel": "decode_attn_kernel<512, 8>",
             "avg_kernel_us": round(kern_s * 1e6, 3),
             "bytes_per_launch": int(launch_bytes),
         },
@@ -214,6 +221,29 @@ def cpu_baseline_c3(args, k_bf16, v_bf16, Hq, Hkv, D, per_tok) -> dict:
     }
 
 
+def copy_calibration(mib: int) -> int:
+    """A plain copy of known size: its FETCH_SIZE / WRITE_SIZE readings per
+    dispatch against the bytes it moves give the factor that turns the same
+    counters on the decode kernel into HBM bytes."""
+    import torch
+
+    n = mib * (1 << 20)
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    ev0.record()
+    for _ in range(8):
+        dst.copy_(src)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / 8
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "ms_per_copy": round(ms, 4),
+                      "GB/s (read+write)": round(2 * n / ms / 1e6, 1)}), flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -225,6 +255,9 @@ def main(argv=None) -> int:
     ap.add_argument("--bps", type=int, default=0, help="blocks per split-K work-group (0: auto)")
     ap.add_argument("--unfused", action="store_true",
                     help="time fmkv_cache_append + fmkv_decode_attention instead of fmkv_decode_step")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 8 device-to-device copies of MIB MiB (the reference kernel "
+                         "for scaling HBM byte counters) and exit")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the KV path is "
@@ -235,6 +268,8 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
     if args.bps:
         import fmkv
 
