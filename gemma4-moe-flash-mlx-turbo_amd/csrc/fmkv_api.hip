@@ -108,10 +108,12 @@ int device_cus() {
 
 // Split-K plan: blocks per split such that the grid has about `wg_per_cu`
 // work-groups per CU (each keeps several blocks in flight, so one per CU
-// already saturates HBM; more would only add split partials).
-int32_t choose_bps(int64_t total_head_blocks, int cus, int wg_per_cu) {
+// already saturates HBM; more would only add split partials), `reserved` of
+// them going to other work of the same launch (the new-token column).
+int32_t choose_bps(int64_t total_head_blocks, int cus, int wg_per_cu, int64_t reserved = 0) {
   if (g_bps_override > 0) return g_bps_override;
-  const int64_t target = (int64_t)wg_per_cu * cus;
+  int64_t target = (int64_t)wg_per_cu * cus;
+  if (target - reserved >= target / 2) target -= reserved;
   int64_t bps = (total_head_blocks + target - 1) / target;
   if (bps < 1) bps = 1;
   return (int32_t)bps;
@@ -259,7 +261,6 @@ int prepare_append(const fmkv_cache* c, const void* k, const void* v, int64_t n,
   a->c = c->c;
   a->sqrt_d = c->sqrt_d;
   a->cb_bits = c->desc.bits;
-  a->qp.out = nullptr;
   if (W > 0) {
     const int64_t n_eff = n < W ? n : W;
     *tasks = (n_eff + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens + 1;
@@ -270,51 +271,42 @@ int prepare_append(const fmkv_cache* c, const void* k, const void* v, int64_t n,
   return FMKV_OK;
 }
 
-// Split-K plan, workspace ([part_o | part_ml | q-prep tables]) and launch
-// arguments of decode attention; qp receives the q-prep arguments (launched
-// alone, or inside the append of a decode step).
+// Split-K plan, workspace ([part_o | part_ml]) and launch arguments of
+// decode attention; new_col adds the decode step's new-token column.
 template <typename Owner>
 int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, int64_t nblk,
                              const void* q, int32_t n_q_heads, float scale, float tau, void* out,
-                             int32_t out_dtype, int wg_per_cu, fmkv::AttnArgs* a,
-                             fmkv::QPrepArgs* qp) {
+                             int32_t out_dtype, int wg_per_cu, int new_col, fmkv::AttnArgs* a) {
   int rc = check_attn_args(o->desc, q, n_q_heads, tau, out, out_dtype);
   if (rc) return rc;
   const int H = o->desc.n_kv_heads, D = o->desc.head_dim;
   a->st = st;
   a->group = n_q_heads / H;
   a->n_q_heads = n_q_heads;
+  a->q = static_cast<const uint16_t*>(q);
+  a->qscale = scale * 1.4426950408889634f;
   std::memcpy(a->sign_bits, o->sign_bits, sizeof(a->sign_bits));
   a->c = o->c;
   if (nblk < 1) nblk = 1;
-  a->bps = choose_bps(nblk * H * n_seqs, o->cus, wg_per_cu);
+  a->bps = choose_bps(nblk * H * n_seqs, o->cus, wg_per_cu, (int64_t)new_col * H * n_seqs);
   a->max_splits = (int32_t)((nblk + a->bps - 1) / a->bps);
-  a->direct = a->max_splits == 1;
+  a->new_col = new_col;
+  a->part_stride = a->max_splits + new_col;
+  a->direct = a->max_splits == 1 && !new_col;
+  a->k_new = a->v_new = nullptr;
   a->out = out;
   a->out_f32 = out_dtype == FMKV_DTYPE_F32;
-  const size_t n_rows = a->direct ? 0 : (size_t)n_seqs * a->max_splits * n_q_heads;
-  const size_t tab_off = (n_rows * (D + 2) * sizeof(float) + 255) / 256 * 256;
-  const size_t tab_bytes = (size_t)n_seqs * H * fmkv::qprep_bytes(D);
-  rc = o->ws.ensure(tab_off + tab_bytes);
+  const size_t n_rows = a->direct ? 0 : (size_t)n_seqs * a->part_stride * n_q_heads;
+  rc = o->ws.ensure(n_rows * (D + 2) * sizeof(float));
   if (rc) return rc;
   a->part_o = n_rows ? o->ws.ptr : nullptr;
   a->part_ml = n_rows ? o->ws.ptr + n_rows * D : nullptr;
-  uint8_t* tab = reinterpret_cast<uint8_t*>(o->ws.ptr) + tab_off;
-  a->qprep = tab;
-  qp->q = static_cast<const uint16_t*>(q);
-  qp->n_q_heads = n_q_heads;
-  qp->group = n_q_heads / H;
-  qp->qscale = scale * 1.4426950408889634f;
-  qp->c = o->c;
-  std::memcpy(qp->sign_bits, o->sign_bits, sizeof(qp->sign_bits));
-  qp->out = tab;
   return FMKV_OK;
 }
 
 // Decode attention over the first T positions of a cache.
 int prepare_attention(fmkv_cache* c, int64_t T, const void* q, int32_t n_q_heads, float scale,
-                      float tau, void* out, int32_t out_dtype, fmkv::AttnArgs* a,
-                      fmkv::QPrepArgs* qp) {
+                      float tau, void* out, int32_t out_dtype, int new_col, fmkv::AttnArgs* a) {
   const int64_t W = c->desc.window;
   a->seq_lens = nullptr;
   a->seq_len = T;
@@ -325,7 +317,7 @@ int prepare_attention(fmkv_cache* c, int64_t T, const void* q, int32_t n_q_heads
   const int64_t nblk =
       (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
   return prepare_attention_common(c, cache_store(c), 1, nblk, q, n_q_heads, scale, tau, out,
-                                  out_dtype, fmkv::kAttnWgPerCu, a, qp);
+                                  out_dtype, fmkv::kAttnWgPerCu, new_col, a);
 }
 
 int prepare_paged_append(const fmkv_pool* p, const void* k, const void* v,
@@ -349,16 +341,14 @@ int prepare_paged_append(const fmkv_pool* p, const void* k, const void* v,
   a->c = p->c;
   a->sqrt_d = p->sqrt_d;
   a->cb_bits = p->desc.bits;
-  a->qp.out = nullptr;
-  *tasks = (n_new + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens + 1;
+  *tasks =(n_new + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens + 1;
   return FMKV_OK;
 }
 
 int prepare_paged_attention(fmkv_pool* p, const void* q, const int32_t* block_tables,
                             int32_t max_blocks, const int32_t* seq_lens, int32_t n_seqs,
                             int32_t max_seq_len, int32_t n_q_heads, float scale, float tau,
-                            void* out, int32_t out_dtype, fmkv::AttnArgs* a,
-                            fmkv::QPrepArgs* qp) {
+                            void* out, int32_t out_dtype, int new_col, fmkv::AttnArgs* a) {
   if (n_seqs < 0 || max_seq_len < 0 || max_blocks < 1)
     return fail(FMKV_ERR_INVALID_ARG, "bad n_seqs / max_seq_len / max_blocks");
   if (n_seqs > 0 && (!block_tables || !seq_lens))
@@ -375,7 +365,7 @@ int prepare_paged_attention(fmkv_pool* p, const void* q, const int32_t* block_ta
   // more work-groups than for one sequence
   return prepare_attention_common(p, pool_store(p, block_tables, max_blocks),
                                   n_seqs > 0 ? n_seqs : 1, nblk, q, n_q_heads, scale, tau, out,
-                                  out_dtype, 4 * fmkv::kAttnWgPerCu, a, qp);
+                                  out_dtype, 4 * fmkv::kAttnWgPerCu, new_col, a);
 }
 
 }  // namespace
@@ -476,17 +466,26 @@ int fmkv_decode_step(fmkv_cache* c, const void* k, const void* v, int64_t n, con
   int64_t tasks = 0;
   int rc = prepare_append(c, k, v, n, &ap, &tasks);
   if (rc) return rc;
+  // one new token: the attention launch appends it itself (new-token column)
+  const int fused = n == 1 ? 1 : 0;
   fmkv::AttnArgs at;
-  rc = prepare_attention(c, c->offset + n, q, n_q_heads, scale, tau, out, out_dtype, &at, &ap.qp);
+  rc = prepare_attention(c, c->offset + n, q, n_q_heads, scale, tau, out, out_dtype, fused, &at);
   if (rc) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = fmkv::launch_append(ap, 1, (int)tasks, s);
-  if (e != hipSuccess) return hip_fail(e, "append launch");
-  c->offset += n;
+  hipError_t e;
+  if (fused) {
+    at.k_new = ap.k;
+    at.v_new = ap.v;
+  } else {
+    e = fmkv::launch_append(ap, 1, (int)tasks, s);
+    if (e != hipSuccess) return hip_fail(e, "append launch");
+    c->offset += n;
+  }
   hipEvent_t e0, e1;
   next_events(&e0, &e1);
   e = fmkv::launch_decode_attention(at, 1, c->desc.n_kv_heads, s, e0, e1);
   if (e != hipSuccess) return hip_fail(e, "decode attention launch");
+  if (fused) c->offset += n;
   return FMKV_OK;
 }
 
@@ -502,15 +501,12 @@ int fmkv_decode_attention(fmkv_cache* c, const void* q, int32_t n_q_heads, float
                           void* out, int32_t out_dtype, void* stream) {
   if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
   fmkv::AttnArgs a;
-  fmkv::QPrepArgs qp;
-  int rc = prepare_attention(c, c->offset, q, n_q_heads, scale, tau, out, out_dtype, &a, &qp);
+  int rc = prepare_attention(c, c->offset, q, n_q_heads, scale, tau, out, out_dtype, 0, &a);
   if (rc) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = fmkv::launch_qprep(qp, c->desc.head_dim, c->desc.bits, c->desc.n_kv_heads, 1, s);
-  if (e != hipSuccess) return hip_fail(e, "q preparation launch");
   hipEvent_t e0, e1;
   next_events(&e0, &e1);
-  e = fmkv::launch_decode_attention(a, 1, c->desc.n_kv_heads, s, e0, e1);
+  hipError_t e = fmkv::launch_decode_attention(a, 1, c->desc.n_kv_heads, s, e0, e1);
   if (e != hipSuccess) return hip_fail(e, "decode attention launch");
   return FMKV_OK;
 }
@@ -632,17 +628,13 @@ int fmkv_paged_decode_attention(fmkv_pool* p, const void* q, const int32_t* bloc
                                 void* out, int32_t out_dtype, void* stream) {
   if (!p) return fail(FMKV_ERR_INVALID_ARG, "pool is null");
   fmkv::AttnArgs a;
-  fmkv::QPrepArgs qp;
   int rc = prepare_paged_attention(p, q, block_tables, max_blocks, seq_lens, n_seqs, max_seq_len,
-                                   n_q_heads, scale, tau, out, out_dtype, &a, &qp);
+                                   n_q_heads, scale, tau, out, out_dtype, 0, &a);
   if (rc || n_seqs == 0) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e =
-      fmkv::launch_qprep(qp, p->desc.head_dim, p->desc.bits, p->desc.n_kv_heads, n_seqs, s);
-  if (e != hipSuccess) return hip_fail(e, "q preparation launch");
   hipEvent_t e0, e1;
   next_events(&e0, &e1);
-  e = fmkv::launch_decode_attention(a, n_seqs, p->desc.n_kv_heads, s, e0, e1);
+  hipError_t e = fmkv::launch_decode_attention(a, n_seqs, p->desc.n_kv_heads, s, e0, e1);
   if (e != hipSuccess) return hip_fail(e, "paged decode attention launch");
   return FMKV_OK;
 }
@@ -659,13 +651,22 @@ int fmkv_paged_decode_step(fmkv_pool* p, const void* k, const void* v,
   int rc = prepare_paged_append(p, k, v, block_tables, max_blocks, start_pos, n_seqs, n_new, &ap,
                                 &tasks);
   if (rc) return rc;
+  // one new token per sequence: the attention launch appends it itself, at
+  // position seq_lens[s] - 1 (= start_pos[s])
+  const int fused = n_new == 1 ? 1 : 0;
   fmkv::AttnArgs at;
   rc = prepare_paged_attention(p, q, block_tables, max_blocks, seq_lens, n_seqs, max_seq_len,
-                               n_q_heads, scale, tau, out, out_dtype, &at, &ap.qp);
+                               n_q_heads, scale, tau, out, out_dtype, fused, &at);
   if (rc || n_seqs == 0) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = fmkv::launch_append(ap, n_seqs, tasks, s);
-  if (e != hipSuccess) return hip_fail(e, "paged append launch");
+  hipError_t e;
+  if (fused) {
+    at.k_new = ap.k;
+    at.v_new = ap.v;
+  } else {
+    e = fmkv::launch_append(ap, n_seqs, tasks, s);
+    if (e != hipSuccess) return hip_fail(e, "paged append launch");
+  }
   hipEvent_t e0, e1;
   next_events(&e0, &e1);
   e = fmkv::launch_decode_attention(at, n_seqs, p->desc.n_kv_heads, s, e0, e1);

@@ -14,7 +14,7 @@
 // with -ffp-contract=off, so codes and scales are bit-identical to it.
 #include "fmkv_device.h"
 #include "fmkv_internal.h"
-#include "fmkv_qprep.h"
+#include "fmkv_quant.h"
 
 namespace fmkv {
 namespace {
@@ -26,40 +26,6 @@ __constant__ float kCbBounds3[7] = {-1.748f, -1.050f, -0.501f, 0.0f, 0.501f, 1.0
 __constant__ float kCbBounds4[15] = {-2.401f, -1.844f, -1.437f, -1.099f, -0.800f,
                                      -0.522f, -0.258f, 0.0f,    0.258f,  0.522f,
                                      0.800f,  1.099f,  1.437f,  1.844f,  2.401f};
-
-// MLX affine_quantize for the group spanning 64/E lanes (see oracle).
-template <int E, int BITS>
-__device__ inline void affine_quant(const float (&y)[E], uint32_t (&code)[E], float& scale_o,
-                                    float& bias_o, int lane) {
-  constexpr int kLanesPerGroup = 64 / E;
-  float mx = y[0], mn = y[0];
-#pragma unroll
-  for (int i = 1; i < E; i++) {
-    mx = fmaxf(mx, y[i]);
-    mn = fminf(mn, y[i]);
-  }
-  mx = group_max<kLanesPerGroup>(mx, lane);
-  mn = group_min<kLanesPerGroup>(mn, lane);
-  const float n_bins = (float)((1 << BITS) - 1);
-  float scale = fmaxf((mx - mn) / n_bins, 1e-7f);
-  const bool side = fabsf(mn) > fabsf(mx);
-  scale = side ? scale : -scale;
-  const float edge = side ? mn : mx;
-  const float q0 = rintf(edge / scale);
-  float bias = 0.0f;
-  if (q0 != 0.0f) {
-    scale = edge / q0;
-    bias = edge;
-  }
-#pragma unroll
-  for (int i = 0; i < E; i++) {
-    float q = rintf((y[i] - bias) / scale);
-    q = fminf(fmaxf(q, 0.0f), n_bins);
-    code[i] = (uint32_t)q;
-  }
-  scale_o = scale;
-  bias_o = bias;
-}
 
 // Sum of squares in the oracle's order: per-lane left to right, then a
 // xor-butterfly over all 64 lanes.
@@ -120,15 +86,6 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = blockIdx.y, seq = blockIdx.z, bx = blockIdx.x;
-  if constexpr (MODE == kAffine) {
-    // decode step: the last column of work-groups prepares q for the
-    // attention launch that follows, in the shadow of the append's loads
-    if (a.qp.out && bx == (int)gridDim.x - 1) {
-      static_assert(kAppendThreads == kQPrepThreads, "q-prep work-group size");
-      qprep_workgroup<D, BITS>(a.qp, a.st.n_kv_heads, h, seq, tid);
-      return;
-    }
-  }
   const int64_t pos0 = a.start_pos ? (int64_t)a.start_pos[seq] : a.start_scalar;
   const int64_t end = pos0 + a.n_new;
   const int64_t W = a.window;
@@ -277,8 +234,7 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
 
 template <int D, int BITS, int MODE>
 hipError_t launch_t(const AppendArgs& a, int n_seqs, int max_tasks, hipStream_t s) {
-  const int qcol = (MODE == kAffine && a.qp.out) ? 1 : 0;
-  dim3 grid(max_tasks + qcol, a.st.n_kv_heads, n_seqs);
+  dim3 grid(max_tasks, a.st.n_kv_heads, n_seqs);
   hipLaunchKernelGGL((append_kernel<D, BITS, MODE>), grid, dim3(kAppendThreads), 0, s, a);
   return hipGetLastError();
 }
@@ -288,9 +244,7 @@ hipError_t launch_t(const AppendArgs& a, int n_seqs, int max_tasks, hipStream_t 
 hipError_t launch_append(const AppendArgs& a, int n_seqs, int max_tasks, hipStream_t s) {
   const BlockLayout& L = a.st.layout;
   if (n_seqs <= 0) return hipSuccess;
-  if (max_tasks <= 0 && !a.qp.out) return hipSuccess;
-  if (a.qp.out && L.mode != kAffine) return hipErrorInvalidValue;
-  if (max_tasks < 0) max_tasks = 0;
+  if (max_tasks <= 0) return hipSuccess;
   if (L.mode == kAffine) {
     switch (L.head_dim * 16 + L.bits) {
       case 128 * 16 + 4: return launch_t<128, 4, kAffine>(a, n_seqs, max_tasks, s);

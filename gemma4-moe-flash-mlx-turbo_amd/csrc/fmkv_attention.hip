@@ -18,8 +18,9 @@
 // neither tracks them nor inserts waits of its own on LDS reads; every stage
 // read is preceded by the vmcnt wait covering it, computed from the number
 // of copies issued after that stage. The compiler issues no vector-memory
-// loads of its own in this kernel (the one candidate, the sign-bit lookup,
-// is written so that it cannot become one).
+// loads of its own in the split columns (the one candidate, the sign-bit
+// lookup, is written so that it cannot become one); only the new-token
+// column, which tracks no copies, loads through the compiler.
 //
 // Per block (16 tokens), per 64-dim group g of the wave's half:
 //   QK^T  S^T[16 tok x 16 col] += K[16 x 32] . Q^T[32 x 16] on MFMA
@@ -38,15 +39,21 @@
 // in the accumulator is cheaper but inflates the fp32 partial sums ~64x at 4
 // bits, which outlier channels turn into visible error.)
 //
-// q_rot = (FWHT(q * scale * log2 e) * c) o s arrives as a table of MFMA B
-// operands (fmkv_qprep.h), written once per step by the append launch of a
-// decode step or by qprep_kernel, and copied to LDS ahead of the first
-// blocks. Epilogue: the pairs' results merge in LDS, the inverse rotation
+// q_rot = (FWHT(q * scale * log2 e) * c) o s is computed by every work-group
+// in its prologue, while its first blocks are in flight: the raw q rows are
+// copied to LDS ahead of the blocks and turned into a table of MFMA B
+// operands. Epilogue: the pairs' results merge in LDS, the inverse rotation
 // o . R^T = c * FWHT(o o s) follows, and the result is the final output (one
 // split) or a split partial for combine_kernel.
+//
+// Decode step (a.new_col): the grid has one more column whose work-groups
+// append the step's new token (rotate, quantize, slot write -- the append
+// kernel's arithmetic) and contribute its attention as one more partial; the
+// split columns leave the new token's slot out. A decode step is then this
+// launch and the combine.
 #include "fmkv_device.h"
 #include "fmkv_internal.h"
-#include "fmkv_qprep.h"
+#include "fmkv_quant.h"
 
 namespace fmkv {
 namespace {
@@ -80,11 +87,14 @@ struct AttnPlan {
   static constexpr int kStagesA = kFit < 2 ? 2 : (kFit > 8 ? 8 : kFit);
   static constexpr int kStages = kStagesA * kCopies <= 63 ? kStagesA : 63 / kCopies;
   static constexpr int kQS = D + 4;  // padded row stride (LDS banks)
-  static constexpr int kMergeBytes = kAttnPairs * 8 * kQS * 4;
-  static constexpr int kStageRegion = cmax(kAttnPairs * kStages * kStageBytes, kMergeBytes);
-  // prologue: the q-prep table; loop: the score exchange
+  // a pair's merge rows [8 heads][kQS] floats reuse its own stages
+  static constexpr int kStageRegion = kAttnPairs * kStages * kStageBytes;
+  static_assert(8 * kQS * 4 <= kStages * kStageBytes, "merge rows fit in a pair's stages");
+  // prologue: the raw q rows, then the q table (B operands + group sums);
+  // loop: the score exchange
+  static constexpr int kTabBytes = 2 * NG * kChunk + 8 * NG * 4;
   static constexpr int kXBytes = kAttnWaves * 2 * 64 * 16;
-  static constexpr int kScratch = cmax((int)qprep_bytes(D), kXBytes);
+  static constexpr int kScratch = cmax(cmax(kTabBytes, kXBytes), 8 * D * 2);
   static_assert(NG % 2 == 0 && kCodeChunks >= 1, "layout");
   static_assert(kStages * kCopies <= 63, "vmcnt immediates");
   static_assert(8 * GH <= 64, "one partial instruction copies a wave's scale/bias");
@@ -165,6 +175,258 @@ __device__ inline half4_t v_operand(const u32x4 w, int g, int ct) {
 __device__ inline float lo16(uint32_t w) { return f16_bits_to_f32(w); }
 __device__ inline float hi16(uint32_t w) { return f16_bits_to_f32(w >> 16); }
 
+// Dim of head_dim fed to lane k-group j, element i, of the QK MFMA s (0/1)
+// of group g is g*64 + j*16 + s*8 + i (8-bit) or g*64 + s*32 + j*8 + i
+// (4-bit), matching the K-code placement of fmkv_layout.h. For the E = D/64
+// consecutive dims of lane l (d0 = l*E) this gives the entry and position
+// they occupy: (g, s, j) and the first element i0.
+template <int E, int BITS>
+struct QSlot {
+  int g, s, j, i0;
+  __device__ explicit QSlot(int lane) {
+    const int d0 = lane * E, o = d0 & 63;
+    g = d0 >> 6;
+    s = BITS == 8 ? (o >> 3) & 1 : o >> 5;
+    j = BITS == 8 ? o >> 4 : (o >> 3) & 3;
+    i0 = o & 7;
+  }
+};
+
+template <int E>
+__device__ inline void store_halves(uint8_t* p, const _Float16 (&h)[E]) {
+  if constexpr (E == 8)
+    *reinterpret_cast<half8_t*>(p) = (half8_t){h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]};
+  else if constexpr (E == 4)
+    *reinterpret_cast<half4_t*>(p) = (half4_t){h[0], h[1], h[2], h[3]};
+  else
+    *reinterpret_cast<half2_t*>(p) = (half2_t){h[0], h[1]};
+}
+
+// Raw bf16 q row of GQA head `wave` of (seq, kvh) (D * 2 bytes) to LDS at
+// dst + wave * D * 2, copied by that wave itself (lanes < D / 8).
+template <int D>
+__device__ inline void copy_q_row(const AttnArgs& a, uint8_t* dst, int seq, int kvh, int wave,
+                                  int lane) {
+  if (wave < a.group && lane < D / 8) {
+    const uint16_t* qh =
+        a.q + ((int64_t)seq * a.n_q_heads + (int64_t)kvh * a.group + wave) * D;
+    dma16(lds_addr(dst + wave * D * 2), lane * 16, buffer_rsrc(qh, (uint32_t)(D * 2)));
+  }
+}
+
+// q_rot = (FWHT(q * qscale) * c) o s of the work-group's GQA heads (q . R,
+// R from src/cache.rs:47-62, times the softmax scale in base 2), from the
+// raw rows at the start of `tab` (each wave's own row has landed: the
+// caller waited for its copy), written over them as the QK B operands:
+//   entry e = 2 g + s at e KiB + 16 lane, lane (j, c) = (lane / 16,
+//     lane % 16): 8 f16 of head c & 7 -- the f16 high part of q_rot for
+//     c < 8, the residual for c >= 8, zero past the group;
+//   float qsum[8][NG] after the 2 NG entries: per head and group, sum q_rot.
+// Wave w computes head w before the first barrier, so the rotation overlaps
+// the other waves' copy issue. Every thread of the work-group calls it (it
+// holds two barriers).
+template <int D, int BITS>
+__device__ void build_q_table(const AttnArgs& a, uint8_t* tab, int wave, int lane) {
+  constexpr int E = D / 64, NG = D / 64, LPG = 64 / E;
+  const bool hv = wave < a.group;
+  float x[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) x[i] = 0.0f;
+  if (hv) {
+    const uint32_t* raw = reinterpret_cast<const uint32_t*>(tab + (wave * D + lane * E) * 2);
+#pragma unroll
+    for (int k = 0; k < E / 2; k++) {
+      const uint32_t w = raw[k];
+      x[2 * k] = __uint_as_float(w << 16) * a.qscale;
+      x[2 * k + 1] = __uint_as_float(w & 0xffff0000u) * a.qscale;
+    }
+  }
+  const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
+  float gsum = 0.0f;
+  if (hv) {
+    wave_fwht<E>(x, lane);
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      x[i] = apply_sign(x[i] * a.c, sbits, i);
+      gsum += x[i];
+    }
+  }
+  gsum = group_sum<LPG>(gsum, lane);
+  const QSlot<E, BITS> qs(lane);
+  _Float16 hi[E], lo[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) {
+    hi[i] = (_Float16)x[i];
+    lo[i] = (_Float16)(x[i] - (float)hi[i]);
+  }
+  __syncthreads();  // every raw row is read before the table replaces them
+  uint8_t* ent = tab + (2 * qs.g + qs.s) * kChunk + qs.i0 * 2;
+  store_halves<E>(ent + (qs.j * 16 + wave) * 16, hi);
+  store_halves<E>(ent + (qs.j * 16 + wave + 8) * 16, lo);
+  if ((lane & (LPG - 1)) == 0)
+    reinterpret_cast<float*>(tab + 2 * NG * kChunk)[wave * NG + qs.g] = gsum;
+  __syncthreads();
+}
+
+// Codes of token t, dims d0 .. d0+E-1, into a head-block's K region. A
+// token's K bytes are its own (lane slot (j, t) of each chunk), so whole
+// words are written; at 4 bits the 8/E lanes sharing a word OR theirs first.
+template <int BITS, int E>
+__device__ inline void store_k_codes(uint8_t* kbase, int t, int d0, const uint32_t (&code)[E],
+                                     int lane) {
+  if constexpr (BITS == 8) {
+    int64_t off;
+    int sh;
+    k_code_pos(8, t, d0, &off, &sh);
+    uint8_t* p = kbase + off + sh / 8;  // E consecutive bytes
+    uint32_t w[E / 4 > 0 ? E / 4 : 1];
+    if constexpr (E >= 4) {
+#pragma unroll
+      for (int k = 0; k < E / 4; k++)
+        w[k] = code[4 * k] | (code[4 * k + 1] << 8) | (code[4 * k + 2] << 16) | (code[4 * k + 3] << 24);
+    }
+    if constexpr (E == 8)
+      *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+    else if constexpr (E == 4)
+      *reinterpret_cast<uint32_t*>(p) = w[0];
+    else
+      *reinterpret_cast<uint16_t*>(p) = (uint16_t)(code[0] | (code[1] << 8));
+  } else {
+    int64_t off = 0;
+    uint32_t w = 0;
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      int sh;
+      k_code_pos(4, t, d0 + i, &off, &sh);  // the same word for the E dims
+      w |= code[i] << sh;
+    }
+    constexpr int N = 8 / E;  // lanes sharing the word
+#pragma unroll
+    for (int m = 1; m < N; m <<= 1) w |= (uint32_t)__shfl_xor((int)w, m);
+    if ((lane & (N - 1)) == 0) *reinterpret_cast<uint32_t*>(kbase + off) = w;
+  }
+}
+
+// Codes of token t into a head-block's V region, where each 32-bit word
+// holds codes of four tokens: byte stores at 8 bits; at 4 bits the token's
+// nibble is cleared and set with atomics, leaving the other tokens' nibbles
+// untouched at every moment (the split columns may be reading the block).
+template <int BITS, int E>
+__device__ inline void store_v_codes(uint8_t* vbase, int t, int d0, const uint32_t (&code)[E]) {
+#pragma unroll
+  for (int i = 0; i < E; i++) {
+    int64_t off;
+    int sh;
+    v_code_pos(BITS, t, d0 + i, &off, &sh);
+    if constexpr (BITS == 8) {
+      vbase[off + sh / 8] = (uint8_t)code[i];
+    } else {
+      uint32_t* w = reinterpret_cast<uint32_t*>(vbase + off);
+      atomicAnd(w, ~(0xfu << sh));
+      atomicOr(w, code[i] << sh);
+    }
+  }
+}
+
+// The new-token column of a decode step, one work-group per (seq, kvh): the
+// token at position T - 1 is rotated and quantized exactly as the append
+// kernel does it (src/cache.rs:94-129 with the affine codes), written to its
+// slot (ring: (T - 1) mod W; paged: through the block table), and -- as the
+// reference's current token attends to its own quantized K/V
+// (src/cache.rs:295-298) -- contributes partial slot n_splits: m = q_rot .
+// k_deq (base 2), l = 1, o = v_deq . R^T, the same row for every head of the
+// group. Wave 0 handles K, wave 1 V.
+template <int D, int BITS>
+__device__ void new_token_column(const AttnArgs& a, uint8_t* tab, int64_t T, int n_splits,
+                                 int kvh, int seq, int wave, int lane) {
+  constexpr BlockLayout L = make_layout(D, BITS, kAffine);
+  constexpr int E = D / 64, LPG = 64 / E;
+  const int G = a.group;
+  copy_q_row<D>(a, tab, seq, kvh, wave, lane);
+  wait_vmcnt<0>();
+  build_q_table<D, BITS>(a, tab, wave, lane);
+  if (wave >= 2) return;  // no barrier follows
+
+  const bool isv = wave == 1;
+  const int d0 = lane * E;
+  const int64_t pbase = ((int64_t)seq * a.part_stride + n_splits) * a.n_q_heads + (int64_t)kvh * G;
+  if (T < 1) {  // no token: an empty partial
+    for (int h = 0; h < G; h++) {
+      if (isv) {
+#pragma unroll
+        for (int i = 0; i < E; i++) a.part_o[(pbase + h) * D + d0 + i] = 0.0f;
+      } else if (lane == 0) {
+        a.part_ml[(pbase + h) * 2 + 0] = -1e30f;
+        a.part_ml[(pbase + h) * 2 + 1] = 0.0f;
+      }
+    }
+    return;
+  }
+
+  float x[E];
+  load_row<E>((isv ? a.v_new : a.k_new) + ((int64_t)seq * a.st.n_kv_heads + kvh) * D + d0, x);
+  const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
+  wave_fwht<E>(x, lane);
+#pragma unroll
+  for (int i = 0; i < E; i++) x[i] = apply_sign(x[i] * a.c, sbits, i);
+  uint32_t code[E];
+  float scale, bias;
+  affine_quant<E, BITS>(x, code, scale, bias, lane);
+  const uint16_t s16 = f32_to_f16_bits(scale), b16 = f32_to_f16_bits(bias);
+
+  // slot write (a bad block-table entry skips it; the token still attends)
+  const int64_t pos = T - 1;
+  const int64_t slot = a.window > 0 ? pos % a.window : pos;
+  const int64_t lb = slot / kBlockTokens;
+  const int t = (int)(slot % kBlockTokens);
+  int64_t phys = lb;
+  bool ok = true;
+  if (a.st.block_table) {
+    ok = lb < a.st.table_stride;
+    phys = ok ? (int64_t)a.st.block_table[(int64_t)seq * a.st.table_stride + lb] : -1;
+  }
+  ok = ok && phys >= 0 && phys < a.st.n_blocks;
+  if (ok) {
+    uint8_t* blk = a.st.base + phys * a.st.block_stride + (int64_t)kvh * a.st.head_stride;
+    if (isv)
+      store_v_codes<BITS, E>(blk + L.v_codes, t, d0, code);
+    else
+      store_k_codes<BITS, E>(blk + L.k_codes, t, d0, code, lane);
+    if ((lane & (LPG - 1)) == 0)
+      *reinterpret_cast<uint32_t*>(blk + (isv ? L.v_meta : L.k_meta) + scale_pos(lane / LPG, t)) =
+          (uint32_t)s16 | ((uint32_t)b16 << 16);
+  }
+
+  // the dequantized row in the rotated domain, as the split columns read it
+  const float sf = f16_bits_to_f32(s16), bf = f16_bits_to_f32(b16);
+  float y[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) y[i] = (float)code[i] * sf + bf;
+  if (!isv) {
+    const QSlot<E, BITS> qs(lane);
+    const uint8_t* ent = tab + (2 * qs.g + qs.s) * kChunk + qs.i0 * 2;
+    for (int h = 0; h < G; h++) {
+      const _Float16* qh = reinterpret_cast<const _Float16*>(ent + (qs.j * 16 + h) * 16);
+      const _Float16* ql = reinterpret_cast<const _Float16*>(ent + (qs.j * 16 + h + 8) * 16);
+      float p = 0.0f;
+#pragma unroll
+      for (int i = 0; i < E; i++) p += ((float)qh[i] + (float)ql[i]) * y[i];
+      p = group_sum<64>(p, lane);
+      if (lane == 0) {
+        a.part_ml[(pbase + h) * 2 + 0] = p;
+        a.part_ml[(pbase + h) * 2 + 1] = 1.0f;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < E; i++) y[i] = apply_sign(y[i], sbits, i);
+    wave_fwht<E>(y, lane);
+    for (int h = 0; h < G; h++)
+#pragma unroll
+      for (int i = 0; i < E; i++) a.part_o[(pbase + h) * D + d0 + i] = y[i] * a.c;
+  }
+}
+
 // Two waves per SIMD (register budget <= 256 each).
 template <int D, int BITS>
 __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -197,6 +459,10 @@ void decode_attn_kernel(AttnArgs a) {
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
   const int n_splits = n_splits_for(geo, a.bps, a.max_splits);
+  if (a.new_col && split == (int)gridDim.x - 1) {
+    new_token_column<D, BITS>(a, scratch, T, n_splits, kvh, seq, wave, lane);
+    return;
+  }
   if (split >= n_splits) return;
   const int64_t b_begin = geo.blk_lo + (int64_t)split * a.bps;
   int64_t b_end = b_begin + a.bps;
@@ -243,24 +509,26 @@ void decode_attn_kernel(AttnArgs a) {
     if (lane < 8 * GH) dma16(sl + P::kMetaOff + half * 2 * MH, meta_voff, rs);
   };
 
-  // ---- copies: the q-prep table of (seq, kvh) (wave w: its KiB entries w,
-  // w + 8, ...), then the first stages; the table is waited for alone ----
+  // ---- copies: each wave's raw q row, then the first stages; the q row is
+  // waited for alone and rotated while the stages land ----
   constexpr int NE = 2 * NG;  // B-operand entries; the group sums follow
   if (lane == 0) xflag[wave] = 0;
-  {
-    const uint8_t* tab = a.qprep + ((int64_t)seq * gridDim.y + kvh) * qprep_bytes(D);
-    const u32x4 rt = buffer_rsrc(tab, (uint32_t)qprep_bytes(D));
-    for (int e = wave; e <= NE; e += kAttnWaves)
-      dma16(lds_addr(scratch + e * kChunk), e * kChunk + lane * 16, rt);
-  }
+  // The first NQ stages go out before the rotation, the rest after it: the
+  // rotation's first barrier then waits for less copy issue, which stalls
+  // while the whole chip's first requests queue up.
+  constexpr int NQ = (NST + 1) / 2;
+  copy_q_row<D>(a, scratch, seq, kvh, wave, lane);
 #pragma unroll
-  for (int s = 0; s < NST; s++)
+  for (int s = 0; s < NQ; s++)
     if (s < nb) copy_block(s, pb0 + (int64_t)kAttnPairs * s);
-  wait_copies<CP, NST>(nb < NST ? nb : NST);  // the table copies preceded every block
-  __syncthreads();
+  wait_copies<CP, NQ>(nb < NQ ? nb : NQ);  // the q copy preceded every block
+  build_q_table<D, BITS>(a, scratch, wave, lane);
+#pragma unroll
+  for (int s = NQ; s < NST; s++)
+    if (s < nb) copy_block(s, pb0 + (int64_t)kAttnPairs * s);
 
-  // B operands of this wave's groups (hi / residual halves of q_rot, see
-  // fmkv_qprep.h) and their q sums for the bias term
+  // B operands of this wave's groups (hi / residual halves of q_rot) and
+  // their q sums for the bias term
   half8_t bq[GH][2];
   float qs[GH];
   const float* qsum = reinterpret_cast<const float*>(scratch + NE * kChunk);  // [head][NG]
@@ -292,6 +560,10 @@ void decode_attn_kernel(AttnArgs a) {
   const int64_t vis_lo = a.window > 0 ? 0 : a.vis_begin;
   const int64_t vis_hi = a.window > 0 ? (T < a.window ? T : a.window) : T;
   const bool ring_trim = a.window > 0 && a.vis_begin > T - a.window;
+  // a decode step's new token is the new-token column's (its slot may still
+  // hold the position it replaces, or be written meanwhile)
+  int64_t ex_slot = -1;
+  if (a.new_col && T > 0) ex_slot = a.window > 0 ? (T - 1) % a.window : T - 1;
 
   // LDS operands, read one group ahead of their use so that the read
   // latency overlaps the previous group's MFMAs
@@ -350,12 +622,13 @@ void decode_attn_kernel(AttnArgs a) {
     // visibility: whole block in the common case (uniform test), per token
     // only at the edges of the visible range
     const int64_t t0 = b * kBlockTokens;
-    const bool full = t0 >= vis_lo && t0 + kBlockTokens <= vis_hi && !ring_trim;
+    const bool full = t0 >= vis_lo && t0 + kBlockTokens <= vis_hi && !ring_trim &&
+                      (uint64_t)(ex_slot - t0) >= (uint64_t)kBlockTokens;
     if (!full) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int64_t slot = t0 + 4 * j + i;
-        bool vis = slot >= vis_lo && slot < vis_hi;
+        bool vis = slot >= vis_lo && slot < vis_hi && slot != ex_slot;
         if (ring_trim) vis = vis && slot_position(slot, T, a.window) >= a.vis_begin;
         if (!vis) s[i] = -INFINITY;
       }
@@ -436,22 +709,28 @@ void decode_attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) o[k][i] = o[k][i] + row_ror8(o[k][i]);
 
-  __syncthreads();  // every wave is done with its stages (all copies waited for)
-  float* R = reinterpret_cast<float*>(stage);  // [pair][head][QS]
+  // The pair's own stages become its merge rows [head][QS] as soon as both of
+  // its waves are done with them (all copies were waited for in the last
+  // block), without waiting for the other pairs.
+  __hip_atomic_store(&xflag[wave], nb + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  while (__hip_atomic_load(&xflag[wave ^ 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+         nb + 1)
+    __builtin_amdgcn_s_sleep(1);
+  float* const Rp = reinterpret_cast<float*>(pstage);
   if (hi && col_valid) {
 #pragma unroll
     for (int gi = 0; gi < GH; gi++)
 #pragma unroll
       for (int ct = 0; ct < 4; ct++) {
         const int d = (g0 + gi) * 64 + ct * 16 + 4 * j;
-        *reinterpret_cast<float4_t*>(&R[(pair * 8 + head) * QS + d]) = o[gi * 4 + ct] + bacc[gi];
+        *reinterpret_cast<float4_t*>(&Rp[head * QS + d]) = o[gi * 4 + ct] + bacc[gi];
       }
     if (half == 0 && j == 0) {
       ml_s[pair][head][0] = m_run;
       ml_s[pair][head][1] = l_run;
     }
   }
-  __syncthreads();
+  __syncthreads();  // every pair's rows are written
 
   // head w on wave w
   if (wave < G) {
@@ -471,7 +750,9 @@ void decode_attn_kernel(AttnArgs a) {
     for (int i = 0; i < E; i++) {
       float v = 0.0f;
 #pragma unroll
-      for (int q = 0; q < kAttnPairs; q++) v = fmaf(wgt[q], R[(q * 8 + hh) * QS + lane * E + i], v);
+      for (int q = 0; q < kAttnPairs; q++)
+        v = fmaf(wgt[q], reinterpret_cast<const float*>(stage + q * NST * SB)[hh * QS + lane * E + i],
+                 v);
       x[i] = apply_sign(v, sbits, i);
     }
     wave_fwht<E>(x, lane);
@@ -488,7 +769,7 @@ void decode_attn_kernel(AttnArgs a) {
       }
     } else {
       const int64_t pbase =
-          ((int64_t)seq * a.max_splits + split) * a.n_q_heads + (int64_t)kvh * G;
+          ((int64_t)seq * a.part_stride + split) * a.n_q_heads + (int64_t)kvh * G;
       float* dst = a.part_o + (pbase + hh) * D + lane * E;
       if constexpr (E % 4 == 0) {
 #pragma unroll
@@ -522,9 +803,9 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
   const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
-  const int n_splits = n_splits_for(geo, a.bps, a.max_splits);
+  const int n_splits = n_splits_for(geo, a.bps, a.max_splits) + a.new_col;
   const int64_t stride = (int64_t)a.n_q_heads;
-  const int64_t base = (int64_t)seq * a.max_splits * stride + h;
+  const int64_t base = (int64_t)seq * a.part_stride * stride + h;
 
   // split maxima are finite (the split kernel starts from -1e30): the first
   // merge scales the empty state by exp2(-inf) = 0
@@ -573,23 +854,10 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
   }
 }
 
-// One work-group per (KV head, sequence).
-template <int D, int BITS>
-__global__ __launch_bounds__(kQPrepThreads) void qprep_kernel(QPrepArgs a) {
-  qprep_workgroup<D, BITS>(a, (int)gridDim.x, blockIdx.x, blockIdx.y, threadIdx.x);
-}
-
-template <int D, int BITS>
-hipError_t launch_qprep_t(const QPrepArgs& a, int n_kv_heads, int n_seqs, hipStream_t s) {
-  hipLaunchKernelGGL((qprep_kernel<D, BITS>), dim3(n_kv_heads, n_seqs), dim3(kQPrepThreads), 0, s,
-                     a);
-  return hipGetLastError();
-}
-
 template <int D, int BITS>
 hipError_t launch_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                     hipEvent_t ev0, hipEvent_t ev1) {
-  dim3 grid(a.max_splits, n_kv_heads, n_seqs);
+  dim3 grid(a.max_splits + a.new_col, n_kv_heads, n_seqs);
   if (ev0) (void)hipEventRecord(ev0, s);
   hipLaunchKernelGGL((decode_attn_kernel<D, BITS>), grid, dim3(kAttnWaves * 64), 0, s, a);
   hipError_t e = hipGetLastError();
@@ -611,20 +879,6 @@ hipError_t launch_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads
     case 256 * 16 + 8: return launch_t<256, 8>(a, n_seqs, n_kv_heads, s, e0, e1);
     case 512 * 16 + 4: return launch_t<512, 4>(a, n_seqs, n_kv_heads, s, e0, e1);
     case 512 * 16 + 8: return launch_t<512, 8>(a, n_seqs, n_kv_heads, s, e0, e1);
-  }
-  return hipErrorInvalidValue;
-}
-
-hipError_t launch_qprep(const QPrepArgs& a, int head_dim, int bits, int n_kv_heads, int n_seqs,
-                        hipStream_t s) {
-  if (n_seqs <= 0) return hipSuccess;
-  switch (head_dim * 16 + bits) {
-    case 128 * 16 + 4: return launch_qprep_t<128, 4>(a, n_kv_heads, n_seqs, s);
-    case 128 * 16 + 8: return launch_qprep_t<128, 8>(a, n_kv_heads, n_seqs, s);
-    case 256 * 16 + 4: return launch_qprep_t<256, 4>(a, n_kv_heads, n_seqs, s);
-    case 256 * 16 + 8: return launch_qprep_t<256, 8>(a, n_kv_heads, n_seqs, s);
-    case 512 * 16 + 4: return launch_qprep_t<512, 4>(a, n_kv_heads, n_seqs, s);
-    case 512 * 16 + 8: return launch_qprep_t<512, 8>(a, n_kv_heads, n_seqs, s);
   }
   return hipErrorInvalidValue;
 }

@@ -26,22 +26,6 @@ struct Store {
 constexpr int kAttnPairs = 4;
 constexpr int kAttnWaves = 2 * kAttnPairs;
 
-// q preparation (fmkv_qprep.h): per (sequence, KV head) a table of the
-// decode kernel's MFMA B operands and group sums, (2 D/64 + 1) KiB.
-constexpr int kQPrepThreads = 256;
-__host__ __device__ constexpr int64_t qprep_bytes(int head_dim) {
-  return (2 * (head_dim / 64) + 1) * 1024;
-}
-
-struct QPrepArgs {
-  const uint16_t* q;   // bf16 [n_seqs][n_q_heads][D]
-  int32_t n_q_heads;
-  int32_t group;       // q heads per KV head
-  float qscale;        // softmax scale * log2(e)
-  float c;             // 1/sqrt(D)
-  uint32_t sign_bits[16];  // RHT signs of dims 0..D-1, bit d set = -1
-  uint8_t* out;        // tables, [n_seqs][n_kv_heads][qprep_bytes(D)]
-};
 #ifndef FMKV_ATTN_WG_PER_CU
 #define FMKV_ATTN_WG_PER_CU 1
 #endif
@@ -59,27 +43,35 @@ struct AppendArgs {
   float c;             // 1/sqrt(D) (f32)
   float sqrt_d;        // sqrt(D) (f32), codebook mode
   int32_t cb_bits;     // codebook bits
-  QPrepArgs qp;        // qp.out != null: the launch also prepares q (decode step)
 };
 
 struct AttnArgs {
   Store st;
-  const int32_t* seq_lens;  // per sequence, or null -> seq_len
+  const int32_t* seq_lens;  // per sequence, or null -> seq_len (visible positions,
+                            // the new token of a decode step included)
   int64_t seq_len;
   int64_t window;
   int64_t vis_begin;
-  int32_t group;      // q heads per kv head
+  int32_t group;      // q heads per kv head (<= 8)
   int32_t n_q_heads;
-  const uint8_t* qprep;    // q-prep tables of this call
+  const uint16_t* q;  // bf16 [n_seqs][n_q_heads][D]
+  float qscale;       // softmax scale * log2(e)
   uint32_t sign_bits[16];  // RHT signs of dims 0..D-1, bit d set = -1
-  float c;
+  float c;            // 1/sqrt(D)
   int32_t bps;        // blocks per split
-  int32_t max_splits;
-  float* part_o;      // [n_seqs][max_splits][n_q_heads][D]
-  float* part_ml;     // [n_seqs][max_splits][n_q_heads][2]
+  int32_t max_splits; // split columns of the grid
+  int32_t part_stride;  // partial slots per sequence: max_splits + new_col
+  float* part_o;      // [n_seqs][part_stride][n_q_heads][D]
+  float* part_ml;     // [n_seqs][part_stride][n_q_heads][2]
   void* out;          // [n_seqs][n_q_heads][D]
   int32_t out_f32;
-  int32_t direct;     // 1: no combine, write out
+  int32_t direct;     // 1: one split and no new-token column; no combine, write out
+  // Decode step (new_col = 1): one more grid column appends the new token
+  // (position seq_len - 1) of every (sequence, KV head) and contributes its
+  // attention as partial slot n_splits; the split columns leave its slot out.
+  int32_t new_col;
+  const uint16_t* k_new;  // bf16 [n_seqs][n_kv_heads][D]
+  const uint16_t* v_new;
 };
 
 struct ReadArgs {
@@ -102,12 +94,7 @@ struct FetchArgs {
   int32_t out_f32;
 };
 
-// With a.qp.out set the launch carries one more column of work-groups that
-// fill the q-prep tables (n_seqs x n_kv_heads); max_tasks may then be 0.
 hipError_t launch_append(const AppendArgs& a, int n_seqs, int max_tasks, hipStream_t s);
-// The q-prep tables on their own (attention without a fused append).
-hipError_t launch_qprep(const QPrepArgs& a, int head_dim, int bits, int n_kv_heads, int n_seqs,
-                        hipStream_t s);
 // ev_begin / ev_end (optional) are recorded around the split-K kernel only.
 hipError_t launch_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                                    hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr);

@@ -1,0 +1,55 @@
+// Group-64 affine quantization of one rotated row held by a wave, shared by
+// the append kernel and the decode step's new-token column (so both write
+// bit-identical codes).
+//
+// MLX affine_quantize (the quantizer the reference calls at
+// src/model/mod.rs:669-675), restated: per group, scale = max((max - min) /
+// (2^b - 1), 1e-7), negated unless |min| > |max|; the edge value of larger
+// magnitude (max on a tie) is represented exactly: q0 = rint(edge / scale),
+// and when q0 != 0 the scale
+// becomes edge / q0 and the bias the edge itself, else the bias is 0; codes
+// are clip(rint((y - bias) / scale), 0, 2^b - 1) with the f32 scale and
+// bias, which are then stored as f16. rint rounds half to even. Every
+// operation is written in the oracle's order (the build disables FMA
+// contraction).
+#pragma once
+#include "fmkv_device.h"
+
+namespace fmkv {
+
+// Lane holds E = D/64 consecutive values of the row; the group spans 64/E
+// lanes. Returns the codes and the f32 scale and bias of the lane's group.
+template <int E, int BITS>
+__device__ inline void affine_quant(const float (&y)[E], uint32_t (&code)[E], float& scale_o,
+                                    float& bias_o, int lane) {
+  constexpr int kLanesPerGroup = 64 / E;
+  float mx = y[0], mn = y[0];
+#pragma unroll
+  for (int i = 1; i < E; i++) {
+    mx = fmaxf(mx, y[i]);
+    mn = fminf(mn, y[i]);
+  }
+  mx = group_max<kLanesPerGroup>(mx, lane);
+  mn = group_min<kLanesPerGroup>(mn, lane);
+  const float n_bins = (float)((1 << BITS) - 1);
+  float scale = fmaxf((mx - mn) / n_bins, 1e-7f);
+  const bool side = fabsf(mn) > fabsf(mx);
+  scale = side ? scale : -scale;
+  const float edge = side ? mn : mx;
+  const float q0 = rintf(edge / scale);
+  float bias = 0.0f;
+  if (q0 != 0.0f) {
+    scale = edge / q0;
+    bias = edge;
+  }
+#pragma unroll
+  for (int i = 0; i < E; i++) {
+    float q = rintf((y[i] - bias) / scale);
+    q = fminf(fmaxf(q, 0.0f), n_bins);
+    code[i] = (uint32_t)q;
+  }
+  scale_o = scale;
+  bias_o = bias;
+}
+
+}  // namespace fmkv

@@ -1,9 +1,12 @@
-"""Fused decode step (append + attention in one call) on the GPU.
+"""Decode step (append + attention in one call) on the GPU.
 
-The step must equal the two separate calls bit for bit (same kernels, the q
-rotation only moves into the append launch), store codes bit-identical to the
-oracle's, and attend within the path tolerance (max-abs 2e-2, mean-abs 2e-3)
-of the oracle's exact attention over its dequantized cache."""
+With one new token the attention launch appends it itself (its new-token
+column) and adds the token's attention as one more split partial. The step
+must store codes bit-identical to the oracle's and to a separate append,
+attend within the path tolerance (max-abs 2e-2, mean-abs 2e-3) of the
+oracle's exact attention over its dequantized cache, and agree with the two
+separate calls to 1e-3 + 1e-4 relative (the same cache read; only the new
+token's score is summed in a different order)."""
 import numpy as np
 import pytest
 
@@ -23,7 +26,7 @@ def q_rows(seed, Hq, Hkv, D):
     (128, 4, 4, 4, 0),
     (256, 8, 2, 12, 32),
 ])
-def test_step_equals_append_then_attention(gpu, ora, D, bits, Hkv, Hq, W):
+def test_step_matches_oracle_and_two_calls(gpu, ora, D, bits, Hkv, Hq, W):
     import torch
 
     cap = 0 if W else 400
@@ -45,9 +48,8 @@ def test_step_equals_append_then_attention(gpu, ora, D, bits, Hkv, Hq, W):
         oc.append(k, v)
         torch.cuda.synchronize()
         assert a.offset() == b.offset() == oc.offset
-        assert torch.equal(out_a, out_b), f"step {step}: fused step differs from the two calls"
-        if step % 9 == 0 or step == 39:
-            check_attention(out_a, oc.attention(q, 0.05), f"step {step}")
+        assert torch.allclose(out_a, out_b, rtol=1e-4, atol=1e-3), f"step {step}: step vs two calls"
+        check_attention(out_a, oc.attention(q, 0.05), f"step {step}")
     ca, ma = a.read_codes()
     cb, mb = b.read_codes()
     torch.cuda.synchronize()
@@ -55,6 +57,32 @@ def test_step_equals_append_then_attention(gpu, ora, D, bits, Hkv, Hq, W):
     filled = min(oc.offset, oc.n_slots)
     assert np.array_equal(host_u32(ca)[:filled], oc.codes[:filled])
     assert np.array_equal(host_u16(ma)[:filled], oc.meta[:filled])
+
+
+@pytest.mark.parametrize("D,bits,Hkv,Hq,W", [(512, 8, 2, 16, 0), (256, 4, 8, 16, 32)])
+def test_steps_from_empty_cache(gpu, ora, D, bits, Hkv, Hq, W):
+    """Single-token steps from position 0: the first step attends to the new
+    token alone; block boundaries (16, 17) and, for the ring, the first wraps
+    (32, 33) pass."""
+    import torch
+
+    cap = 0 if W else 64
+    cache = gpu.KVCache.new_quantized_with_window(D, bits, W, Hkv, cap)
+    oc = ora.OracleCache(Hkv, D, bits, W, cap)
+    for step in range(40):
+        k = kv_batch(500 + 2 * step, 1, Hkv, D, special=False)
+        v = kv_batch(501 + 2 * step, 1, Hkv, D, special=False)
+        q = q_rows(600 + step, Hq, Hkv, D)
+        out = cache.decode_step(dev_bf16(k), dev_bf16(v), dev_bf16(q), 1.0 / np.sqrt(D),
+                                dtype=torch.float32)
+        oc.append(k, v)
+        torch.cuda.synchronize()
+        check_attention(out, oc.attention(q, 1.0 / np.sqrt(D)), f"step {step}")
+    codes, meta = cache.read_codes()
+    torch.cuda.synchronize()
+    filled = min(oc.offset, oc.n_slots)
+    assert np.array_equal(host_u32(codes)[:filled], oc.codes[:filled])
+    assert np.array_equal(host_u16(meta)[:filled], oc.meta[:filled])
 
 
 def test_step_validation_leaves_cache_unchanged(gpu):
@@ -77,7 +105,7 @@ def test_step_validation_leaves_cache_unchanged(gpu):
 
 
 @pytest.mark.parametrize("D,bits,Hkv,Hq", [(256, 4, 8, 16), (512, 8, 2, 16)])
-def test_paged_step_equals_append_then_attention(gpu, ora, D, bits, Hkv, Hq):
+def test_paged_step_matches_oracle_and_two_calls(gpu, ora, D, bits, Hkv, Hq):
     import torch
 
     lens = [3, 40, 129, 16, 1, 250]
@@ -115,7 +143,7 @@ def test_paged_step_equals_append_then_attention(gpu, ora, D, bits, Hkv, Hq):
         pb.append(dev_bf16(k1), dev_bf16(v1), dtab, start)
         out_b = pb.attention(dev_bf16(q), dtab, seq_lens, mx, 0.05, dtype=torch.float32)
         torch.cuda.synchronize()
-        assert torch.equal(out_a, out_b), f"step {step}"
+        assert torch.allclose(out_a, out_b, rtol=1e-4, atol=1e-3), f"step {step}: step vs two calls"
         for s in range(n_seqs):
             oracles[s].append(k1[s], v1[s])
             check_attention(out_a[s], oracles[s].attention(q[s], 0.05), f"step {step} seq {s}")
