@@ -64,6 +64,10 @@ constexpr int kChunk = 1024;  // bytes per full LDS copy instruction (64 lanes x
 
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
+// Online softmax: how far (base 2) a score may exceed the running reference
+// max before the accumulators are rescaled to a new one.
+constexpr float kRescaleSlack = 8.0f;
+
 // Staging plan of one (head_dim, bits). A stage holds one head-block as
 //   [K codes][V codes][wave 0: K meta, V meta of its groups][wave 1: ...];
 // each wave copies its groups' code chunks and, with one partial
@@ -636,8 +640,13 @@ void decode_attn_kernel(AttnArgs a) {
     float mb = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     mb = xor16_max(mb);
     mb = xor32_max(mb);
+    // The reference max moves only when a score exceeds it by more than
+    // kRescaleSlack (base 2): O, l and the bias sums are then rescaled, which
+    // costs a multiply per accumulator; below that, p = 2^(s - m_run) stays
+    // under 2^kRescaleSlack, exact in f32 and far inside f16 range for
+    // p * v_scale. Any reference gives the same softmax.
     const float m_new = fmaxf(m_run, mb);
-    if (__any(m_new > m_run)) {
+    if (__any(m_new > m_run + kRescaleSlack)) {
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       // until something has been accumulated, O and the bias sums are zero
       // and need no rescaling (the common case of the first block)
@@ -667,7 +676,7 @@ void decode_attn_kernel(AttnArgs a) {
       float x[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        x[i] = p[i] * lo16(vm_g[i]);
+        x[i] = fmaf(p[i], lo16(vm_g[i]), 0.0f);  // one v_fma_mix; = the rounded product
         bacc[gi] = fmaf(p[i], hi16(vm_g[i]), bacc[gi]);
       }
       const half2_t h01 = pkrtz(x[0], x[1]);
