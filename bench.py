@@ -189,6 +189,256 @@ def run_c3(args) -> dict:
     return res
 
 
+def _step_fn(lib, fmkv, h, kd, vd, qd, Hq, Hkv, D, out, stream, pool):
+    """fmkv_decode_step of one token; inputs cycle through `pool` resident rows."""
+    row, qrow = Hkv * D * 2, Hq * D * 2
+    kp, vp, qp, op = kd.data_ptr(), vd.data_ptr(), qd.data_ptr(), out.data_ptr()
+
+    def step(i):
+        t = i % pool
+        rc = lib.fmkv_decode_step(h, kp + t * row, vp + t * row, 1, qp + t * qrow, Hq, 1.0, 0.0, op,
+                                  fmkv.DTYPE_BF16, stream)
+        if rc:
+            raise RuntimeError(lib.fmkv_last_error().decode())
+    return step
+
+
+def run_c2(args) -> dict:
+    """Sliding-window layer: batch 1, Hq 16, Hkv 8, head_dim 256, a ring of
+    1024 slots, 4-bit group 64; 8192 single-token decode steps (8 wraps),
+    attention after every append. Eager: one fmkv_decode_step call per step
+    from Python. Graph: one wrap (1024 steps) captured into a HIP graph and
+    replayed -- in steady state a ring step depends on the position only
+    through (T - 1) mod W, so the same graph replays exactly."""
+    import torch
+
+    import fmkv
+    import synth
+
+    Hq, Hkv, D, bits, W = 16, 8, 256, 4, 1024
+    per_tok = bytes_per_token_head(D, bits)
+    pool = 1024
+    ch = synth.outlier_channels(7, Hkv, D)
+    kd = dev_bf16(synth.kv_rows(51, pool, Hkv, D, ch))
+    vd = dev_bf16(synth.kv_rows(52, pool, Hkv, D, ch))
+    qd = dev_bf16(synth.q_rows(53, Hq, Hkv, D, ch, batch=pool))
+    cache = fmkv.KVCache.new_quantized_with_window(D, bits, W, Hkv)
+    out = torch.empty((Hq, D), dtype=torch.bfloat16, device="cuda")
+    lib = fmkv.load_library()
+    s = torch.cuda.Stream()
+    n_steps = 8192
+    with torch.cuda.stream(s):
+        step = _step_fn(lib, fmkv, cache._h, kd, vd, qd, Hq, Hkv, D, out, s.cuda_stream, pool)
+        for i in range(W + 64):  # fill the ring, then steady state
+            step(i)
+        s.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        ev0.record(s)
+        for i in range(n_steps):
+            step(i)
+        ev1.record(s)
+        s.synchronize()
+        eager_wall = time.perf_counter() - t0
+        eager_gpu_ms = ev0.elapsed_time(ev1)
+
+        # one wrap in a graph (no allocation or memset inside the captured region)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(W):
+                step(i)
+        s.synchronize()
+        g.replay()
+        s.synchronize()
+        reps = n_steps // W
+        ev0.record(s)
+        for _ in range(reps):
+            g.replay()
+        ev1.record(s)
+        s.synchronize()
+        graph_ms = ev0.elapsed_time(ev1)
+    read = W * Hkv * per_tok + 2 * Hq * D * 2 + Hkv * (2 * D * 2 + per_tok)
+    graph_us = graph_ms * 1e3 / (reps * W)
+    log(f"c2: eager {eager_wall / n_steps * 1e6:.1f} us/step wall ({eager_gpu_ms * 1e3 / n_steps:.1f} "
+        f"us GPU span), graph {graph_us:.2f} us/step")
+    return {
+        "metric": "sliding-window decode steps/s (ring W=1024, 8192 steps, attention after every append)",
+        "value": round(1e6 / graph_us, 1),
+        "unit": "steps/s",
+        "n_gpus": 1, "steps": n_steps, "warmup": W + 64,
+        "ms_per_step": round(graph_us / 1e3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
+        "data": "synthetic (seeded N(0,1), 4 outlier channels x20; 1024 resident input rows cycled)",
+        "config": {"workload": "gemma4-sliding-layer ring decode: Hq 16, Hkv 8, head_dim 256, window "
+                               "1024, 4-bit group-64, 1 token append + attention per step, HIP graph "
+                               "of 1024 steps replayed 8 times",
+                   "batch": 1, "window": W, "n_q_heads": Hq, "n_kv_heads": Hkv, "head_dim": D,
+                   "bits": bits},
+        "tokens_per_s": round(1e6 / graph_us, 1),
+        "step_GBps": round(read / (graph_us * 1e-6) / 1e9, 1),
+        "eager": {"us_per_step_wall": round(eager_wall / n_steps * 1e6, 2),
+                  "us_per_step_gpu_span": round(eager_gpu_ms * 1e3 / n_steps, 2)},
+    }
+
+
+def run_c4(args) -> dict:
+    """Batched ragged decode: 32 sequences with lengths uniform in
+    [512, 16384] (seeded), Hq 16, Hkv 8, head_dim 256, 4-bit group 64, paged
+    pool of 16-token blocks with block ids in a seeded shuffled order. One
+    step appends one token per sequence and attends over all of them
+    (fmkv_paged_decode_step)."""
+    import torch
+
+    import fmkv
+    import synth
+
+    Hq, Hkv, D, bits, n_seqs = 16, 8, 256, 4, 32
+    per_tok = bytes_per_token_head(D, bits)
+    steps, warm = args.steps if args.steps < 256 else 64, 8
+    lens = (512 + (synth.splitmix64(404, n_seqs) % np.uint64(16384 - 512 + 1))).astype(np.int64)
+    cap = lens + warm + steps + 1
+    need = (cap + 15) // 16
+    max_blocks = int(need.max())
+    n_blocks = int(need.sum())
+    perm = np.argsort(synth.splitmix64(405, n_blocks)).astype(np.int32)
+    tables = np.zeros((n_seqs, max_blocks), np.int32)
+    o = 0
+    for s_, nb in enumerate(need):
+        tables[s_, :nb] = perm[o:o + nb]
+        o += int(nb)
+    pool = fmkv.PagedPool(fmkv.make_desc(Hkv, D, bits), n_blocks)
+    dtab = torch.from_numpy(tables).cuda()
+    ch = synth.outlier_channels(9, Hkv, D)
+    chunk = 2048
+    kc = dev_bf16(synth.kv_rows(61, chunk, Hkv, D, ch))[None]
+    vc = dev_bf16(synth.kv_rows(62, chunk, Hkv, D, ch))[None]
+    for s_ in range(n_seqs):  # prefill each sequence from a resident 2048-row chunk
+        for p0 in range(0, int(lens[s_]), chunk):
+            n = min(chunk, int(lens[s_]) - p0)
+            pool.append(kc[:, :n].contiguous(), vc[:, :n].contiguous(), dtab[s_:s_ + 1].contiguous(),
+                        torch.tensor([p0], dtype=torch.int32, device="cuda"))
+    torch.cuda.synchronize()
+    kd = dev_bf16(synth.kv_rows(63, n_seqs * (warm + steps), Hkv, D, ch))
+    vd = dev_bf16(synth.kv_rows(64, n_seqs * (warm + steps), Hkv, D, ch))
+    qd = dev_bf16(synth.q_rows(65, Hq, Hkv, D, ch, batch=n_seqs * (warm + steps)))
+    out = torch.empty((n_seqs, Hq, D), dtype=torch.bfloat16, device="cuda")
+    starts = [torch.tensor(lens + i, dtype=torch.int32, device="cuda") for i in range(warm + steps)]
+    slens = [t + 1 for t in starts]
+    lib = fmkv.load_library()
+    stream = torch.cuda.current_stream().cuda_stream
+    row, qrow = n_seqs * Hkv * D * 2, n_seqs * Hq * D * 2
+
+    def step(i):
+        mx = int(lens.max()) + i + 1
+        rc = lib.fmkv_paged_decode_step(pool._h, kd.data_ptr() + i * row, vd.data_ptr() + i * row,
+                                        dtab.data_ptr(), max_blocks, starts[i].data_ptr(),
+                                        slens[i].data_ptr(), n_seqs, 1, mx, qd.data_ptr() + i * qrow,
+                                        Hq, 1.0, 0.0, out.data_ptr(), fmkv.DTYPE_BF16, stream)
+        if rc:
+            raise RuntimeError(lib.fmkv_last_error().decode())
+
+    for i in range(warm):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(warm, warm + steps):
+        step(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / steps
+    tok = float((lens + warm + steps / 2 + 1).sum())
+    read = tok * Hkv * per_tok + n_seqs * (2 * Hq * D * 2 + Hkv * (2 * D * 2 + per_tok))
+    gbs = read / (us * 1e-6) / 1e9
+    log(f"c4: {us:.1f} us/step, {gbs:.0f} GB/s over {read / 1e6:.0f} MB/step")
+    return {
+        "metric": "batched ragged paged decode GB/s (32 seqs, lengths U[512,16384])",
+        "value": round(gbs, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": steps, "warmup": warm, "ms_per_step": round(us / 1e3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
+        "data": "synthetic (seeded N(0,1), 4 outlier channels x20; prefill from a resident 2048-row chunk)",
+        "config": {"workload": "batched ragged decode, paged pool of 16-token blocks (shuffled ids): "
+                               "32 sequences, Hq 16, Hkv 8, head_dim 256, 4-bit group-64, 1 token "
+                               "append + attention per sequence per step",
+                   "n_seqs": n_seqs, "total_context": int(lens.sum()), "n_q_heads": Hq,
+                   "n_kv_heads": Hkv, "head_dim": D, "bits": bits},
+        "hbm_frac_of_value": round(gbs / HBM_PEAK_GBS, 4),
+        "bytes_per_step": int(read),
+    }
+
+
+def run_c5(args) -> dict:
+    """Decode-step cache traffic of a 30-layer Gemma-4-26B-A4B-shaped stack:
+    25 sliding layers (ring of 1024, Hkv 8, head_dim 256, 4-bit) and 5 global
+    layers (Hkv 2, head_dim 512, 8-bit) at i % 6 == 5; chunked-prefill appends
+    of 2048 tokens to 131072 positions, then decode steps of every layer."""
+    import torch
+
+    import fmkv
+    import synth
+
+    Hq, T0, chunk = 16, args.c5_context, 2048
+    steps, warm = 16, 4
+    glob = [i % 6 == 5 for i in range(30)]
+    caches, shapes = [], []
+    for g in glob:
+        if g:
+            caches.append(fmkv.KVCache.new_quantized(512, 8, 2, capacity=T0 + warm + steps + 16))
+            shapes.append((2, 512, 8))
+        else:
+            caches.append(fmkv.KVCache.new_quantized_with_window(256, 4, 1024, 8))
+            shapes.append((8, 256, 4))
+    inputs = {}
+    for (Hkv, D, bits) in set(shapes):
+        ch = synth.outlier_channels(11 + D, Hkv, D)
+        inputs[D] = (dev_bf16(synth.kv_rows(71 + D, chunk, Hkv, D, ch)),
+                     dev_bf16(synth.kv_rows(72 + D, chunk, Hkv, D, ch)),
+                     dev_bf16(synth.q_rows(73 + D, Hq, Hkv, D, ch, batch=64)))
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for p0 in range(0, T0, chunk):
+        for c_, (Hkv, D, bits) in zip(caches, shapes):
+            c_.append(inputs[D][0], inputs[D][1])
+    ev1.record()
+    torch.cuda.synchronize()
+    prefill_ms = ev0.elapsed_time(ev1)
+    lib = fmkv.load_library()
+    stream = torch.cuda.current_stream().cuda_stream
+    outs = {D: torch.empty((Hq, D), dtype=torch.bfloat16, device="cuda") for D in inputs}
+    fns = [_step_fn(lib, fmkv, c_._h, inputs[D][0], inputs[D][1], inputs[D][2], Hq, Hkv, D, outs[D],
+                    stream, 64) for c_, (Hkv, D, bits) in zip(caches, shapes)]
+    for i in range(warm):
+        for f in fns:
+            f(i)
+    torch.cuda.synchronize()
+    ev0.record()
+    for i in range(warm, warm + steps):
+        for f in fns:
+            f(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / steps
+    Tg = T0 + warm + steps / 2 + 1
+    read = 5 * Tg * 2 * bytes_per_token_head(512, 8) + 25 * 1024 * 8 * bytes_per_token_head(256, 4)
+    gbs = read / (us * 1e-6) / 1e9
+    log(f"c5: prefill {prefill_ms:.1f} ms, decode {us:.1f} us/step (30 layers), {gbs:.0f} GB/s")
+    return {
+        "metric": "30-layer stack decode-step cache GB/s at 131072 context",
+        "value": round(gbs, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": steps, "warmup": warm, "ms_per_step": round(us / 1e3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
+        "data": "synthetic (seeded N(0,1), 4 outlier channels x20; resident 2048-row chunks reused)",
+        "config": {"workload": "gemma4-26B-A4B-shaped 30-layer stack: 25 sliding (W 1024, Hkv 8, "
+                               "head_dim 256, 4-bit) + 5 global (Hkv 2, head_dim 512, 8-bit) layers, "
+                               "chunked prefill of 2048, then 1-token decode steps",
+                   "context": T0, "layers": 30, "batch": 1},
+        "hbm_frac_of_value": round(gbs / HBM_PEAK_GBS, 4),
+        "prefill_ms": round(prefill_ms, 2),
+        "prefill_tokens_per_s_per_layer": round(T0 / (prefill_ms / 1e3) * 30, 1),
+        "bytes_per_step": int(read),
+    }
+
+
 def cpu_baseline_c3(args, k_bf16, v_bf16, Hq, Hkv, D, per_tok) -> dict:
     """The reference's decode read on its bf16 cache (SDPA, MLX CPU op order),
     timed with the oracle on this host: one full 32K-context step per rep,
@@ -258,6 +508,10 @@ def main(argv=None) -> int:
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 8 device-to-device copies of MIB MiB (the reference kernel "
                          "for scaling HBM byte counters) and exit")
+    ap.add_argument("--workload", choices=["c3", "c2", "c4", "c5"], default="c3",
+                    help="c3 (default): global layer at 32K; c2: sliding ring, 8192 steps; "
+                         "c4: 32 ragged paged sequences; c5: 30-layer stack")
+    ap.add_argument("--c5-context", type=int, default=131072)
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the KV path is "
@@ -274,7 +528,7 @@ def main(argv=None) -> int:
         import fmkv
 
         fmkv.set_blocks_per_split(args.bps)
-    res = run_c3(args)
+    res = {"c3": run_c3, "c2": run_c2, "c4": run_c4, "c5": run_c5}[args.workload](args)
     print(json.dumps(res), flush=True)
     return 0
 

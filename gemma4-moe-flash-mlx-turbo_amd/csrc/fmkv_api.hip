@@ -110,11 +110,13 @@ int device_cus() {
 // work-groups per CU (each keeps several blocks in flight, so one per CU
 // already saturates HBM; more would only add split partials), `reserved` of
 // them going to other work of the same launch (the new-token column).
-int32_t choose_bps(int64_t total_head_blocks, int cus, int wg_per_cu, int64_t reserved = 0) {
+int32_t choose_bps(int64_t total_head_blocks, int cus, int wg_per_cu, int64_t reserved = 0,
+                   int64_t min_bps = 1) {
   if (g_bps_override > 0) return g_bps_override;
   int64_t target = (int64_t)wg_per_cu * cus;
   if (target - reserved >= target / 2) target -= reserved;
   int64_t bps = (total_head_blocks + target - 1) / target;
+  if (bps < min_bps) bps = min_bps;
   if (bps < 1) bps = 1;
   return (int32_t)bps;
 }
@@ -276,7 +278,8 @@ int prepare_append(const fmkv_cache* c, const void* k, const void* v, int64_t n,
 template <typename Owner>
 int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, int64_t nblk,
                              const void* q, int32_t n_q_heads, float scale, float tau, void* out,
-                             int32_t out_dtype, int wg_per_cu, int new_col, fmkv::AttnArgs* a) {
+                             int32_t out_dtype, int wg_per_cu, int min_bps, int new_col,
+                             fmkv::AttnArgs* a) {
   int rc = check_attn_args(o->desc, q, n_q_heads, tau, out, out_dtype);
   if (rc) return rc;
   const int H = o->desc.n_kv_heads, D = o->desc.head_dim;
@@ -288,7 +291,10 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   std::memcpy(a->sign_bits, o->sign_bits, sizeof(a->sign_bits));
   a->c = o->c;
   if (nblk < 1) nblk = 1;
-  a->bps = choose_bps(nblk * H * n_seqs, o->cus, wg_per_cu, (int64_t)new_col * H * n_seqs);
+  // one sequence: the new-token column takes CUs of its own; many sequences:
+  // the dispatcher fills CUs as work-groups finish
+  const int64_t reserved = n_seqs == 1 ? (int64_t)new_col * H : 0;
+  a->bps = choose_bps(nblk * H * n_seqs, o->cus, wg_per_cu, reserved, min_bps);
   a->max_splits = (int32_t)((nblk + a->bps - 1) / a->bps);
   a->new_col = new_col;
   a->part_stride = a->max_splits + new_col;
@@ -317,7 +323,7 @@ int prepare_attention(fmkv_cache* c, int64_t T, const void* q, int32_t n_q_heads
   const int64_t nblk =
       (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
   return prepare_attention_common(c, cache_store(c), 1, nblk, q, n_q_heads, scale, tau, out,
-                                  out_dtype, fmkv::kAttnWgPerCu, new_col, a);
+                                  out_dtype, fmkv::kAttnWgPerCu, 1, new_col, a);
 }
 
 int prepare_paged_append(const fmkv_pool* p, const void* k, const void* v,
@@ -361,11 +367,13 @@ int prepare_paged_attention(fmkv_pool* p, const void* q, const int32_t* block_ta
   a->window = 0;
   a->vis_begin = 0;
   const int64_t nblk = (max_seq_len + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens;
-  // ragged lengths: the bound counts every sequence at max_seq_len, so aim at
-  // more work-groups than for one sequence
+  // Ragged lengths: the bound counts every sequence at max_seq_len, so the
+  // plan aims at several work-groups per CU (the dispatcher balances their
+  // uneven sizes), but at least 64 blocks each (a work-group's prologue and
+  // epilogue cost about as much as a dozen blocks).
   return prepare_attention_common(p, pool_store(p, block_tables, max_blocks),
                                   n_seqs > 0 ? n_seqs : 1, nblk, q, n_q_heads, scale, tau, out,
-                                  out_dtype, 4 * fmkv::kAttnWgPerCu, new_col, a);
+                                  out_dtype, 8 * fmkv::kAttnWgPerCu, 64, new_col, a);
 }
 
 }  // namespace

@@ -148,26 +148,37 @@ __device__ inline void wait_copies(int pending) {
 
 __device__ inline u32x4 lds16(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-// K operand (8 codes as exact f16) of MFMA s of group g; `w` is the lane's
-// 16 bytes of the group's chunk (8-bit) or of the two groups' chunk (4-bit).
+// 8-bit codes enter the MFMAs as the exact f16 values 1024 + code (one
+// v_perm per two codes): the QK accumulator starts at -1024 * sum(q operand)
+// and the PV accumulator loses 1024 * sum(P') at the end, both from the
+// exact f16 operand values. At 8 bits the offset costs the f32 partial sums
+// at most 3 of their 24 bits; 4-bit codes (range 16) convert exactly
+// instead, as the offset would cost them 7.
+template <int BITS>
+constexpr bool kBiasedCodes = BITS == 8;
+
+// K operand (8 codes as exact f16, + 1024 at 8 bits) of MFMA s of group g;
+// `w` is the lane's 16 bytes of the group's chunk (8-bit) or of the two
+// groups' chunk (4-bit).
 template <int BITS>
 __device__ inline half8_t k_operand(const u32x4 w, int g, int s) {
   if constexpr (BITS == 8) {
     const uint32_t w0 = w[2 * s], w1 = w[2 * s + 1];
-    return cat8(u8x2_to_h2(w0, 0x04010400u), u8x2_to_h2(w0, 0x04030402u),
-                u8x2_to_h2(w1, 0x04010400u), u8x2_to_h2(w1, 0x04030402u));
+    return cat8(u8x2_to_h2_biased(w0, 0x04010400u), u8x2_to_h2_biased(w0, 0x04030402u),
+                u8x2_to_h2_biased(w1, 0x04010400u), u8x2_to_h2_biased(w1, 0x04030402u));
   } else {
     const uint32_t x = w[(g & 1) * 2 + s];
     return cat8(u4x2_to_h2(x, 0), u4x2_to_h2(x, 1), u4x2_to_h2(x, 2), u4x2_to_h2(x, 3));
   }
 }
 
-// V codes of column tile ct (0..3) of group g: tokens 4j..4j+3 of one dim.
+// V codes of column tile ct (0..3) of group g: tokens 4j..4j+3 of one dim
+// (+ 1024 at 8 bits).
 template <int BITS>
 __device__ inline half4_t v_operand(const u32x4 w, int g, int ct) {
   if constexpr (BITS == 8) {
     const uint32_t x = w[ct];
-    return cat4(u8x2_to_h2(x, 0x04010400u), u8x2_to_h2(x, 0x04030402u));
+    return cat4(u8x2_to_h2_biased(x, 0x04010400u), u8x2_to_h2_biased(x, 0x04030402u));
   } else {
     const int ctc = (g & 1) * 4 + ct;  // column tile inside the 128-dim chunk
     const uint32_t x = w[ctc >> 1];
@@ -543,6 +554,21 @@ void decode_attn_kernel(AttnArgs a) {
       bq[gi][s] = *reinterpret_cast<const half8_t*>(scratch + ((g0 + gi) * 2 + s) * kChunk + lane * 16);
     qs[gi] = (hi && col_valid) ? qsum[head * NG + g0 + gi] : 0.0f;
   }
+  // biased 8-bit codes: the QK accumulator of group gi starts at -1024 x this
+  // column's q operand summed over the group's 64 dims (16 per lane, 4 lanes)
+  float kq[GH];
+#pragma unroll
+  for (int gi = 0; gi < GH; gi++) {
+    float t = 0.0f;
+    if constexpr (kBiasedCodes<BITS>) {
+#pragma unroll
+      for (int s = 0; s < 2; s++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) t += (float)bq[gi][s][i];
+      t = xor32_sum(xor16_sum(t));
+    }
+    kq[gi] = -1024.0f * t;
+  }
   __syncthreads();  // the table is consumed: the region becomes the score exchange
   float4_t* const xs = reinterpret_cast<float4_t*>(scratch);  // [wave][parity][lane]
 
@@ -551,8 +577,9 @@ void decode_attn_kernel(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < GH * 4; i++) o[i] = (float4_t){0.f, 0.f, 0.f, 0.f};
   float bacc[GH];
+  float psum[GH];  // biased 8-bit codes: this lane's running sum of P' per group
 #pragma unroll
-  for (int gi = 0; gi < GH; gi++) bacc[gi] = 0.0f;
+  for (int gi = 0; gi < GH; gi++) bacc[gi] = psum[gi] = 0.0f;
   // m_run starts finite (-1e30): exp2(-inf - m) is 0 for masked tokens and
   // exp2(m_old - m_new) underflows to 0 at the first visible token, so the
   // softmax needs no special cases.
@@ -594,7 +621,7 @@ void decode_attn_kernel(AttnArgs a) {
         km = kmeta(sp, gi + 1);
       }
       const int g = g0 + gi;
-      float4_t acc = (float4_t){0.f, 0.f, 0.f, 0.f};
+      float4_t acc = (float4_t){kq[gi], kq[gi], kq[gi], kq[gi]};
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand<BITS>(kw_g, g, 0), bq[gi][0], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand<BITS>(kw_g, g, 1), bq[gi][1], acc, 0, 0, 0);
 #pragma unroll
@@ -654,7 +681,10 @@ void decode_attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < GH * 4; i++) o[i] *= alpha;
 #pragma unroll
-        for (int gi = 0; gi < GH; gi++) bacc[gi] *= alpha;
+        for (int gi = 0; gi < GH; gi++) {
+          bacc[gi] *= alpha;
+          if constexpr (kBiasedCodes<BITS>) psum[gi] *= alpha;
+        }
       }
       l_run *= alpha;
       m_run = m_new;
@@ -684,6 +714,8 @@ void decode_attn_kernel(AttnArgs a) {
       const half4_t bp = cat4(
           pkrtz(fmaf(-lo_sel, (float)h01[0], x[0]), fmaf(-lo_sel, (float)h01[1], x[1])),
           pkrtz(fmaf(-lo_sel, (float)h23[0], x[2]), fmaf(-lo_sel, (float)h23[1], x[3])));
+      if constexpr (kBiasedCodes<BITS>)
+        psum[gi] += ((float)bp[0] + (float)bp[1]) + ((float)bp[2] + (float)bp[3]);
       const int g = g0 + gi;
 #pragma unroll
       for (int ct = 0; ct < 4; ct++)
@@ -712,6 +744,18 @@ void decode_attn_kernel(AttnArgs a) {
   for (int gi = 0; gi < GH; gi++) {
     bacc[gi] = xor16_sum(bacc[gi]);
     bacc[gi] = xor32_sum(bacc[gi]);
+  }
+  if constexpr (kBiasedCodes<BITS>) {
+    // the V codes entered the MFMAs as 1024 + code: remove 1024 x the
+    // column's P' summed over all tokens (4 per lane, 4 lanes)
+#pragma unroll
+    for (int gi = 0; gi < GH; gi++) {
+      const float t = xor32_sum(xor16_sum(psum[gi]));
+#pragma unroll
+      for (int ct = 0; ct < 4; ct++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[gi * 4 + ct][i] = fmaf(-1024.0f, t, o[gi * 4 + ct][i]);
+    }
   }
 #pragma unroll
   for (int k = 0; k < GH * 4; k++)

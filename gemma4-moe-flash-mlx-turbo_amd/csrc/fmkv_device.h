@@ -61,6 +61,12 @@ __device__ inline float xor32_max(float v) {
 // Two 8-bit codes -> two exact f16 values: v_perm builds {c, 0x64} halves,
 // i.e. 1024 + c, and the packed subtract removes the 1024 exactly.
 // sel 0x04010400 takes bytes (0, 1) of w, 0x04030402 bytes (2, 3).
+// The same two codes as the exact f16 values 1024 + c (one v_perm): for
+// MFMAs whose accumulator removes the 1024 * sum(other operand) term.
+__device__ inline half2_t u8x2_to_h2_biased(uint32_t w, uint32_t sel) {
+  return __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w, sel));
+}
+
 __device__ inline half2_t u8x2_to_h2(uint32_t w, uint32_t sel) {
   uint32_t x = __builtin_amdgcn_perm(0x64646464u, w, sel);
   return __builtin_bit_cast(half2_t, x) - (half2_t){(_Float16)1024.0f, (_Float16)1024.0f};
