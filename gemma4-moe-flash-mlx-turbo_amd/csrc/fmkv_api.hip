@@ -295,6 +295,9 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   // the dispatcher fills CUs as work-groups finish
   const int64_t reserved = n_seqs == 1 ? (int64_t)new_col * H : 0;
   a->bps = choose_bps(nblk * H * n_seqs, o->cus, wg_per_cu, reserved, min_bps);
+  // the split columns are the grid's z dimension (at most 65535)
+  if ((nblk + a->bps - 1) / a->bps + new_col > 65535)
+    a->bps = (int32_t)((nblk + 65534 - new_col) / (65535 - new_col));
   a->max_splits = (int32_t)((nblk + a->bps - 1) / a->bps);
   a->new_col = new_col;
   a->part_stride = a->max_splits + new_col;

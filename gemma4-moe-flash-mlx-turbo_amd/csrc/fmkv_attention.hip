@@ -467,14 +467,18 @@ void decode_attn_kernel(AttnArgs a) {
   const bool hi = c < 8;
   const int G = a.group;
   const bool col_valid = head < G;
-  const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  // grid (KV head, sequence, split column): consecutive work-groups, which
+  // the dispatcher deals round-robin to the XCDs, are the KV heads of one
+  // split and then the sequences, so each XCD gets a like share of the work;
+  // the new-token column comes last
+  const int kvh = blockIdx.x, seq = blockIdx.y, split = blockIdx.z;
   const int g0 = half * GH;  // this wave's first group
 
   const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
   const int n_splits = n_splits_for(geo, a.bps, a.max_splits);
-  if (a.new_col && split == (int)gridDim.x - 1) {
+  if (a.new_col && split == (int)gridDim.z - 1) {
     new_token_column<D, BITS>(a, scratch, T, n_splits, kvh, seq, wave, lane);
     return;
   }
@@ -556,7 +560,7 @@ void decode_attn_kernel(AttnArgs a) {
   }
   // biased 8-bit codes: the QK accumulator of group gi starts at -1024 x this
   // column's q operand summed over the group's 64 dims (16 per lane, 4 lanes)
-  float kq[GH];
+  float4_t kq[GH];
 #pragma unroll
   for (int gi = 0; gi < GH; gi++) {
     float t = 0.0f;
@@ -567,7 +571,8 @@ void decode_attn_kernel(AttnArgs a) {
         for (int i = 0; i < 8; i++) t += (float)bq[gi][s][i];
       t = xor32_sum(xor16_sum(t));
     }
-    kq[gi] = -1024.0f * t;
+    const float k = -1024.0f * t;
+    kq[gi] = (float4_t){k, k, k, k};
   }
   __syncthreads();  // the table is consumed: the region becomes the score exchange
   float4_t* const xs = reinterpret_cast<float4_t*>(scratch);  // [wave][parity][lane]
@@ -621,8 +626,8 @@ void decode_attn_kernel(AttnArgs a) {
         km = kmeta(sp, gi + 1);
       }
       const int g = g0 + gi;
-      float4_t acc = (float4_t){kq[gi], kq[gi], kq[gi], kq[gi]};
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand<BITS>(kw_g, g, 0), bq[gi][0], acc, 0, 0, 0);
+      float4_t acc =
+          __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand<BITS>(kw_g, g, 0), bq[gi][0], kq[gi], 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand<BITS>(kw_g, g, 1), bq[gi][1], acc, 0, 0, 0);
 #pragma unroll
       for (int i = 0; i < 4; i++)
@@ -695,7 +700,9 @@ void decode_attn_kernel(AttnArgs a) {
     l_run += (p[0] + p[1]) + (p[2] + p[3]);
 
     // O^T += V^T . P'^T with P' = p * v_scale as f16 hi (c < 8) / residual
-    // (c >= 8)
+    // (c >= 8): x = p * v_scale in f32, hi = f16(x), residual = f16(x - hi),
+    // one mixed-precision FMA per element for each
+    const half2_t one2 = (half2_t){(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
     for (int gi = 0; gi < GH; gi++) {
       const u32x4 vw_g = vw, vm_g = vm;
@@ -711,11 +718,12 @@ void decode_attn_kernel(AttnArgs a) {
       }
       const half2_t h01 = pkrtz(x[0], x[1]);
       const half2_t h23 = pkrtz(x[2], x[3]);
-      const half4_t bp = cat4(
-          pkrtz(fmaf(-lo_sel, (float)h01[0], x[0]), fmaf(-lo_sel, (float)h01[1], x[1])),
-          pkrtz(fmaf(-lo_sel, (float)h23[0], x[2]), fmaf(-lo_sel, (float)h23[1], x[3])));
+      const half2_t b01 = pkrtz(fmaf(-lo_sel, (float)h01[0], x[0]), fmaf(-lo_sel, (float)h01[1], x[1]));
+      const half2_t b23 = pkrtz(fmaf(-lo_sel, (float)h23[0], x[2]), fmaf(-lo_sel, (float)h23[1], x[3]));
+      const half4_t bp = cat4(b01, b23);
+      // the column's sum of P' (exact f16 values) for the 1024 offset
       if constexpr (kBiasedCodes<BITS>)
-        psum[gi] += ((float)bp[0] + (float)bp[1]) + ((float)bp[2] + (float)bp[3]);
+        psum[gi] = __builtin_amdgcn_fdot2(b23, one2, __builtin_amdgcn_fdot2(b01, one2, psum[gi], false), false);
       const int g = g0 + gi;
 #pragma unroll
       for (int ct = 0; ct < 4; ct++)
@@ -910,7 +918,7 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
 template <int D, int BITS>
 hipError_t launch_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                     hipEvent_t ev0, hipEvent_t ev1) {
-  dim3 grid(a.max_splits + a.new_col, n_kv_heads, n_seqs);
+  dim3 grid(n_kv_heads, n_seqs, a.max_splits + a.new_col);
   if (ev0) (void)hipEventRecord(ev0, s);
   hipLaunchKernelGGL((decode_attn_kernel<D, BITS>), grid, dim3(kAttnWaves * 64), 0, s, a);
   hipError_t e = hipGetLastError();

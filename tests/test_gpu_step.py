@@ -7,6 +7,9 @@ attend within the path tolerance (max-abs 2e-2, mean-abs 2e-3) of the
 oracle's exact attention over its dequantized cache, and agree with the two
 separate calls to 1e-3 + 1e-4 relative (the same cache read; only the new
 token's score is summed in a different order)."""
+
+# fused step vs append + attention (see the module docstring)
+TWO_CALLS_RTOL, TWO_CALLS_ATOL = 1e-4, 1e-3
 import numpy as np
 import pytest
 
@@ -48,7 +51,8 @@ def test_step_matches_oracle_and_two_calls(gpu, ora, D, bits, Hkv, Hq, W):
         oc.append(k, v)
         torch.cuda.synchronize()
         assert a.offset() == b.offset() == oc.offset
-        assert torch.allclose(out_a, out_b, rtol=1e-4, atol=1e-3), f"step {step}: step vs two calls"
+        assert torch.allclose(out_a, out_b, rtol=TWO_CALLS_RTOL, atol=TWO_CALLS_ATOL), \
+            f"step {step}: step vs two calls"
         check_attention(out_a, oc.attention(q, 0.05), f"step {step}")
     ca, ma = a.read_codes()
     cb, mb = b.read_codes()
@@ -143,7 +147,8 @@ def test_paged_step_matches_oracle_and_two_calls(gpu, ora, D, bits, Hkv, Hq):
         pb.append(dev_bf16(k1), dev_bf16(v1), dtab, start)
         out_b = pb.attention(dev_bf16(q), dtab, seq_lens, mx, 0.05, dtype=torch.float32)
         torch.cuda.synchronize()
-        assert torch.allclose(out_a, out_b, rtol=1e-4, atol=1e-3), f"step {step}: step vs two calls"
+        assert torch.allclose(out_a, out_b, rtol=TWO_CALLS_RTOL, atol=TWO_CALLS_ATOL), \
+            f"step {step}: step vs two calls"
         for s in range(n_seqs):
             oracles[s].append(k1[s], v1[s])
             check_attention(out_a[s], oracles[s].attention(q[s], 0.05), f"step {step} seq {s}")
