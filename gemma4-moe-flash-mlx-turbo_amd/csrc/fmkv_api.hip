@@ -230,7 +230,8 @@ int check_attn_args(const fmkv_cache_desc& d, const void* q, int32_t n_q_heads, 
     return fail(FMKV_ERR_INVALID_ARG, "n_q_heads must be a multiple of n_kv_heads");
   if (n_q_heads / d.n_kv_heads > 8)
     return fail(FMKV_ERR_UNSUPPORTED, "at most 8 query heads per KV head");
-  if (tau != 0.0f) return fail(FMKV_ERR_UNSUPPORTED, "sparse-V threshold is not implemented");
+  if (!(tau >= 0.0f) || !std::isfinite(tau))
+    return fail(FMKV_ERR_INVALID_ARG, "sparse_v_tau must be finite and >= 0");
   if (out_dtype != FMKV_DTYPE_BF16 && out_dtype != FMKV_DTYPE_F32)
     return fail(FMKV_ERR_INVALID_ARG, "out_dtype must be FMKV_DTYPE_BF16 or FMKV_DTYPE_F32");
   return FMKV_OK;
@@ -301,15 +302,20 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   a->max_splits = (int32_t)((nblk + a->bps - 1) / a->bps);
   a->new_col = new_col;
   a->part_stride = a->max_splits + new_col;
-  a->direct = a->max_splits == 1 && !new_col;
+  // sparse-V (tau > 0) always goes through the split partials and the
+  // combine, which normalises by the stats pass's full softmax sum
+  a->tau = tau;
+  a->direct = a->max_splits == 1 && !new_col && tau == 0.0f;
   a->k_new = a->v_new = nullptr;
   a->out = out;
   a->out_f32 = out_dtype == FMKV_DTYPE_F32;
   const size_t n_rows = a->direct ? 0 : (size_t)n_seqs * a->part_stride * n_q_heads;
-  rc = o->ws.ensure(n_rows * (D + 2) * sizeof(float));
+  const size_t n_stats = tau > 0.0f ? 3 * (size_t)n_seqs * n_q_heads : 0;
+  rc = o->ws.ensure((n_rows * (D + 2) + n_stats) * sizeof(float));
   if (rc) return rc;
   a->part_o = n_rows ? o->ws.ptr : nullptr;
   a->part_ml = n_rows ? o->ws.ptr + n_rows * D : nullptr;
+  a->tau_stats = n_stats ? o->ws.ptr + n_rows * (D + 2) : nullptr;
   return FMKV_OK;
 }
 
@@ -477,8 +483,9 @@ int fmkv_decode_step(fmkv_cache* c, const void* k, const void* v, int64_t n, con
   int64_t tasks = 0;
   int rc = prepare_append(c, k, v, n, &ap, &tasks);
   if (rc) return rc;
-  // one new token: the attention launch appends it itself (new-token column)
-  const int fused = n == 1 ? 1 : 0;
+  // one new token: the attention launch appends it itself (new-token
+  // column); sparse-V attention runs after a separate append
+  const int fused = n == 1 && tau == 0.0f ? 1 : 0;
   fmkv::AttnArgs at;
   rc = prepare_attention(c, c->offset + n, q, n_q_heads, scale, tau, out, out_dtype, fused, &at);
   if (rc) return rc;
@@ -664,7 +671,7 @@ int fmkv_paged_decode_step(fmkv_pool* p, const void* k, const void* v,
   if (rc) return rc;
   // one new token per sequence: the attention launch appends it itself, at
   // position seq_lens[s] - 1 (= start_pos[s])
-  const int fused = n_new == 1 ? 1 : 0;
+  const int fused = n_new == 1 && tau == 0.0f ? 1 : 0;
   fmkv::AttnArgs at;
   rc = prepare_paged_attention(p, q, block_tables, max_blocks, seq_lens, n_seqs, max_seq_len,
                                n_q_heads, scale, tau, out, out_dtype, fused, &at);

@@ -68,6 +68,14 @@ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 // max before the accumulators are rescaled to a new one.
 constexpr float kRescaleSlack = 8.0f;
 
+// Kernel modes. Dense: softmax attention. Sparse-V (src/model/
+// gemma4_attention.rs:196-234, weights below tau zeroed without
+// renormalisation) takes two passes over the cache: kStats streams only the
+// keys and writes each split's (m, l); kGated is the dense pass with every
+// score below its head's threshold theta = M + log2(tau * L) dropped, and the
+// combine divides by the full L of the stats pass.
+constexpr int kDense = 0, kStats = 1, kGated = 2;
+
 // Staging plan of one (head_dim, bits). A stage holds one head-block as
 //   [K codes][V codes][wave 0: K meta, V meta of its groups][wave 1: ...];
 // each wave copies its groups' code chunks and, with one partial
@@ -443,7 +451,7 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, int64_t T, int
 }
 
 // Two waves per SIMD (register budget <= 256 each).
-template <int D, int BITS>
+template <int D, int BITS, int MODE>
 __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void decode_attn_kernel(AttnArgs a) {
   using P = AttnPlan<D, BITS>;
@@ -451,7 +459,9 @@ void decode_attn_kernel(AttnArgs a) {
   constexpr int NG = P::NG, GH = P::GH;
   constexpr int E = D / 64;
   constexpr int QS = P::kQS;
-  constexpr int CP = P::kCopies, NST = P::kStages, SB = P::kStageBytes;
+  // copy instructions per wave per block (the stats pass copies no V codes)
+  constexpr int CP = MODE == kStats ? P::kWaveChunks + 1 : P::kCopies;
+  constexpr int NST = P::kStages, SB = P::kStageBytes;
   constexpr int MH = P::kMetaHalf;
 
   __shared__ __align__(16) uint8_t stage[P::kStageRegion];
@@ -478,9 +488,11 @@ void decode_attn_kernel(AttnArgs a) {
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
   const int n_splits = n_splits_for(geo, a.bps, a.max_splits);
-  if (a.new_col && split == (int)gridDim.z - 1) {
-    new_token_column<D, BITS>(a, scratch, T, n_splits, kvh, seq, wave, lane);
-    return;
+  if constexpr (MODE == kDense) {
+    if (a.new_col && split == (int)gridDim.z - 1) {
+      new_token_column<D, BITS>(a, scratch, T, n_splits, kvh, seq, wave, lane);
+      return;
+    }
   }
   if (split >= n_splits) return;
   const int64_t b_begin = geo.blk_lo + (int64_t)split * a.bps;
@@ -523,7 +535,8 @@ void decode_attn_kernel(AttnArgs a) {
     for (int k = 0; k < P::kWaveChunks; k++) {
       const int ch = kc0 + k;
       dma16(sl + (int)L.k_codes + ch * kChunk, (int)L.k_codes + ch * kChunk + lane * 16, rs);
-      dma16(sl + (int)L.v_codes + ch * kChunk, (int)L.v_codes + ch * kChunk + lane * 16, rs);
+      if constexpr (MODE != kStats)
+        dma16(sl + (int)L.v_codes + ch * kChunk, (int)L.v_codes + ch * kChunk + lane * 16, rs);
     }
     if (lane < 8 * GH) dma16(sl + P::kMetaOff + half * 2 * MH, meta_voff, rs);
   };
@@ -600,6 +613,17 @@ void decode_attn_kernel(AttnArgs a) {
   // hold the position it replaces, or be written meanwhile)
   int64_t ex_slot = -1;
   if (a.new_col && T > 0) ex_slot = a.window > 0 ? (T - 1) % a.window : T - 1;
+  // sparse-V: this column's score threshold (scalar loads of the group's
+  // thresholds, then a per-lane select)
+  float theta = -INFINITY;
+  if constexpr (MODE == kGated) {
+    typedef const float __attribute__((address_space(4)))* cfloat_ptr;
+    const cfloat_ptr th = (cfloat_ptr)(uintptr_t)(a.tau_stats + (int64_t)seq * a.n_q_heads + kvh * G);
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      if (k < G) theta = head == k ? th[k] : theta;
+    if (!col_valid) theta = -INFINITY;
+  }
 
   // LDS operands, read one group ahead of their use so that the read
   // latency overlaps the previous group's MFMAs
@@ -634,7 +658,11 @@ void decode_attn_kernel(AttnArgs a) {
         sv[i] = fmaf(lo16(km_g[i]), acc[i], fmaf(hi16(km_g[i]), qs[gi], sv[i]));
       __builtin_amdgcn_sched_barrier(0);
     }
-    u32x4 vw = codes(sp, (int)L.v_codes, 0), vm = vmeta(sp, 0);  // in flight during the softmax
+    u32x4 vw, vm;
+    if constexpr (MODE != kStats) {
+      vw = codes(sp, (int)L.v_codes, 0);  // in flight during the softmax
+      vm = vmeta(sp, 0);
+    }
 
     // exchange the half scores with the partner wave: publish (the release
     // orders the data before the flag), then wait for the partner's; both
@@ -669,6 +697,10 @@ void decode_attn_kernel(AttnArgs a) {
         if (!vis) s[i] = -INFINITY;
       }
     }
+    if constexpr (MODE == kGated) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) s[i] = s[i] >= theta ? s[i] : -INFINITY;
+    }
     float mb = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     mb = xor16_max(mb);
     mb = xor32_max(mb);
@@ -698,6 +730,7 @@ void decode_attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(s[i] - m_run);
     l_run += (p[0] + p[1]) + (p[2] + p[3]);
+    if constexpr (MODE == kStats) return;
 
     // O^T += V^T . P'^T with P' = p * v_scale as f16 hi (c < 8) / residual
     // (c >= 8): x = p * v_scale in f32, hi = f16(x), residual = f16(x - hi),
@@ -748,6 +781,27 @@ void decode_attn_kernel(AttnArgs a) {
   // ---- epilogue: merge the four pairs, inverse rotation, store ----
   l_run = xor16_sum(l_run);
   l_run = xor32_sum(l_run);
+  if constexpr (MODE == kStats) {
+    // the split's softmax statistics per head: max and sum over the pairs
+    if (hi && col_valid && half == 0 && j == 0) {
+      ml_s[pair][head][0] = m_run;
+      ml_s[pair][head][1] = l_run;
+    }
+    __syncthreads();
+    if (wave == 0 && lane < G) {
+      float M = ml_s[0][lane][0];
+#pragma unroll
+      for (int q = 1; q < kAttnPairs; q++) M = fmaxf(M, ml_s[q][lane][0]);
+      float Lsum = 0.0f;
+#pragma unroll
+      for (int q = 0; q < kAttnPairs; q++)
+        Lsum = fmaf(__builtin_amdgcn_exp2f(ml_s[q][lane][0] - M), ml_s[q][lane][1], Lsum);
+      const int64_t r = ((int64_t)seq * a.part_stride + split) * a.n_q_heads + (int64_t)kvh * G + lane;
+      a.part_ml[r * 2 + 0] = M;
+      a.part_ml[r * 2 + 1] = Lsum;
+    }
+    return;
+  }
 #pragma unroll
   for (int gi = 0; gi < GH; gi++) {
     bacc[gi] = xor16_sum(bacc[gi]);
@@ -904,9 +958,18 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
       }
     }
     const int64_t o_idx = ((int64_t)seq * a.n_q_heads + h) * D + blockIdx.x * 64 + tid * 4;
+    // sparse-V: the kept weights are normalised by the full sum L of the
+    // stats pass (no renormalisation, gemma4_attention.rs:226-232), taken at
+    // its max M
+    float gated = 0.0f;
+    if (a.tau > 0.0f) {
+      const int64_t nh = (int64_t)gridDim.z * a.n_q_heads, r = (int64_t)seq * a.n_q_heads + h;
+      const float Mf = a.tau_stats[nh + r], Lf = a.tau_stats[2 * nh + r];
+      gated = (Lf > 0.0f && Mx != -INFINITY) ? exp2f(Mx - Mf) / Lf : 0.0f;
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const float v = L > 0.0f ? s[i] / L : 0.0f;
+      const float v = a.tau > 0.0f ? s[i] * gated : (L > 0.0f ? s[i] / L : 0.0f);
       if (a.out_f32)
         reinterpret_cast<float*>(a.out)[o_idx + i] = v;
       else
@@ -915,13 +978,48 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
   }
 }
 
+// Sparse-V thresholds from the stats pass, one thread per (q head,
+// sequence): the full softmax max M and sum L over the splits' (m, l), and
+// theta = M + log2(tau * L), so that a weight 2^(s - M) / L >= tau exactly
+// when its base-2 score s >= theta. No visible token: theta = +inf.
+__global__ __launch_bounds__(64) void tau_threshold_kernel(AttnArgs a) {
+  const int seq = blockIdx.y, h = blockIdx.x * 64 + threadIdx.x;
+  if (h >= a.n_q_heads) return;
+  const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
+  const SeqGeom geo =
+      seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
+  const int n_splits = n_splits_for(geo, a.bps, a.max_splits);
+  const int64_t base = (int64_t)seq * a.part_stride * a.n_q_heads + h;
+  float M = -INFINITY, L = 0.0f;
+  for (int sp = 0; sp < n_splits; sp++) {
+    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (base + (int64_t)sp * a.n_q_heads) * 2);
+    const float mn = fmaxf(M, ml.x);
+    L = fmaf(ml.y, exp2f(ml.x - mn), L * exp2f(M - mn));
+    M = mn;
+  }
+  const int64_t nh = (int64_t)gridDim.y * a.n_q_heads, r = (int64_t)seq * a.n_q_heads + h;
+  a.tau_stats[r] = L > 0.0f ? M + log2f(a.tau * L) : INFINITY;
+  a.tau_stats[nh + r] = M;
+  a.tau_stats[2 * nh + r] = L;
+}
+
 template <int D, int BITS>
 hipError_t launch_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                     hipEvent_t ev0, hipEvent_t ev1) {
   dim3 grid(n_kv_heads, n_seqs, a.max_splits + a.new_col);
-  if (ev0) (void)hipEventRecord(ev0, s);
-  hipLaunchKernelGGL((decode_attn_kernel<D, BITS>), grid, dim3(kAttnWaves * 64), 0, s, a);
-  hipError_t e = hipGetLastError();
+  hipError_t e;
+  if (a.tau > 0.0f) {  // sparse-V: stats pass, thresholds, gated pass, combine
+    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, kStats>), grid, dim3(kAttnWaves * 64), 0, s, a);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(tau_threshold_kernel, dim3((a.n_q_heads + 63) / 64, n_seqs), dim3(64), 0, s, a);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (ev0) (void)hipEventRecord(ev0, s);
+    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, kGated>), grid, dim3(kAttnWaves * 64), 0, s, a);
+  } else {
+    if (ev0) (void)hipEventRecord(ev0, s);
+    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, kDense>), grid, dim3(kAttnWaves * 64), 0, s, a);
+  }
+  e = hipGetLastError();
   if (ev1) (void)hipEventRecord(ev1, s);
   if (e != hipSuccess || a.direct) return e;
   dim3 cgrid(D / 64, a.n_q_heads, n_seqs);

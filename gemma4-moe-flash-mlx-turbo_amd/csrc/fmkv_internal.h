@@ -72,6 +72,12 @@ struct AttnArgs {
   int32_t new_col;
   const uint16_t* k_new;  // bf16 [n_seqs][n_kv_heads][D]
   const uint16_t* v_new;
+  // Sparse-V threshold (0: dense). With tau > 0 a stats pass writes, per
+  // (sequence, q head), the base-2 score threshold theta = M + log2(tau * L)
+  // and the full softmax max M and sum L: tau_stats = [theta | M | L], each
+  // [n_seqs][n_q_heads].
+  float tau;
+  float* tau_stats;
 };
 
 struct ReadArgs {

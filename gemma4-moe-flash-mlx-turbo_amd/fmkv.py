@@ -326,18 +326,19 @@ class PagedPool:
                                            _stream(stream)))
 
     def attention(self, q, block_tables, seq_lens, max_seq_len: int, scale: float = 1.0,
-                  out=None, dtype=torch.bfloat16, stream=None):
+                  sparse_v_tau: float = 0.0, out=None, dtype=torch.bfloat16, stream=None):
         """q bf16 [n_seqs, n_q_heads, D]; seq_lens int32 [n_seqs]."""
         if out is None:
             out = torch.empty(q.shape, dtype=dtype, device=q.device)
         _check(self._lib.fmkv_paged_decode_attention(
             self._h, _ptr(q), _ptr(block_tables), block_tables.shape[1], _ptr(seq_lens),
-            q.shape[0], max_seq_len, q.shape[1], scale, 0.0, _ptr(out), _dtype_code(out.dtype),
-            _stream(stream)))
+            q.shape[0], max_seq_len, q.shape[1], scale, sparse_v_tau, _ptr(out),
+            _dtype_code(out.dtype), _stream(stream)))
         return out
 
     def decode_step(self, keys, values, block_tables, start_pos, seq_lens, max_seq_len: int, q,
-                    scale: float = 1.0, out=None, dtype=torch.bfloat16, stream=None):
+                    scale: float = 1.0, sparse_v_tau: float = 0.0, out=None, dtype=torch.bfloat16,
+                    stream=None):
         """append(keys, values, ...) at start_pos, then attention over seq_lens
         (= start_pos + n_new) in one call."""
         if out is None:
@@ -345,7 +346,7 @@ class PagedPool:
         _check(self._lib.fmkv_paged_decode_step(
             self._h, _ptr(keys), _ptr(values), _ptr(block_tables), block_tables.shape[1],
             _ptr(start_pos), _ptr(seq_lens), keys.shape[0], keys.shape[1], max_seq_len, _ptr(q),
-            q.shape[1], scale, 0.0, _ptr(out), _dtype_code(out.dtype), _stream(stream)))
+            q.shape[1], scale, sparse_v_tau, _ptr(out), _dtype_code(out.dtype), _stream(stream)))
         return out
 
     def read_codes(self, stream=None):

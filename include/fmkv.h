@@ -100,17 +100,21 @@ int fmkv_cache_trim(fmkv_cache* cache, int64_t keep_last);
  * at src/model/gemma4_attention.rs:94-103 for L == 1 (Gemma-4: scale 1.0).
  * The current position attends to its own quantized K/V, as in the
  * reference where the round trip precedes the concat (src/cache.rs:295-298).
- * sparse_v_tau must be 0 (the tau gate of gemma4_attention.rs:196-234 is not
- * implemented; nonzero returns FMKV_ERR_UNSUPPORTED). */
+ * sparse_v_tau > 0 is the reference's sparse-V decode
+ * (src/model/gemma4_attention.rs:196-234): softmax weights below tau are
+ * zeroed without renormalisation. It reads the keys twice (a statistics
+ * pass, then the gated pass); 0 is plain softmax attention. Negative or
+ * non-finite tau returns FMKV_ERR_INVALID_ARG. */
 int fmkv_decode_attention(fmkv_cache* cache, const void* q_bf16, int32_t n_q_heads, float scale,
                           float sparse_v_tau, void* out, int32_t out_dtype, void* stream);
 
 /* One decode step of an attention layer, as Gemma4Attention::forward runs it
  * (src/model/gemma4_attention.rs:84-103): cache.update_and_fetch(k, v) for
  * n_tokens new positions, then attention of q over every visible position --
- * fmkv_cache_append followed by fmkv_decode_attention, with the q rotation
- * done inside the append launch. Arguments and errors as those two calls;
- * nothing is launched or changed when validation fails. */
+ * fmkv_cache_append followed by fmkv_decode_attention. With one new token
+ * and sparse_v_tau == 0 this is a single attention launch (plus the split
+ * combine) that also appends the token. Arguments and errors as those two
+ * calls; nothing is launched or changed when validation fails. */
 int fmkv_decode_step(fmkv_cache* cache, const void* k_bf16, const void* v_bf16, int64_t n_tokens,
                      const void* q_bf16, int32_t n_q_heads, float scale, float sparse_v_tau,
                      void* out, int32_t out_dtype, void* stream);
@@ -151,7 +155,8 @@ int fmkv_paged_append(fmkv_pool* pool, const void* k_bf16, const void* v_bf16,
 
 /* Decode attention for n_seqs sequences; seq_lens: int32 device [n_seqs]
  * (positions visible, current token included); max_seq_len bounds them.
- * q: bf16 [n_seqs][n_q_heads][head_dim]; out: [n_seqs][n_q_heads][head_dim]. */
+ * q: bf16 [n_seqs][n_q_heads][head_dim]; out: [n_seqs][n_q_heads][head_dim].
+ * scale and sparse_v_tau as in fmkv_decode_attention. */
 int fmkv_paged_decode_attention(fmkv_pool* pool, const void* q_bf16, const int32_t* block_tables,
                                 int32_t max_blocks, const int32_t* seq_lens, int32_t n_seqs,
                                 int32_t max_seq_len, int32_t n_q_heads, float scale,
@@ -159,9 +164,10 @@ int fmkv_paged_decode_attention(fmkv_pool* pool, const void* q_bf16, const int32
 
 /* Batched decode step: fmkv_paged_append of n_new tokens per sequence at
  * start_pos, then fmkv_paged_decode_attention with seq_lens (which the
- * caller sets to start_pos + n_new), the q rotation riding in the append
- * launch (the per-layer sequence of src/model/gemma4_attention.rs:84-103 for
- * a batch of requests). */
+ * caller sets to start_pos + n_new) -- the per-layer sequence of
+ * src/model/gemma4_attention.rs:84-103 for a batch of requests. With one new
+ * token per sequence and sparse_v_tau == 0 the attention launch appends the
+ * tokens itself (at seq_lens - 1). */
 int fmkv_paged_decode_step(fmkv_pool* pool, const void* k_bf16, const void* v_bf16,
                            const int32_t* block_tables, int32_t max_blocks,
                            const int32_t* start_pos, const int32_t* seq_lens, int32_t n_seqs,

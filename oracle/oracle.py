@@ -404,3 +404,15 @@ class OracleCache:
         if k.shape[0] == 0:
             return np.zeros(q.shape)
         return attention_f64(q, k, v, None, scale, tau)
+
+    def attention_weights(self, q_bf16, scale: float = 1.0) -> np.ndarray:
+        """Exact softmax weights [Hq, T] over the visible positions (the
+        `weights` of src/model/gemma4_attention.rs:224 before the tau gate)."""
+        k, _ = self.dequant_kv()
+        q = bf16_to_f32(q_bf16).astype(np.float64)
+        hq, hkv = q.shape[0], k.shape[1]
+        rep = hq // hkv
+        s = np.einsum("hd,thd->ht", q, np.repeat(k, rep, axis=1)) * scale
+        s -= s.max(axis=1, keepdims=True)
+        w = np.exp(s)
+        return w / w.sum(axis=1, keepdims=True)

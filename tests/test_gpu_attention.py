@@ -123,8 +123,8 @@ def test_attention_rejects_bad_arguments(gpu):
     cache = gpu.KVCache.new_quantized(256, 4, 2, capacity=32)
     q = torch.ones((4, 256), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(gpu.Exception_) as ei:
-        cache.attention(q, sparse_v_tau=1e-4)
-    assert ei.value.code == gpu.FMKV_ERR_UNSUPPORTED
+        cache.attention(q, sparse_v_tau=-1e-4)
+    assert ei.value.code == gpu.FMKV_ERR_INVALID_ARG
     with pytest.raises(gpu.Exception_):
         cache.attention(torch.ones((3, 256), dtype=torch.bfloat16, device="cuda"))
     with pytest.raises(gpu.Exception_):

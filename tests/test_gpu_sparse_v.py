@@ -1,0 +1,183 @@
+"""Sparse-V decode attention on the GPU against the oracle.
+
+src/model/gemma4_attention.rs:196-234: at decode with tau > 0 the softmax
+weights below tau are zeroed without renormalisation before the product
+with V. The oracle (ora_attention_f64) applies the same rule to the exact
+f64 weights; the kernel compares its f32 scores with the base-2 threshold
+M + log2(tau * L) of a statistics pass. Tolerance: max-abs 2e-2, mean-abs
+2e-3 (bf16 outputs also allow half a bf16 ulp of the reference)."""
+import numpy as np
+import pytest
+
+import synth
+from gpu_util import check_attention, dev_bf16, kv_batch
+
+pytestmark = pytest.mark.gpu
+
+
+def q_batch(seed, Hq, Hkv, D):
+    return synth.q_rows(seed + 100, Hq, Hkv, D, synth.outlier_channels(seed, Hkv, D))
+
+
+def filled(gpu, ora, D, bits, Hkv, T, window=0, seed=0):
+    cap = 0 if window else T + 16
+    cache = gpu.KVCache.new_quantized_with_window(D, bits, window, Hkv, cap)
+    oc = ora.OracleCache(Hkv, D, bits, window, cap)
+    k, v = kv_batch(seed, T, Hkv, D), kv_batch(seed + 1, T, Hkv, D)
+    cache.append(dev_bf16(k), dev_bf16(v))
+    oc.append(k, v)
+    return cache, oc
+
+
+def kept_fraction(oc, q, scale, tau):
+    """Share of (head, token) weights at or above tau (so a test is known to
+    exercise the gate rather than keep or drop everything)."""
+    w = oc.attention_weights(q, scale)
+    return float(np.mean(w >= tau))
+
+
+@pytest.mark.parametrize("D,bits,Hkv,Hq", [(512, 8, 2, 16), (256, 4, 8, 16), (128, 4, 4, 4),
+                                           (256, 8, 2, 12)])
+@pytest.mark.parametrize("T", [1, 33, 700, 1500])
+def test_sparse_v_matches_oracle(gpu, ora, D, bits, Hkv, Hq, T):
+    import torch
+
+    cache, oc = filled(gpu, ora, D, bits, Hkv, T, seed=T)
+    q = q_batch(T, Hq, Hkv, D)
+    # peaked (Gemma-4 scale 1.0) to soft: with the x20 outlier channels only
+    # scale 0.003 leaves many weights near the thresholds
+    for scale, tau in ((1.0, 1e-3), (1.0, 0.05), (0.05, 1.0 / (2 * T)), (0.05, 0.02), (0.003, 1e-3)):
+        ref = oc.attention(q, scale, tau)
+        out32 = cache.attention(dev_bf16(q), scale, sparse_v_tau=tau, dtype=torch.float32)
+        out16 = cache.attention(dev_bf16(q), scale, sparse_v_tau=tau, dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        check_attention(out32, ref, f"f32 scale={scale} tau={tau}")
+        check_attention(out16, ref, f"bf16 scale={scale} tau={tau}")
+
+
+def test_sparse_v_gate_is_exercised(gpu, ora):
+    """A soft softmax with tau at the 99th percentile of the weights: about 1%
+    of the weights are kept, and the result differs from dense attention by
+    far more than the tolerance."""
+    import torch
+
+    D, bits, Hkv, Hq, T = 512, 8, 2, 16, 1500
+    cache, oc = filled(gpu, ora, D, bits, Hkv, T, seed=5)
+    q = q_batch(5, Hq, Hkv, D)
+    scale = 0.003
+    tau = float(np.quantile(oc.attention_weights(q, scale), 0.99))
+    frac = kept_fraction(oc, q, scale, tau)
+    assert 0.005 < frac < 0.05, frac
+    dense = oc.attention(q, scale)
+    ref = oc.attention(q, scale, tau)
+    assert np.abs(dense - ref).max() > 0.1
+    out = cache.attention(dev_bf16(q), scale, sparse_v_tau=tau, dtype=torch.float32)
+    torch.cuda.synchronize()
+    check_attention(out, ref, "gated")
+
+
+def test_sparse_v_limits(gpu, ora):
+    """tau above every weight: zero output; a tau below every weight: dense."""
+    import torch
+
+    D, bits, Hkv, Hq, T = 256, 4, 8, 16, 300
+    cache, oc = filled(gpu, ora, D, bits, Hkv, T, seed=7)
+    q = q_batch(7, Hq, Hkv, D)
+    out = cache.attention(dev_bf16(q), 1.0, sparse_v_tau=1.5, dtype=torch.float32)
+    tiny = cache.attention(dev_bf16(q), 1.0, sparse_v_tau=1e-30, dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out).item() == 0
+    check_attention(tiny, oc.attention(q, 1.0), "tau 1e-30 vs dense")
+
+
+@pytest.mark.parametrize("bps", [1, 2, 3, 5])
+def test_sparse_v_split_counts_agree(gpu, ora, bps):
+    import torch
+
+    D, bits, Hkv, Hq, T = 512, 8, 2, 16, 700
+    cache, oc = filled(gpu, ora, D, bits, Hkv, T, seed=4)
+    q = q_batch(9, Hq, Hkv, D)
+    tau = 1.0 / 1400
+    ref = oc.attention(q, 0.05, tau)
+    gpu.set_blocks_per_split(bps)
+    try:
+        out = cache.attention(dev_bf16(q), 0.05, sparse_v_tau=tau, dtype=torch.float32)
+        torch.cuda.synchronize()
+    finally:
+        gpu.set_blocks_per_split(0)
+    check_attention(out, ref, f"bps={bps}")
+
+
+@pytest.mark.parametrize("D,bits", [(256, 4), (256, 8)])
+def test_sparse_v_ring_steps(gpu, ora, D, bits):
+    """Sliding layer W = 64: decode steps through two wraps with tau > 0 (the
+    step appends, then runs both passes)."""
+    import torch
+
+    Hkv, Hq, W = 8, 16, 64
+    cache = gpu.KVCache.new_quantized_with_window(D, bits, W, Hkv, 0)
+    oc = ora.OracleCache(Hkv, D, bits, W, 0)
+    k0, v0 = kv_batch(1, 40, Hkv, D), kv_batch(2, 40, Hkv, D)
+    cache.append(dev_bf16(k0), dev_bf16(v0))
+    oc.append(k0, v0)
+    for step in range(100):
+        k = kv_batch(100 + 2 * step, 1, Hkv, D, special=False)
+        v = kv_batch(101 + 2 * step, 1, Hkv, D, special=False)
+        q = q_batch(300 + step, Hq, Hkv, D)
+        out = cache.decode_step(dev_bf16(k), dev_bf16(v), dev_bf16(q), 0.05, sparse_v_tau=0.01,
+                                dtype=torch.float32)
+        oc.append(k, v)
+        torch.cuda.synchronize()
+        if step % 9 == 0 or step > 90:
+            check_attention(out, oc.attention(q, 0.05, 0.01), f"step {step}")
+
+
+def test_sparse_v_paged(gpu, ora):
+    """Paged pool, ragged sequences, shuffled block ids: gated decode step."""
+    import torch
+
+    D, bits, Hkv, Hq = 256, 4, 8, 16
+    lens = [37, 300, 16, 901]
+    n_seqs = len(lens)
+    need = [(n + 2 + 15) // 16 for n in lens]
+    max_blocks, n_blocks = max(need), sum(need)
+    perm = np.argsort(synth.splitmix64(77, n_blocks)).astype(np.int32)
+    tables = np.zeros((n_seqs, max_blocks), np.int32)
+    o = 0
+    for s, nb in enumerate(need):
+        tables[s, :nb] = perm[o:o + nb]
+        o += nb
+    pool = gpu.PagedPool(gpu.make_desc(Hkv, D, bits), n_blocks)
+    dtab = torch.from_numpy(tables).cuda()
+    oracles = []
+    for s, n in enumerate(lens):
+        oc = ora.OracleCache(Hkv, D, bits, 0, n + 2)
+        k, v = kv_batch(20 * s, n, Hkv, D), kv_batch(20 * s + 1, n, Hkv, D)
+        oc.append(k, v)
+        oracles.append(oc)
+        pool.append(dev_bf16(k[None]), dev_bf16(v[None]), dtab[s:s + 1].contiguous(),
+                    torch.zeros(1, dtype=torch.int32, device="cuda"))
+    k1 = np.stack([kv_batch(700 + s, 1, Hkv, D, special=False) for s in range(n_seqs)])
+    v1 = np.stack([kv_batch(800 + s, 1, Hkv, D, special=False) for s in range(n_seqs)])
+    start = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    q = np.stack([q_batch(950 + s, Hq, Hkv, D) for s in range(n_seqs)])
+    tau = 2e-3
+    out = pool.decode_step(dev_bf16(k1), dev_bf16(v1), dtab, start, start + 1, max(lens) + 1,
+                           dev_bf16(q), 0.05, sparse_v_tau=tau, dtype=torch.float32)
+    torch.cuda.synchronize()
+    for s in range(n_seqs):
+        oracles[s].append(k1[s], v1[s])
+        check_attention(out[s], oracles[s].attention(q[s], 0.05, tau), f"seq {s}")
+
+
+def test_sparse_v_rejects_bad_tau(gpu):
+    import torch
+
+    cache = gpu.KVCache.new_quantized_with_window(256, 4, 0, 8, 64)
+    k = torch.zeros((4, 8, 256), dtype=torch.bfloat16, device="cuda")
+    cache.append(k, k)
+    q = torch.zeros((16, 256), dtype=torch.bfloat16, device="cuda")
+    for bad in (-1e-3, float("nan"), float("inf")):
+        with pytest.raises(gpu.Exception_) as e:
+            cache.attention(q, 1.0, sparse_v_tau=bad)
+        assert e.value.code == gpu.FMKV_ERR_INVALID_ARG

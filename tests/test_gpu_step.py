@@ -100,8 +100,8 @@ def test_step_validation_leaves_cache_unchanged(gpu):
     assert cache.offset() == 0
     q = torch.ones((4, 256), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(gpu.Exception_) as ei:
-        cache.decode_step(k, k, q, sparse_v_tau=0.5)
-    assert ei.value.code == gpu.FMKV_ERR_UNSUPPORTED
+        cache.decode_step(k, k, q, sparse_v_tau=-0.5)
+    assert ei.value.code == gpu.FMKV_ERR_INVALID_ARG
     assert cache.offset() == 0
     out = cache.decode_step(k, k, q, dtype=torch.float32)
     torch.cuda.synchronize()

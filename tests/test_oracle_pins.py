@@ -361,6 +361,26 @@ def test_attention_matches_numpy(ora, tau):
                        atol=1e-12)
 
 
+def test_cache_attention_weights_agree_with_attention(ora):
+    """OracleCache.attention_weights (used to size the sparse-V tests) gives the
+    weights that OracleCache.attention applies: rows sum to 1, w @ V is the
+    dense result and (w * [w >= tau]) @ V the gated one."""
+    H, D, hq = 2, 128, 4
+    oc = ora.OracleCache(H, D, 4, 0, 80)
+    rng = np.random.default_rng(11)
+    kv = [synth.f32_to_bf16_bits(rng.standard_normal((70, H, D)).astype(np.float32)) for _ in range(2)]
+    oc.append(kv[0], kv[1])
+    q = synth.f32_to_bf16_bits(rng.standard_normal((hq, D)).astype(np.float32))
+    w = oc.attention_weights(q, 0.2)
+    assert w.shape == (hq, 70) and np.allclose(w.sum(axis=1), 1.0, atol=1e-12)
+    _, v = oc.dequant_kv()
+    vh = np.repeat(v, hq // H, axis=1)  # [t, hq, d]
+    assert np.allclose(np.einsum("ht,thd->hd", w, vh), oc.attention(q, 0.2), atol=1e-10)
+    tau = np.median(w)
+    wg = np.where(w >= tau, w, 0.0)
+    assert np.allclose(np.einsum("ht,thd->hd", wg, vh), oc.attention(q, 0.2, tau), atol=1e-10)
+
+
 def test_lse_merge_equals_full_softmax(ora):
     rng = np.random.default_rng(5)
     s = rng.standard_normal(40) * 5
