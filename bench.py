@@ -103,13 +103,15 @@ def run_c3(args) -> dict:
     outp = out.data_ptr()
     i = 0
 
+    tau = float(args.sparse_v_tau)
+
     def step():
         nonlocal i
         if args.unfused:
             rc = lib.fmkv_cache_append(h, kp[i], vp[i], 1, stream)
-            rc |= lib.fmkv_decode_attention(h, qp[i], Hq, 1.0, 0.0, outp, fmkv.DTYPE_BF16, stream)
+            rc |= lib.fmkv_decode_attention(h, qp[i], Hq, 1.0, tau, outp, fmkv.DTYPE_BF16, stream)
         else:
-            rc = lib.fmkv_decode_step(h, kp[i], vp[i], 1, qp[i], Hq, 1.0, 0.0, outp,
+            rc = lib.fmkv_decode_step(h, kp[i], vp[i], 1, qp[i], Hq, 1.0, tau, outp,
                                       fmkv.DTYPE_BF16, stream)
         if rc:
             raise RuntimeError(lib.fmkv_last_error().decode())
@@ -166,7 +168,7 @@ def run_c3(args) -> dict:
             "workload": "gemma4-global-layer decode at 32K: Hq 16, Hkv 2, head_dim 512, "
                         "8-bit group-64 affine, f16 scale/bias, 1 token append + attention per step",
             "context": T0, "batch": 1, "n_q_heads": Hq, "n_kv_heads": Hkv, "head_dim": D,
-            "bits": bits, "group": 64,
+            "bits": bits, "group": 64, "sparse_v_tau": tau,
         },
         "hbm_frac_of_value": round(value / HBM_PEAK_GBS, 4),
         "append_tokens_per_s": {"chunked_prefill_2048": round(append_prefill_tps, 1)},
@@ -503,6 +505,9 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--bps", type=int, default=0, help="blocks per split-K work-group (0: auto)")
+    ap.add_argument("--sparse-v-tau", type=float, default=0.0,
+                    help="c3: sparse-V threshold (0: dense softmax attention; > 0 adds the "
+                         "statistics pass and times the gated pass as the split kernel)")
     ap.add_argument("--unfused", action="store_true",
                     help="time fmkv_cache_append + fmkv_decode_attention instead of fmkv_decode_step")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",

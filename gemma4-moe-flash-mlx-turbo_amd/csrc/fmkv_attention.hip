@@ -978,29 +978,33 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
   }
 }
 
-// Sparse-V thresholds from the stats pass, one thread per (q head,
-// sequence): the full softmax max M and sum L over the splits' (m, l), and
+// Sparse-V thresholds from the stats pass, one wave per (q head, sequence):
+// the full softmax max M and sum L over the splits' (m, l) (lane i merges
+// splits i, i + 64, ...; the lanes meet in a butterfly), and
 // theta = M + log2(tau * L), so that a weight 2^(s - M) / L >= tau exactly
 // when its base-2 score s >= theta. No visible token: theta = +inf.
 __global__ __launch_bounds__(64) void tau_threshold_kernel(AttnArgs a) {
-  const int seq = blockIdx.y, h = blockIdx.x * 64 + threadIdx.x;
-  if (h >= a.n_q_heads) return;
+  const int h = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
   const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
   const int n_splits = n_splits_for(geo, a.bps, a.max_splits);
   const int64_t base = (int64_t)seq * a.part_stride * a.n_q_heads + h;
   float M = -INFINITY, L = 0.0f;
-  for (int sp = 0; sp < n_splits; sp++) {
+  for (int sp = lane; sp < n_splits; sp += 64) {
     const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (base + (int64_t)sp * a.n_q_heads) * 2);
     const float mn = fmaxf(M, ml.x);
     L = fmaf(ml.y, exp2f(ml.x - mn), L * exp2f(M - mn));
     M = mn;
   }
-  const int64_t nh = (int64_t)gridDim.y * a.n_q_heads, r = (int64_t)seq * a.n_q_heads + h;
-  a.tau_stats[r] = L > 0.0f ? M + log2f(a.tau * L) : INFINITY;
-  a.tau_stats[nh + r] = M;
-  a.tau_stats[2 * nh + r] = L;
+  const float Mw = group_max<64>(M, lane);
+  L = group_sum<64>(L > 0.0f ? L * exp2f(M - Mw) : 0.0f, lane);
+  if (lane == 0) {
+    const int64_t nh = (int64_t)gridDim.y * a.n_q_heads, r = (int64_t)seq * a.n_q_heads + h;
+    a.tau_stats[r] = L > 0.0f ? Mw + log2f(a.tau * L) : INFINITY;
+    a.tau_stats[nh + r] = Mw;
+    a.tau_stats[2 * nh + r] = L;
+  }
 }
 
 template <int D, int BITS>
@@ -1011,7 +1015,7 @@ hipError_t launch_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s
   if (a.tau > 0.0f) {  // sparse-V: stats pass, thresholds, gated pass, combine
     hipLaunchKernelGGL((decode_attn_kernel<D, BITS, kStats>), grid, dim3(kAttnWaves * 64), 0, s, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(tau_threshold_kernel, dim3((a.n_q_heads + 63) / 64, n_seqs), dim3(64), 0, s, a);
+    hipLaunchKernelGGL(tau_threshold_kernel, dim3(a.n_q_heads, n_seqs), dim3(64), 0, s, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (ev0) (void)hipEventRecord(ev0, s);
     hipLaunchKernelGGL((decode_attn_kernel<D, BITS, kGated>), grid, dim3(kAttnWaves * 64), 0, s, a);
