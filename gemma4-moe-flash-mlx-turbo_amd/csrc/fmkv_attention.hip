@@ -51,6 +51,8 @@
 // kernel's arithmetic) and contribute its attention as one more partial; the
 // split columns leave the new token's slot out. A decode step is then this
 // launch and the combine.
+#include <hip/hip_ext.h>
+
 #include "fmkv_device.h"
 #include "fmkv_internal.h"
 #include "fmkv_quant.h"
@@ -1007,24 +1009,32 @@ __global__ __launch_bounds__(64) void tau_threshold_kernel(AttnArgs a) {
   }
 }
 
+// The split kernel of one mode; with events, they are recorded by the
+// dispatch itself (start and end of the kernel's execution, as a kernel
+// trace times it), else a plain launch.
+template <int D, int BITS, int MODE>
+hipError_t launch_split(const AttnArgs& a, dim3 grid, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
+  if (ev0 && ev1)
+    hipExtLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE>), grid, dim3(kAttnWaves * 64), 0, s, ev0,
+                          ev1, 0, a);
+  else
+    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE>), grid, dim3(kAttnWaves * 64), 0, s, a);
+  return hipGetLastError();
+}
+
 template <int D, int BITS>
 hipError_t launch_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                     hipEvent_t ev0, hipEvent_t ev1) {
   dim3 grid(n_kv_heads, n_seqs, a.max_splits + a.new_col);
   hipError_t e;
   if (a.tau > 0.0f) {  // sparse-V: stats pass, thresholds, gated pass, combine
-    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, kStats>), grid, dim3(kAttnWaves * 64), 0, s, a);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = launch_split<D, BITS, kStats>(a, grid, s, nullptr, nullptr)) != hipSuccess) return e;
     hipLaunchKernelGGL(tau_threshold_kernel, dim3(a.n_q_heads, n_seqs), dim3(64), 0, s, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    if (ev0) (void)hipEventRecord(ev0, s);
-    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, kGated>), grid, dim3(kAttnWaves * 64), 0, s, a);
+    e = launch_split<D, BITS, kGated>(a, grid, s, ev0, ev1);
   } else {
-    if (ev0) (void)hipEventRecord(ev0, s);
-    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, kDense>), grid, dim3(kAttnWaves * 64), 0, s, a);
+    e = launch_split<D, BITS, kDense>(a, grid, s, ev0, ev1);
   }
-  e = hipGetLastError();
-  if (ev1) (void)hipEventRecord(ev1, s);
   if (e != hipSuccess || a.direct) return e;
   dim3 cgrid(D / 64, a.n_q_heads, n_seqs);
   hipLaunchKernelGGL((combine_kernel<D>), cgrid, dim3(256), 0, s, a);

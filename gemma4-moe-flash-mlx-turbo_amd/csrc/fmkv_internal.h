@@ -101,7 +101,8 @@ struct FetchArgs {
 };
 
 hipError_t launch_append(const AppendArgs& a, int n_seqs, int max_tasks, hipStream_t s);
-// ev_begin / ev_end (optional) are recorded around the split-K kernel only.
+// ev_begin / ev_end (optional, both or neither) are recorded by the split-K
+// kernel's dispatch: the start and end of its execution.
 hipError_t launch_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                                    hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr);
 hipError_t launch_read_codes(const ReadArgs& a, hipStream_t s);
