@@ -180,7 +180,7 @@ def run_c3(args) -> dict:
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": TRAFFIC_BYTES_PER_LAUNCH,
             "traffic_source": TRAFFIC_SOURCE,
-            "kernel": "decode_attn_kernel<512, 8>",
+            "kernel": "decode_attn_kernel<512, 8, 0>",
             "avg_kernel_us": round(kern_s * 1e6, 3),
             "bytes_per_launch": int(launch_bytes),
         },
