@@ -251,7 +251,7 @@ __device__ inline void copy_q_row(const AttnArgs& a, uint8_t* dst, int seq, int 
 // the other waves' copy issue. Every thread of the work-group calls it (it
 // holds two barriers).
 template <int D, int BITS>
-__device__ void build_q_table(const AttnArgs& a, uint8_t* tab, int wave, int lane) {
+__device__ void build_q_table(const AttnArgs& a, uint8_t* tab, int wave, int lane, uint32_t sbits) {
   constexpr int E = D / 64, NG = D / 64, LPG = 64 / E;
   const bool hv = wave < a.group;
   float x[E];
@@ -266,7 +266,6 @@ __device__ void build_q_table(const AttnArgs& a, uint8_t* tab, int wave, int lan
       x[2 * k + 1] = __uint_as_float(w & 0xffff0000u) * a.qscale;
     }
   }
-  const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
   float gsum = 0.0f;
   if (hv) {
     wave_fwht<E>(x, lane);
@@ -369,7 +368,8 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, int64_t T, int
   const int G = a.group;
   copy_q_row<D>(a, tab, seq, kvh, wave, lane);
   wait_vmcnt<0>();
-  build_q_table<D, BITS>(a, tab, wave, lane);
+  const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
+  build_q_table<D, BITS>(a, tab, wave, lane, sbits);
   if (wave >= 2) return;  // no barrier follows
 
   const bool isv = wave == 1;
@@ -390,7 +390,6 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, int64_t T, int
 
   float x[E];
   load_row<E>((isv ? a.v_new : a.k_new) + ((int64_t)seq * a.st.n_kv_heads + kvh) * D + d0, x);
-  const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
   wave_fwht<E>(x, lane);
 #pragma unroll
   for (int i = 0; i < E; i++) x[i] = apply_sign(x[i] * a.c, sbits, i);
@@ -556,7 +555,9 @@ void decode_attn_kernel(AttnArgs a) {
   for (int s = 0; s < NQ; s++)
     if (s < nb) copy_block(s, pb0 + (int64_t)kAttnPairs * s);
   wait_copies<CP, NQ>(nb < NQ ? nb : NQ);  // the q copy preceded every block
-  build_q_table<D, BITS>(a, scratch, wave, lane);
+  // this lane's RHT signs, for the q rotation and the inverse rotation
+  const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
+  build_q_table<D, BITS>(a, scratch, wave, lane, sbits);
 #pragma unroll
   for (int s = NQ; s < NST; s++)
     if (s < nb) copy_block(s, pb0 + (int64_t)kAttnPairs * s);
@@ -809,22 +810,22 @@ void decode_attn_kernel(AttnArgs a) {
     bacc[gi] = xor16_sum(bacc[gi]);
     bacc[gi] = xor32_sum(bacc[gi]);
   }
-  if constexpr (kBiasedCodes<BITS>) {
-    // the V codes entered the MFMAs as 1024 + code: remove 1024 x the
-    // column's P' summed over all tokens (4 per lane, 4 lanes)
-#pragma unroll
-    for (int gi = 0; gi < GH; gi++) {
-      const float t = xor32_sum(xor16_sum(psum[gi]));
-#pragma unroll
-      for (int ct = 0; ct < 4; ct++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) o[gi * 4 + ct][i] = fmaf(-1024.0f, t, o[gi * 4 + ct][i]);
-    }
-  }
+  // fold the residual columns (c >= 8) into the high-part columns (c < 8)
 #pragma unroll
   for (int k = 0; k < GH * 4; k++)
 #pragma unroll
     for (int i = 0; i < 4; i++) o[k][i] = o[k][i] + row_ror8(o[k][i]);
+  if constexpr (kBiasedCodes<BITS>) {
+    // the V codes entered the MFMAs as 1024 + code: the merged row loses
+    // 1024 x the head's P' (both column halves) summed over all tokens,
+    // taken together with the bias sum of each group
+#pragma unroll
+    for (int gi = 0; gi < GH; gi++) {
+      float t = xor32_sum(xor16_sum(psum[gi]));
+      t = t + row_ror8(t);
+      bacc[gi] = fmaf(-1024.0f, t, bacc[gi]);
+    }
+  }
 
   // The pair's own stages become its merge rows [head][QS] as soon as both of
   // its waves are done with them (all copies were waited for in the last
@@ -852,7 +853,6 @@ void decode_attn_kernel(AttnArgs a) {
   // head w on wave w
   if (wave < G) {
     const int hh = wave;
-    const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
     float M = ml_s[0][hh][0];
 #pragma unroll
     for (int q = 1; q < kAttnPairs; q++) M = fmaxf(M, ml_s[q][hh][0]);
