@@ -63,7 +63,7 @@ def run_c3(args) -> dict:
     Hq, Hkv, D, bits, T0 = 16, 2, 512, 8, args.context
     per_tok = bytes_per_token_head(D, bits)
     n_dec = args.warmup + 2 * args.steps + 1
-    cache = fmkv.KVCache.new_quantized(D, bits, Hkv, capacity=T0 + n_dec + 16)
+    cache = fmkv.KVCache.new_quantized(D, bits, Hkv, capacity=T0 + n_dec + args.graph_steps + 16)
 
     # ---- prefill: chunked appends of 2048 tokens (timed separately) ----
     chunk = 2048
@@ -151,6 +151,43 @@ def run_c3(args) -> dict:
     log(f"step {ms_per_step*1e3:.1f} us, split kernel {kern_s*1e6:.2f} us over {n_rec} launches, "
         f"{achieved:.0f} GB/s, splits={cache.decode_splits()}")
 
+    # The next graph_steps steps captured into a HIP graph and replayed: a
+    # replay repeats the same appends (the same codes into the same slots)
+    # and the same attention reads, so it redoes exactly the steps' work,
+    # without the per-launch cost of eager submission. Informational; the
+    # headline value above is eager.
+    graph_us = None
+    if args.graph_steps > 0 and tau == 0.0:
+        gs = torch.cuda.Stream()
+        gs.wait_stream(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        j0 = i
+        try:
+            with torch.cuda.graph(g, stream=gs):
+                for j in range(args.graph_steps):
+                    t = (j0 + j) % n_dec
+                    rc = lib.fmkv_decode_step(h, kp[t], vp[t], 1, qp[t], Hq, 1.0, tau, outp,
+                                              fmkv.DTYPE_BF16, gs.cuda_stream)
+                    if rc:
+                        raise RuntimeError(lib.fmkv_last_error().decode())
+        except RuntimeError as e:  # e.g. a workspace that would have to grow
+            log(f"graph capture skipped: {e}")
+            g = None
+        if g is not None:
+            with torch.cuda.stream(gs):  # replay() launches on the current stream
+                g.replay()
+                gs.synchronize()
+                reps = 4
+                gev0, gev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                gev0.record(gs)
+                for _ in range(reps):
+                    g.replay()
+                gev1.record(gs)
+                gs.synchronize()
+            graph_us = gev0.elapsed_time(gev1) * 1e3 / (reps * args.graph_steps)
+            log(f"graph: {graph_us:.2f} us/step over {reps} replays of {args.graph_steps} steps")
+
     res = {
         "metric": "decode-attn GB/s & % HBM peak over quantized KV at 32K ctx; append tokens/s",
         "value": round(value, 2),
@@ -172,6 +209,7 @@ def run_c3(args) -> dict:
         },
         "hbm_frac_of_value": round(value / HBM_PEAK_GBS, 4),
         "append_tokens_per_s": {"chunked_prefill_2048": round(append_prefill_tps, 1)},
+        "graph_step_us": None if graph_us is None else round(graph_us, 3),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
@@ -505,6 +543,8 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--bps", type=int, default=0, help="blocks per split-K work-group (0: auto)")
+    ap.add_argument("--graph-steps", type=int, default=64,
+                    help="c3: also time this many steps captured in a HIP graph (0: skip)")
     ap.add_argument("--sparse-v-tau", type=float, default=0.0,
                     help="c3: sparse-V threshold (0: dense softmax attention; > 0 adds the "
                          "statistics pass and times the gated pass as the split kernel)")

@@ -1,0 +1,67 @@
+"""Decode steps captured in a HIP graph replay exactly the eager results.
+
+A graph of n consecutive `fmkv_decode_step` calls repeats, on every replay,
+the same appends (the same codes into the same slots) and the same
+attention reads. Linear cache: a replay rewrites positions nobody beyond
+them reads, so every replay reproduces the eager outputs of those steps
+bit for bit. Ring of W slots: the graph spans one whole wrap (n = W), and
+replay r reproduces the r-th eager pass over the same inputs (from the
+second pass on, every slot holds what the previous pass wrote). The
+workspace is sized by an eager step before the capture (nothing may
+allocate inside it), and the steps stay inside one split plan. Each replay
+is followed by unrelated eager work and a synchronisation, and every
+replay is checked."""
+import pytest
+
+from gpu_util import dev_bf16, kv_batch
+import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("D,bits,Hkv,Hq,W,T0", [
+    (512, 8, 2, 16, 0, 295),   # global layer: positions 296..304 stay in 19 blocks
+    (256, 4, 8, 16, 64, 200),  # sliding ring: 4 blocks once full
+])
+def test_graph_replays_match_eager(gpu, D, bits, Hkv, Hq, W, T0):
+    import torch
+
+    cap = 0 if W else T0 + 32
+    caches = [gpu.KVCache.new_quantized_with_window(D, bits, W, Hkv, cap) for _ in range(2)]
+    k0, v0 = dev_bf16(kv_batch(1, T0, Hkv, D)), dev_bf16(kv_batch(2, T0, Hkv, D))
+    n = W if W else 8
+    ks = [dev_bf16(kv_batch(10 + j, 1, Hkv, D, special=False)) for j in range(n + 1)]
+    vs = [dev_bf16(kv_batch(40 + j, 1, Hkv, D, special=False)) for j in range(n + 1)]
+    qs = [dev_bf16(synth.q_rows(70 + j, Hq, Hkv, D, None)) for j in range(n + 1)]
+    for c in caches:
+        c.append(k0, v0)
+        c.decode_step(ks[0], vs[0], qs[0], 1.0, dtype=torch.float32)  # sizes the workspace
+    eager, graphed = caches
+    passes = 3 if W else 1
+    want = [[eager.decode_step(ks[j], vs[j], qs[j], 1.0, dtype=torch.float32) for j in range(1, n + 1)]
+            for _ in range(passes)]
+    torch.cuda.synchronize()
+
+    outs = [torch.empty((Hq, D), dtype=torch.float32, device="cuda") for _ in range(n)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for j in range(n):
+            graphed.decode_step(ks[j + 1], vs[j + 1], qs[j + 1], 1.0, out=outs[j], stream=s)
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        noise = torch.randn(1 << 16, device="cuda").sum()  # unrelated eager work
+        torch.cuda.synchronize()
+        assert torch.isfinite(noise)
+        w = want[min(rep, passes - 1)]
+        for j in range(n):
+            assert torch.equal(outs[j], w[j]), f"replay {rep} step {j}"
+    ca, ma = eager.read_codes()
+    cb, mb = graphed.read_codes()
+    torch.cuda.synchronize()
+    assert torch.equal(ca, cb) and torch.equal(ma, mb)
