@@ -239,6 +239,36 @@ int check_attn_args(const fmkv_cache_desc& d, const void* q, int32_t n_q_heads, 
 
 // Validation and launch arguments of an append of n tokens at the cache's
 // offset (no state change).
+// The layer prologue's arguments (no HIP call): affine mode, a k_norm
+// weight, positive finite eps and theta, rope_dims a power of 2 in
+// [2 * head_dim / 64, head_dim] (the rotated pairs then sit in different
+// lanes of the append kernel's row layout).
+int check_prologue(const fmkv_cache_desc& d, const fmkv_kv_prologue* pro) {
+  if (!pro) return fail(FMKV_ERR_INVALID_ARG, "prologue is null");
+  if (d.mode != FMKV_MODE_AFFINE)
+    return fail(FMKV_ERR_UNSUPPORTED, "the fused prologue is for affine-mode caches");
+  if (!pro->k_norm_weight) return fail(FMKV_ERR_INVALID_ARG, "k_norm_weight must be a device pointer");
+  if (!(pro->eps > 0.0f) || !std::isfinite(pro->eps))
+    return fail(FMKV_ERR_INVALID_ARG, "eps must be finite and > 0");
+  if (!(pro->rope_theta > 0.0f) || !std::isfinite(pro->rope_theta))
+    return fail(FMKV_ERR_INVALID_ARG, "rope_theta must be finite and > 0");
+  const int rd = pro->rope_dims;
+  if (rd < 2 * (d.head_dim / 64) || rd > d.head_dim || (rd & (rd - 1)) != 0)
+    return fail(FMKV_ERR_UNSUPPORTED,
+                "rope_dims must be a power of 2 in [2 * head_dim / 64, head_dim]");
+  if (pro->v_from_k != 0 && pro->v_from_k != 1)
+    return fail(FMKV_ERR_INVALID_ARG, "v_from_k must be 0 or 1");
+  return FMKV_OK;
+}
+
+void set_prologue(const fmkv_kv_prologue* pro, fmkv::AppendArgs* a) {
+  a->k_norm_w = static_cast<const uint16_t*>(pro->k_norm_weight);
+  a->eps = pro->eps;
+  a->rope_dims = pro->rope_dims;
+  a->rope_theta = pro->rope_theta;
+  a->v_from_k = pro->v_from_k;
+}
+
 int prepare_append(const fmkv_cache* c, const void* k, const void* v, int64_t n,
                    fmkv::AppendArgs* a, int64_t* tasks) {
   if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
@@ -474,6 +504,22 @@ int fmkv_cache_append(fmkv_cache* c, const void* k, const void* v, int64_t n, vo
   return FMKV_OK;
 }
 
+int fmkv_cache_append_projected(fmkv_cache* c, const void* k, const void* v, int64_t n,
+                                const fmkv_kv_prologue* pro, void* stream) {
+  if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
+  int rc = check_prologue(c->desc, pro);
+  if (rc) return rc;
+  fmkv::AppendArgs a;
+  int64_t tasks = 0;
+  rc = prepare_append(c, k, pro->v_from_k ? k : v, n, &a, &tasks);
+  if (rc || n == 0) return rc;
+  set_prologue(pro, &a);
+  hipError_t e = fmkv::launch_append(a, 1, (int)tasks, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "append launch");
+  c->offset += n;
+  return FMKV_OK;
+}
+
 int fmkv_decode_step(fmkv_cache* c, const void* k, const void* v, int64_t n, const void* q,
                      int32_t n_q_heads, float scale, float tau, void* out, int32_t out_dtype,
                      void* stream) {
@@ -635,6 +681,24 @@ int fmkv_paged_append(fmkv_pool* p, const void* k, const void* v, const int32_t*
   int rc = prepare_paged_append(p, k, v, block_tables, max_blocks, start_pos, n_seqs, n_new, &a,
                                 &tasks);
   if (rc || n_seqs == 0 || n_new == 0) return rc;
+  hipError_t e = fmkv::launch_append(a, n_seqs, tasks, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "paged append launch");
+  return FMKV_OK;
+}
+
+int fmkv_paged_append_projected(fmkv_pool* p, const void* k, const void* v,
+                                const int32_t* block_tables, int32_t max_blocks,
+                                const int32_t* start_pos, int32_t n_seqs, int32_t n_new,
+                                const fmkv_kv_prologue* pro, void* stream) {
+  if (!p) return fail(FMKV_ERR_INVALID_ARG, "pool is null");
+  int rc = check_prologue(p->desc, pro);
+  if (rc) return rc;
+  fmkv::AppendArgs a;
+  int tasks = 0;
+  rc = prepare_paged_append(p, k, pro->v_from_k ? k : v, block_tables, max_blocks, start_pos, n_seqs,
+                            n_new, &a, &tasks);
+  if (rc || n_seqs == 0 || n_new == 0) return rc;
+  set_prologue(pro, &a);
   hipError_t e = fmkv::launch_append(a, n_seqs, tasks, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "paged append launch");
   return FMKV_OK;

@@ -9,7 +9,10 @@
 //  - affine mode: MLX group-64 affine quantization (4/8-bit, f16 scale/bias);
 //  - codebook mode: the reference's own TurboQuant Lloyd-Max binning;
 //  - slot write: ring slot pos % W for sliding layers, pos for global layers,
-//    block table for paged pools.
+//    block table for paged pools;
+//  - optionally, the layer's prologue first (src/model/gemma4_attention.rs
+//    :52-81): K = RoPE(k_norm(k_proj)) rounded to bf16, V = v_norm(v_proj)
+//    in f32 (or v_norm of the raw K for K==V layers).
 // Every float op is written out in the oracle's order and the file is built
 // with -ffp-contract=off, so codes and scales are bit-identical to it.
 #include "fmkv_device.h"
@@ -38,6 +41,69 @@ __device__ inline float canonical_sumsq(const float (&x)[E], int lane) {
     acc = acc + sq;
   }
   return group_sum<64>(acc, lane);
+}
+
+__device__ inline float bf16_round(float v) { return __uint_as_float((uint32_t)f32_to_bf16(v) << 16); }
+
+// Value of lane (lane ^ m) for a runtime m in {1, 2, ..., 32}.
+__device__ inline float xor_partner_rt(float v, int m, int lane) {
+  switch (m) {
+    case 1: return xor_partner<1>(v, lane);
+    case 2: return xor_partner<2>(v, lane);
+    case 4: return xor_partner<4>(v, lane);
+    case 8: return xor_partner<8>(v, lane);
+    case 16: return xor_partner<16>(v, lane);
+    default: return xor_partner<32>(v, lane);
+  }
+}
+
+// k_norm then RoPE of one K row (src/model/gemma4_attention.rs:63, :78-81),
+// in the oracle's order: fast::rms_norm (x * r) * w with
+// r = 1 / sqrt(sum(x^2) / D + eps) (the canonical sum), rounded to bf16;
+// then MLX fast::rope (non-traditional): pair (d, d + rope_dims/2) turns by
+// a = f32(pos) * f32(theta^(-2i/rope_dims)), cos/sin of the f32 angle taken
+// in double; rounded to bf16. The pair partner sits in lane
+// lane ^ (rope_dims / 2 / E).
+template <int D>
+__device__ inline void k_prologue(float (&x)[D / 64], const AppendArgs& a, int64_t pos, int lane) {
+  constexpr int E = D / 64;
+  const float ms = canonical_sumsq<E>(x, lane) / (float)D;
+  const float r = 1.0f / sqrtf(ms + a.eps);
+  float w[E];
+  load_row<E>(a.k_norm_w + lane * E, w);
+#pragma unroll
+  for (int i = 0; i < E; i++) x[i] = bf16_round((x[i] * r) * w[i]);
+  const int half = a.rope_dims >> 1;
+  float p[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) p[i] = xor_partner_rt(x[i], half / E, lane);
+#pragma unroll
+  for (int i = 0; i < E; i++) {
+    const int d = lane * E + i;
+    if (d < a.rope_dims) {
+      const bool lower = d < half;
+      const int fi = lower ? d : d - half;
+      const float f = (float)pow((double)a.rope_theta, -2.0 * (double)fi / (double)a.rope_dims);
+      const float ang = (float)pos * f;
+      const float c = (float)cos((double)ang), s = (float)sin((double)ang);
+      x[i] = lower ? bf16_round((x[i] * c) - (p[i] * s)) : bf16_round((p[i] * s) + (x[i] * c));
+    }
+  }
+}
+
+// v_norm of one V row (src/model/norm.rs:16-29, MLX ops on bf16 in the
+// oracle's order): x2 = bf16(x * x); mean = bf16(sum(x2) / D) (canonical
+// sum); out = x * (1 / sqrt(mean + eps)) in f32.
+template <int D>
+__device__ inline void v_prologue(float (&x)[D / 64], float eps, int lane) {
+  constexpr int E = D / 64;
+  float acc = bf16_round(x[0] * x[0]);
+#pragma unroll
+  for (int i = 1; i < E; i++) acc = acc + bf16_round(x[i] * x[i]);
+  const float mean = bf16_round(group_sum<64>(acc, lane) / (float)D);
+  const float rms = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+  for (int i = 0; i < E; i++) x[i] = x[i] * rms;
 }
 
 __device__ inline int cb_index(float z, int bits) {
@@ -140,8 +206,8 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
     const int r = wv + k * kWaves;
     rows[k] = row_of(r >> 1);
     const int row = rows[k] < 0 ? 0 : rows[k];
-    const uint16_t* src =
-        ((r & 1) ? a.v : a.k) + (((int64_t)seq * a.n_new + row) * H + h) * D + lane * E;
+    const uint16_t* src = ((r & 1) && !a.v_from_k ? a.v : a.k) +
+                          (((int64_t)seq * a.n_new + row) * H + h) * D + lane * E;
     load_row<E>(src, x[k]);
   }
   if (tid < kBlockTokens) cov_row[tid] = row_of(tid);
@@ -170,6 +236,12 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
     const int t = r >> 1, isv = r & 1;
     if (rows[k] < 0) continue;
     uint32_t* stage = isv ? vst : kst;
+    if (a.k_norm_w) {
+      if (isv)
+        v_prologue<D>(x[k], a.eps, lane);
+      else
+        k_prologue<D>(x[k], a, pos0 + rows[k], lane);
+    }
     if constexpr (MODE == kAffine) {
       wave_fwht<E>(x[k], lane);
 #pragma unroll

@@ -43,6 +43,13 @@ struct AppendArgs {
   float c;             // 1/sqrt(D) (f32)
   float sqrt_d;        // sqrt(D) (f32), codebook mode
   int32_t cb_bits;     // codebook bits
+  // The layer's prologue before the append (k_norm, v_norm, RoPE at each
+  // token's position); k_norm_w null: the rows are stored as given.
+  const uint16_t* k_norm_w = nullptr;  // bf16 [D]
+  float eps = 0.0f;
+  int32_t rope_dims = 0;
+  float rope_theta = 0.0f;
+  int32_t v_from_k = 0;  // V rows are v_norm of the raw K rows (K==V layers)
 };
 
 struct AttnArgs {

@@ -42,6 +42,7 @@ EXPORTED = (
     "fmkv_cache_destroy", "fmkv_cache_offset", "fmkv_cache_stored_len", "fmkv_cache_append",
     "fmkv_cache_trim", "fmkv_decode_attention", "fmkv_cache_fetch", "fmkv_cache_read_codes",
     "fmkv_pool_create", "fmkv_pool_destroy", "fmkv_paged_append", "fmkv_paged_decode_attention",
+    "fmkv_cache_append_projected", "fmkv_paged_append_projected",
     "fmkv_pool_read_codes", "fmkv_set_blocks_per_split", "fmkv_cache_decode_splits",
     "fmkv_profile_enable", "fmkv_profile_collect", "fmkv_decode_step", "fmkv_paged_decode_step",
 )
@@ -66,6 +67,38 @@ class CacheDesc(ctypes.Structure):
         ("capacity", ctypes.c_int64),
         ("sign_seed", ctypes.c_uint64),
     ]
+
+
+class KvPrologue(ctypes.Structure):
+    """fmkv_kv_prologue: the layer's k_norm / v_norm / RoPE fused into the
+    append (src/model/gemma4_attention.rs:52-81)."""
+    _fields_ = [
+        ("k_norm_weight", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("rope_dims", ctypes.c_int32),
+        ("rope_theta", ctypes.c_float),
+        ("v_from_k", ctypes.c_int32),
+    ]
+
+
+def make_prologue(k_norm_weight: torch.Tensor, eps: float, rope_dims: int, rope_theta: float,
+                  v_from_k: bool = False) -> KvPrologue:
+    """k_norm_weight: bf16 [head_dim] on the device. The struct holds a
+    reference to the tensor, so the weight lives as long as the prologue
+    (the C struct itself carries only the device address)."""
+    if k_norm_weight.dtype != torch.bfloat16 or k_norm_weight.dim() != 1:
+        raise ValueError("k_norm_weight must be bf16 [head_dim]")
+    if not k_norm_weight.is_contiguous():
+        raise ValueError("k_norm_weight must be contiguous")
+    pro = KvPrologue(k_norm_weight.data_ptr(), eps, rope_dims, rope_theta, 1 if v_from_k else 0)
+    pro.weight = k_norm_weight
+    return pro
+
+
+def _check_prologue_weight(prologue: KvPrologue, head_dim: int) -> None:
+    w = getattr(prologue, "weight", None)
+    if w is not None and w.numel() != head_dim:
+        raise ValueError(f"k_norm_weight has {w.numel()} elements; head_dim is {head_dim}")
 
 
 _lib = None
@@ -99,6 +132,9 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         "fmkv_pool_create": ([P(CacheDesc), i64, P(vp)], ctypes.c_int),
         "fmkv_pool_destroy": ([vp], ctypes.c_int),
         "fmkv_paged_append": ([vp, vp, vp, vp, i32, vp, i32, i32, vp], ctypes.c_int),
+        "fmkv_cache_append_projected": ([vp, vp, vp, i64, P(KvPrologue), vp], ctypes.c_int),
+        "fmkv_paged_append_projected": ([vp, vp, vp, vp, i32, vp, i32, i32, P(KvPrologue), vp],
+                                        ctypes.c_int),
         "fmkv_paged_decode_attention": ([vp, vp, vp, i32, vp, i32, i32, i32, ctypes.c_float,
                                          ctypes.c_float, vp, i32, vp], ctypes.c_int),
         "fmkv_pool_read_codes": ([vp, vp, vp, vp], ctypes.c_int),
@@ -224,6 +260,18 @@ class KVCache:
         _check(self._lib.fmkv_cache_append(self._h, _ptr(keys), _ptr(values), keys.shape[0],
                                            _stream(stream)))
 
+    def append_projected(self, keys: torch.Tensor, values: torch.Tensor | None,
+                         prologue: KvPrologue, stream=None) -> None:
+        """append() of raw k_proj / v_proj rows through the layer's prologue
+        (k_norm + RoPE on K, v_norm on V; values None with prologue.v_from_k)."""
+        if values is None:
+            values = keys
+        self._check_kv(keys, values)
+        _check_prologue_weight(prologue, self.desc.head_dim)
+        _check(self._lib.fmkv_cache_append_projected(self._h, _ptr(keys), _ptr(values),
+                                                     keys.shape[0], ctypes.byref(prologue),
+                                                     _stream(stream)))
+
     def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor, stream=None,
                          fetch: bool = False):
         """Store new positions; with fetch=True also return the visible
@@ -324,6 +372,17 @@ class PagedPool:
         _check(self._lib.fmkv_paged_append(self._h, _ptr(keys), _ptr(values), _ptr(block_tables),
                                            block_tables.shape[1], _ptr(start_pos), n_seqs, n_new,
                                            _stream(stream)))
+
+    def append_projected(self, keys, values, block_tables, start_pos, prologue: KvPrologue,
+                         stream=None) -> None:
+        """append() of raw projections through the layer's prologue."""
+        if values is None:
+            values = keys
+        n_seqs, n_new = keys.shape[0], keys.shape[1]
+        _check_prologue_weight(prologue, self.desc.head_dim)
+        _check(self._lib.fmkv_paged_append_projected(
+            self._h, _ptr(keys), _ptr(values), _ptr(block_tables), block_tables.shape[1],
+            _ptr(start_pos), n_seqs, n_new, ctypes.byref(prologue), _stream(stream)))
 
     def attention(self, q, block_tables, seq_lens, max_seq_len: int, scale: float = 1.0,
                   sparse_v_tau: float = 0.0, out=None, dtype=torch.bfloat16, stream=None):

@@ -108,6 +108,29 @@ int fmkv_cache_trim(fmkv_cache* cache, int64_t keep_last);
 int fmkv_decode_attention(fmkv_cache* cache, const void* q_bf16, int32_t n_q_heads, float scale,
                           float sparse_v_tau, void* out, int32_t out_dtype, void* stream);
 
+/* The layer's prologue before the cache store, fused into the append
+ * (src/model/gemma4_attention.rs:52-81; no separate pass over K/V):
+ *   K = RoPE(k_norm(k_proj)) -- fast::rms_norm with the layer's weight
+ *       (norm.rs:5-14), rounded to bf16, then fast::rope (non-traditional,
+ *       scale 1, at each token's position), rounded to bf16;
+ *   V = v_norm(v_proj) -- RMSNormNoScale (norm.rs:16-29), f32 -- or, with
+ *       v_from_k, v_norm of the raw K (K==V global layers, :54-59).
+ * rope_dims = head_dim * partial_rotary_factor (config.rs:209-225), a power
+ * of 2 in [2 * head_dim / 64, head_dim]. Affine-mode caches only. */
+typedef struct fmkv_kv_prologue {
+  const void* k_norm_weight; /* bf16 [head_dim], device */
+  float eps;                 /* rms_norm_eps (k_norm and v_norm) */
+  int32_t rope_dims;
+  float rope_theta;
+  int32_t v_from_k;          /* 1: V is taken from k_proj (v_proj ignored, may be NULL) */
+} fmkv_kv_prologue;
+
+/* fmkv_cache_append of raw projections through the prologue; RoPE positions
+ * start at the cache offset (the reference's cache.offset(), :73). */
+int fmkv_cache_append_projected(fmkv_cache* cache, const void* k_proj_bf16,
+                                const void* v_proj_bf16, int64_t n_tokens,
+                                const fmkv_kv_prologue* prologue, void* stream);
+
 /* One decode step of an attention layer, as Gemma4Attention::forward runs it
  * (src/model/gemma4_attention.rs:84-103): cache.update_and_fetch(k, v) for
  * n_tokens new positions, then attention of q over every visible position --
@@ -152,6 +175,13 @@ int fmkv_pool_destroy(fmkv_pool* pool);
 int fmkv_paged_append(fmkv_pool* pool, const void* k_bf16, const void* v_bf16,
                       const int32_t* block_tables, int32_t max_blocks, const int32_t* start_pos,
                       int32_t n_seqs, int32_t n_new, void* stream);
+
+/* fmkv_paged_append of raw projections through the prologue (see
+ * fmkv_cache_append_projected); RoPE positions start at start_pos. */
+int fmkv_paged_append_projected(fmkv_pool* pool, const void* k_proj_bf16, const void* v_proj_bf16,
+                                const int32_t* block_tables, int32_t max_blocks,
+                                const int32_t* start_pos, int32_t n_seqs, int32_t n_new,
+                                const fmkv_kv_prologue* prologue, void* stream);
 
 /* Decode attention for n_seqs sequences; seq_lens: int32 device [n_seqs]
  * (positions visible, current token included); max_seq_len bounds them.

@@ -475,6 +475,95 @@ void ora_codebook_round_trip(const uint32_t* packed, const uint16_t* norms, int6
 }
 
 /* ------------------------------------------------------------------------ */
+/* pre-append prologue: k_norm, v_norm, RoPE                                 */
+/* (src/model/gemma4_attention.rs:52-81, src/model/norm.rs:5-29; MLX         */
+/* fast::rms_norm and fast::rope, third-party, restated)                     */
+/* ------------------------------------------------------------------------ */
+
+/* Sum in the kernels' order (as canonical_sumsq, of the values themselves). */
+static float canonical_sum(const float* x, int d) {
+  float p[64];
+  int e = d / 64;
+  for (int l = 0; l < 64; l++) {
+    float acc = x[l * e];
+    for (int i = 1; i < e; i++) acc = acc + x[l * e + i];
+    p[l] = acc;
+  }
+  for (int m = 1; m < 64; m <<= 1) {
+    float q[64];
+    for (int l = 0; l < 64; l++) q[l] = p[l] + p[l ^ m];
+    memcpy(p, q, sizeof(p));
+  }
+  return p[0];
+}
+
+/* MLX fast::rope as gemma4_attention.rs:74-81 calls it (traditional =
+ * false, scale 1.0, offset = the cache offset): for i < dims/2 the pair
+ * (x_i, x_{i+dims/2}) turns by the angle a = f32(pos) * f_i with
+ * f_i = theta^(-2i/dims) rounded to f32; dims >= rope_dims pass through.
+ * The angle is formed in f32 as MLX forms it; its cos and sin are taken in
+ * double and rounded to f32. */
+float ora_rope_inv_freq(int i, int rope_dims, float theta) {
+  return (float)pow((double)theta, -2.0 * (double)i / (double)rope_dims);
+}
+
+void ora_rope_cos_sin(int64_t pos, int i, int rope_dims, float theta, float* c, float* s) {
+  const float a = (float)pos * ora_rope_inv_freq(i, rope_dims, theta);
+  *c = (float)cos((double)a);
+  *s = (float)sin((double)a);
+}
+
+/* One K row (gemma4_attention.rs:63 then :78-81): k_norm = fast::rms_norm
+ * (x * r) * w with r = 1 / sqrt(sum(x^2) / d + eps) in f32 (the sum in the
+ * kernels' order), rounded to bf16; then RoPE at pos, rounded to bf16. */
+void ora_k_prologue(const uint16_t* x_bf16, int d, const uint16_t* w_bf16, float eps, int64_t pos,
+                    int rope_dims, float theta, uint16_t* out_bf16) {
+  float x[512], y[512];
+  for (int j = 0; j < d; j++) x[j] = ora_bf16_to_f32(x_bf16[j]);
+  const float ms = canonical_sumsq(x, d) / (float)d;
+  const float r = 1.0f / sqrtf(ms + eps);
+  for (int j = 0; j < d; j++)
+    y[j] = ora_bf16_to_f32(ora_f32_to_bf16((x[j] * r) * ora_bf16_to_f32(w_bf16[j])));
+  const int half = rope_dims / 2;
+  for (int i = 0; i < half; i++) {
+    float c, s;
+    ora_rope_cos_sin(pos, i, rope_dims, theta, &c, &s);
+    const float x1 = y[i], x2 = y[i + half];
+    out_bf16[i] = ora_f32_to_bf16((x1 * c) - (x2 * s));
+    out_bf16[i + half] = ora_f32_to_bf16((x1 * s) + (x2 * c));
+  }
+  for (int j = rope_dims; j < d; j++) out_bf16[j] = ora_f32_to_bf16(y[j]);
+}
+
+/* One V row, RMSNormNoScale as norm.rs:16-29 chains MLX ops on a bf16
+ * array: x2 = bf16(x * x); mean = bf16(sum(x2) / d) (the sum in the
+ * kernels' order); rms = 1 / sqrt(mean + eps) in f32 (the eps Array is f32,
+ * so the sum promotes); out = x * rms in f32 (bf16 * f32 promotes). */
+void ora_v_prologue(const uint16_t* x_bf16, int d, float eps, float* out) {
+  float x2[512];
+  for (int j = 0; j < d; j++) {
+    const float x = ora_bf16_to_f32(x_bf16[j]);
+    x2[j] = ora_bf16_to_f32(ora_f32_to_bf16(x * x));
+  }
+  const float mean = ora_bf16_to_f32(ora_f32_to_bf16(canonical_sum(x2, d) / (float)d));
+  const float rms = 1.0f / sqrtf(mean + eps);
+  for (int j = 0; j < d; j++) out[j] = ora_bf16_to_f32(x_bf16[j]) * rms;
+}
+
+/* Rows [n][h][d] of one append: token t at position pos0 + t. v_bf16 NULL:
+ * a K==V layer, whose V is v_norm of the raw K (gemma4_attention.rs:54-59). */
+void ora_kv_prologue(const uint16_t* k_bf16, const uint16_t* v_bf16, int64_t n, int h, int d,
+                     int64_t pos0, const uint16_t* w_bf16, float eps, int rope_dims, float theta,
+                     uint16_t* k_out_bf16, float* v_out) {
+  for (int64_t t = 0; t < n; t++)
+    for (int hh = 0; hh < h; hh++) {
+      const int64_t r = (t * h + hh) * d;
+      ora_k_prologue(k_bf16 + r, d, w_bf16, eps, pos0 + t, rope_dims, theta, k_out_bf16 + r);
+      ora_v_prologue((v_bf16 ? v_bf16 : k_bf16) + r, d, eps, v_out + r);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* cache index semantics                                                     */
 /* ------------------------------------------------------------------------ */
 

@@ -69,6 +69,16 @@ void ora_codebook_dequant_rotated(const uint32_t* packed, const uint16_t* norms,
 void ora_codebook_round_trip(const uint32_t* packed, const uint16_t* norms, int64_t rows, int d,
                              int bits, const float* signs, uint16_t* out_bf16);
 
+/* pre-append prologue: k_norm, v_norm, RoPE */
+float ora_rope_inv_freq(int i, int rope_dims, float theta);
+void ora_rope_cos_sin(int64_t pos, int i, int rope_dims, float theta, float* c, float* s);
+void ora_k_prologue(const uint16_t* x_bf16, int d, const uint16_t* w_bf16, float eps, int64_t pos,
+                    int rope_dims, float theta, uint16_t* out_bf16);
+void ora_v_prologue(const uint16_t* x_bf16, int d, float eps, float* out);
+void ora_kv_prologue(const uint16_t* k_bf16, const uint16_t* v_bf16, int64_t n, int h, int d,
+                     int64_t pos0, const uint16_t* w_bf16, float eps, int rope_dims, float theta,
+                     uint16_t* k_out_bf16, float* v_out);
+
 /* cache index semantics */
 int64_t ora_ring_slot(int64_t pos, int64_t window);
 int64_t ora_slot_position(int64_t slot, int64_t offset, int64_t window);

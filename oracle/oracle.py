@@ -57,6 +57,11 @@ def lib() -> ctypes.CDLL:
             "ora_codebook_quantize": ([_vp, i64, i32, i32, _vp, _vp, _vp], None),
             "ora_codebook_dequant_rotated": ([_vp, _vp, i64, i32, i32, _vp], None),
             "ora_codebook_round_trip": ([_vp, _vp, i64, i32, i32, _vp, _vp], None),
+            "ora_rope_inv_freq": ([i32, i32, f32], f32),
+            "ora_rope_cos_sin": ([i64, i32, i32, f32, ctypes.POINTER(f32), ctypes.POINTER(f32)], None),
+            "ora_k_prologue": ([_vp, i32, _vp, f32, i64, i32, f32, _vp], None),
+            "ora_v_prologue": ([_vp, i32, f32, _vp], None),
+            "ora_kv_prologue": ([_vp, _vp, i64, i32, i32, i64, _vp, f32, i32, f32, _vp, _vp], None),
             "ora_ring_slot": ([i64, i64], i64),
             "ora_slot_position": ([i64, i64, i64], i64),
             "ora_causal_mask": ([i64, i64, _vp], None),
@@ -175,6 +180,20 @@ def rotate_rows_f32(x, sgn) -> np.ndarray:
     y = np.empty(x.shape, np.float32)
     lib().ora_rotate_rows_f32(_p(x), x.size // d, d, _p(_c(sgn, np.float32)), _p(y))
     return y
+
+
+def kv_prologue(k_bf16, v_bf16, pos0: int, w_bf16, eps: float, rope_dims: int, theta: float):
+    """K = RoPE(k_norm(k)) (bf16) and V = v_norm(v) (f32) of rows [n, h, d]
+    at positions pos0.. (src/model/gemma4_attention.rs:52-81, norm.rs:5-29);
+    v_bf16 None: V from the raw K (K==V layers)."""
+    k = _c(k_bf16, np.uint16)
+    n, h, d = k.shape
+    v = None if v_bf16 is None else _c(v_bf16, np.uint16)
+    ko = np.empty(k.shape, np.uint16)
+    vo = np.empty(k.shape, np.float32)
+    lib().ora_kv_prologue(_p(k), None if v is None else _p(v), n, h, d, pos0, _p(_c(w_bf16, np.uint16)),
+                          eps, rope_dims, theta, _p(ko), _p(vo))
+    return ko, vo
 
 
 def unrotate_rows_f64(y, sgn) -> np.ndarray:
@@ -348,13 +367,34 @@ class OracleCache:
         packed, norms = codebook_quantize(x_bf16, self.bits, self.sgn)
         return packed, norms[..., None]
 
+    def quantize_rows_f32(self, x):
+        """[..., D] f32 rows (a V row after v_norm) -> (packed, meta); affine mode."""
+        y = rotate_rows_f32(x, self.sgn)
+        packed, sc, bi = affine_quantize(y, self.bits)
+        meta = np.empty(sc.shape[:-1] + (2 * sc.shape[-1],), np.uint16)
+        meta[..., 0::2] = sc
+        meta[..., 1::2] = bi
+        return packed, meta
+
     def append(self, k_bf16, v_bf16) -> None:
         k_bf16 = np.asarray(k_bf16)
-        n = k_bf16.shape[0]
-        if self.W == 0 and self.offset + n > self.n_slots:
-            raise ValueError("capacity exceeded")
         kp, km = self.quantize_rows(k_bf16)
         vp, vm = self.quantize_rows(np.asarray(v_bf16))
+        self._store(kp, km, vp, vm)
+
+    def append_projected(self, k_bf16, v_bf16, w_bf16, eps: float, rope_dims: int,
+                         theta: float) -> None:
+        """append() of raw k_proj / v_proj rows through the layer's prologue
+        (kv_prologue at the cache offset); v_bf16 None: a K==V layer."""
+        k, v = kv_prologue(k_bf16, v_bf16, self.offset, w_bf16, eps, rope_dims, theta)
+        kp, km = self.quantize_rows(k)
+        vp, vm = self.quantize_rows_f32(v)
+        self._store(kp, km, vp, vm)
+
+    def _store(self, kp, km, vp, vm) -> None:
+        n = kp.shape[0]
+        if self.W == 0 and self.offset + n > self.n_slots:
+            raise ValueError("capacity exceeded")
         first = 0 if self.W == 0 else max(0, n - self.W)
         for i in range(first, n):
             s = ring_slot(self.offset + i, self.W)

@@ -420,3 +420,96 @@ def test_oracle_cache_ring_and_trim(ora):
     assert list(c.visible_positions()) == list(range(total - 10, total))
     k, v = c.dequant_kv()
     assert k.shape == (10, 2, 128) and np.allclose(k, v)
+
+
+# ------------------------------------------------------------ layer prologue
+def _bf16_rows(seed, shape, scale=1.0):
+    rng = np.random.default_rng(seed)
+    return synth.f32_to_bf16_bits((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+@pytest.mark.parametrize("d,rope_dims,theta", [(256, 256, 10000.0), (512, 128, 1e6), (128, 32, 10000.0)])
+def test_rope_is_the_textbook_rotation(ora, d, rope_dims, theta):
+    """K at position p is the position-0 K (k_norm only: RoPE at 0 turns by 0)
+    with each pair (i, i + rope_dims/2) turned by a = f32(p) * f32(theta^(-2i/
+    rope_dims)), computed here in f64; dims past rope_dims are unchanged.
+    Interleaved pairs, a flipped sign or another frequency law fail."""
+    x = _bf16_rows(21, (d,))
+    w = _bf16_rows(22, (d,), 0.3)
+    k0 = np.empty(d, np.uint16)
+    ora.lib().ora_k_prologue(ora._p(x), d, ora._p(w), 1e-6, 0, rope_dims, theta, ora._p(k0))
+    y0 = ora.bf16_to_f32(k0).astype(np.float64)
+    half = rope_dims // 2
+    i = np.arange(half)
+    f = (np.float64(theta) ** (-2.0 * i / rope_dims)).astype(np.float32)
+    for p in (1, 7, 1000, 100003):
+        kp = np.empty(d, np.uint16)
+        ora.lib().ora_k_prologue(ora._p(x), d, ora._p(w), 1e-6, p, rope_dims, theta, ora._p(kp))
+        got = ora.bf16_to_f32(kp).astype(np.float64)
+        a = (np.float32(p) * f).astype(np.float64)
+        x1, x2 = y0[:half], y0[half:rope_dims]
+        want = np.concatenate([x1 * np.cos(a) - x2 * np.sin(a), x1 * np.sin(a) + x2 * np.cos(a),
+                               y0[rope_dims:]])
+        # one bf16 rounding of the result (2^-8 relative) on top of exact math
+        assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + 1e-30), p
+        assert np.array_equal(got[rope_dims:], y0[rope_dims:])
+
+
+def test_k_norm_closed_forms(ora):
+    """fast::rms_norm: a constant row c gives w * c / sqrt(c^2 + eps); a random
+    row gives x * w / sqrt(mean(x^2) + eps) (one bf16 rounding)."""
+    d = 256
+    w = _bf16_rows(23, (d,))
+    wf = ora.bf16_to_f32(w).astype(np.float64)
+    for c, eps in ((0.75, 1e-6), (-3.0, 1e-2)):
+        x = synth.f32_to_bf16_bits(np.full(d, c, np.float32))
+        out = np.empty(d, np.uint16)
+        ora.lib().ora_k_prologue(ora._p(x), d, ora._p(w), eps, 0, d, 10000.0, ora._p(out))
+        want = wf * c / math.sqrt(c * c + eps)
+        assert np.allclose(ora.bf16_to_f32(out), want, rtol=2.0 ** -8, atol=0)
+    x = _bf16_rows(24, (d,), 2.0)
+    xf = ora.bf16_to_f32(x).astype(np.float64)
+    out = np.empty(d, np.uint16)
+    ora.lib().ora_k_prologue(ora._p(x), d, ora._p(w), 1e-6, 0, d, 10000.0, ora._p(out))
+    want = xf * wf / math.sqrt(np.mean(xf * xf) + 1e-6)
+    assert np.allclose(ora.bf16_to_f32(out), want, rtol=2.0 ** -7, atol=1e-30)
+
+
+def test_v_norm_closed_forms(ora):
+    """RMSNormNoScale (norm.rs:16-29): x / sqrt(mean(bf16(x^2)) + eps) with the
+    mean rounded to bf16; unit RMS for any row; a zero row stays zero."""
+    d = 512
+    x = _bf16_rows(25, (d,), 5.0)
+    xf = ora.bf16_to_f32(x).astype(np.float64)
+    out = np.empty(d, np.float32)
+    ora.lib().ora_v_prologue(ora._p(x), d, 1e-6, ora._p(out))
+    x2 = ora.bf16_to_f32(synth.f32_to_bf16_bits((xf * xf).astype(np.float32))).astype(np.float64)
+    mean = float(ora.bf16_to_f32(synth.f32_to_bf16_bits(np.array([np.mean(x2)], np.float32)))[0])
+    assert np.allclose(out, xf / math.sqrt(mean + 1e-6), rtol=1e-5, atol=0)
+    assert abs(math.sqrt(np.mean(out.astype(np.float64) ** 2)) - 1.0) < 1e-2
+    z = np.zeros(d, np.uint16)
+    ora.lib().ora_v_prologue(ora._p(z), d, 1e-6, ora._p(out))
+    assert np.all(out == 0)
+
+
+def test_kv_prologue_rows_and_k_eq_v(ora):
+    """Rows [n, h, d] take position pos0 + token; with no v_proj the V rows are
+    v_norm of the raw K rows (gemma4_attention.rs:54-59)."""
+    n, h, d = 3, 2, 128
+    k = _bf16_rows(26, (n, h, d))
+    v = _bf16_rows(27, (n, h, d))
+    w = _bf16_rows(28, (d,))
+    ko, vo = ora.kv_prologue(k, v, 40, w, 1e-6, 64, 10000.0)
+    ko2, vo2 = ora.kv_prologue(k, None, 40, w, 1e-6, 64, 10000.0)
+    assert np.array_equal(ko, ko2)
+    for t in range(n):
+        for hh in range(h):
+            one = np.empty(d, np.uint16)
+            ora.lib().ora_k_prologue(ora._p(np.ascontiguousarray(k[t, hh])), d, ora._p(w), 1e-6,
+                                     40 + t, 64, 10000.0, ora._p(one))
+            assert np.array_equal(ko[t, hh], one)
+            vv = np.empty(d, np.float32)
+            ora.lib().ora_v_prologue(ora._p(np.ascontiguousarray(v[t, hh])), d, 1e-6, ora._p(vv))
+            assert np.array_equal(vo[t, hh], vv)
+            ora.lib().ora_v_prologue(ora._p(np.ascontiguousarray(k[t, hh])), d, 1e-6, ora._p(vv))
+            assert np.array_equal(vo2[t, hh], vv)
