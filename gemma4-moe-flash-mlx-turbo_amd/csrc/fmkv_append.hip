@@ -1,5 +1,5 @@
-// Append kernel: rotate -> quantize -> slot write, one work-group per
-// (touched head-block, KV head, sequence).
+// Append kernel: rotate -> quantize -> slot write, one work-group of 8
+// waves per (touched head-block, KV head, sequence).
 //
 // Replaces the store half of KVCache::update_and_fetch (src/cache.rs:266-310)
 // and its quantizer turbo_round_trip_kv (src/cache.rs:94-129):
@@ -22,7 +22,7 @@
 namespace fmkv {
 namespace {
 
-constexpr int kAppendThreads = 256;
+constexpr int kAppendThreads = 512;
 
 __constant__ float kCbBounds2[3] = {-0.982f, 0.0f, 0.982f};
 __constant__ float kCbBounds3[7] = {-1.748f, -1.050f, -0.501f, 0.0f, 0.501f, 1.050f, 1.748f};
@@ -44,67 +44,6 @@ __device__ inline float canonical_sumsq(const float (&x)[E], int lane) {
 }
 
 __device__ inline float bf16_round(float v) { return __uint_as_float((uint32_t)f32_to_bf16(v) << 16); }
-
-// Value of lane (lane ^ m) for a runtime m in {1, 2, ..., 32}.
-__device__ inline float xor_partner_rt(float v, int m, int lane) {
-  switch (m) {
-    case 1: return xor_partner<1>(v, lane);
-    case 2: return xor_partner<2>(v, lane);
-    case 4: return xor_partner<4>(v, lane);
-    case 8: return xor_partner<8>(v, lane);
-    case 16: return xor_partner<16>(v, lane);
-    default: return xor_partner<32>(v, lane);
-  }
-}
-
-// k_norm then RoPE of one K row (src/model/gemma4_attention.rs:63, :78-81),
-// in the oracle's order: fast::rms_norm (x * r) * w with
-// r = 1 / sqrt(sum(x^2) / D + eps) (the canonical sum), rounded to bf16;
-// then MLX fast::rope (non-traditional): pair (d, d + rope_dims/2) turns by
-// a = f32(pos) * f32(theta^(-2i/rope_dims)), cos/sin of the f32 angle taken
-// in double; rounded to bf16. The pair partner sits in lane
-// lane ^ (rope_dims / 2 / E).
-template <int D>
-__device__ inline void k_prologue(float (&x)[D / 64], const AppendArgs& a, int64_t pos, int lane) {
-  constexpr int E = D / 64;
-  const float ms = canonical_sumsq<E>(x, lane) / (float)D;
-  const float r = 1.0f / sqrtf(ms + a.eps);
-  float w[E];
-  load_row<E>(a.k_norm_w + lane * E, w);
-#pragma unroll
-  for (int i = 0; i < E; i++) x[i] = bf16_round((x[i] * r) * w[i]);
-  const int half = a.rope_dims >> 1;
-  float p[E];
-#pragma unroll
-  for (int i = 0; i < E; i++) p[i] = xor_partner_rt(x[i], half / E, lane);
-#pragma unroll
-  for (int i = 0; i < E; i++) {
-    const int d = lane * E + i;
-    if (d < a.rope_dims) {
-      const bool lower = d < half;
-      const int fi = lower ? d : d - half;
-      const float f = (float)pow((double)a.rope_theta, -2.0 * (double)fi / (double)a.rope_dims);
-      const float ang = (float)pos * f;
-      const float c = (float)cos((double)ang), s = (float)sin((double)ang);
-      x[i] = lower ? bf16_round((x[i] * c) - (p[i] * s)) : bf16_round((p[i] * s) + (x[i] * c));
-    }
-  }
-}
-
-// v_norm of one V row (src/model/norm.rs:16-29, MLX ops on bf16 in the
-// oracle's order): x2 = bf16(x * x); mean = bf16(sum(x2) / D) (canonical
-// sum); out = x * (1 / sqrt(mean + eps)) in f32.
-template <int D>
-__device__ inline void v_prologue(float (&x)[D / 64], float eps, int lane) {
-  constexpr int E = D / 64;
-  float acc = bf16_round(x[0] * x[0]);
-#pragma unroll
-  for (int i = 1; i < E; i++) acc = acc + bf16_round(x[i] * x[i]);
-  const float mean = bf16_round(group_sum<64>(acc, lane) / (float)D);
-  const float rms = 1.0f / sqrtf(mean + eps);
-#pragma unroll
-  for (int i = 0; i < E; i++) x[i] = x[i] * rms;
-}
 
 __device__ inline int cb_index(float z, int bits) {
   int idx = 0;
@@ -138,19 +77,35 @@ __device__ inline uint32_t v_clear_mask(int w, const int* cov) {
   return m;
 }
 
-template <int D, int BITS, int MODE>
+// Position of a lane's pair partner for RoPE, and its value: lane ^ m via
+// the LDS crossbar (m = rope_dims / 2 / E is known only at run time).
+__device__ inline float lane_xor_value(float v, int m, int lane) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ m) << 2, __float_as_int(v)));
+}
+
+// One work-group per (touched head-block, KV head, sequence), 8 waves: wave
+// w handles the K (w < 4) or V (w >= 4) rows of the four tokens 4q..4q+3,
+// q = w & 3, all four rows in lockstep (independent chains for the
+// scheduler). Codes are combined in registers (the elements of one K word;
+// the four tokens that share a V word) before one LDS atomic per word; the
+// block is then copied out with 16-byte stores. PRO: the layer's prologue
+// (k_norm + RoPE on K, v_norm on V) runs on the rows first.
+template <int D, int BITS, int MODE, bool PRO>
 __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
   constexpr int E = D / 64;
+  constexpr int R = 4;  // rows per wave
   constexpr BlockLayout L = make_layout(D, BITS, MODE);
   constexpr int kWords = (int)(L.code_bytes / 4);
-  constexpr int kWaves = kAppendThreads / 64;
-  constexpr int kRowsPerWave = 2 * kBlockTokens / kWaves;  // K and V rows of 16 slots
-  __shared__ uint32_t kst[kWords];
-  __shared__ uint32_t vst[kWords];
+  constexpr int kHalfMax = PRO ? D / 2 : 1;
+  __shared__ __align__(16) uint32_t kst[kWords];
+  __shared__ __align__(16) uint32_t vst[kWords];
   __shared__ int cov_row[kBlockTokens];
+  __shared__ float rope_f[kHalfMax];              // f32 theta^(-2i/rope_dims)
+  __shared__ float2 rope_cs[R][R][kHalfMax];      // per K wave: (cos, sin) per row, angle
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int isv = wv >> 2, quad = wv & 3;
   const int h = blockIdx.y, seq = blockIdx.z, bx = blockIdx.x;
   const int64_t pos0 = a.start_pos ? (int64_t)a.start_pos[seq] : a.start_scalar;
   const int64_t end = pos0 + a.n_new;
@@ -195,22 +150,27 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
   if (phys < 0 || phys >= a.st.n_blocks) return;
   uint8_t* blk = a.st.base + phys * a.st.block_stride + (int64_t)h * a.st.head_stride;
 
-  // this wave's input rows (r = wave + k * waves: slot r / 2, K or V by
-  // r & 1) are loaded first, so that they share one memory round trip with
-  // the V-word read below; rows not written here re-read row 0 unused
+  // the wave's four rows (rows not written here re-read row 0, unused)
   const int H = a.st.n_kv_heads;
-  float x[kRowsPerWave][E];
-  int rows[kRowsPerWave];
+  int rows[R];
+  bool any = false, all4 = true;
+  float x[R][E];
 #pragma unroll
-  for (int k = 0; k < kRowsPerWave; k++) {
-    const int r = wv + k * kWaves;
-    rows[k] = row_of(r >> 1);
-    const int row = rows[k] < 0 ? 0 : rows[k];
-    const uint16_t* src = ((r & 1) && !a.v_from_k ? a.v : a.k) +
+  for (int r = 0; r < R; r++) {
+    rows[r] = row_of(quad * R + r);
+    any = any || rows[r] >= 0;
+    all4 = all4 && rows[r] >= 0;
+    const int row = rows[r] < 0 ? 0 : rows[r];
+    const uint16_t* src = (isv && !a.v_from_k ? a.v : a.k) +
                           (((int64_t)seq * a.n_new + row) * H + h) * D + lane * E;
-    load_row<E>(src, x[k]);
+    load_row<E>(src, x[r]);
   }
+  const int half = a.rope_dims >> 1;
   if (tid < kBlockTokens) cov_row[tid] = row_of(tid);
+  if constexpr (PRO) {
+    for (int i = tid; i < half; i += kAppendThreads)
+      rope_f[i] = (float)pow((double)a.rope_theta, -2.0 * (double)i / (double)a.rope_dims);
+  }
   __syncthreads();
 
   bool all_cov = true;
@@ -227,87 +187,215 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
       vst[w] = 0u;
     }
   }
-  __syncthreads();
 
-  const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
+  if constexpr (PRO) {
+    if (!isv) {
+      // (cos, sin) of every (row, angle) pair once, spread over the lanes;
+      // angle a = f32(pos) * f32(theta^(-2i/rope_dims)), cos/sin in double
+      for (int j = lane; j < half; j += 64) {
+        const float f = rope_f[j];
 #pragma unroll
-  for (int k = 0; k < kRowsPerWave; k++) {
-    const int r = wv + k * kWaves;
-    const int t = r >> 1, isv = r & 1;
-    if (rows[k] < 0) continue;
-    uint32_t* stage = isv ? vst : kst;
-    if (a.k_norm_w) {
-      if (isv)
-        v_prologue<D>(x[k], a.eps, lane);
-      else
-        k_prologue<D>(x[k], a, pos0 + rows[k], lane);
-    }
-    if constexpr (MODE == kAffine) {
-      wave_fwht<E>(x[k], lane);
-#pragma unroll
-      for (int i = 0; i < E; i++) x[k][i] = apply_sign(x[k][i] * a.c, sbits, i);
-      uint32_t code[E];
-      float scale, bias;
-      affine_quant<E, BITS>(x[k], code, scale, bias, lane);
-#pragma unroll
-      for (int i = 0; i < E; i++) {
-        int64_t off;
-        int sh;
-        if (isv)
-          v_code_pos(BITS, t, lane * E + i, &off, &sh);
-        else
-          k_code_pos(BITS, t, lane * E + i, &off, &sh);
-        atomicOr(&stage[off >> 2], code[i] << sh);
+        for (int r = 0; r < R; r++) {
+          const float ang = (float)(pos0 + (rows[r] < 0 ? 0 : rows[r])) * f;
+          double sn, cs;
+          sincos((double)ang, &sn, &cs);
+          rope_cs[quad][r][j] = make_float2((float)cs, (float)sn);
+        }
       }
-      if ((lane % (64 / E)) == 0) {
-        const int g = lane / (64 / E);
-        const uint32_t sb = (uint32_t)f32_to_f16_bits(scale) |
-                            ((uint32_t)f32_to_f16_bits(bias) << 16);
-        *reinterpret_cast<uint32_t*>(blk + (isv ? L.v_meta : L.k_meta) + scale_pos(g, t)) = sb;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // k_norm (src/model/gemma4_attention.rs:63): r = 1 / sqrt(sum(x^2) / D
+      // + eps) with the canonical sum, x * r * w rounded to bf16
+      float w[E];
+      load_row<E>(a.k_norm_w + lane * E, w);
+      float rn[R];
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        rn[r] = 1.0f / sqrtf(canonical_sumsq<E>(x[r], lane) / (float)D + a.eps);
+#pragma unroll
+      for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int i = 0; i < E; i++) x[r][i] = bf16_round((x[r][i] * rn[r]) * w[i]);
+      // RoPE (non-traditional, :78-81): pair (d, d + rope_dims/2); the
+      // partner of lane l's dims sits in lane l ^ (rope_dims / 2 / E)
+      const int m = half / E;
+      float p[R][E];
+#pragma unroll
+      for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int i = 0; i < E; i++) p[r][i] = lane_xor_value(x[r][i], m, lane);
+      if (lane * E < a.rope_dims) {
+        const bool lower = lane * E < half;
+        const int f0 = lower ? lane * E : lane * E - half;
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+          for (int i = 0; i < E; i++) {
+            const float2 cs = rope_cs[quad][r][f0 + i];
+            x[r][i] = lower ? bf16_round((x[r][i] * cs.x) - (p[r][i] * cs.y))
+                            : bf16_round((p[r][i] * cs.y) + (x[r][i] * cs.x));
+          }
       }
     } else {
-      constexpr int bits = BITS;
-      const float norm = sqrtf(canonical_sumsq<E>(x[k], lane));
-      const float den = norm + 1e-8f;
+      // v_norm (src/model/norm.rs:16-29): x2 = bf16(x * x); mean =
+      // bf16(sum(x2) / D) (canonical sum); out = x * (1 / sqrt(mean + eps))
+      float acc[R];
 #pragma unroll
-      for (int i = 0; i < E; i++) x[k][i] = x[k][i] / den;
-      wave_fwht<E>(x[k], lane);
-      const int64_t row_bits = (int64_t)D * bits;
+      for (int r = 0; r < R; r++) {
+        acc[r] = bf16_round(x[r][0] * x[r][0]);
 #pragma unroll
-      for (int i = 0; i < E; i++) {
-        const float z = apply_sign(x[k][i] * a.c, sbits, i) * a.sqrt_d;
-        const uint32_t idx = (uint32_t)cb_index(z, bits);
-        const int64_t bit = t * row_bits + (int64_t)(lane * E + i) * bits;
-        const int wi = (int)(bit >> 5), off = (int)(bit & 31);
-        atomicOr(&stage[wi], idx << off);
-        if (off + bits > 32) atomicOr(&stage[wi + 1], idx >> (32 - off));
+        for (int i = 1; i < E; i++) acc[r] = acc[r] + bf16_round(x[r][i] * x[r][i]);
       }
-      if (lane == 0)
-        *reinterpret_cast<uint16_t*>(blk + (isv ? L.v_meta : L.k_meta) + t * 2) =
-            f32_to_f16_bits(norm);
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const float mean = bf16_round(group_sum<64>(acc[r], lane) / (float)D);
+        const float rms = 1.0f / sqrtf(mean + a.eps);
+#pragma unroll
+        for (int i = 0; i < E; i++) x[r][i] = x[r][i] * rms;
+      }
+    }
+  }
+
+  // x * (1/sqrt D) and the RHT sign as one multiplication by +-c
+  const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
+  float sc[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) sc[i] = ((sbits >> i) & 1u) ? -a.c : a.c;
+
+  uint32_t code[R][E];
+  uint32_t meta[R];
+  if constexpr (MODE == kAffine) {
+#pragma unroll
+    for (int r = 0; r < R; r++) wave_fwht<E>(x[r], lane);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+      for (int i = 0; i < E; i++) x[r][i] = x[r][i] * sc[i];
+      float scale, bias;
+      affine_quant<E, BITS>(x[r], code[r], scale, bias, lane);
+      meta[r] = (uint32_t)f32_to_f16_bits(scale) | ((uint32_t)f32_to_f16_bits(bias) << 16);
+    }
+  } else {
+    float norm[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      norm[r] = sqrtf(canonical_sumsq<E>(x[r], lane));
+      const float den = norm[r] + 1e-8f;
+#pragma unroll
+      for (int i = 0; i < E; i++) x[r][i] = x[r][i] / den;
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) wave_fwht<E>(x[r], lane);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+      for (int i = 0; i < E; i++) code[r][i] = (uint32_t)cb_index((x[r][i] * sc[i]) * a.sqrt_d, BITS);
+      meta[r] = (uint32_t)f32_to_f16_bits(norm[r]);
     }
   }
   __syncthreads();
 
-  uint32_t* kdst = reinterpret_cast<uint32_t*>(blk + L.k_codes);
-  uint32_t* vdst = reinterpret_cast<uint32_t*>(blk + L.v_codes);
-  for (int w = tid; w < kWords; w += kAppendThreads) {
+  if (any) {
+    uint32_t* stage = isv ? vst : kst;
+    if constexpr (MODE == kAffine) {
+      if (!isv) {
+        // G consecutive elements of a lane fall into one K word
+        constexpr int G = E < 32 / BITS ? E : 32 / BITS;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          if (rows[r] < 0) continue;
+#pragma unroll
+          for (int i0 = 0; i0 < E; i0 += G) {
+            int64_t off = 0;
+            int sh;
+            uint32_t word = 0;
+#pragma unroll
+            for (int j = 0; j < G; j++) {
+              k_code_pos(BITS, quad * R + r, lane * E + i0 + j, &off, &sh);
+              word |= code[r][i0 + j] << sh;
+            }
+            atomicOr(&stage[off >> 2], word);
+          }
+        }
+      } else {
+        // the four tokens of the quad share each V word
+#pragma unroll
+        for (int i = 0; i < E; i++) {
+          int64_t off = 0;
+          int sh;
+          uint32_t word = 0;
+#pragma unroll
+          for (int r = 0; r < R; r++) {
+            v_code_pos(BITS, quad * R + r, lane * E + i, &off, &sh);
+            if (rows[r] >= 0) word |= code[r][i] << sh;
+          }
+          atomicOr(&stage[off >> 2], word);
+        }
+      }
+      if ((lane % (64 / E)) == 0) {
+        const int g = lane / (64 / E);
+        uint32_t* mp = reinterpret_cast<uint32_t*>(blk + (isv ? L.v_meta : L.k_meta) +
+                                                   scale_pos(g, quad * R));
+        if (all4) {
+          *reinterpret_cast<uint4*>(mp) = make_uint4(meta[0], meta[1], meta[2], meta[3]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < R; r++)
+            if (rows[r] >= 0) mp[r] = meta[r];
+        }
+      }
+    } else {
+      // token row = bit stream, index j at bit j * bits: the lane's E
+      // indices are E * bits consecutive bits
+      constexpr int64_t row_bits = (int64_t)D * BITS;
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        if (rows[r] < 0) continue;
+        uint64_t v = 0;
+#pragma unroll
+        for (int i = 0; i < E; i++) v |= (uint64_t)code[r][i] << (i * BITS);
+        const int64_t bit = (quad * R + r) * row_bits + (int64_t)lane * E * BITS;
+        const int wi = (int)(bit >> 5), off = (int)(bit & 31);
+        v <<= off;
+        atomicOr(&stage[wi], (uint32_t)v);
+        if (off + E * BITS > 32) atomicOr(&stage[wi + 1], (uint32_t)(v >> 32));
+        if (lane == 0)
+          *reinterpret_cast<uint16_t*>(blk + (isv ? L.v_meta : L.k_meta) + (quad * R + r) * 2) =
+              (uint16_t)meta[r];
+      }
+    }
+  }
+  __syncthreads();
+
+  // 16-byte copy-out; K (and codebook V) chunks belong to one token each
+  uint4* kdst = reinterpret_cast<uint4*>(blk + L.k_codes);
+  uint4* vdst = reinterpret_cast<uint4*>(blk + L.v_codes);
+  const uint4* ks = reinterpret_cast<const uint4*>(kst);
+  const uint4* vs = reinterpret_cast<const uint4*>(vst);
+  for (int c = tid; c < kWords / 4; c += kAppendThreads) {
     int tk;
     if constexpr (MODE == kAffine) {
-      tk = ((w & 255) >> 2) & 15;
-      vdst[w] = vst[w];
+      tk = c & 15;
+      vdst[c] = vs[c];
     } else {
-      tk = (int)((int64_t)w * 4 / (L.code_bytes / kBlockTokens));
-      if (cov_row[tk] >= 0) vdst[w] = vst[w];
+      tk = (int)((int64_t)c * 16 / (L.code_bytes / kBlockTokens));
+      if (cov_row[tk] >= 0) vdst[c] = vs[c];
     }
-    if (cov_row[tk] >= 0) kdst[w] = kst[w];
+    if (cov_row[tk] >= 0) kdst[c] = ks[c];
   }
 }
 
 template <int D, int BITS, int MODE>
 hipError_t launch_t(const AppendArgs& a, int n_seqs, int max_tasks, hipStream_t s) {
   dim3 grid(max_tasks, a.st.n_kv_heads, n_seqs);
-  hipLaunchKernelGGL((append_kernel<D, BITS, MODE>), grid, dim3(kAppendThreads), 0, s, a);
+  if constexpr (MODE == kAffine) {
+    if (a.k_norm_w) {
+      hipLaunchKernelGGL((append_kernel<D, BITS, MODE, true>), grid, dim3(kAppendThreads), 0, s, a);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((append_kernel<D, BITS, MODE, false>), grid, dim3(kAppendThreads), 0, s, a);
   return hipGetLastError();
 }
 

@@ -136,7 +136,8 @@ __device__ inline void load_row(const uint16_t* src, float (&x)[E]) {
 }
 
 // Value of lane (lane ^ M), in registers: DPP quad_perm (M = 1, 2), row
-// shifts (M = 4: lanes with bit 2 clear read lane + 4, the others lane - 4),
+// shifts under bank masks (M = 4: lanes with bit 2 clear read lane + 4,
+// the others lane - 4),
 // row_ror:8 (M = 8) and the permlane swaps (M = 16, 32).
 template <int M>
 __device__ inline float xor_partner(float v, int lane) {
@@ -146,9 +147,10 @@ __device__ inline float xor_partner(float v, int lane) {
   } else if constexpr (M == 2) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xf, 0xf, false));
   } else if constexpr (M == 4) {
-    const int up = __builtin_amdgcn_update_dpp(0, iv, 0x104, 0xf, 0xf, false);  // lane + 4
-    const int dn = __builtin_amdgcn_update_dpp(0, iv, 0x114, 0xf, 0xf, false);  // lane - 4
-    return __builtin_bit_cast(float, (lane & 4) ? dn : up);
+    // banks 0 and 2 (lane bit 2 clear) read lane + 4 (row_shl:4); banks 1
+    // and 3 then read lane - 4 (row_shr:4) over the first result
+    const int up = __builtin_amdgcn_update_dpp(iv, iv, 0x104, 0xf, 0x5, false);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(up, iv, 0x114, 0xf, 0xA, false));
   } else if constexpr (M == 8) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xf, 0xf, false));
   } else if constexpr (M == 16) {
@@ -194,14 +196,25 @@ __device__ inline float group_min(float v, int lane) {
 }
 
 // One cross-lane FWHT stage at lane stride M: (a, b) -> (a + b, a - b), the
-// upper lane of each pair computing partner - own.
+// upper lane of each pair computing partner - own. Both are one fused
+// multiply-add fma(+-1, own, partner): the product is exact, so the result
+// is the sum rounded once, bit-identical to the add or subtract.
+// At M = 16 and 32 the permlane swap hands every lane the pair (value of
+// the lane with bit M clear, value of the lane with bit M set) = (a, b), so
+// fma(+-1, b, a) needs no select.
 template <int M, int E>
 __device__ inline void fwht_lane_stage(float (&x)[E], int lane) {
-  const bool upper = (lane & M) != 0;
+  const float sgn = (lane & M) ? -1.0f : 1.0f;
 #pragma unroll
   for (int i = 0; i < E; i++) {
-    const float p = xor_partner<M>(x[i], lane);
-    x[i] = upper ? (p - x[i]) : (x[i] + p);
+    if constexpr (M == 16 || M == 32) {
+      const uint32_t u = __float_as_uint(x[i]);
+      const auto r = M == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                             : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+      x[i] = __builtin_fmaf(sgn, __uint_as_float(r[1]), __uint_as_float(r[0]));
+    } else {
+      x[i] = __builtin_fmaf(sgn, x[i], xor_partner<M>(x[i], lane));
+    }
   }
 }
 

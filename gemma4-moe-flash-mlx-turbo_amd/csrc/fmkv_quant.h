@@ -42,9 +42,29 @@ __device__ inline void affine_quant(const float (&y)[E], uint32_t (&code)[E], fl
     scale = edge / q0;
     bias = edge;
   }
+  // Codes rint((y - bias) / scale) without a division per element: with
+  // inv = RN(1 / scale) and t = RN((y - bias) * inv), |t - Q| <= 2^-14 for
+  // the exact quotient |Q| < 512 (|Q| <= 2 * (2^b - 1) by the choice of
+  // scale), and the correctly rounded quotient lies within 2^-16 of Q. So
+  // when t is more than 2^-13 from every half-integer, rint(t) equals rint
+  // of the correctly rounded quotient. Lanes with an element closer than
+  // that (about 2^-11 of elements), or a non-finite t, divide exactly.
+  const float inv = 1.0f / scale;
+  float qv[E];
+  bool exact = false;
 #pragma unroll
   for (int i = 0; i < E; i++) {
-    float q = rintf((y[i] - bias) / scale);
+    qv[i] = (y[i] - bias) * inv;
+    const float fr = qv[i] - floorf(qv[i]);
+    exact = exact || !(fabsf(fr - 0.5f) > 0x1p-13f);
+  }
+  if (exact) {
+#pragma unroll
+    for (int i = 0; i < E; i++) qv[i] = (y[i] - bias) / scale;
+  }
+#pragma unroll
+  for (int i = 0; i < E; i++) {
+    float q = rintf(qv[i]);
     q = fminf(fmaxf(q, 0.0f), n_bins);
     code[i] = (uint32_t)q;
   }
