@@ -257,17 +257,21 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
     }
   }
 
-  // x * (1/sqrt D) and the RHT sign as one multiplication by +-c
+  // x * (1/sqrt D), the RHT sign and the sign wave_fwht_signed leaves on
+  // the lane as one multiplication by +-c (sign flips are exact; a -0 in
+  // place of +0 changes no code, scale or bias: min/max, the scale rule,
+  // rint and the codebook boundaries treat both zeros alike)
   const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
+  const float cl = fwht_lane_sign(lane) * a.c;
   float sc[E];
 #pragma unroll
-  for (int i = 0; i < E; i++) sc[i] = ((sbits >> i) & 1u) ? -a.c : a.c;
+  for (int i = 0; i < E; i++) sc[i] = ((sbits >> i) & 1u) ? -cl : cl;
 
   uint32_t code[R][E];
   uint32_t meta[R];
   if constexpr (MODE == kAffine) {
 #pragma unroll
-    for (int r = 0; r < R; r++) wave_fwht<E>(x[r], lane);
+    for (int r = 0; r < R; r++) wave_fwht_signed<E>(x[r], lane);
 #pragma unroll
     for (int r = 0; r < R; r++) {
 #pragma unroll
@@ -286,7 +290,7 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
       for (int i = 0; i < E; i++) x[r][i] = x[r][i] / den;
     }
 #pragma unroll
-    for (int r = 0; r < R; r++) wave_fwht<E>(x[r], lane);
+    for (int r = 0; r < R; r++) wave_fwht_signed<E>(x[r], lane);
 #pragma unroll
     for (int r = 0; r < R; r++) {
 #pragma unroll

@@ -268,10 +268,13 @@ __device__ void build_q_table(const AttnArgs& a, uint8_t* tab, int wave, int lan
   }
   float gsum = 0.0f;
   if (hv) {
-    wave_fwht<E>(x, lane);
+    // the sign-tracking FWHT: an exact zero may come out as -0, which no
+    // score, sum or code of this kernel can tell from +0
+    wave_fwht_signed<E>(x, lane);
+    const float cs = fwht_lane_sign(lane) * a.c;
 #pragma unroll
     for (int i = 0; i < E; i++) {
-      x[i] = apply_sign(x[i] * a.c, sbits, i);
+      x[i] = apply_sign(x[i] * cs, sbits, i);
       gsum += x[i];
     }
   }
@@ -390,9 +393,10 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, int64_t T, int
 
   float x[E];
   load_row<E>((isv ? a.v_new : a.k_new) + ((int64_t)seq * a.st.n_kv_heads + kvh) * D + d0, x);
-  wave_fwht<E>(x, lane);
+  wave_fwht_signed<E>(x, lane);
+  const float cs = fwht_lane_sign(lane) * a.c;
 #pragma unroll
-  for (int i = 0; i < E; i++) x[i] = apply_sign(x[i] * a.c, sbits, i);
+  for (int i = 0; i < E; i++) x[i] = apply_sign(x[i] * cs, sbits, i);
   uint32_t code[E];
   float scale, bias;
   affine_quant<E, BITS>(x, code, scale, bias, lane);
@@ -444,10 +448,11 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, int64_t T, int
   } else {
 #pragma unroll
     for (int i = 0; i < E; i++) y[i] = apply_sign(y[i], sbits, i);
-    wave_fwht<E>(y, lane);
+    wave_fwht_signed<E>(y, lane);
+    const float cs = fwht_lane_sign(lane) * a.c;
     for (int h = 0; h < G; h++)
 #pragma unroll
-      for (int i = 0; i < E; i++) a.part_o[(pbase + h) * D + d0 + i] = y[i] * a.c;
+      for (int i = 0; i < E; i++) a.part_o[(pbase + h) * D + d0 + i] = y[i] * cs;
   }
 }
 
@@ -872,13 +877,14 @@ void decode_attn_kernel(AttnArgs a) {
                  v);
       x[i] = apply_sign(v, sbits, i);
     }
-    wave_fwht<E>(x, lane);
+    wave_fwht_signed<E>(x, lane);
+    const float cs = fwht_lane_sign(lane) * a.c;
     const int64_t qh0 = (int64_t)seq * a.n_q_heads + (int64_t)kvh * G;
     if (a.direct) {
       const int64_t o_idx = (qh0 + hh) * D + lane * E;
 #pragma unroll
       for (int i = 0; i < E; i++) {
-        const float v = Lsum > 0.0f ? (x[i] * a.c) / Lsum : 0.0f;
+        const float v = Lsum > 0.0f ? (x[i] * cs) / Lsum : 0.0f;
         if (a.out_f32)
           reinterpret_cast<float*>(a.out)[o_idx + i] = v;
         else
@@ -892,10 +898,10 @@ void decode_attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < E; i += 4)
           *reinterpret_cast<float4_t*>(dst + i) =
-              (float4_t){x[i] * a.c, x[i + 1] * a.c, x[i + 2] * a.c, x[i + 3] * a.c};
+              (float4_t){x[i] * cs, x[i + 1] * cs, x[i + 2] * cs, x[i + 3] * cs};
       } else {
 #pragma unroll
-        for (int i = 0; i < E; i++) dst[i] = x[i] * a.c;
+        for (int i = 0; i < E; i++) dst[i] = x[i] * cs;
       }
       if (lane == 0) {
         a.part_ml[(pbase + hh) * 2 + 0] = M;

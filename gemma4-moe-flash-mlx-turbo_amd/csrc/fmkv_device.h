@@ -135,24 +135,23 @@ __device__ inline void load_row(const uint16_t* src, float (&x)[E]) {
   }
 }
 
-// Value of lane (lane ^ M), in registers: DPP quad_perm (M = 1, 2), row
-// shifts under bank masks (M = 4: lanes with bit 2 clear read lane + 4,
-// the others lane - 4),
-// row_ror:8 (M = 8) and the permlane swaps (M = 16, 32).
+// Value of lane (lane ^ M): DPP quad_perm (M = 1, 2) and row_ror:8 (M = 8)
+// as plain DPP moves (every lane reads a valid lane, so nothing is
+// materialised for masked lanes and the move can fuse into its user), the
+// LDS crossbar's swizzle for M = 4 (no VALU), and the permlane swaps for
+// M = 16, 32.
 template <int M>
 __device__ inline float xor_partner(float v, int lane) {
   const int iv = __builtin_bit_cast(int, v);
   if constexpr (M == 1) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xf, 0xf, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xf, 0xf, true));
   } else if constexpr (M == 2) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xf, 0xf, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xf, 0xf, true));
   } else if constexpr (M == 4) {
-    // banks 0 and 2 (lane bit 2 clear) read lane + 4 (row_shl:4); banks 1
-    // and 3 then read lane - 4 (row_shr:4) over the first result
-    const int up = __builtin_amdgcn_update_dpp(iv, iv, 0x104, 0xf, 0x5, false);
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(up, iv, 0x114, 0xf, 0xA, false));
+    // swizzle bit mode: and 0x1f, or 0, xor 4 within each 32-lane half
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(iv, 0x101F));
   } else if constexpr (M == 8) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xf, 0xf, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x128, 0xf, 0xf, true));
   } else if constexpr (M == 16) {
     auto r = __builtin_amdgcn_permlane16_swap((uint32_t)iv, (uint32_t)iv, false, false);
     return __uint_as_float((lane & 16) ? r[0] : r[1]);
@@ -195,13 +194,72 @@ __device__ inline float group_min(float v, int lane) {
   return v;
 }
 
-// One cross-lane FWHT stage at lane stride M: (a, b) -> (a + b, a - b), the
-// upper lane of each pair computing partner - own. Both are one fused
-// multiply-add fma(+-1, own, partner): the product is exact, so the result
-// is the sum rounded once, bit-identical to the add or subtract.
-// At M = 16 and 32 the permlane swap hands every lane the pair (value of
-// the lane with bit M clear, value of the lane with bit M set) = (a, b), so
-// fma(+-1, b, a) needs no select.
+// Partner value for a cross-lane FWHT stage: as xor_partner, with the LDS
+// crossbar for M = 16 (swizzle xor 16) and M = 32 (bpermute), so that every
+// stage costs one VALU operation besides a fusable DPP move.
+template <int M>
+__device__ inline float fwht_partner(float v, int lane) {
+  if constexpr (M == 16) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+  } else if constexpr (M == 32) {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __float_as_int(v)));
+  } else {
+    return xor_partner<M>(v, lane);
+  }
+}
+
+// Sign carried by a lane's values after wave_fwht_signed: (-1)^popcount(lane).
+__device__ inline float fwht_lane_sign(int lane) {
+  return (__builtin_popcount(lane & 63) & 1) ? -1.0f : 1.0f;
+}
+
+// Canonical unnormalised FWHT of a D = 64*E row held as E contiguous values
+// per lane: stages h = 1 .. E/2 in registers, then h = E .. D/2 across lanes
+// (lane xor h/E); (a, b) -> (a + b, a - b) exactly as the oracle.
+//
+// The lane stages carry a per-lane sign instead of selecting add or
+// subtract: with z = sigma * y on both lanes of a pair (sigma depends only
+// on lane bits other than M), z' = z_own + s * z_partner, s = -1 on the
+// upper lane, equals sigma * (a + b) on the lower lane and -sigma * (a - b)
+// on the upper one; the product s * z is exact and RN(-x) = -RN(x), so each
+// stage is one fma rounding exactly like the add or subtract it stands for.
+// On return the true row value is fwht_lane_sign(lane) * x[i], except that
+// an exact cancellation can come out as -0 where the oracle has +0.
+template <int E>
+__device__ inline void wave_fwht_signed(float (&x)[E], int lane) {
+#pragma unroll
+  for (int h = 1; h < E; h <<= 1)
+#pragma unroll
+    for (int i = 0; i < E; i += 2 * h)
+#pragma unroll
+      for (int jj = i; jj < i + h; jj++) {
+        const float a = x[jj], b = x[jj + h];
+        x[jj] = a + b;
+        x[jj + h] = a - b;
+      }
+#define FMKV_FWHT_STAGE(M)                                                       \
+  {                                                                              \
+    const float s = (lane & (M)) ? -1.0f : 1.0f;                                 \
+    _Pragma("unroll") for (int i = 0; i < E; i++)                                \
+        x[i] = __builtin_fmaf(fwht_partner<(M)>(x[i], lane), s, x[i]);           \
+  }
+  FMKV_FWHT_STAGE(1)
+  FMKV_FWHT_STAGE(2)
+  FMKV_FWHT_STAGE(4)
+  FMKV_FWHT_STAGE(8)
+  FMKV_FWHT_STAGE(16)
+  FMKV_FWHT_STAGE(32)
+#undef FMKV_FWHT_STAGE
+}
+
+// The same transform with true values, bit for bit including the sign of
+// zero: the sign-tracking stages above turn an exact cancellation's +0 into
+// -0 once the lane sign is applied, which only consumers that cannot tell
+// the zeros apart (quantizers, sums) may accept. Here the lower lane of a
+// pair computes fma(1, own, partner) = own + partner and the upper lane
+// fma(-1, own, partner) = partner - own, as the oracle; at M = 16 and 32 the
+// permlane swap hands every lane the pair (a, b) (lower lane's value first),
+// so fma(+-1, b, a) needs no select.
 template <int M, int E>
 __device__ inline void fwht_lane_stage(float (&x)[E], int lane) {
   const float sgn = (lane & M) ? -1.0f : 1.0f;
@@ -218,9 +276,6 @@ __device__ inline void fwht_lane_stage(float (&x)[E], int lane) {
   }
 }
 
-// Canonical unnormalised FWHT of a D = 64*E row held as E contiguous values
-// per lane: stages h = 1 .. E/2 in registers, then h = E .. D/2 across lanes
-// (lane xor h/E); (a, b) -> (a + b, a - b) exactly as the oracle.
 template <int E>
 __device__ inline void wave_fwht(float (&x)[E], int lane) {
 #pragma unroll

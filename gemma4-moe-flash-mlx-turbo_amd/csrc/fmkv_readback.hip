@@ -131,7 +131,7 @@ __global__ __launch_bounds__(64) void fetch_kernel(FetchArgs a) {
       x[e] = w * a.signs[d];
     }
   }
-  wave_fwht<E>(x, lane);
+  wave_fwht<E>(x, lane);  // true values: the output is compared bit for bit
   void* dst = isv ? a.v_out : a.k_out;
   const int64_t base = (i * H + h) * D + lane * E;
 #pragma unroll
