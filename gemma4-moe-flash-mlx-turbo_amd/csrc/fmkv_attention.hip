@@ -104,9 +104,10 @@ struct AttnPlan {
   // a pair's merge rows [8 heads][kQS] floats reuse its own stages
   static constexpr int kStageRegion = kAttnPairs * kStages * kStageBytes;
   static_assert(8 * kQS * 4 <= kStages * kStageBytes, "merge rows fit in a pair's stages");
-  // prologue: the raw q rows, then the q table (B operands + group sums);
-  // loop: the score exchange
-  static constexpr int kTabBytes = 2 * NG * kChunk + 8 * NG * 4;
+  // prologue: the raw q rows, then the q table (B operands, group sums of
+  // q_rot, group sums of the f16 high and residual parts); loop: the score
+  // exchange
+  static constexpr int kTabBytes = 2 * NG * kChunk + 8 * NG * 4 + 8 * NG * 8;
   static constexpr int kXBytes = kAttnWaves * 2 * 64 * 16;
   static constexpr int kScratch = cmax(cmax(kTabBytes, kXBytes), 8 * D * 2);
   static_assert(NG % 2 == 0 && kCodeChunks >= 1, "layout");
@@ -246,7 +247,10 @@ __device__ inline void copy_q_row(const AttnArgs& a, uint8_t* dst, int seq, int 
 //   entry e = 2 g + s at e KiB + 16 lane, lane (j, c) = (lane / 16,
 //     lane % 16): 8 f16 of head c & 7 -- the f16 high part of q_rot for
 //     c < 8, the residual for c >= 8, zero past the group;
-//   float qsum[8][NG] after the 2 NG entries: per head and group, sum q_rot.
+//   float qsum[8][NG] after the 2 NG entries: per head and group, sum q_rot;
+//   float opsum[8][NG][2] after that: per head and group, the sums of the
+//     f16 high parts and of the residuals (the accumulator start of biased
+//     8-bit codes).
 // Wave w computes head w before the first barrier, so the rotation overlaps
 // the other waves' copy issue. Every thread of the work-group calls it (it
 // holds two barriers).
@@ -281,17 +285,26 @@ __device__ void build_q_table(const AttnArgs& a, uint8_t* tab, int wave, int lan
   gsum = group_sum<LPG>(gsum, lane);
   const QSlot<E, BITS> qs(lane);
   _Float16 hi[E], lo[E];
+  float hsum = 0.0f, lsum = 0.0f;
 #pragma unroll
   for (int i = 0; i < E; i++) {
     hi[i] = (_Float16)x[i];
     lo[i] = (_Float16)(x[i] - (float)hi[i]);
+    hsum += (float)hi[i];
+    lsum += (float)lo[i];
   }
+  hsum = group_sum<LPG>(hsum, lane);
+  lsum = group_sum<LPG>(lsum, lane);
   __syncthreads();  // every raw row is read before the table replaces them
   uint8_t* ent = tab + (2 * qs.g + qs.s) * kChunk + qs.i0 * 2;
   store_halves<E>(ent + (qs.j * 16 + wave) * 16, hi);
   store_halves<E>(ent + (qs.j * 16 + wave + 8) * 16, lo);
-  if ((lane & (LPG - 1)) == 0)
+  if ((lane & (LPG - 1)) == 0) {
     reinterpret_cast<float*>(tab + 2 * NG * kChunk)[wave * NG + qs.g] = gsum;
+    float* op = reinterpret_cast<float*>(tab + 2 * NG * kChunk + 8 * NG * 4);
+    op[(wave * NG + qs.g) * 2 + 0] = hsum;
+    op[(wave * NG + qs.g) * 2 + 1] = lsum;
+  }
   __syncthreads();
 }
 
@@ -580,18 +593,15 @@ void decode_attn_kernel(AttnArgs a) {
     qs[gi] = (hi && col_valid) ? qsum[head * NG + g0 + gi] : 0.0f;
   }
   // biased 8-bit codes: the QK accumulator of group gi starts at -1024 x this
-  // column's q operand summed over the group's 64 dims (16 per lane, 4 lanes)
+  // column's q operand summed over the group's 64 dims (the table's high or
+  // residual sum of the column's head)
   float4_t kq[GH];
+  const float* opsum = reinterpret_cast<const float*>(scratch + NE * kChunk + 8 * NG * 4);
 #pragma unroll
   for (int gi = 0; gi < GH; gi++) {
     float t = 0.0f;
-    if constexpr (kBiasedCodes<BITS>) {
-#pragma unroll
-      for (int s = 0; s < 2; s++)
-#pragma unroll
-        for (int i = 0; i < 8; i++) t += (float)bq[gi][s][i];
-      t = xor32_sum(xor16_sum(t));
-    }
+    if constexpr (kBiasedCodes<BITS>)
+      t = col_valid ? opsum[(head * NG + g0 + gi) * 2 + (hi ? 0 : 1)] : 0.0f;
     const float k = -1024.0f * t;
     kq[gi] = (float4_t){k, k, k, k};
   }
