@@ -133,13 +133,19 @@ void sign_bits_of(const fmkv_cache_desc& d, uint32_t out[16]) {
 struct Workspace {
   float* ptr = nullptr;
   size_t bytes = 0;
-  int ensure(size_t need) {
+  // zero: a new allocation starts zeroed (head-block staging, whose
+  // unwritten slots are read, masked, as the cache's own are)
+  int ensure(size_t need, bool zero = false) {
     if (need <= bytes) return FMKV_OK;
     if (ptr) (void)hipFree(ptr);
     ptr = nullptr;
     bytes = 0;
     hipError_t e = hipMalloc(&ptr, need);
-    if (e != hipSuccess) return fail(FMKV_ERR_OOM, "split workspace allocation failed");
+    if (e != hipSuccess) return fail(FMKV_ERR_OOM, "workspace allocation failed");
+    if (zero) {
+      e = hipMemset(ptr, 0, need);
+      if (e != hipSuccess) return hip_fail(e, "hipMemset(workspace)");
+    }
     bytes = need;
     return FMKV_OK;
   }
@@ -163,6 +169,7 @@ struct fmkv_cache {
   int64_t offset;
   int64_t vis_begin;
   Workspace ws;
+  Workspace stage;  // prefill on a ring: the chunk's quantized rows
   int cus;
 };
 
@@ -477,6 +484,7 @@ int fmkv_cache_destroy(fmkv_cache* c) {
   if (c->arena) (void)hipFree(c->arena);
   if (c->d_signs) (void)hipFree(c->d_signs);
   c->ws.release();
+  c->stage.release();
   delete c;
   return FMKV_OK;
 }
@@ -516,6 +524,83 @@ int fmkv_cache_append_projected(fmkv_cache* c, const void* k, const void* v, int
   set_prologue(pro, &a);
   hipError_t e = fmkv::launch_append(a, 1, (int)tasks, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "append launch");
+  c->offset += n;
+  return FMKV_OK;
+}
+
+int fmkv_prefill_step(fmkv_cache* c, const void* k, const void* v, int64_t n, const void* q,
+                      int32_t n_q_heads, float scale, void* out, int32_t out_dtype, void* stream) {
+  if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
+  if (n < 1) return fail(FMKV_ERR_INVALID_ARG, "a prefill step appends at least one token");
+  int rc = check_attn_args(c->desc, q, n_q_heads, 0.0f, out, out_dtype);
+  if (rc) return rc;
+  if (!std::isfinite(scale)) return fail(FMKV_ERR_INVALID_ARG, "scale must be finite");
+  const int32_t group = n_q_heads / c->desc.n_kv_heads;
+  if (n > (int64_t)65535 * (64 / group))
+    return fail(FMKV_ERR_INVALID_ARG, "n_tokens too large for one prefill step");
+  fmkv::AppendArgs ap;
+  int64_t tasks = 0;
+  rc = prepare_append(c, k, v, n, &ap, &tasks);
+  if (rc) return rc;
+  const int64_t p0 = c->offset, W = c->desc.window;
+  const int H = c->desc.n_kv_heads;
+  const int64_t bb = c->layout.block_bytes;
+  fmkv::PrefillArgs pa;
+  pa.old_st = cache_store(c);
+  pa.new_st = pa.old_st;
+  pa.p0 = p0;
+  pa.n_q = (int32_t)n;
+  pa.window = W;
+  pa.vis_begin = c->vis_begin;
+  pa.p_split = 0;
+  pa.new_blk0 = 0;
+  pa.group = group;
+  pa.n_q_heads = n_q_heads;
+  pa.q = static_cast<const uint16_t*>(q);
+  pa.qscale = scale * 1.4426950408889634f;
+  std::memcpy(pa.sign_bits, c->sign_bits, sizeof(pa.sign_bits));
+  pa.c = c->c;
+  pa.out = out;
+  pa.out_f32 = out_dtype == FMKV_DTYPE_F32 ? 1 : 0;
+  fmkv::AppendArgs as = ap;
+  int64_t nsb = 0;
+  if (W > 0) {
+    // the chunk's rows go to a staging store first (block 0 = absolute
+    // block p0 / 16), so the ring keeps every position the queries need
+    nsb = (p0 % fmkv::kBlockTokens + n + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens;
+    rc = c->stage.ensure((size_t)(nsb * H * bb), true);
+    if (rc) return rc;
+    fmkv::Store st;
+    st.base = reinterpret_cast<uint8_t*>(c->stage.ptr);
+    st.block_stride = bb;
+    st.head_stride = nsb * bb;
+    st.block_table = nullptr;
+    st.table_stride = 0;
+    st.n_blocks = nsb;
+    st.n_kv_heads = H;
+    st.layout = c->layout;
+    as.st = st;
+    as.start_scalar = p0 % fmkv::kBlockTokens;
+    as.window = 0;
+    pa.new_st = st;
+    pa.p_split = p0;
+    pa.new_blk0 = p0 / fmkv::kBlockTokens;
+  }
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (W > 0) {
+    e = fmkv::launch_append(as, 1, (int)nsb, s);
+    if (e != hipSuccess) return hip_fail(e, "staging append launch");
+    e = fmkv::launch_prefill_attention(pa, s);
+    if (e != hipSuccess) return hip_fail(e, "prefill attention launch");
+    e = fmkv::launch_append(ap, 1, (int)tasks, s);
+    if (e != hipSuccess) return hip_fail(e, "append launch");
+  } else {
+    e = fmkv::launch_append(ap, 1, (int)tasks, s);
+    if (e != hipSuccess) return hip_fail(e, "append launch");
+    e = fmkv::launch_prefill_attention(pa, s);
+    if (e != hipSuccess) return hip_fail(e, "prefill attention launch");
+  }
   c->offset += n;
   return FMKV_OK;
 }

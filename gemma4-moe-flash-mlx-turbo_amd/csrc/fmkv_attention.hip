@@ -56,19 +56,10 @@
 #include "fmkv_device.h"
 #include "fmkv_internal.h"
 #include "fmkv_quant.h"
+#include "fmkv_attn_common.h"
 
 namespace fmkv {
 namespace {
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-constexpr int kChunk = 1024;  // bytes per full LDS copy instruction (64 lanes x 16 B)
-
-constexpr int cmax(int a, int b) { return a > b ? a : b; }
-
-// Online softmax: how far (base 2) a score may exceed the running reference
-// max before the accumulators are rescaled to a new one.
-constexpr float kRescaleSlack = 8.0f;
 
 // Kernel modes. Dense: softmax attention. Sparse-V (src/model/
 // gemma4_attention.rs:196-234, weights below tau zeroed without
@@ -114,119 +105,6 @@ struct AttnPlan {
   static_assert(kStages * kCopies <= 63, "vmcnt immediates");
   static_assert(8 * GH <= 64, "one partial instruction copies a wave's scale/bias");
 };
-
-__device__ inline uint32_t lds_addr(const void* p) {
-  return (uint32_t)reinterpret_cast<uintptr_t>(p);  // low half of the flat LDS address
-}
-
-// Raw buffer resource over [base, base + bytes); reads past the end return 0.
-__device__ inline u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  u32x4 r;
-  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)a);
-  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) & 0xffffu;  // stride 0
-  r[2] = bytes;
-  r[3] = 0x00020000u;
-  return r;
-}
-
-// One copy instruction: each active lane moves 16 bytes from rsrc + voff to
-// LDS at lds + 16 * lane.
-__device__ inline void dma16(uint32_t lds, int voff, const u32x4 rs) {
-  asm volatile("buffer_load_dwordx4 %1, %2, 0 offen lds" :: "{m0}"(lds), "v"(voff), "s"(rs)
-               : "memory");
-}
-
-template <int N>
-__device__ inline void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
-}
-
-// Wait until at most `pending` (wave-uniform) blocks' copies, CP
-// instructions each, are outstanding; P bounds pending.
-template <int CP, int P>
-__device__ inline void wait_copies(int pending) {
-  if constexpr (P > 0) {
-    if (pending >= P) {
-      wait_vmcnt<P * CP>();
-      return;
-    }
-    wait_copies<CP, P - 1>(pending);
-  } else {
-    wait_vmcnt<0>();
-  }
-}
-
-__device__ inline u32x4 lds16(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
-
-// 8-bit codes enter the MFMAs as the exact f16 values 1024 + code (one
-// v_perm per two codes): the QK accumulator starts at -1024 * sum(q operand)
-// and the PV accumulator loses 1024 * sum(P') at the end, both from the
-// exact f16 operand values. At 8 bits the offset costs the f32 partial sums
-// at most 3 of their 24 bits; 4-bit codes (range 16) convert exactly
-// instead, as the offset would cost them 7.
-template <int BITS>
-constexpr bool kBiasedCodes = BITS == 8;
-
-// K operand (8 codes as exact f16, + 1024 at 8 bits) of MFMA s of group g;
-// `w` is the lane's 16 bytes of the group's chunk (8-bit) or of the two
-// groups' chunk (4-bit).
-template <int BITS>
-__device__ inline half8_t k_operand(const u32x4 w, int g, int s) {
-  if constexpr (BITS == 8) {
-    const uint32_t w0 = w[2 * s], w1 = w[2 * s + 1];
-    return cat8(u8x2_to_h2_biased(w0, 0x04010400u), u8x2_to_h2_biased(w0, 0x04030402u),
-                u8x2_to_h2_biased(w1, 0x04010400u), u8x2_to_h2_biased(w1, 0x04030402u));
-  } else {
-    const uint32_t x = w[(g & 1) * 2 + s];
-    return cat8(u4x2_to_h2(x, 0), u4x2_to_h2(x, 1), u4x2_to_h2(x, 2), u4x2_to_h2(x, 3));
-  }
-}
-
-// V codes of column tile ct (0..3) of group g: tokens 4j..4j+3 of one dim
-// (+ 1024 at 8 bits).
-template <int BITS>
-__device__ inline half4_t v_operand(const u32x4 w, int g, int ct) {
-  if constexpr (BITS == 8) {
-    const uint32_t x = w[ct];
-    return cat4(u8x2_to_h2_biased(x, 0x04010400u), u8x2_to_h2_biased(x, 0x04030402u));
-  } else {
-    const int ctc = (g & 1) * 4 + ct;  // column tile inside the 128-dim chunk
-    const uint32_t x = w[ctc >> 1];
-    const int k0 = (ctc & 1) * 2;
-    return cat4(u4x2_to_h2(x, k0), u4x2_to_h2(x, k0 + 1));
-  }
-}
-
-__device__ inline float lo16(uint32_t w) { return f16_bits_to_f32(w); }
-__device__ inline float hi16(uint32_t w) { return f16_bits_to_f32(w >> 16); }
-
-// Dim of head_dim fed to lane k-group j, element i, of the QK MFMA s (0/1)
-// of group g is g*64 + j*16 + s*8 + i (8-bit) or g*64 + s*32 + j*8 + i
-// (4-bit), matching the K-code placement of fmkv_layout.h. For the E = D/64
-// consecutive dims of lane l (d0 = l*E) this gives the entry and position
-// they occupy: (g, s, j) and the first element i0.
-template <int E, int BITS>
-struct QSlot {
-  int g, s, j, i0;
-  __device__ explicit QSlot(int lane) {
-    const int d0 = lane * E, o = d0 & 63;
-    g = d0 >> 6;
-    s = BITS == 8 ? (o >> 3) & 1 : o >> 5;
-    j = BITS == 8 ? o >> 4 : (o >> 3) & 3;
-    i0 = o & 7;
-  }
-};
-
-template <int E>
-__device__ inline void store_halves(uint8_t* p, const _Float16 (&h)[E]) {
-  if constexpr (E == 8)
-    *reinterpret_cast<half8_t*>(p) = (half8_t){h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]};
-  else if constexpr (E == 4)
-    *reinterpret_cast<half4_t*>(p) = (half4_t){h[0], h[1], h[2], h[3]};
-  else
-    *reinterpret_cast<half2_t*>(p) = (half2_t){h[0], h[1]};
-}
 
 // Raw bf16 q row of GQA head `wave` of (seq, kvh) (D * 2 bytes) to LDS at
 // dst + wave * D * 2, copied by that wave itself (lanes < D / 8).

@@ -87,6 +87,32 @@ struct AttnArgs {
   float* tau_stats;
 };
 
+// Prefill (chunked) attention: n_q queries at positions p0 .. p0 + n_q - 1,
+// query p attending to key positions [lo(p), p], lo(p) = max(vis_begin,
+// p - window + 1) (window 0: vis_begin). Keys below p_split come from
+// old_st (a ring of window slots when window > 0, else linear), keys from
+// p_split on from new_st, whose block 0 holds absolute block new_blk0 (a
+// staging copy of the chunk for rings; the cache itself, p_split 0, for
+// linear caches, which append before attending).
+struct PrefillArgs {
+  Store old_st;
+  Store new_st;
+  int64_t p0;
+  int32_t n_q;
+  int64_t window;
+  int64_t vis_begin;
+  int64_t p_split;
+  int64_t new_blk0;
+  int32_t group;      // q heads per kv head (<= 8)
+  int32_t n_q_heads;
+  const uint16_t* q;  // bf16 [n_q][n_q_heads][D]
+  float qscale;       // softmax scale * log2(e)
+  uint32_t sign_bits[16];
+  float c;            // 1/sqrt(D)
+  void* out;          // [n_q][n_q_heads][D]
+  int32_t out_f32;
+};
+
 struct ReadArgs {
   Store st;
   int64_t n_slots;    // slots to convert (ring: W; linear: capacity; pool: n_blocks*16)
@@ -112,6 +138,7 @@ hipError_t launch_append(const AppendArgs& a, int n_seqs, int max_tasks, hipStre
 // kernel's dispatch: the start and end of its execution.
 hipError_t launch_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                                    hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr);
+hipError_t launch_prefill_attention(const PrefillArgs& a, hipStream_t s);
 hipError_t launch_read_codes(const ReadArgs& a, hipStream_t s);
 hipError_t launch_fetch(const FetchArgs& a, hipStream_t s);
 

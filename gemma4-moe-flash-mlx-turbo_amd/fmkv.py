@@ -45,6 +45,7 @@ EXPORTED = (
     "fmkv_cache_append_projected", "fmkv_paged_append_projected",
     "fmkv_pool_read_codes", "fmkv_set_blocks_per_split", "fmkv_cache_decode_splits",
     "fmkv_profile_enable", "fmkv_profile_collect", "fmkv_decode_step", "fmkv_paged_decode_step",
+    "fmkv_prefill_step",
 )
 
 
@@ -144,6 +145,7 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         "fmkv_profile_collect": ([P(ctypes.c_double), P(i32)], ctypes.c_int),
         "fmkv_decode_step": ([vp, vp, vp, i64, vp, i32, ctypes.c_float, ctypes.c_float, vp, i32,
                               vp], ctypes.c_int),
+        "fmkv_prefill_step": ([vp, vp, vp, i64, vp, i32, ctypes.c_float, vp, i32, vp], ctypes.c_int),
         "fmkv_paged_decode_step": ([vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, vp, i32,
                                     ctypes.c_float, ctypes.c_float, vp, i32, vp], ctypes.c_int),
     }
@@ -318,6 +320,24 @@ class KVCache:
         _check(self._lib.fmkv_decode_step(self._h, _ptr(keys), _ptr(values), keys.shape[0],
                                           _ptr(q), q.shape[0], scale, sparse_v_tau, _ptr(out),
                                           _dtype_code(out.dtype), _stream(stream)))
+        return out
+
+    def prefill_step(self, keys: torch.Tensor, values: torch.Tensor, q: torch.Tensor,
+                     scale: float = 1.0, out: torch.Tensor | None = None, dtype=torch.bfloat16,
+                     stream=None) -> torch.Tensor:
+        """update_and_fetch of an L-token chunk and the chunk's causal (sliding:
+        banded) attention (src/model/gemma4_attention.rs:84-104 with L > 1,
+        masks src/model/mod.rs:682-753). keys/values bf16 [L, n_kv_heads, D];
+        q bf16 [L, n_q_heads, D]; returns [L, n_q_heads, D]."""
+        self._check_kv(keys, values)
+        if (q.dtype != torch.bfloat16 or q.dim() != 3 or q.shape[0] != keys.shape[0]
+                or q.shape[2] != self.desc.head_dim):
+            raise ValueError("q must be bf16 [n_tokens, n_q_heads, head_dim]")
+        if out is None:
+            out = torch.empty(q.shape, dtype=dtype, device=q.device)
+        _check(self._lib.fmkv_prefill_step(self._h, _ptr(keys), _ptr(values), keys.shape[0],
+                                           _ptr(q), q.shape[1], scale, _ptr(out),
+                                           _dtype_code(out.dtype), _stream(stream)))
         return out
 
     def decode_splits(self) -> int:

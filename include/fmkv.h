@@ -142,6 +142,22 @@ int fmkv_decode_step(fmkv_cache* cache, const void* k_bf16, const void* v_bf16, 
                      const void* q_bf16, int32_t n_q_heads, float scale, float sparse_v_tau,
                      void* out, int32_t out_dtype, void* stream);
 
+/* One prefill (chunked-prefill) pass of an attention layer, as
+ * Gemma4Attention::forward runs it for L = n_tokens > 1
+ * (src/model/gemma4_attention.rs:84-104): cache.update_and_fetch(k, v) of the
+ * chunk, then attention of its n_tokens queries q [n_tokens][n_q_heads][D]
+ * (bf16, post-RoPE) with the mask of create_attention_mask (global layers) or
+ * create_sliding_mask (sliding layers, src/model/mod.rs:682-753): query
+ * position p attends to the visible positions j <= p, and on a ring of W
+ * slots also j > p - W. A ring attends before its slots are overwritten (the
+ * chunk's rows are quantized into a handle-owned staging area first), so
+ * every query sees its whole window. out: [n_tokens][n_q_heads][D] in
+ * out_dtype. Affine mode; at most 8 query heads per KV head; n_tokens >= 1.
+ * Nothing is launched or changed when validation fails. */
+int fmkv_prefill_step(fmkv_cache* cache, const void* k_bf16, const void* v_bf16, int64_t n_tokens,
+                      const void* q_bf16, int32_t n_q_heads, float scale, void* out,
+                      int32_t out_dtype, void* stream);
+
 /* The fetch half of update_and_fetch and KVCache::peek_kv (src/cache.rs:247-257):
  * dequantized, un-rotated K and V of the visible positions in chronological
  * order, [stored_len][n_kv_heads][head_dim] in out_dtype. */

@@ -402,6 +402,43 @@ class OracleCache:
             self.codes[s, 1], self.meta[s, 1] = vp[i], vm[i]
         self.offset += n
 
+    def _dequant_rows(self, packed, meta) -> np.ndarray:
+        """Un-rotated f64 rows of quantized rows (packed, meta)."""
+        if self.mode == 0:
+            y = affine_dequantize(packed, np.ascontiguousarray(meta[..., 0::2]),
+                                  np.ascontiguousarray(meta[..., 1::2]), self.D, self.bits)
+        else:
+            y = codebook_dequant_rotated(packed, np.ascontiguousarray(meta[..., 0]), self.D, self.bits)
+        return unrotate_rows_f64(y, self.sgn)
+
+    def prefill(self, k_bf16, v_bf16, q_bf16, scale: float = 1.0) -> np.ndarray:
+        """update_and_fetch of an L-token chunk, then the chunk's attention
+        (src/model/gemma4_attention.rs:84-104 with L > 1) under the mask of
+        src/model/mod.rs:682-753: query position p = offset + i sees the
+        visible keys j <= p, and on a ring of W slots only j > p - W. The keys
+        are the positions visible before the chunk plus the chunk's own
+        quantized rows (update_and_fetch returns both before trimming,
+        src/cache.rs:266-310). Returns [L, Hq, D] f64."""
+        k_bf16, v_bf16 = np.asarray(k_bf16), np.asarray(v_bf16)
+        n = k_bf16.shape[0]
+        p0 = self.offset
+        old_pos = self.visible_positions()
+        ko, vo = self.dequant_kv(old_pos)
+        kp, km = self.quantize_rows(k_bf16)
+        vp, vm = self.quantize_rows(v_bf16)
+        kn, vn = self._dequant_rows(kp, km), self._dequant_rows(vp, vm)
+        self._store(kp, km, vp, vm)
+        pos = np.concatenate([old_pos, np.arange(p0, p0 + n)])
+        kk, vv = np.concatenate([ko, kn]), np.concatenate([vo, vn])
+        q = bf16_to_f32(q_bf16).astype(np.float64)
+        out = np.empty(q.shape, np.float64)
+        for i in range(n):
+            p = p0 + i
+            lo = self.vis_begin if self.W == 0 else max(self.vis_begin, p - self.W + 1)
+            valid = ((pos >= lo) & (pos <= p)).astype(np.uint8)
+            out[i] = attention_f64(q[i], kk, vv, valid, scale)
+        return out
+
     def trim(self, keep_last: int) -> None:
         self.vis_begin = max(self.vis_begin, self.offset - keep_last)
 

@@ -513,3 +513,31 @@ def test_kv_prologue_rows_and_k_eq_v(ora):
             assert np.array_equal(vo[t, hh], vv)
             ora.lib().ora_v_prologue(ora._p(np.ascontiguousarray(k[t, hh])), d, 1e-6, ora._p(vv))
             assert np.array_equal(vo2[t, hh], vv)
+
+
+@pytest.mark.parametrize("W,keep", [(0, 0), (0, 30), (32, 0), (48, 0)])
+def test_prefill_equals_token_by_token_decode(ora, W, keep):
+    """A chunk's prefill attention (src/model/gemma4_attention.rs:84-104 with
+    L > 1, masks src/model/mod.rs:682-753) equals decoding its tokens one at
+    a time: causal on linear caches; on a ring the band j > p - W is exactly
+    the last W positions a ring holds at decode. A mask edge off by one, a
+    ring read after the chunk overwrote its slots, a lost trim or a wrong
+    position offset fails this; the stored codes are the same as well."""
+    H, D, bits, Hq = 2, 128, 4, 4
+    cap = 0 if W else 200
+    a = ora.OracleCache(H, D, bits, W, cap)
+    b = ora.OracleCache(H, D, bits, W, cap)
+    k0, v0 = _bf16_rows(40, (37, H, D)), _bf16_rows(41, (37, H, D))
+    for c in (a, b):
+        c.append(k0, v0)
+        if keep:
+            c.trim(keep)
+    L = 45
+    k, v, q = _bf16_rows(42, (L, H, D)), _bf16_rows(43, (L, H, D)), _bf16_rows(44, (L, Hq, D))
+    got = a.prefill(k, v, q, 0.7)
+    for i in range(L):
+        b.append(k[i:i + 1], v[i:i + 1])
+        want = b.attention(q[i], 0.7)
+        assert np.allclose(got[i], want, rtol=1e-10, atol=1e-12), i
+    assert np.array_equal(a.codes, b.codes) and np.array_equal(a.meta, b.meta)
+    assert a.offset == b.offset
