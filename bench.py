@@ -429,6 +429,76 @@ def run_c4(args) -> dict:
     }
 
 
+def run_prefill(args) -> dict:
+    """Chunked-prefill attention of one layer (fmkv_prefill_step): 2048-token
+    chunks after a prefix of --context tokens. Global layer: Hq 16, Hkv 2,
+    head_dim 512, 8-bit, causal; --prefill-sliding: Hq 16, Hkv 8, head_dim
+    256, 4-bit, ring W 1024 (band mask). A step appends the chunk and attends
+    its 2048 queries. Algorithmic FLOPs: 4 * Hq * D per visible (query, key)
+    pair (QK and PV multiply-adds)."""
+    import torch
+
+    import fmkv
+    import synth
+
+    if args.prefill_sliding:
+        Hq, Hkv, D, bits, W = 16, 8, 256, 4, 1024
+    else:
+        Hq, Hkv, D, bits, W = 16, 2, 512, 8, 0
+    L, T0 = 2048, args.context
+    steps = args.steps if args.steps <= 16 else 4
+    warm = 1
+    cap = 0 if W else T0 + (steps + warm) * L + 16
+    cache = fmkv.KVCache.new_quantized_with_window(D, bits, W, Hkv, cap)
+    for c0 in range(0, T0, L):
+        n = min(L, T0 - c0)
+        k = dev_bf16(synth.kv_rows(31, n, Hkv, D, None, dist="t3", offset=c0))
+        v = dev_bf16(synth.kv_rows(32, n, Hkv, D, None, offset=c0))
+        cache.append(k, v)
+    kc = dev_bf16(synth.kv_rows(51, L, Hkv, D, None, dist="t3"))
+    vc = dev_bf16(synth.kv_rows(52, L, Hkv, D, None))
+    qc = dev_bf16(synth.q_rows(53, Hq, Hkv, D, None, batch=L))
+    out = torch.empty((L, Hq, D), dtype=torch.bfloat16, device="cuda")
+
+    def visible_pairs(p0):
+        p = np.arange(p0, p0 + L, dtype=np.float64)
+        lo = np.maximum(0.0, p - W + 1) if W else np.zeros_like(p)
+        return float(np.sum(p - lo + 1))
+
+    for _ in range(warm):
+        cache.prefill_step(kc, vc, qc, 1.0, out=out)
+    torch.cuda.synchronize()
+    pairs = 0.0
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_begin = cache.offset()
+    ev0.record()
+    for i in range(steps):
+        pairs += visible_pairs(t_begin + i * L)
+        cache.prefill_step(kc, vc, qc, 1.0, out=out)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    flops = 4.0 * Hq * D * pairs / steps
+    tflops = flops / (ms * 1e-3) / 1e12
+    tps = L / (ms * 1e-3)
+    log(f"prefill chunk {L} at {t_begin}..{cache.offset()}: {ms:.3f} ms/chunk, {tps/1e6:.2f} M tokens/s, "
+        f"{tflops:.1f} TFLOP/s")
+    name = "sliding (ring W 1024)" if W else "global"
+    return {
+        "metric": "prefill attention tokens/s (2048-token chunks)",
+        "value": round(tps, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u8" if bits == 8 else "u4",
+        "data": "synthetic (seeded SplitMix64: K Student-t(3), V and q N(0,1))",
+        "config": {"workload": f"{name} layer chunked prefill: Hq {Hq}, Hkv {Hkv}, head_dim {D}, "
+                               f"{bits}-bit group-64, 2048-token chunks after {T0} tokens",
+                   "context": T0, "chunk": L},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tflops / 2500.0, 4), "traffic": None,
+                     "kernel": "prefill_attn_kernel (with the chunk's append)"},
+    }
+
+
 def run_c5(args) -> dict:
     """Decode-step cache traffic of a 30-layer Gemma-4-26B-A4B-shaped stack:
     25 sliding layers (ring of 1024, Hkv 8, head_dim 256, 4-bit) and 5 global
@@ -575,9 +645,12 @@ def main(argv=None) -> int:
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 8 device-to-device copies of MIB MiB (the reference kernel "
                          "for scaling HBM byte counters) and exit")
-    ap.add_argument("--workload", choices=["c3", "c2", "c4", "c5"], default="c3",
+    ap.add_argument("--workload", choices=["c3", "c2", "c4", "c5", "prefill"], default="c3",
                     help="c3 (default): global layer at 32K; c2: sliding ring, 8192 steps; "
-                         "c4: 32 ragged paged sequences; c5: 30-layer stack")
+                         "c4: 32 ragged paged sequences; c5: 30-layer stack; prefill: "
+                         "2048-token chunked-prefill attention after --context tokens")
+    ap.add_argument("--prefill-sliding", action="store_true",
+                    help="prefill workload on the sliding-layer shape (ring W 1024)")
     ap.add_argument("--c5-context", type=int, default=131072)
     args = ap.parse_args(argv)
     if args.gpus != 1:
@@ -595,7 +668,8 @@ def main(argv=None) -> int:
         import fmkv
 
         fmkv.set_blocks_per_split(args.bps)
-    res = {"c3": run_c3, "c2": run_c2, "c4": run_c4, "c5": run_c5}[args.workload](args)
+    res = {"c3": run_c3, "c2": run_c2, "c4": run_c4, "c5": run_c5,
+           "prefill": run_prefill}[args.workload](args)
     print(json.dumps(res), flush=True)
     return 0
 
