@@ -243,6 +243,8 @@ void prefill_attn_kernel(PrefillArgs a) {
 #pragma unroll
   for (int gi = 0; gi < GH; gi++) bacc[gi] = psum[gi] = 0.0f;
   float m_run = -1e30f, l_run = 0.0f;
+  float neg_one;
+  asm("v_mov_b32 %0, -1.0" : "=v"(neg_one));
 
   auto codes = [&](const uint8_t* sp, int region_off, int gi) {
     const int g = g0 + gi;
@@ -347,8 +349,11 @@ void prefill_attn_kernel(PrefillArgs a) {
       }
       const half2_t h01 = pkrtz(x[0], x[1]);
       const half2_t h23 = pkrtz(x[2], x[3]);
-      const half2_t r01 = pkrtz(x[0] - (float)h01[0], x[1] - (float)h01[1]);
-      const half2_t r23 = pkrtz(x[2] - (float)h23[0], x[3] - (float)h23[1]);
+      // residual x - hi (exact) as one mixed-precision fma each (an opaque
+      // -1 keeps the f16 operand inside the fma instead of a convert and a
+      // subtract)
+      const half2_t r01 = pkrtz(fmaf(neg_one, (float)h01[0], x[0]), fmaf(neg_one, (float)h01[1], x[1]));
+      const half2_t r23 = pkrtz(fmaf(neg_one, (float)h23[0], x[2]), fmaf(neg_one, (float)h23[1], x[3]));
       const half4_t bh = cat4(h01, h23), bl = cat4(r01, r23);
       if constexpr (kBiasedCodes<BITS>) {
         float t = __builtin_amdgcn_fdot2(h01, one2, psum[gi], false);
