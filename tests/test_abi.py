@@ -79,3 +79,16 @@ def test_ring_and_global_arena_sizes():
     assert a == b * 8 * 64
     b, a = fmkv.layout_bytes(fmkv.make_desc(2, 512, 8, capacity=32768))
     assert a == 17408 * 2 * 2048 == 2 * 32768 * 1088
+
+
+def test_entry_points_reject_null_handles_before_hip():
+    """Prefill, decode step and projected append validate their handle first
+    (no device needed)."""
+    lib = fmkv.load_library()
+    assert lib.fmkv_prefill_step(None, None, None, 4, None, 8, 1.0, None,
+                                 fmkv.DTYPE_BF16, None) == fmkv.FMKV_ERR_INVALID_ARG
+    assert lib.fmkv_decode_step(None, None, None, 1, None, 8, 1.0, 0.0, None,
+                                fmkv.DTYPE_BF16, None) == fmkv.FMKV_ERR_INVALID_ARG
+    pro = fmkv.KvPrologue(None, 1e-6, 128, 1e4, 0)
+    assert lib.fmkv_cache_append_projected(None, None, None, 1, pro, None) == fmkv.FMKV_ERR_INVALID_ARG
+    assert b"null" in lib.fmkv_last_error()
