@@ -549,6 +549,8 @@ int fmkv_prefill_step(fmkv_cache* c, const void* k, const void* v, int64_t n, co
   pa.old_st = cache_store(c);
   pa.new_st = pa.old_st;
   pa.p0 = p0;
+  pa.start_pos = nullptr;
+  pa.n_seqs = 1;
   pa.n_q = (int32_t)n;
   pa.window = W;
   pa.vis_begin = c->vis_begin;
@@ -755,6 +757,52 @@ int fmkv_pool_destroy(fmkv_pool* p) {
   if (p->d_signs) (void)hipFree(p->d_signs);
   p->ws.release();
   delete p;
+  return FMKV_OK;
+}
+
+int fmkv_paged_prefill_step(fmkv_pool* p, const void* k, const void* v,
+                            const int32_t* block_tables, int32_t max_blocks,
+                            const int32_t* start_pos, int32_t n_seqs, int32_t n_new,
+                            const void* q, int32_t n_q_heads, float scale, void* out,
+                            int32_t out_dtype, void* stream) {
+  if (!p) return fail(FMKV_ERR_INVALID_ARG, "pool is null");
+  if (n_seqs < 1 || n_new < 1)
+    return fail(FMKV_ERR_INVALID_ARG, "a prefill step needs n_seqs >= 1 and n_new >= 1");
+  int rc = check_attn_args(p->desc, q, n_q_heads, 0.0f, out, out_dtype);
+  if (rc) return rc;
+  if (!std::isfinite(scale)) return fail(FMKV_ERR_INVALID_ARG, "scale must be finite");
+  const int32_t group = n_q_heads / p->desc.n_kv_heads;
+  if ((int64_t)n_new > (int64_t)65535 * (64 / group))
+    return fail(FMKV_ERR_INVALID_ARG, "n_new too large for one prefill step");
+  fmkv::AppendArgs ap;
+  int tasks = 0;
+  rc = prepare_paged_append(p, k, v, block_tables, max_blocks, start_pos, n_seqs, n_new, &ap,
+                            &tasks);
+  if (rc) return rc;
+  fmkv::PrefillArgs pa;
+  pa.old_st = ap.st;
+  pa.new_st = ap.st;
+  pa.p0 = 0;
+  pa.start_pos = start_pos;
+  pa.n_seqs = n_seqs;
+  pa.n_q = n_new;
+  pa.window = 0;
+  pa.vis_begin = 0;
+  pa.p_split = 0;
+  pa.new_blk0 = 0;
+  pa.group = group;
+  pa.n_q_heads = n_q_heads;
+  pa.q = static_cast<const uint16_t*>(q);
+  pa.qscale = scale * 1.4426950408889634f;
+  std::memcpy(pa.sign_bits, p->sign_bits, sizeof(pa.sign_bits));
+  pa.c = p->c;
+  pa.out = out;
+  pa.out_f32 = out_dtype == FMKV_DTYPE_F32 ? 1 : 0;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = fmkv::launch_append(ap, n_seqs, tasks, s);
+  if (e != hipSuccess) return hip_fail(e, "paged append launch");
+  e = fmkv::launch_prefill_attention(pa, s);
+  if (e != hipSuccess) return hip_fail(e, "prefill attention launch");
   return FMKV_OK;
 }
 

@@ -96,8 +96,10 @@ struct AttnArgs {
 // linear caches, which append before attending).
 struct PrefillArgs {
   Store old_st;
-  Store new_st;
+  Store new_st;  // a paged pool: its block_table maps each sequence's blocks
   int64_t p0;
+  const int32_t* start_pos;  // paged: per sequence p0 (device), else null -> p0
+  int32_t n_seqs;            // grid z; q and out gain a leading [n_seqs]
   int32_t n_q;
   int64_t window;
   int64_t vis_begin;

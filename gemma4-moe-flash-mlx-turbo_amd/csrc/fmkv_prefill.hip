@@ -29,6 +29,9 @@
 //         the bias terms are summed on the side.
 // Blocks wholly outside a pair's rows' windows are skipped by that pair.
 //
+// A paged pool runs one sequence per grid z with its own start position and
+// block table (linear sequences: the append goes first).
+//
 // Keys come from two stores: positions below p_split from old_st (the ring
 // of a sliding layer, read before the chunk's own append can overwrite
 // positions early queries still need), the rest from new_st (a staging
@@ -104,8 +107,16 @@ void prefill_attn_kernel(PrefillArgs a) {
   const int g0 = half * GH;
   const int G = a.group;
   const int QP = kPfRows / G;  // query positions per work-group
-  const int kvh = blockIdx.y;
+  const int kvh = blockIdx.y, seq = blockIdx.z;
   const int qi0 = blockIdx.x * QP;
+  // per-sequence start and block table (paged) through scalar loads, which
+  // never wait for the copies in flight
+  typedef const int32_t __attribute__((address_space(4)))* cint_ptr;
+  const int64_t p0 = a.start_pos ? (int64_t)((cint_ptr)(uintptr_t)a.start_pos)[seq] : a.p0;
+  const cint_ptr table =
+      a.new_st.block_table
+          ? (cint_ptr)(uintptr_t)(a.new_st.block_table + (int64_t)seq * a.new_st.table_stride)
+          : nullptr;
   const int nq = a.n_q - qi0 < QP ? a.n_q - qi0 : QP;  // valid positions of the tile
 
   // visible keys of position p: [lo(p), p]
@@ -118,20 +129,20 @@ void prefill_attn_kernel(PrefillArgs a) {
   const int row = pair * 16 + c;
   const int rq = row / G, rh = row - rq * G;
   const bool row_valid = rq < nq;
-  const int64_t p_row = a.p0 + qi0 + rq;
+  const int64_t p_row = p0 + qi0 + rq;
   const int64_t row_lo = lo_of(p_row);
   // the pair's positions [pA, pB] (pair-uniform)
   const int pq0 = (pair * 16) / G;
   int pq1 = (pair * 16 + 15) / G;
   if (pq1 > nq - 1) pq1 = nq - 1;
   const bool pair_any = pq0 <= pq1;
-  const int64_t pA = a.p0 + qi0 + pq0, pB = a.p0 + qi0 + pq1;
+  const int64_t pA = p0 + qi0 + pq0, pB = p0 + qi0 + pq1;
   const int64_t pair_lo_min = lo_of(pA), pair_lo_max = lo_of(pB);
   const bool pair_full_rows = (pair * 16 + 15) / G < nq;  // all 16 rows are real queries
 
   // ---- virtual blocks of the work-group: [lo(first), last] in 16-key
   // blocks, the part below p_split from old_st, the rest from new_st ----
-  const int64_t wg_lo = lo_of(a.p0 + qi0), wg_hi = a.p0 + qi0 + nq - 1;
+  const int64_t wg_lo = lo_of(p0 + qi0), wg_hi = p0 + qi0 + nq - 1;
   const int64_t b_lo = wg_lo / kBlockTokens, b_hi = wg_hi / kBlockTokens;
   const int64_t ps = a.p_split;
   int64_t old_last = (ps + kBlockTokens - 1) / kBlockTokens - 1;  // last block with keys < ps
@@ -159,7 +170,13 @@ void prefill_attn_kernel(PrefillArgs a) {
       v.b = new_first + (i - n_old);
       v.vlo = v.b * kBlockTokens > ps ? v.b * kBlockTokens : ps;
       v.vhi = (v.b + 1) * kBlockTokens;
-      const int64_t phys = v.b - a.new_blk0;
+      int64_t phys = v.b - a.new_blk0;
+      if (table) {
+        // a table entry outside the pool (or a position past the table's
+        // width) reads a valid block rather than faulting
+        phys = v.b < a.new_st.table_stride ? (int64_t)table[v.b] : 0;
+        phys = phys < 0 ? 0 : (phys >= a.new_st.n_blocks ? a.new_st.n_blocks - 1 : phys);
+      }
       v.ptr = a.new_st.base + phys * a.new_st.block_stride + (int64_t)kvh * a.new_st.head_stride;
     }
     return v;
@@ -180,7 +197,8 @@ void prefill_attn_kernel(PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < E; i++) x[i] = 0.0f;
     if (rq_ < nq) {
-      load_row<E>(a.q + ((int64_t)(qi0 + rq_) * a.n_q_heads + (int64_t)kvh * G + rh_) * D + lane * E, x);
+      load_row<E>(a.q + (((int64_t)seq * a.n_q + qi0 + rq_) * a.n_q_heads + (int64_t)kvh * G + rh_) * D +
+                      lane * E, x);
 #pragma unroll
       for (int i = 0; i < E; i++) x[i] = x[i] * a.qscale;
     }
@@ -424,7 +442,8 @@ void prefill_attn_kernel(PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < E; i++) x[i] = apply_sign(Rr[r * RS + lane * E + i], sbits, i);
     wave_fwht_signed<E>(x, lane);
-    const int64_t o_idx = ((int64_t)(qi0 + rq_) * a.n_q_heads + (int64_t)kvh * G + rh_) * D + lane * E;
+    const int64_t o_idx =
+        (((int64_t)seq * a.n_q + qi0 + rq_) * a.n_q_heads + (int64_t)kvh * G + rh_) * D + lane * E;
 #pragma unroll
     for (int i = 0; i < E; i++) {
       const float v = l > 0.0f ? (x[i] * cs_lane) / l : 0.0f;
@@ -439,7 +458,7 @@ void prefill_attn_kernel(PrefillArgs a) {
 template <int D, int BITS>
 hipError_t launch_t(const PrefillArgs& a, hipStream_t s) {
   const int qp = kPfRows / a.group;
-  dim3 grid((a.n_q + qp - 1) / qp, a.new_st.n_kv_heads, 1);
+  dim3 grid((a.n_q + qp - 1) / qp, a.new_st.n_kv_heads, a.n_seqs);
   hipLaunchKernelGGL((prefill_attn_kernel<D, BITS>), grid, dim3(kPfWaves * 64), 0, s, a);
   return hipGetLastError();
 }

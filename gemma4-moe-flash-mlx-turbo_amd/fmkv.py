@@ -45,7 +45,7 @@ EXPORTED = (
     "fmkv_cache_append_projected", "fmkv_paged_append_projected",
     "fmkv_pool_read_codes", "fmkv_set_blocks_per_split", "fmkv_cache_decode_splits",
     "fmkv_profile_enable", "fmkv_profile_collect", "fmkv_decode_step", "fmkv_paged_decode_step",
-    "fmkv_prefill_step",
+    "fmkv_prefill_step", "fmkv_paged_prefill_step",
 )
 
 
@@ -146,6 +146,8 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         "fmkv_decode_step": ([vp, vp, vp, i64, vp, i32, ctypes.c_float, ctypes.c_float, vp, i32,
                               vp], ctypes.c_int),
         "fmkv_prefill_step": ([vp, vp, vp, i64, vp, i32, ctypes.c_float, vp, i32, vp], ctypes.c_int),
+        "fmkv_paged_prefill_step": ([vp, vp, vp, vp, i32, vp, i32, i32, vp, i32, ctypes.c_float, vp,
+                                     i32, vp], ctypes.c_int),
         "fmkv_paged_decode_step": ([vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, vp, i32,
                                     ctypes.c_float, ctypes.c_float, vp, i32, vp], ctypes.c_int),
     }
@@ -403,6 +405,21 @@ class PagedPool:
         _check(self._lib.fmkv_paged_append_projected(
             self._h, _ptr(keys), _ptr(values), _ptr(block_tables), block_tables.shape[1],
             _ptr(start_pos), n_seqs, n_new, ctypes.byref(prologue), _stream(stream)))
+
+    def prefill_step(self, keys, values, block_tables, start_pos, q, scale: float = 1.0,
+                     out=None, dtype=torch.bfloat16, stream=None):
+        """append(keys, values, ...) at start_pos, then each sequence's causal
+        attention of its n_new queries. keys/values bf16 [n_seqs, n_new,
+        n_kv_heads, D]; q bf16 [n_seqs, n_new, n_q_heads, D]."""
+        if q.dim() != 4 or q.shape[:2] != keys.shape[:2]:
+            raise ValueError("q must be bf16 [n_seqs, n_new, n_q_heads, head_dim]")
+        if out is None:
+            out = torch.empty(q.shape, dtype=dtype, device=q.device)
+        _check(self._lib.fmkv_paged_prefill_step(
+            self._h, _ptr(keys), _ptr(values), _ptr(block_tables), block_tables.shape[1],
+            _ptr(start_pos), keys.shape[0], keys.shape[1], _ptr(q), q.shape[2], scale, _ptr(out),
+            _dtype_code(out.dtype), _stream(stream)))
+        return out
 
     def attention(self, q, block_tables, seq_lens, max_seq_len: int, scale: float = 1.0,
                   sparse_v_tau: float = 0.0, out=None, dtype=torch.bfloat16, stream=None):

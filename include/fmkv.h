@@ -221,6 +221,19 @@ int fmkv_paged_decode_step(fmkv_pool* pool, const void* k_bf16, const void* v_bf
                            int32_t n_q_heads, float scale, float sparse_v_tau, void* out,
                            int32_t out_dtype, void* stream);
 
+/* Batched chunked prefill: fmkv_paged_append of n_new tokens per sequence at
+ * start_pos, then each sequence's causal attention of those n_new queries
+ * over its positions [0, start_pos + i] (src/model/gemma4_attention.rs
+ * :84-104 with L > 1, mask of create_attention_mask, src/model/mod.rs
+ * :682-704) -- fmkv_prefill_step for a batch of requests. q: bf16
+ * [n_seqs][n_new][n_q_heads][head_dim]; out: the same shape in out_dtype.
+ * Affine mode; at most 8 query heads per KV head. */
+int fmkv_paged_prefill_step(fmkv_pool* pool, const void* k_bf16, const void* v_bf16,
+                            const int32_t* block_tables, int32_t max_blocks,
+                            const int32_t* start_pos, int32_t n_seqs, int32_t n_new,
+                            const void* q_bf16, int32_t n_q_heads, float scale, void* out,
+                            int32_t out_dtype, void* stream);
+
 /* Canonical codes of every pool block, indexed by (physical block * 16 + t). */
 int fmkv_pool_read_codes(const fmkv_pool* pool, void* codes, void* meta, void* stream);
 

@@ -127,3 +127,49 @@ def test_prefill_rejects_bad_arguments(gpu):
     with pytest.raises(gpu.Exception_) as e:
         cb.prefill_step(k, k, q)
     assert e.value.code == gpu.FMKV_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("D,bits,Hkv,Hq", [(512, 8, 2, 16), (256, 4, 8, 16)])
+def test_paged_prefill_ragged_starts(gpu, ora, D, bits, Hkv, Hq):
+    """fmkv_paged_prefill_step: four sequences with prefixes of 0, 21, 64 and
+    150 tokens on shuffled blocks take a 40-token chunk each in one call;
+    every sequence's outputs match its own oracle, its codes sit at the
+    block-table addresses."""
+    import torch
+
+    starts, n_new = [0, 21, 64, 150], 40
+    n_seqs = len(starts)
+    need = [(p0 + n_new + 15) // 16 for p0 in starts]
+    n_blocks = sum(need) + 5
+    perm = np.argsort(synth.splitmix64(91, n_blocks)).astype(np.int32)
+    tables = np.zeros((n_seqs, max(need)), np.int32)
+    o = 0
+    for s, nb in enumerate(need):
+        tables[s, :nb] = perm[o:o + nb]
+        o += nb
+    pool = gpu.PagedPool(gpu.make_desc(Hkv, D, bits), n_blocks)
+    dtab = torch.from_numpy(tables).cuda()
+    oracles = []
+    for s, p0 in enumerate(starts):
+        oc = ora.OracleCache(Hkv, D, bits, 0, p0 + n_new)
+        if p0:
+            k0, v0 = kv_batch(200 + s, p0, Hkv, D), kv_batch(300 + s, p0, Hkv, D)
+            oc.append(k0, v0)
+            pool.append(dev_bf16(k0[None]), dev_bf16(v0[None]), dtab[s:s + 1].contiguous(),
+                        torch.zeros(1, dtype=torch.int32, device="cuda"))
+        oracles.append(oc)
+    k = np.stack([kv_batch(400 + s, n_new, Hkv, D) for s in range(n_seqs)])
+    v = np.stack([kv_batch(500 + s, n_new, Hkv, D) for s in range(n_seqs)])
+    q = np.stack([q_chunk(600 + s, n_new, Hq, Hkv, D) for s in range(n_seqs)])
+    out = pool.prefill_step(dev_bf16(k), dev_bf16(v), dtab,
+                            torch.tensor(starts, dtype=torch.int32, device="cuda"), dev_bf16(q),
+                            1.0, dtype=torch.float32)
+    codes, meta = pool.read_codes()
+    torch.cuda.synchronize()
+    c, m = host_u32(codes), host_u16(meta)
+    for s, p0 in enumerate(starts):
+        check_attention(out[s], oracles[s].prefill(k[s], v[s], q[s], 1.0), f"seq {s}")
+        p = np.arange(p0 + n_new)
+        slots = tables[s, p // 16].astype(np.int64) * 16 + p % 16
+        assert np.array_equal(c[slots], oracles[s].codes[p]), f"seq {s} codes"
+        assert np.array_equal(m[slots], oracles[s].meta[p]), f"seq {s} scales"
