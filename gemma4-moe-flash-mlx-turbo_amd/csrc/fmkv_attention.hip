@@ -9,7 +9,10 @@
 // block through LDS (a flag handshake inside the pair, no work-group
 // barrier) and then run identical online-softmax bookkeeping. Two waves per
 // SIMD hide each other's latencies. The pairs' (m, l, O) meet once, in LDS,
-// at the end.
+// at the end. Small head-blocks (head_dim 128, head_dim 256 at 4 bits) in
+// work-groups of 8 blocks or more use eight single-wave streams instead
+// (b_begin + w, b_begin + w + 8, ...), each wave owning every group, with
+// no exchange (AttnPlan).
 //
 // Memory path: each wave copies its half of its pair's next blocks
 // HBM -> LDS with buffer_load_dwordx4 ... lds (16 bytes per lane, no VGPRs
@@ -69,37 +72,53 @@ namespace {
 // combine divides by the full L of the stats pass.
 constexpr int kDense = 0, kStats = 1, kGated = 2;
 
-// Staging plan of one (head_dim, bits). A stage holds one head-block as
+// Staging plan of one (head_dim, bits, stream kind). A block stream is a
+// wave pair (each wave owns half the 64-dim groups, SOLO false) or a single
+// wave owning every group (SOLO true). Pairs finish one block soonest; solo
+// streams, eight per work-group and with no score exchange, finish more
+// blocks per unit of time when a head-block is small (at most 1024 code
+// bits per token: head_dim 128, head_dim 256 at 4 bits), so the launch
+// picks them for work-groups of many blocks (kSoloMinBlocks).
+// A stage holds one head-block as
 //   [K codes][V codes][wave 0: K meta, V meta of its groups][wave 1: ...];
 // each wave copies its groups' code chunks and, with one partial
-// instruction, its groups' scale/bias. Stages per pair: about 136 KiB of
-// staging per work-group, at least two, and the largest wait (stages x
-// copies per block) within the 6-bit vmcnt field.
+// instruction, its groups' scale/bias. Stages per stream: about 136 KiB of
+// staging per work-group (144 KiB for single-wave streams, which need no
+// score-exchange area), at least two, and the largest wait (stages x copies
+// per block) within the 6-bit vmcnt field.
 template <int D, int BITS>
+constexpr bool kSoloCapable = D * BITS <= 1024;
+constexpr int kSoloMinBlocks = 8;  // blocks per work-group from which solo streams pay
+
+template <int D, int BITS, bool SOLO>
 struct AttnPlan {
   static constexpr BlockLayout L = make_layout(D, BITS, kAffine);
   static constexpr int NG = D / 64;
-  static constexpr int GH = NG / 2;  // groups per wave
+  static constexpr bool kSolo = SOLO;
+  static_assert(!SOLO || kSoloCapable<D, BITS>, "solo streams for small head-blocks only");
+  static constexpr int kWPS = kSolo ? 1 : 2;            // waves per stream
+  static constexpr int kStreams = kAttnWaves / kWPS;
+  static constexpr int GH = NG / kWPS;  // groups per wave
   static constexpr int kCodeChunks = (int)(L.code_bytes / kChunk);  // per K or V region
   // code chunks a wave copies per region: its groups' chunks (at 4 bits one
   // chunk holds two groups; at head_dim 128 both waves copy the one chunk)
   static constexpr int kWaveChunks = BITS == 8 ? GH : (GH >= 2 ? GH / 2 : 1);
   static constexpr int kMetaHalf = GH * 64;  // one wave's K (or V) scale/bias bytes
   static constexpr int kMetaOff = 2 * kCodeChunks * kChunk;
-  static constexpr int kStageBytes = kMetaOff + 4 * kMetaHalf;
+  static constexpr int kStageBytes = kMetaOff + 2 * kWPS * kMetaHalf;
   static constexpr int kCopies = 2 * kWaveChunks + 1;  // copy instructions per wave per block
-  static constexpr int kFit = (136 * 1024) / (kAttnPairs * kStageBytes);
+  static constexpr int kFit = ((kSolo ? 144 : 136) * 1024) / (kStreams * kStageBytes);
   static constexpr int kStagesA = kFit < 2 ? 2 : (kFit > 8 ? 8 : kFit);
   static constexpr int kStages = kStagesA * kCopies <= 63 ? kStagesA : 63 / kCopies;
   static constexpr int kQS = D + 4;  // padded row stride (LDS banks)
-  // a pair's merge rows [8 heads][kQS] floats reuse its own stages
-  static constexpr int kStageRegion = kAttnPairs * kStages * kStageBytes;
-  static_assert(8 * kQS * 4 <= kStages * kStageBytes, "merge rows fit in a pair's stages");
+  // a stream's merge rows [8 heads][kQS] floats reuse its own stages
+  static constexpr int kStageRegion = kStreams * kStages * kStageBytes;
+  static_assert(8 * kQS * 4 <= kStages * kStageBytes, "merge rows fit in a stream's stages");
   // prologue: the raw q rows, then the q table (B operands, group sums of
   // q_rot, group sums of the f16 high and residual parts); loop: the score
   // exchange
   static constexpr int kTabBytes = 2 * NG * kChunk + 8 * NG * 4 + 8 * NG * 8;
-  static constexpr int kXBytes = kAttnWaves * 2 * 64 * 16;
+  static constexpr int kXBytes = kSolo ? 0 : kAttnWaves * 2 * 64 * 16;
   static constexpr int kScratch = cmax(cmax(kTabBytes, kXBytes), 8 * D * 2);
   static_assert(NG % 2 == 0 && kCodeChunks >= 1, "layout");
   static_assert(kStages * kCopies <= 63, "vmcnt immediates");
@@ -348,10 +367,10 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, int64_t T, int
 }
 
 // Two waves per SIMD (register budget <= 256 each).
-template <int D, int BITS, int MODE>
+template <int D, int BITS, int MODE, bool SOLO>
 __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void decode_attn_kernel(AttnArgs a) {
-  using P = AttnPlan<D, BITS>;
+  using P = AttnPlan<D, BITS, SOLO>;
   constexpr BlockLayout L = P::L;
   constexpr int NG = P::NG, GH = P::GH;
   constexpr int E = D / 64;
@@ -363,12 +382,13 @@ void decode_attn_kernel(AttnArgs a) {
 
   __shared__ __align__(16) uint8_t stage[P::kStageRegion];
   __shared__ __align__(16) uint8_t scratch[P::kScratch];  // q-prep table, then score exchange
-  __shared__ float ml_s[kAttnPairs][8][2];
+  __shared__ float ml_s[P::kStreams][8][2];
   __shared__ int xflag[kAttnWaves];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-  const int pair = wave >> 1, half = wave & 1;
+  constexpr int NS = P::kStreams;
+  const int stream = P::kSolo ? wave : wave >> 1, half = P::kSolo ? 0 : wave & 1;
   const int j = lane >> 4, c = lane & 15;
   const int head = c & 7;
   const bool hi = c < 8;
@@ -412,10 +432,10 @@ void decode_attn_kernel(AttnArgs a) {
     return hbase + phys * a.st.block_stride;
   };
 
-  // this pair's blocks: pb0 + 4 i, i < nb
-  const int64_t pb0 = b_begin + pair;
-  const int nb = pb0 < b_end ? (int)((b_end - pb0 + kAttnPairs - 1) / kAttnPairs) : 0;
-  uint8_t* const pstage = stage + pair * NST * SB;
+  // this stream's blocks: pb0 + NS i, i < nb
+  const int64_t pb0 = b_begin + stream;
+  const int nb = pb0 < b_end ? (int)((b_end - pb0 + NS - 1) / NS) : 0;
+  uint8_t* const pstage = stage + stream * NST * SB;
   const uint32_t pstage_lds = lds_addr(pstage);
 
   // This wave's part of block lb into stage st: its groups' K and V code
@@ -449,14 +469,14 @@ void decode_attn_kernel(AttnArgs a) {
   copy_q_row<D>(a, scratch, seq, kvh, wave, lane);
 #pragma unroll
   for (int s = 0; s < NQ; s++)
-    if (s < nb) copy_block(s, pb0 + (int64_t)kAttnPairs * s);
+    if (s < nb) copy_block(s, pb0 + (int64_t)NS * s);
   wait_copies<CP, NQ>(nb < NQ ? nb : NQ);  // the q copy preceded every block
   // this lane's RHT signs, for the q rotation and the inverse rotation
   const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
   build_q_table<D, BITS>(a, scratch, wave, lane, sbits);
 #pragma unroll
   for (int s = NQ; s < NST; s++)
-    if (s < nb) copy_block(s, pb0 + (int64_t)kAttnPairs * s);
+    if (s < nb) copy_block(s, pb0 + (int64_t)NS * s);
 
   // B operands of this wave's groups (hi / residual halves of q_rot) and
   // their q sums for the bias term
@@ -560,23 +580,29 @@ void decode_attn_kernel(AttnArgs a) {
       vm = vmeta(sp, 0);
     }
 
-    // exchange the half scores with the partner wave: publish (the release
-    // orders the data before the flag), then wait for the partner's; both
-    // waves add the halves in the same order, so they hold identical scores
-    const int par = it & 1;
-    xs[(wave * 2 + par) * 64 + lane] = sv;
-    __hip_atomic_store(&xflag[wave], it + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-    while (__hip_atomic_load(&xflag[wave ^ 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
-           it + 1)
-      __builtin_amdgcn_s_sleep(1);
-    const float4_t sp_other = xs[((wave ^ 1) * 2 + par) * 64 + lane];
-    const float4_t s0 = half == 0 ? sv : sp_other;
-    const float4_t s1 = half == 0 ? sp_other : sv;
+    // pairs: exchange the half scores with the partner wave: publish (the
+    // release orders the data before the flag), then wait for the partner's;
+    // both waves add the halves in the same order, so they hold identical
+    // scores
     float s[4];
+    if constexpr (P::kSolo) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const float t = s0[i] + s1[i];
-      s[i] = t + row_ror8(t);
+      for (int i = 0; i < 4; i++) s[i] = sv[i] + row_ror8(sv[i]);
+    } else {
+      const int par = it & 1;
+      xs[(wave * 2 + par) * 64 + lane] = sv;
+      __hip_atomic_store(&xflag[wave], it + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      while (__hip_atomic_load(&xflag[wave ^ 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+             it + 1)
+        __builtin_amdgcn_s_sleep(1);
+      const float4_t sp_other = xs[((wave ^ 1) * 2 + par) * 64 + lane];
+      const float4_t s0 = half == 0 ? sv : sp_other;
+      const float4_t s1 = half == 0 ? sp_other : sv;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float t = s0[i] + s1[i];
+        s[i] = t + row_ror8(t);
+      }
     }
 
     // visibility: whole block in the common case (uniform test), per token
@@ -669,8 +695,8 @@ void decode_attn_kernel(AttnArgs a) {
   for (int i = 0; i < nb; i++) {
     const int rest = nb - 1 - i;
     wait_copies<CP, NST - 1>(rest < NST - 1 ? rest : NST - 1);
-    process(pstage + st * SB, pb0 + (int64_t)kAttnPairs * i, i);
-    if (i + NST < nb) copy_block(st, pb0 + (int64_t)kAttnPairs * (i + NST));
+    process(pstage + st * SB, pb0 + (int64_t)NS * i, i);
+    if (i + NST < nb) copy_block(st, pb0 + (int64_t)NS * (i + NST));
     st = st + 1 == NST ? 0 : st + 1;
   }
 
@@ -680,17 +706,17 @@ void decode_attn_kernel(AttnArgs a) {
   if constexpr (MODE == kStats) {
     // the split's softmax statistics per head: max and sum over the pairs
     if (hi && col_valid && half == 0 && j == 0) {
-      ml_s[pair][head][0] = m_run;
-      ml_s[pair][head][1] = l_run;
+      ml_s[stream][head][0] = m_run;
+      ml_s[stream][head][1] = l_run;
     }
     __syncthreads();
     if (wave == 0 && lane < G) {
       float M = ml_s[0][lane][0];
 #pragma unroll
-      for (int q = 1; q < kAttnPairs; q++) M = fmaxf(M, ml_s[q][lane][0]);
+      for (int q = 1; q < NS; q++) M = fmaxf(M, ml_s[q][lane][0]);
       float Lsum = 0.0f;
 #pragma unroll
-      for (int q = 0; q < kAttnPairs; q++)
+      for (int q = 0; q < NS; q++)
         Lsum = fmaf(__builtin_amdgcn_exp2f(ml_s[q][lane][0] - M), ml_s[q][lane][1], Lsum);
       const int64_t r = ((int64_t)seq * a.part_stride + split) * a.n_q_heads + (int64_t)kvh * G + lane;
       a.part_ml[r * 2 + 0] = M;
@@ -720,13 +746,15 @@ void decode_attn_kernel(AttnArgs a) {
     }
   }
 
-  // The pair's own stages become its merge rows [head][QS] as soon as both of
-  // its waves are done with them (all copies were waited for in the last
-  // block), without waiting for the other pairs.
-  __hip_atomic_store(&xflag[wave], nb + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-  while (__hip_atomic_load(&xflag[wave ^ 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
-         nb + 1)
-    __builtin_amdgcn_s_sleep(1);
+  // The stream's own stages become its merge rows [head][QS] as soon as its
+  // waves are done with them (all copies were waited for in the last block),
+  // without waiting for the other streams.
+  if constexpr (!P::kSolo) {
+    __hip_atomic_store(&xflag[wave], nb + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    while (__hip_atomic_load(&xflag[wave ^ 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+           nb + 1)
+      __builtin_amdgcn_s_sleep(1);
+  }
   float* const Rp = reinterpret_cast<float*>(pstage);
   if (hi && col_valid) {
 #pragma unroll
@@ -737,21 +765,21 @@ void decode_attn_kernel(AttnArgs a) {
         *reinterpret_cast<float4_t*>(&Rp[head * QS + d]) = o[gi * 4 + ct] + bacc[gi];
       }
     if (half == 0 && j == 0) {
-      ml_s[pair][head][0] = m_run;
-      ml_s[pair][head][1] = l_run;
+      ml_s[stream][head][0] = m_run;
+      ml_s[stream][head][1] = l_run;
     }
   }
-  __syncthreads();  // every pair's rows are written
+  __syncthreads();  // every stream's rows are written
 
   // head w on wave w
   if (wave < G) {
     const int hh = wave;
     float M = ml_s[0][hh][0];
 #pragma unroll
-    for (int q = 1; q < kAttnPairs; q++) M = fmaxf(M, ml_s[q][hh][0]);
-    float wgt[kAttnPairs], Lsum = 0.0f;
+    for (int q = 1; q < NS; q++) M = fmaxf(M, ml_s[q][hh][0]);
+    float wgt[NS], Lsum = 0.0f;
 #pragma unroll
-    for (int q = 0; q < kAttnPairs; q++) {
+    for (int q = 0; q < NS; q++) {
       wgt[q] = __builtin_amdgcn_exp2f(ml_s[q][hh][0] - M);
       Lsum = fmaf(wgt[q], ml_s[q][hh][1], Lsum);
     }
@@ -760,7 +788,7 @@ void decode_attn_kernel(AttnArgs a) {
     for (int i = 0; i < E; i++) {
       float v = 0.0f;
 #pragma unroll
-      for (int q = 0; q < kAttnPairs; q++)
+      for (int q = 0; q < NS; q++)
         v = fmaf(wgt[q], reinterpret_cast<const float*>(stage + q * NST * SB)[hh * QS + lane * E + i],
                  v);
       x[i] = apply_sign(v, sbits, i);
@@ -906,14 +934,22 @@ __global__ __launch_bounds__(64) void tau_threshold_kernel(AttnArgs a) {
 // The split kernel of one mode; with events, they are recorded by the
 // dispatch itself (start and end of the kernel's execution, as a kernel
 // trace times it), else a plain launch.
+template <int D, int BITS, int MODE, bool SOLO>
+hipError_t launch_kind(const AttnArgs& a, dim3 grid, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
+  if (ev0 && ev1)
+    hipExtLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SOLO>), grid, dim3(kAttnWaves * 64), 0,
+                          s, ev0, ev1, 0, a);
+  else
+    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SOLO>), grid, dim3(kAttnWaves * 64), 0, s, a);
+  return hipGetLastError();
+}
+
 template <int D, int BITS, int MODE>
 hipError_t launch_split(const AttnArgs& a, dim3 grid, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
-  if (ev0 && ev1)
-    hipExtLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE>), grid, dim3(kAttnWaves * 64), 0, s, ev0,
-                          ev1, 0, a);
-  else
-    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE>), grid, dim3(kAttnWaves * 64), 0, s, a);
-  return hipGetLastError();
+  if constexpr (kSoloCapable<D, BITS>) {
+    if (a.bps >= kSoloMinBlocks) return launch_kind<D, BITS, MODE, true>(a, grid, s, ev0, ev1);
+  }
+  return launch_kind<D, BITS, MODE, false>(a, grid, s, ev0, ev1);
 }
 
 template <int D, int BITS>

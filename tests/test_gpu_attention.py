@@ -71,6 +71,30 @@ def test_attention_split_counts_agree(gpu, ora, bps):
     check_attention(out, ref, f"bps={bps}")
 
 
+@pytest.mark.parametrize("D,bits,Hkv,Hq", [(256, 4, 8, 16), (128, 4, 4, 4), (128, 8, 2, 12),
+                                           (256, 4, 2, 12)])
+@pytest.mark.parametrize("bps", [7, 8, 13, 40])
+def test_attention_stream_kinds_agree(gpu, ora, D, bits, Hkv, Hq, bps):
+    """Head-blocks of at most 1024 code bits per token are streamed by wave
+    pairs in work-groups of fewer than 8 blocks and by single waves from 8
+    blocks on: both kinds, dense and sparse-V, against the oracle over a
+    context that ends inside a block."""
+    import torch
+
+    T, tau = 1500, 1.0 / 3000
+    cache, oc = filled_cache(gpu, ora, D, bits, Hkv, T, chunks=[700, 800], seed=11)
+    q = q_batch(12, Hq, Hkv, D)
+    gpu.set_blocks_per_split(bps)
+    try:
+        out = cache.attention(dev_bf16(q), 1.0, dtype=torch.float32)
+        gated = cache.attention(dev_bf16(q), 1.0, sparse_v_tau=tau, dtype=torch.float32)
+        torch.cuda.synchronize()
+    finally:
+        gpu.set_blocks_per_split(0)
+    check_attention(out, oc.attention(q, 1.0), f"dense bps={bps}")
+    check_attention(gated, oc.attention(q, 1.0, tau), f"sparse-V bps={bps}")
+
+
 @pytest.mark.parametrize("D,bits", [(256, 4), (256, 8)])
 def test_attention_ring_through_wraps(gpu, ora, D, bits):
     """Sliding layer: W = 64, one append per decode step, attention after every
