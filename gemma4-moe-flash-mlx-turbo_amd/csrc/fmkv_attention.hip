@@ -557,6 +557,8 @@ void decode_attn_kernel(AttnArgs a) {
   auto process = [&](const uint8_t* sp, int64_t b, int it) {
     // this half's S^T = K . q_rot^T, * scale + bias * sum(q), per group
     float4_t sv = (float4_t){0.f, 0.f, 0.f, 0.f};
+    // (pair waves keep each group's MFMA chain in program order; a solo
+    // wave's four independent groups interleave, 2% faster on 4-bit D=256)
     u32x4 kw = codes(sp, (int)L.k_codes, 0), km = kmeta(sp, 0);
 #pragma unroll
     for (int gi = 0; gi < GH; gi++) {
@@ -572,7 +574,7 @@ void decode_attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; i++)
         sv[i] = fmaf(lo16(km_g[i]), acc[i], fmaf(hi16(km_g[i]), qs[gi], sv[i]));
-      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (!P::kSolo) __builtin_amdgcn_sched_barrier(0);
     }
     u32x4 vw, vm;
     if constexpr (MODE != kStats) {
@@ -684,7 +686,7 @@ void decode_attn_kernel(AttnArgs a) {
       for (int ct = 0; ct < 4; ct++)
         o[gi * 4 + ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(v_operand<BITS>(vw_g, g, ct), bp,
                                                                o[gi * 4 + ct], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (!P::kSolo) __builtin_amdgcn_sched_barrier(0);
     }
   };
 
