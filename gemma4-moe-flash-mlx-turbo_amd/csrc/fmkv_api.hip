@@ -316,8 +316,8 @@ int prepare_append(const fmkv_cache* c, const void* k, const void* v, int64_t n,
 template <typename Owner>
 int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, int64_t nblk,
                              const void* q, int32_t n_q_heads, float scale, float tau, void* out,
-                             int32_t out_dtype, int wg_per_cu, int min_bps, int new_col,
-                             fmkv::AttnArgs* a) {
+                             int32_t out_dtype, int wg_per_cu, int min_bps, int first_mult,
+                             int new_col, fmkv::AttnArgs* a) {
   int rc = check_attn_args(o->desc, q, n_q_heads, tau, out, out_dtype);
   if (rc) return rc;
   const int H = o->desc.n_kv_heads, D = o->desc.head_dim;
@@ -336,7 +336,11 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   // the split columns are the grid's z dimension (at most 65535)
   if ((nblk + a->bps - 1) / a->bps + new_col > 65535)
     a->bps = (int32_t)((nblk + 65534 - new_col) / (65535 - new_col));
-  a->max_splits = (int32_t)((nblk + a->bps - 1) / a->bps);
+  // split 0 of each sequence takes first_mult x bps blocks
+  const int64_t bps0 = (int64_t)a->bps * first_mult;
+  a->bps0 = (int32_t)(bps0 < nblk ? bps0 : nblk);
+  if (a->bps0 < a->bps) a->bps0 = a->bps;
+  a->max_splits = (int32_t)(nblk <= a->bps0 ? 1 : 1 + (nblk - a->bps0 + a->bps - 1) / a->bps);
   a->new_col = new_col;
   a->part_stride = a->max_splits + new_col;
   // sparse-V (tau > 0) always goes through the split partials and the
@@ -369,7 +373,7 @@ int prepare_attention(fmkv_cache* c, int64_t T, const void* q, int32_t n_q_heads
   const int64_t nblk =
       (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
   return prepare_attention_common(c, cache_store(c), 1, nblk, q, n_q_heads, scale, tau, out,
-                                  out_dtype, fmkv::kAttnWgPerCu, 1, new_col, a);
+                                  out_dtype, fmkv::kAttnWgPerCu, 1, 1, new_col, a);
 }
 
 int prepare_paged_append(const fmkv_pool* p, const void* k, const void* v,
@@ -416,11 +420,14 @@ int prepare_paged_attention(fmkv_pool* p, const void* q, const int32_t* block_ta
   // Ragged lengths: the bound counts every sequence at max_seq_len, so the
   // plan aims at several work-groups per CU (the dispatcher balances their
   // uneven sizes), but at least 64 blocks each (a work-group's prologue and
-  // epilogue cost about as much as a dozen blocks). Four per CU measured
-  // best for 32 sequences of 512..16384 tokens (eight: 10% slower).
+  // epilogue cost about as much as a dozen blocks). Each sequence's first
+  // split is four times larger: the big work-groups start first and the
+  // small ones fill the tail. Six per CU measured best for 32 sequences of
+  // 512..16384 tokens (bps 171: 197 us; four per CU with equal splits:
+  // 207 us).
   return prepare_attention_common(p, pool_store(p, block_tables, max_blocks),
                                   n_seqs > 0 ? n_seqs : 1, nblk, q, n_q_heads, scale, tau, out,
-                                  out_dtype, 4 * fmkv::kAttnWgPerCu, 64, new_col, a);
+                                  out_dtype, 6 * fmkv::kAttnWgPerCu, 64, 4, new_col, a);
 }
 
 }  // namespace

@@ -404,7 +404,7 @@ void decode_attn_kernel(AttnArgs a) {
   const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
-  const int n_splits = n_splits_for(geo, a.bps, a.max_splits);
+  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits);
   if constexpr (MODE == kDense) {
     if (a.new_col && split == (int)gridDim.z - 1) {
       new_token_column<D, BITS>(a, scratch, T, n_splits, kvh, seq, wave, lane);
@@ -412,8 +412,9 @@ void decode_attn_kernel(AttnArgs a) {
     }
   }
   if (split >= n_splits) return;
-  const int64_t b_begin = geo.blk_lo + (int64_t)split * a.bps;
-  int64_t b_end = b_begin + a.bps;
+  const int64_t b_begin =
+      geo.blk_lo + (split == 0 ? 0 : a.bps0 + (int64_t)(split - 1) * a.bps);
+  int64_t b_end = b_begin + (split == 0 ? a.bps0 : a.bps);
   if (b_end > geo.blk_hi) b_end = geo.blk_hi;
 
   // Table entries are read through the constant address space: a uniform
@@ -844,7 +845,7 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
   const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
-  const int n_splits = n_splits_for(geo, a.bps, a.max_splits) + a.new_col;
+  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits) + a.new_col;
   const int64_t stride = (int64_t)a.n_q_heads;
   const int64_t base = (int64_t)seq * a.part_stride * stride + h;
 
@@ -914,7 +915,7 @@ __global__ __launch_bounds__(64) void tau_threshold_kernel(AttnArgs a) {
   const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
-  const int n_splits = n_splits_for(geo, a.bps, a.max_splits);
+  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits);
   const int64_t base = (int64_t)seq * a.part_stride * a.n_q_heads + h;
   float M = -INFINITY, L = 0.0f;
   for (int sp = lane; sp < n_splits; sp += 64) {

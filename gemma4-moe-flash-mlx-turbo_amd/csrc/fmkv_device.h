@@ -327,11 +327,14 @@ __device__ inline SeqGeom seq_geometry(int64_t T, int64_t window, int64_t vis_be
 
 // Split count of a sequence (>= 1, so split 0 always writes a result),
 // never more than the grid provides.
-__device__ inline int n_splits_for(const SeqGeom& g, int bps, int max_splits) {
+// Split 0 covers bps0 blocks, every later split bps (bps0 >= bps): a
+// sequence's first work-group is its largest, so the dispatcher, which
+// takes the grid's split columns in order, starts the big work first and
+// fills the tail with small work-groups.
+__device__ inline int n_splits_for(const SeqGeom& g, int bps0, int bps, int max_splits) {
   // block counts stay below 2^31 / 16: a 32-bit division suffices
   const uint32_t nb = (uint32_t)(g.blk_hi - g.blk_lo);
-  int64_t ns = (nb + (uint32_t)bps - 1u) / (uint32_t)bps;
-  if (ns < 1) ns = 1;
+  int64_t ns = nb <= (uint32_t)bps0 ? 1 : 1 + (nb - (uint32_t)bps0 + (uint32_t)bps - 1u) / (uint32_t)bps;
   if (ns > max_splits) ns = max_splits;
   return (int)ns;
 }

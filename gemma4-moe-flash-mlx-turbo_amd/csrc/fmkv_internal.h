@@ -65,7 +65,8 @@ struct AttnArgs {
   float qscale;       // softmax scale * log2(e)
   uint32_t sign_bits[16];  // RHT signs of dims 0..D-1, bit d set = -1
   float c;            // 1/sqrt(D)
-  int32_t bps;        // blocks per split
+  int32_t bps0;       // blocks of split 0 (>= bps)
+  int32_t bps;        // blocks of every later split
   int32_t max_splits; // split columns of the grid
   int32_t part_stride;  // partial slots per sequence: max_splits + new_col
   float* part_o;      // [n_seqs][part_stride][n_q_heads][D]

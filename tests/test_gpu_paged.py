@@ -11,10 +11,14 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("D,bits,Hkv,Hq", [(256, 4, 8, 16), (512, 8, 2, 16)])
-def test_paged_ragged_decode(gpu, ora, D, bits, Hkv, Hq):
+@pytest.mark.parametrize("bps", [0, 1, 3, 8])
+def test_paged_ragged_decode(gpu, ora, D, bits, Hkv, Hq, bps):
+    """bps: blocks per split (0: the plan's); a paged sequence's first split
+    takes 4 x bps blocks, so 1, 3 and 8 give several splits of both sizes
+    (8: single-wave streams at 4-bit D=256)."""
     import torch
 
-    lens = [5, 40, 100, 17, 1, 64, 300]
+    lens = [5, 40, 100, 17, 1, 64, 300, 700]
     n_seqs = len(lens)
     need = [(n + 1 + 15) // 16 for n in lens]
     max_blocks = max(need)
@@ -46,7 +50,12 @@ def test_paged_ragged_decode(gpu, ora, D, bits, Hkv, Hq):
     seq_lens = torch.tensor([n + 1 for n in lens], dtype=torch.int32, device="cuda")
     q = np.stack([synth.q_rows(900 + s, Hq, Hkv, D, synth.outlier_channels(10 * s, Hkv, D))
                   for s in range(n_seqs)])
-    out = pool.attention(dev_bf16(q), dtab, seq_lens, max(lens) + 1, 0.05, dtype=torch.float32)
+    gpu.set_blocks_per_split(bps)
+    try:
+        out = pool.attention(dev_bf16(q), dtab, seq_lens, max(lens) + 1, 0.05, dtype=torch.float32)
+        torch.cuda.synchronize()
+    finally:
+        gpu.set_blocks_per_split(0)
     codes, meta = pool.read_codes()
     torch.cuda.synchronize()
     c, m = host_u32(codes), host_u16(meta)

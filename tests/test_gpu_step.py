@@ -109,7 +109,10 @@ def test_step_validation_leaves_cache_unchanged(gpu):
 
 
 @pytest.mark.parametrize("D,bits,Hkv,Hq", [(256, 4, 8, 16), (512, 8, 2, 16)])
-def test_paged_step_matches_oracle_and_two_calls(gpu, ora, D, bits, Hkv, Hq):
+@pytest.mark.parametrize("bps", [0, 2, 8])
+def test_paged_step_matches_oracle_and_two_calls(gpu, ora, D, bits, Hkv, Hq, bps):
+    """bps: blocks per split (0: the plan's; 2 and 8 give several splits,
+    the first of 4 x bps blocks)."""
     import torch
 
     lens = [3, 40, 129, 16, 1, 250]
@@ -142,11 +145,15 @@ def test_paged_step_matches_oracle_and_two_calls(gpu, ora, D, bits, Hkv, Hq):
         seq_lens = start + 1
         mx = max(lens) + step + 1
         q = np.stack([q_rows(950 + 10 * step + s, Hq, Hkv, D) for s in range(n_seqs)])
-        out_a = pa.decode_step(dev_bf16(k1), dev_bf16(v1), dtab, start, seq_lens, mx, dev_bf16(q),
-                               0.05, dtype=torch.float32)
-        pb.append(dev_bf16(k1), dev_bf16(v1), dtab, start)
-        out_b = pb.attention(dev_bf16(q), dtab, seq_lens, mx, 0.05, dtype=torch.float32)
-        torch.cuda.synchronize()
+        gpu.set_blocks_per_split(bps)
+        try:
+            out_a = pa.decode_step(dev_bf16(k1), dev_bf16(v1), dtab, start, seq_lens, mx, dev_bf16(q),
+                                   0.05, dtype=torch.float32)
+            pb.append(dev_bf16(k1), dev_bf16(v1), dtab, start)
+            out_b = pb.attention(dev_bf16(q), dtab, seq_lens, mx, 0.05, dtype=torch.float32)
+            torch.cuda.synchronize()
+        finally:
+            gpu.set_blocks_per_split(0)
         assert torch.allclose(out_a, out_b, rtol=TWO_CALLS_RTOL, atol=TWO_CALLS_ATOL), \
             f"step {step}: step vs two calls"
         for s in range(n_seqs):
