@@ -197,6 +197,8 @@ def layout_bytes(desc: CacheDesc) -> tuple[int, int]:
 
 
 def set_blocks_per_split(bps: int) -> None:
+    """Blocks per split-K work-group for decode attention (0: the plan's);
+    a paged sequence's first split takes 4 x bps blocks."""
     _check(load_library().fmkv_set_blocks_per_split(bps))
 
 

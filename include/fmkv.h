@@ -241,7 +241,8 @@ int fmkv_pool_read_codes(const fmkv_pool* pool, void* codes, void* meta, void* s
 /* Tuning and introspection                                                 */
 /* ---------------------------------------------------------------------- */
 
-/* Blocks per split-K work-group for decode attention (0 = automatic). */
+/* Blocks per split-K work-group for decode attention (0 = automatic). In a
+ * paged pool each sequence's first split takes 4 x that many blocks. */
 int fmkv_set_blocks_per_split(int32_t blocks_per_split);
 
 /* Kernel timing (profiling aid, no reference counterpart): while enabled,
