@@ -97,7 +97,10 @@ struct AttnPlan {
   static constexpr bool kSolo = SOLO;
   static_assert(!SOLO || kSoloCapable<D, BITS>, "solo streams for small head-blocks only");
   static constexpr int kWPS = kSolo ? 1 : 2;            // waves per stream
-  static constexpr int kStreams = kAttnWaves / kWPS;
+  // solo work-groups run 12 waves, 3 per SIMD (<= 168 VGPRs each)
+  static constexpr int kWaves = kSolo ? 12 : kAttnWaves;
+  static constexpr int kWavesPerSimd = kWaves / 4;
+  static constexpr int kStreams = kWaves / kWPS;
   static constexpr int GH = NG / kWPS;  // groups per wave
   static constexpr int kCodeChunks = (int)(L.code_bytes / kChunk);  // per K or V region
   // code chunks a wave copies per region: its groups' chunks (at 4 bits one
@@ -118,7 +121,7 @@ struct AttnPlan {
   // q_rot, group sums of the f16 high and residual parts); loop: the score
   // exchange
   static constexpr int kTabBytes = 2 * NG * kChunk + 8 * NG * 4 + 8 * NG * 8;
-  static constexpr int kXBytes = kSolo ? 0 : kAttnWaves * 2 * 64 * 16;
+  static constexpr int kXBytes = kSolo ? 0 : kWaves * 2 * 64 * 16;
   static constexpr int kScratch = cmax(cmax(kTabBytes, kXBytes), 8 * D * 2);
   static_assert(NG % 2 == 0 && kCodeChunks >= 1, "layout");
   static_assert(kStages * kCopies <= 63, "vmcnt immediates");
@@ -193,10 +196,14 @@ __device__ void build_q_table(const AttnArgs& a, uint8_t* tab, int wave, int lan
   hsum = group_sum<LPG>(hsum, lane);
   lsum = group_sum<LPG>(lsum, lane);
   __syncthreads();  // every raw row is read before the table replaces them
+  // waves 0..7 write the 8 columns (zero past the group); more waves write
+  // nothing
   uint8_t* ent = tab + (2 * qs.g + qs.s) * kChunk + qs.i0 * 2;
-  store_halves<E>(ent + (qs.j * 16 + wave) * 16, hi);
-  store_halves<E>(ent + (qs.j * 16 + wave + 8) * 16, lo);
-  if ((lane & (LPG - 1)) == 0) {
+  if (wave < 8) {
+    store_halves<E>(ent + (qs.j * 16 + wave) * 16, hi);
+    store_halves<E>(ent + (qs.j * 16 + wave + 8) * 16, lo);
+  }
+  if (wave < 8 && (lane & (LPG - 1)) == 0) {
     reinterpret_cast<float*>(tab + 2 * NG * kChunk)[wave * NG + qs.g] = gsum;
     float* op = reinterpret_cast<float*>(tab + 2 * NG * kChunk + 8 * NG * 4);
     op[(wave * NG + qs.g) * 2 + 0] = hsum;
@@ -366,9 +373,12 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, int64_t T, int
   }
 }
 
-// Two waves per SIMD (register budget <= 256 each).
+// Pair work-groups: 8 waves, two per SIMD (register budget <= 256 each);
+// solo work-groups: 12 waves, three per SIMD (<= 168).
 template <int D, int BITS, int MODE, bool SOLO>
-__global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__((AttnPlan<D, BITS, SOLO>::kWaves * 64))
+__attribute__((amdgpu_waves_per_eu(AttnPlan<D, BITS, SOLO>::kWavesPerSimd,
+                                   AttnPlan<D, BITS, SOLO>::kWavesPerSimd)))
 void decode_attn_kernel(AttnArgs a) {
   using P = AttnPlan<D, BITS, SOLO>;
   constexpr BlockLayout L = P::L;
@@ -383,7 +393,7 @@ void decode_attn_kernel(AttnArgs a) {
   __shared__ __align__(16) uint8_t stage[P::kStageRegion];
   __shared__ __align__(16) uint8_t scratch[P::kScratch];  // q-prep table, then score exchange
   __shared__ float ml_s[P::kStreams][8][2];
-  __shared__ int xflag[kAttnWaves];
+  __shared__ int xflag[P::kWaves];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -940,10 +950,11 @@ __global__ __launch_bounds__(64) void tau_threshold_kernel(AttnArgs a) {
 template <int D, int BITS, int MODE, bool SOLO>
 hipError_t launch_kind(const AttnArgs& a, dim3 grid, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   if (ev0 && ev1)
-    hipExtLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SOLO>), grid, dim3(kAttnWaves * 64), 0,
-                          s, ev0, ev1, 0, a);
+    hipExtLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SOLO>), grid,
+                          dim3(AttnPlan<D, BITS, SOLO>::kWaves * 64), 0, s, ev0, ev1, 0, a);
   else
-    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SOLO>), grid, dim3(kAttnWaves * 64), 0, s, a);
+    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SOLO>), grid,
+                       dim3(AttnPlan<D, BITS, SOLO>::kWaves * 64), 0, s, a);
   return hipGetLastError();
 }
 
