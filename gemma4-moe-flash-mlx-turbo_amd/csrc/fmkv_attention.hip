@@ -10,9 +10,9 @@
 // barrier) and then run identical online-softmax bookkeeping. Two waves per
 // SIMD hide each other's latencies. The pairs' (m, l, O) meet once, in LDS,
 // at the end. Small head-blocks (head_dim 128, head_dim 256 at 4 bits) in
-// work-groups of 8 blocks or more use eight single-wave streams instead
-// (b_begin + w, b_begin + w + 8, ...), each wave owning every group, with
-// no exchange (AttnPlan).
+// work-groups of 8 blocks or more use twelve single-wave streams instead
+// (b_begin + w, b_begin + w + 12, ...; three waves per SIMD), each wave
+// owning every group, with no exchange (AttnPlan).
 //
 // Memory path: each wave copies its half of its pair's next blocks
 // HBM -> LDS with buffer_load_dwordx4 ... lds (16 bytes per lane, no VGPRs
@@ -75,7 +75,7 @@ constexpr int kDense = 0, kStats = 1, kGated = 2;
 // Staging plan of one (head_dim, bits, stream kind). A block stream is a
 // wave pair (each wave owns half the 64-dim groups, SOLO false) or a single
 // wave owning every group (SOLO true). Pairs finish one block soonest; solo
-// streams, eight per work-group and with no score exchange, finish more
+// streams, twelve per work-group and with no score exchange, finish more
 // blocks per unit of time when a head-block is small (at most 1024 code
 // bits per token: head_dim 128, head_dim 256 at 4 bits), so the launch
 // picks them for work-groups of many blocks (kSoloMinBlocks).
