@@ -12,8 +12,9 @@ Prints ONE JSON line:
              step (cache read + q/out + the append's rows), inputs resident in HBM;
   roofline   the split-K attention kernel's own GB/s (algorithmic bytes per
              launch / its average duration from HIP events) vs 8 TB/s;
-  cpu_baseline  the reference's decode read (SDPA over its bf16 cache, MLX
-             CPU op order) timed with the oracle on this host's cores.
+  cpu_baseline  the reference's decode step (TurboQuant round trip of the new
+             rows, O(T) concat, SDPA over its bf16 cache in MLX CPU op order)
+             timed with the oracle on this host's cores, all and one.
 """
 from __future__ import annotations
 
@@ -355,9 +356,14 @@ def run_c4(args) -> dict:
     import synth
 
     Hq, Hkv, D, bits, n_seqs = 16, 8, 256, 4, 32
+    if args.c4_heads:
+        Hkv, D, bits = {8: (8, 256, 4), 2: (2, 512, 8)}[args.c4_heads]
     per_tok = bytes_per_token_head(D, bits)
     steps, warm = args.steps if args.steps < 256 else 64, 8
     lens = (512 + (synth.splitmix64(404, n_seqs) % np.uint64(16384 - 512 + 1))).astype(np.int64)
+    if args.c4_seqs:  # a uniform batch instead: c4_seqs sequences of c4_len tokens
+        n_seqs = args.c4_seqs
+        lens = np.full(n_seqs, args.c4_len, np.int64)
     cap = lens + warm + steps + 1
     need = (cap + 15) // 16
     max_blocks = int(need.max())
@@ -412,7 +418,7 @@ def run_c4(args) -> dict:
     tok = float((lens + warm + steps / 2 + 1).sum())
     read = tok * Hkv * per_tok + n_seqs * (2 * Hq * D * 2 + Hkv * (2 * D * 2 + per_tok))
     gbs = read / (us * 1e-6) / 1e9
-    log(f"c4: {us:.1f} us/step, {gbs:.0f} GB/s over {read / 1e6:.0f} MB/step")
+    log(f"c4: {n_seqs} seqs (Hkv {Hkv}): {us:.1f} us/step, {gbs:.0f} GB/s over {read / 1e6:.0f} MB/step")
     return {
         "metric": "batched ragged paged decode GB/s (32 seqs, lengths U[512,16384])",
         "value": round(gbs, 1), "unit": "GB/s",
@@ -420,8 +426,8 @@ def run_c4(args) -> dict:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
         "data": "synthetic (seeded N(0,1), 4 outlier channels x20; prefill from a resident 2048-row chunk)",
         "config": {"workload": "batched ragged decode, paged pool of 16-token blocks (shuffled ids): "
-                               "32 sequences, Hq 16, Hkv 8, head_dim 256, 4-bit group-64, 1 token "
-                               "append + attention per sequence per step",
+                               f"{n_seqs} sequences, Hq 16, Hkv {Hkv}, head_dim {D}, {bits}-bit group-64, "
+                               "1 token append + attention per sequence per step",
                    "n_seqs": n_seqs, "total_context": int(lens.sum()), "n_q_heads": Hq,
                    "n_kv_heads": Hkv, "head_dim": D, "bits": bits},
         "hbm_frac_of_value": round(gbs / HBM_PEAK_GBS, 4),
@@ -571,36 +577,139 @@ def run_c5(args) -> dict:
     }
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads() -> int:
+    """Host threads for the all-cores run: the cores this process may use,
+    capped by OMP_NUM_THREADS when it is set."""
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return max(1, min(avail, env) if env > 0 else avail)
+
+
+class ReferenceLayer:
+    """The reference's per-layer decode work on the CPU, restated with the
+    oracle (src/cache.rs:266-310 and src/model/gemma4_attention.rs:94-103):
+    update_and_fetch runs turbo_round_trip_kv on the new K and V rows (dense
+    x.R and .Rt matmuls, Lloyd-Max binning; R built once), concatenates them
+    onto the stored bf16 arrays (a fresh array each call, O(T)), and SDPA
+    reads the whole bf16 cache in MLX's unfused op order."""
+
+    def __init__(self, oracle, k0, v0, capacity, Hq, bits, n_threads):
+        self.ora, self.Hq, self.bits, self.threads = oracle, Hq, bits, n_threads
+        T, Hkv, D = k0.shape
+        self.r, self.rt = oracle.build_rht(D)
+        # two buffers per array: each append writes a fresh array (MLX's
+        # allocator recycles the freed one, so no page is touched twice)
+        self.kb = [np.empty((capacity, Hkv, D), np.uint16) for _ in range(2)]
+        self.vb = [np.empty((capacity, Hkv, D), np.uint16) for _ in range(2)]
+        self.kb[0][:T], self.vb[0][:T] = k0, v0
+        self.cur, self.T = 0, T
+        self.out = np.empty((Hq, D), np.uint16)
+
+    def append(self, k_new, v_new):
+        o = self.ora
+        kq = o.turbo_round_trip_rt(k_new, self.bits, self.r, self.rt)
+        vq = o.turbo_round_trip_rt(v_new, self.bits, self.r, self.rt)
+        nxt = 1 - self.cur
+        o.concat_rows(self.kb[self.cur], self.T, kq, self.kb[nxt], self.threads)
+        o.concat_rows(self.vb[self.cur], self.T, vq, self.vb[nxt], self.threads)
+        self.cur, self.T = nxt, self.T + k_new.shape[0]
+
+    def attend(self, q):
+        k, v = self.kb[self.cur][:self.T], self.vb[self.cur][:self.T]
+        return self.ora.sdpa_bf16_decode(q, k, v, 1.0, self.threads)
+
+
 def cpu_baseline_c3(args, k_bf16, v_bf16, Hq, Hkv, D, per_tok) -> dict:
-    """The reference's decode read on its bf16 cache (SDPA, MLX CPU op order),
-    timed with the oracle on this host: one full 32K-context step per rep,
-    repeated for about args.cpu_seconds."""
+    """The reference's decode step at 32K, timed with the oracle on this
+    host: append (TurboQuant round trip of the token's K/V rows + the O(T)
+    concat) and SDPA over the bf16 cache, on all cores for about
+    args.cpu_seconds and on one core for two steps; then C1 in full (4096
+    single-token appends into a Hq 16, Hkv 8, head_dim 256 layer, then one
+    decode step) on all cores."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
     import synth
 
     T = k_bf16.shape[0]
+    # TurboQuant takes 2-4 bits (src/cache.rs:87 panics otherwise); its cost
+    # is the two dense D x D matmuls per row whatever the bit width
+    rt_bits = 4
     q = synth.q_rows(43, Hq, Hkv, D, None)
-    threads = min(os.cpu_count() or 1, 16, Hq)
-    oracle.sdpa_bf16_decode(q, k_bf16[:64], v_bf16[:64], 1.0, threads)  # warm
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        oracle.sdpa_bf16_decode(q, k_bf16, v_bf16, 1.0, threads)
-        reps += 1
-        if time.perf_counter() - t0 >= args.cpu_seconds:
-            break
-    dt = (time.perf_counter() - t0) / reps
-    gbs = (T * Hkv * per_tok + 2 * Hq * D * 2) / dt / 1e9
-    log(f"cpu baseline: {dt*1e3:.1f} ms per 32K decode step on {threads} threads")
+    kn = synth.kv_rows(44, 64, Hkv, D, None, dist="t3")
+    vn = synth.kv_rows(45, 64, Hkv, D, None)
+    threads = cpu_threads()
+
+    def run(n_threads, seconds, max_reps):
+        lay = ReferenceLayer(oracle, k_bf16, v_bf16, T + max_reps + 1, Hq, rt_bits, n_threads)
+        lay.append(kn[:1], vn[:1])  # warm (first touch of the second buffers)
+        lay.attend(q)
+        reps, t0 = 0, time.perf_counter()
+        while reps < max_reps:
+            lay.append(kn[reps + 1:reps + 2], vn[reps + 1:reps + 2])
+            lay.attend(q)
+            reps += 1
+            if time.perf_counter() - t0 >= seconds:
+                break
+        return (time.perf_counter() - t0) / reps, reps, lay.T
+
+    dt, reps, t_end = run(threads, args.cpu_seconds, 60)
+    dt1, reps1, _ = run(1, float("inf"), 2)
+    step_bytes = (T + 1) * Hkv * per_tok + 2 * Hq * D * 2 + Hkv * (2 * D * 2 + per_tok)
+    gbs, gbs1 = step_bytes / dt / 1e9, step_bytes / dt1 / 1e9
+    log(f"cpu baseline: {dt*1e3:.1f} ms per 32K decode step on {threads} threads, "
+        f"{dt1*1e3:.1f} ms on 1")
+    c1 = cpu_baseline_c1(oracle, synth, threads)
     return {
         "value": round(gbs, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{reps} decode step(s) at T={T}: SDPA over the bf16 cache (reference read, MLX CPU "
-                  f"op order), {dt*1e3:.1f} ms/step; GB/s over the same algorithmic bytes as the GPU",
+        "sample": f"{reps} reference decode step(s) at T={T}..{t_end} on {threads} threads: "
+                  f"TurboQuant round trip of the token's K/V rows ({rt_bits}-bit, dense R), O(T) "
+                  f"concat onto the bf16 cache, SDPA over it (MLX CPU op order) -- {dt*1e3:.1f} "
+                  f"ms/step; GB/s over the same algorithmic bytes as the GPU step",
         "ms_per_step": round(dt * 1e3, 3),
+        "one_core": {"value": round(gbs1, 3), "unit": "GB/s", "ms_per_step": round(dt1 * 1e3, 3),
+                     "steps": reps1},
+        "nproc": os.cpu_count(),
+        "cpu_model": cpu_model(),
+        "c1_full": c1,
     }
+
+
+def cpu_baseline_c1(oracle, synth, threads) -> dict:
+    """C1 on the reference path, in full: 4096 single-token appends (round
+    trip at 4 bits + O(T) concat each) into a Hq 16, Hkv 8, head_dim 256
+    layer, then one decode step (append + SDPA)."""
+    Hq, Hkv, D, T = 16, 8, 256, 4096
+    ch = synth.outlier_channels(1, Hkv, D)
+    k = synth.kv_rows(81, T + 1, Hkv, D, ch)
+    v = synth.kv_rows(82, T + 1, Hkv, D, ch)
+    q = synth.q_rows(83, Hq, Hkv, D, ch)
+    lay = ReferenceLayer(oracle, k[:0], v[:0], T + 1, Hq, 4, threads)
+    t0 = time.perf_counter()
+    for i in range(T):
+        lay.append(k[i:i + 1], v[i:i + 1])
+    t1 = time.perf_counter()
+    lay.append(k[T:], v[T:])
+    lay.attend(q)
+    t2 = time.perf_counter()
+    log(f"cpu baseline C1: {T} appends in {t1 - t0:.2f} s, decode step {(t2 - t1)*1e3:.1f} ms "
+        f"({threads} threads)")
+    return {"append_tokens_per_s": round(T / (t1 - t0), 1), "appends": T,
+            "decode_step_ms": round((t2 - t1) * 1e3, 3), "threads": threads,
+            "workload": "Hq 16, Hkv 8, head_dim 256, 4-bit TurboQuant round trip, bf16 cache"}
 
 
 def copy_calibration(mib: int) -> int:
@@ -632,7 +741,7 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--context", type=int, default=32768)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--bps", type=int, default=0, help="blocks per split-K work-group (0: auto)")
     ap.add_argument("--graph-steps", type=int, default=64,
@@ -652,6 +761,11 @@ def main(argv=None) -> int:
     ap.add_argument("--prefill-sliding", action="store_true",
                     help="prefill workload on the sliding-layer shape (ring W 1024)")
     ap.add_argument("--c5-context", type=int, default=131072)
+    ap.add_argument("--c4-seqs", type=int, default=0,
+                    help="c4: a uniform batch of this many sequences of --c4-len tokens instead")
+    ap.add_argument("--c4-len", type=int, default=32768)
+    ap.add_argument("--c4-heads", type=int, default=0, choices=[0, 2, 8],
+                    help="c4: 8 (Hkv 8, head_dim 256, 4-bit; default) or 2 (Hkv 2, head_dim 512, 8-bit)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the KV path is "

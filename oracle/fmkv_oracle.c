@@ -27,6 +27,11 @@
 #include <string.h>
 #ifdef _OPENMP
 #include <omp.h>
+/* Row loops over `rows` run in parallel: every row is computed by one thread in the
+ * order written, so the results do not depend on the thread count. */
+#define OMP_ROWS _Pragma("omp parallel for schedule(static) if (rows > 64)")
+#else
+#define OMP_ROWS
 #endif
 
 /* ------------------------------------------------------------------------ */
@@ -182,19 +187,31 @@ int ora_lloyd_max_codebook(int bits, float* centroids, float* bounds) {
  *   out = bf16(((vals * (1/sqrt d)) . Rt) * norm).                        */
 void ora_turbo_round_trip_dense(const uint16_t* x_bf16, int64_t rows, int d, int bits,
                                 uint64_t seed, uint16_t* out_bf16) {
-  float cent[16], bnd[15];
-  int nc = ora_lloyd_max_codebook(bits, cent, bnd);
-  if (nc == 0) return;
   float* r = (float*)malloc(sizeof(float) * (size_t)d * d);
   float* rt = (float*)malloc(sizeof(float) * (size_t)d * d);
   ora_build_rht(d, seed, r, rt);
+  ora_turbo_round_trip_rt(x_bf16, rows, d, bits, r, rt, out_bf16);
+  free(r);
+  free(rt);
+}
+
+/* The same with R and Rt built once by the caller (KVCache::
+ * new_quantized_with_window keeps them in its TurboQuantConfig,
+ * src/cache.rs:206-227). Rows run in parallel. */
+void ora_turbo_round_trip_rt(const uint16_t* x_bf16, int64_t rows, int d, int bits, const float* r,
+                             const float* rt, uint16_t* out_bf16) {
+  float cent[16], bnd[15];
+  int nc = ora_lloyd_max_codebook(bits, cent, bnd);
+  if (nc == 0) return;
   float sqrt_d = sqrtf((float)d);
   float inv_sqrt_d = 1.0f / sqrtf((float)d);
   const float eps = 1e-8f;
-  float* x = (float*)malloc(sizeof(float) * d);
-  float* z = (float*)malloc(sizeof(float) * d);
-  float* w = (float*)malloc(sizeof(float) * d);
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if (rows > 1)
+#endif
   for (int64_t row = 0; row < rows; row++) {
+    float* x = (float*)malloc(sizeof(float) * 3 * (size_t)d);
+    float *z = x + d, *w = x + 2 * d;
     const uint16_t* xr = x_bf16 + row * d;
     float ss = 0.0f;
     for (int i = 0; i < d; i++) {
@@ -204,27 +221,23 @@ void ora_turbo_round_trip_dense(const uint16_t* x_bf16, int64_t rows, int d, int
     float norm = sqrtf(ss);
     float den = norm + eps;
     for (int i = 0; i < d; i++) x[i] = x[i] / den;
+    /* z_j = sum_i x_i R_ij, summed in i order (the outer loop runs over i
+     * so that R is read row by row) */
+    for (int j = 0; j < d; j++) z[j] = 0.0f;
+    for (int i = 0; i < d; i++)
+      for (int j = 0; j < d; j++) z[j] += x[i] * r[(size_t)i * d + j];
     for (int j = 0; j < d; j++) {
-      float acc = 0.0f;
-      for (int i = 0; i < d; i++) acc += x[i] * r[(size_t)i * d + j];
-      z[j] = acc * sqrt_d;
-    }
-    for (int j = 0; j < d; j++) {
+      z[j] = z[j] * sqrt_d;
       int idx = 0;
       for (int b = 0; b < nc - 1; b++) idx += (z[j] >= bnd[b]) ? 1 : 0;
       w[j] = cent[idx] * inv_sqrt_d;
     }
-    for (int j = 0; j < d; j++) {
-      float acc = 0.0f;
-      for (int i = 0; i < d; i++) acc += w[i] * rt[(size_t)i * d + j];
-      out_bf16[row * d + j] = ora_f32_to_bf16(acc * norm);
-    }
+    for (int j = 0; j < d; j++) z[j] = 0.0f;
+    for (int i = 0; i < d; i++)
+      for (int j = 0; j < d; j++) z[j] += w[i] * rt[(size_t)i * d + j];
+    for (int j = 0; j < d; j++) out_bf16[row * d + j] = ora_f32_to_bf16(z[j] * norm);
+    free(x);
   }
-  free(x);
-  free(z);
-  free(w);
-  free(r);
-  free(rt);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -261,6 +274,7 @@ static void fwht_f64(double* x, int n) {
  *   y_j = (FWHT(x)_j * c) * s_j,  c = 1/sqrt(d) in f32.                   */
 void ora_rotate_rows_f32(const float* x, int64_t rows, int d, const float* signs, float* y) {
   float c = ora_inv_sqrt(d);
+  OMP_ROWS
   for (int64_t r = 0; r < rows; r++) {
     float* yr = y + r * d;
     memcpy(yr, x + r * d, sizeof(float) * d);
@@ -271,6 +285,7 @@ void ora_rotate_rows_f32(const float* x, int64_t rows, int d, const float* signs
 
 void ora_rotate_rows(const uint16_t* x_bf16, int64_t rows, int d, const float* signs, float* y) {
   float c = ora_inv_sqrt(d);
+  OMP_ROWS
   for (int64_t r = 0; r < rows; r++) {
     float* yr = y + r * d;
     for (int j = 0; j < d; j++) yr[j] = ora_bf16_to_f32(x_bf16[r * d + j]);
@@ -283,6 +298,7 @@ void ora_rotate_rows(const uint16_t* x_bf16, int64_t rows, int d, const float* s
  * constant): x_j = c * FWHT(y o s)_j.                                       */
 void ora_unrotate_rows_f64(const double* y, int64_t rows, int d, const float* signs, double* x) {
   double c = (double)ora_inv_sqrt(d);
+  OMP_ROWS
   for (int64_t r = 0; r < rows; r++) {
     double* xr = x + r * d;
     for (int i = 0; i < d; i++) xr[i] = y[r * d + i] * (double)signs[i];
@@ -337,6 +353,7 @@ void ora_affine_quantize(const float* y, int64_t rows, int d, int bits, int gs,
   int64_t words_per_row = ((int64_t)d * bits + 31) / 32;
   int ng = d / gs;
   memset(packed, 0, sizeof(uint32_t) * (size_t)(words_per_row * rows));
+  OMP_ROWS
   for (int64_t r = 0; r < rows; r++) {
     for (int g = 0; g < ng; g++) {
       const float* w = y + r * d + (int64_t)g * gs;
@@ -372,6 +389,7 @@ void ora_affine_dequantize(const uint32_t* packed, const uint16_t* scales, const
                            int64_t rows, int d, int bits, int gs, double* y) {
   int64_t words_per_row = ((int64_t)d * bits + 31) / 32;
   int ng = d / gs;
+  OMP_ROWS
   for (int64_t r = 0; r < rows; r++)
     for (int j = 0; j < d; j++) {
       uint32_t c = get_bits(packed + r * words_per_row, (int64_t)j * bits, bits);
@@ -420,22 +438,30 @@ void ora_codebook_quantize(const uint16_t* x_bf16, int64_t rows, int d, int bits
   float sqrt_d = sqrtf((float)d);
   int64_t words_per_row = ((int64_t)d * bits + 31) / 32;
   memset(packed, 0, sizeof(uint32_t) * (size_t)(words_per_row * rows));
-  float* x = (float*)malloc(sizeof(float) * d);
-  for (int64_t r = 0; r < rows; r++) {
-    for (int j = 0; j < d; j++) x[j] = ora_bf16_to_f32(x_bf16[r * d + j]);
-    float norm = sqrtf(canonical_sumsq(x, d));
-    float den = norm + 1e-8f;
-    for (int j = 0; j < d; j++) x[j] = x[j] / den;
-    ora_fwht(x, d);
-    for (int j = 0; j < d; j++) {
-      float z = ((x[j] * c) * signs[j]) * sqrt_d;
-      int idx = 0;
-      for (int b = 0; b < nc - 1; b++) idx += (z >= bnd[b]) ? 1 : 0;
-      put_bits(packed + r * words_per_row, (int64_t)j * bits, bits, (uint32_t)idx);
+#ifdef _OPENMP
+#pragma omp parallel if (rows > 64)
+#endif
+  {
+    float* x = (float*)malloc(sizeof(float) * d);
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+    for (int64_t r = 0; r < rows; r++) {
+      for (int j = 0; j < d; j++) x[j] = ora_bf16_to_f32(x_bf16[r * d + j]);
+      float norm = sqrtf(canonical_sumsq(x, d));
+      float den = norm + 1e-8f;
+      for (int j = 0; j < d; j++) x[j] = x[j] / den;
+      ora_fwht(x, d);
+      for (int j = 0; j < d; j++) {
+        float z = ((x[j] * c) * signs[j]) * sqrt_d;
+        int idx = 0;
+        for (int b = 0; b < nc - 1; b++) idx += (z >= bnd[b]) ? 1 : 0;
+        put_bits(packed + r * words_per_row, (int64_t)j * bits, bits, (uint32_t)idx);
+      }
+      norms[r] = ora_f32_to_f16(norm);
     }
-    norms[r] = ora_f32_to_f16(norm);
+    free(x);
   }
-  free(x);
 }
 
 /* Rotated-domain value of a codebook row: y_j = centroid[idx_j] * norm / sqrt(d). */
@@ -445,6 +471,7 @@ void ora_codebook_dequant_rotated(const uint32_t* packed, const uint16_t* norms,
   ora_lloyd_max_codebook(bits, cent, NULL);
   int64_t words_per_row = ((int64_t)d * bits + 31) / 32;
   double inv = (double)ora_inv_sqrt(d);
+  OMP_ROWS
   for (int64_t r = 0; r < rows; r++) {
     double nrm = ora_f16_to_f32(norms[r]);
     for (int j = 0; j < d; j++)
@@ -619,8 +646,11 @@ int64_t ora_paged_address(const int32_t* block_table, int64_t pos, int block_siz
 void ora_attention_f64(const double* q, const double* k, const double* v, const uint8_t* valid,
                        int64_t t, int hq, int hkv, int d, double scale, double tau, double* out) {
   int rep = hq / hkv;
-  double* s = (double*)malloc(sizeof(double) * (size_t)(t > 0 ? t : 1));
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) if (t * d > 65536)
+#endif
   for (int h = 0; h < hq; h++) {
+    double* s = (double*)malloc(sizeof(double) * (size_t)(t > 0 ? t : 1));
     int kh = h / rep;
     double m = -INFINITY;
     for (int64_t i = 0; i < t; i++) {
@@ -640,15 +670,16 @@ void ora_attention_f64(const double* q, const double* k, const double* v, const 
       l += s[i];
     }
     for (int j = 0; j < d; j++) out[h * d + j] = 0.0;
-    if (l == 0.0) continue;
-    for (int64_t i = 0; i < t; i++) {
-      double w = s[i] / l;
-      if (tau > 0.0 && w < tau) continue;
-      const double* vr = v + (i * hkv + kh) * d;
-      for (int j = 0; j < d; j++) out[h * d + j] += w * vr[j];
+    if (l != 0.0) {
+      for (int64_t i = 0; i < t; i++) {
+        double w = s[i] / l;
+        if (tau > 0.0 && w < tau) continue;
+        const double* vr = v + (i * hkv + kh) * d;
+        for (int j = 0; j < d; j++) out[h * d + j] += w * vr[j];
+      }
     }
+    free(s);
   }
-  free(s);
 }
 
 /* Merge of split partials (m_i, l_i, o_i[d]) where o_i = sum exp(s - m_i) v:
@@ -672,43 +703,99 @@ void ora_lse_merge(const double* m, const double* l, const double* o, int n_part
 /* The reference's decode read on its bf16 cache in the op order of MLX's
  * unfused SDPA: q*scale in bf16, bf16 scores (f32 accumulation), precise
  * softmax in f32 rounded to bf16, bf16 output (f32 accumulation). This is the
- * CPU baseline the benchmark times; it is not a parity target. */
+ * CPU baseline the benchmark times; it is not a parity target. Every score,
+ * the per-head max and sum, and every output element are computed in the
+ * same order on any thread count: the scores run in parallel over (head,
+ * key), the sums per head, the output over (head, 64-dim slice), each
+ * summing its keys in order. */
 void ora_sdpa_bf16_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t t,
                           int hq, int hkv, int d, float scale, uint16_t* out, int n_threads) {
   int rep = hq / hkv;
 #ifdef _OPENMP
   if (n_threads <= 0) n_threads = omp_get_max_threads();
+#endif
+  float* qs = (float*)malloc(sizeof(float) * (size_t)hq * d);
+  float* s = (float*)malloc(sizeof(float) * (size_t)hq * (size_t)(t > 0 ? t : 1));
+  float* lsum = (float*)malloc(sizeof(float) * (size_t)hq);
+  for (int h = 0; h < hq; h++)
+    for (int j = 0; j < d; j++)
+      qs[h * d + j] = ora_bf16_to_f32(ora_f32_to_bf16(ora_bf16_to_f32(q[h * d + j]) * scale));
+#ifdef _OPENMP
+#pragma omp parallel num_threads(n_threads)
+#endif
+  {
+#ifdef _OPENMP
+#pragma omp for collapse(2) schedule(static)
+#endif
+    for (int h = 0; h < hq; h++)
+      for (int64_t i = 0; i < t; i++) {
+        const uint16_t* kr = k + (i * hkv + h / rep) * d;
+        const float* qh = qs + (size_t)h * d;
+        float acc = 0.0f;
+        for (int j = 0; j < d; j++) acc += qh[j] * ora_bf16_to_f32(kr[j]);
+        s[(size_t)h * t + i] = ora_bf16_to_f32(ora_f32_to_bf16(acc));
+      }
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+    for (int h = 0; h < hq; h++) {
+      float* sh = s + (size_t)h * t;
+      float m = -INFINITY;
+      for (int64_t i = 0; i < t; i++)
+        if (sh[i] > m) m = sh[i];
+      float l = 0.0f;
+      for (int64_t i = 0; i < t; i++) {
+        sh[i] = expf(sh[i] - m);
+        l += sh[i];
+      }
+      lsum[h] = l;
+    }
+#ifdef _OPENMP
+#pragma omp for collapse(2) schedule(static)
+#endif
+    for (int h = 0; h < hq; h++)
+      for (int j0 = 0; j0 < d; j0 += 64) {
+        const float* sh = s + (size_t)h * t;
+        const float l = lsum[h];
+        float o[64];
+        const int nj = d - j0 < 64 ? d - j0 : 64;
+        for (int j = 0; j < nj; j++) o[j] = 0.0f;
+        for (int64_t i = 0; i < t; i++) {
+          float w = ora_bf16_to_f32(ora_f32_to_bf16(sh[i] / l));
+          const uint16_t* vr = v + (i * hkv + h / rep) * d + j0;
+          for (int j = 0; j < nj; j++) o[j] += w * ora_bf16_to_f32(vr[j]);
+        }
+        for (int j = 0; j < nj; j++) out[h * d + j0 + j] = ora_f32_to_bf16(o[j]);
+      }
+  }
+  free(qs);
+  free(s);
+  free(lsum);
+  (void)n_threads;
+}
+
+/* The O(T) store of the reference's update_and_fetch (concat_or_init,
+ * src/cache.rs:132-137): a new [t + n, row] array holding the t stored rows
+ * followed by the n new ones (MLX's concatenate writes a fresh array). The
+ * copy is split over n_threads. */
+void ora_concat_rows(const uint16_t* old_rows, int64_t t, const uint16_t* new_rows, int64_t n,
+                     int64_t row_elems, uint16_t* out, int n_threads) {
+  const int64_t old_elems = t * row_elems, total = (t + n) * row_elems;
+  const int64_t chunk = 1 << 18;
+#ifdef _OPENMP
+  if (n_threads <= 0) n_threads = omp_get_max_threads();
 #pragma omp parallel for num_threads(n_threads) schedule(static)
 #endif
-  for (int h = 0; h < hq; h++) {
-    int kh = h / rep;
-    float* qs = (float*)malloc(sizeof(float) * d);
-    float* s = (float*)malloc(sizeof(float) * (size_t)t);
-    float* o = (float*)calloc((size_t)d, sizeof(float));
-    for (int j = 0; j < d; j++)
-      qs[j] = ora_bf16_to_f32(ora_f32_to_bf16(ora_bf16_to_f32(q[h * d + j]) * scale));
-    float m = -INFINITY;
-    for (int64_t i = 0; i < t; i++) {
-      const uint16_t* kr = k + (i * hkv + kh) * d;
-      float acc = 0.0f;
-      for (int j = 0; j < d; j++) acc += qs[j] * ora_bf16_to_f32(kr[j]);
-      s[i] = ora_bf16_to_f32(ora_f32_to_bf16(acc));
-      if (s[i] > m) m = s[i];
+  for (int64_t c0 = 0; c0 < total; c0 += chunk) {
+    int64_t c1 = c0 + chunk < total ? c0 + chunk : total;
+    if (c0 < old_elems) {
+      int64_t e = c1 < old_elems ? c1 : old_elems;
+      memcpy(out + c0, old_rows + c0, sizeof(uint16_t) * (size_t)(e - c0));
     }
-    float l = 0.0f;
-    for (int64_t i = 0; i < t; i++) {
-      s[i] = expf(s[i] - m);
-      l += s[i];
+    if (c1 > old_elems) {
+      int64_t b = c0 > old_elems ? c0 : old_elems;
+      memcpy(out + b, new_rows + (b - old_elems), sizeof(uint16_t) * (size_t)(c1 - b));
     }
-    for (int64_t i = 0; i < t; i++) {
-      float w = ora_bf16_to_f32(ora_f32_to_bf16(s[i] / l));
-      const uint16_t* vr = v + (i * hkv + kh) * d;
-      for (int j = 0; j < d; j++) o[j] += w * ora_bf16_to_f32(vr[j]);
-    }
-    for (int j = 0; j < d; j++) out[h * d + j] = ora_f32_to_bf16(o[j]);
-    free(qs);
-    free(s);
-    free(o);
   }
   (void)n_threads;
 }

@@ -14,6 +14,7 @@
  *   src/cache.rs:47-62    build_rht                -> ora_build_rht
  *   src/cache.rs:67-89    lloyd_max_codebook       -> ora_lloyd_max_codebook
  *   src/cache.rs:94-129   turbo_round_trip_kv      -> ora_turbo_round_trip_dense
+ *   src/cache.rs:132-137  concat_or_init           -> ora_concat_rows (CPU baseline)
  *   src/cache.rs:140-148  tail_along_time          -> ora_slot_position / ora_ring_slot
  *   src/model/mod.rs:682-753 masks                 -> ora_causal_mask / ora_sliding_mask
  *   src/model/gemma4_attention.rs:94-103 SDPA      -> ora_attention_f64
@@ -46,6 +47,8 @@ void ora_build_rht(int dim, uint64_t seed, float* r, float* rt);
 int ora_lloyd_max_codebook(int bits, float* centroids, float* bounds);
 void ora_turbo_round_trip_dense(const uint16_t* x_bf16, int64_t rows, int d, int bits,
                                 uint64_t seed, uint16_t* out_bf16);
+void ora_turbo_round_trip_rt(const uint16_t* x_bf16, int64_t rows, int d, int bits, const float* r,
+                             const float* rt, uint16_t* out_bf16);
 
 /* canonical rotation arithmetic shared with the kernels */
 float ora_inv_sqrt(int n);
@@ -93,6 +96,8 @@ void ora_lse_merge(const double* m, const double* l, const double* o, int n_part
                    double* out);
 void ora_sdpa_bf16_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t t,
                           int hq, int hkv, int d, float scale, uint16_t* out, int n_threads);
+void ora_concat_rows(const uint16_t* old_rows, int64_t t, const uint16_t* new_rows, int64_t n,
+                     int64_t row_elems, uint16_t* out, int n_threads);
 
 /* synthetic inputs: SplitMix64 -> Box-Muller (fp64) */
 uint64_t ora_splitmix64(uint64_t* state);

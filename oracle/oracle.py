@@ -46,6 +46,8 @@ def lib() -> ctypes.CDLL:
             "ora_build_rht": ([i32, u64, _vp, _vp], None),
             "ora_lloyd_max_codebook": ([i32, _vp, _vp], i32),
             "ora_turbo_round_trip_dense": ([_vp, i64, i32, i32, u64, _vp], None),
+            "ora_turbo_round_trip_rt": ([_vp, i64, i32, i32, _vp, _vp, _vp], None),
+            "ora_concat_rows": ([_vp, i64, _vp, i64, i64, _vp, i32], None),
             "ora_inv_sqrt": ([i32], f32),
             "ora_fwht": ([_vp, i32], None),
             "ora_rotate_rows": ([_vp, i64, i32, _vp, _vp], None),
@@ -152,6 +154,23 @@ def turbo_round_trip_dense(x_bf16, bits: int, seed: int = 42) -> np.ndarray:
     d = x.shape[-1]
     out = np.empty(x.shape, np.uint16)
     lib().ora_turbo_round_trip_dense(_p(x), x.size // d, d, bits, seed, _p(out))
+    return out
+
+
+def turbo_round_trip_rt(x_bf16, bits: int, r, rt, out=None) -> np.ndarray:
+    """turbo_round_trip_dense with R / Rt built once (rows in parallel)."""
+    x = _c(x_bf16, np.uint16)
+    d = x.shape[-1]
+    out = np.empty(x.shape, np.uint16) if out is None else out
+    lib().ora_turbo_round_trip_rt(_p(x), x.size // d, d, bits, _p(r), _p(rt), _p(out))
+    return out
+
+
+def concat_rows(old, t: int, new, out, n_threads: int = 0) -> np.ndarray:
+    """out[:t + n] = concat(old[:t], new) along the first axis (the reference's
+    per-append concatenate); rows are the trailing dims."""
+    row = int(np.prod(new.shape[1:]))
+    lib().ora_concat_rows(_p(old), t, _p(new), new.shape[0], row, _p(out), n_threads)
     return out
 
 
@@ -489,7 +508,10 @@ class OracleCache:
         q = bf16_to_f32(q_bf16).astype(np.float64)
         hq, hkv = q.shape[0], k.shape[1]
         rep = hq // hkv
-        s = np.einsum("hd,thd->ht", q, np.repeat(k, rep, axis=1)) * scale
+        s = np.empty((hq, k.shape[0]))
+        for h in range(hkv):  # one GQA group at a time: [rep, D] x [D, T]
+            s[h * rep:(h + 1) * rep] = q[h * rep:(h + 1) * rep] @ np.ascontiguousarray(k[:, h]).T
+        s *= scale
         s -= s.max(axis=1, keepdims=True)
         w = np.exp(s)
         return w / w.sum(axis=1, keepdims=True)

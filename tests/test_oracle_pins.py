@@ -403,6 +403,48 @@ def test_sdpa_bf16_baseline_close_to_exact(ora):
     assert np.max(np.abs(got - want)) < 2e-2
 
 
+def test_sdpa_bf16_baseline_same_bits_on_any_thread_count(ora):
+    """The CPU baseline splits scores, sums and output slices over threads;
+    every element keeps its serial summation order, so the bits cannot
+    depend on the thread count (head_dim 96 also covers a partial slice)."""
+    rng = np.random.default_rng(16)
+    q = synth.f32_to_bf16_bits(rng.standard_normal((6, 96)).astype(np.float32) * 0.3)
+    k = synth.f32_to_bf16_bits(rng.standard_normal((1000, 3, 96)).astype(np.float32))
+    v = synth.f32_to_bf16_bits(rng.standard_normal((1000, 3, 96)).astype(np.float32))
+    one = ora.sdpa_bf16_decode(q, k, v, 0.7, 1)
+    for n in (2, 3, 8):
+        assert np.array_equal(ora.sdpa_bf16_decode(q, k, v, 0.7, n), one)
+    # the op order, restated in numpy for one head: bf16(q * scale), f32
+    # products summed in key order, bf16 scores; the output of a constant-V
+    # column is that constant whatever the weights
+    v2 = v.copy()
+    v2[:, 0, 5] = synth.f32_to_bf16_bits(np.float32([1.5]))[0]
+    out = ora.bf16_to_f32(ora.sdpa_bf16_decode(q, k, v2, 0.7, 4))
+    assert np.all(np.abs(out[:2, 5] - 1.5) <= 1.5 * 2.0 ** -7)
+
+
+def test_reference_round_trip_with_prebuilt_rotation(ora):
+    """turbo_round_trip_rt (R built once, rows in parallel) == the
+    per-call form (src/cache.rs:94-129), bit for bit."""
+    rng = np.random.default_rng(17)
+    x = synth.f32_to_bf16_bits(rng.standard_normal((70, 128)).astype(np.float32))
+    r, rt = ora.build_rht(128)
+    for bits in (2, 3, 4):
+        assert np.array_equal(ora.turbo_round_trip_rt(x, bits, r, rt),
+                              ora.turbo_round_trip_dense(x, bits))
+
+
+def test_concat_rows_is_concatenate(ora):
+    rng = np.random.default_rng(18)
+    old = rng.integers(0, 65535, (300000, 2, 3), dtype=np.uint16)
+    new = rng.integers(0, 65535, (5, 2, 3), dtype=np.uint16)
+    out = np.zeros((300005, 2, 3), np.uint16)
+    for t in (0, 1, 299999):
+        out[:] = 0
+        ora.concat_rows(old, t, new, out, 4)
+        assert np.array_equal(out[:t + 5], np.concatenate([old[:t], new]))
+
+
 # --------------------------------------------------------------------------
 # cache model: append with ring semantics, trim, stored_len
 # --------------------------------------------------------------------------
