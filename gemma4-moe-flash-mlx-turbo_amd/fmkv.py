@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+from dataclasses import dataclass
 from pathlib import Path
 
 import torch  # imported before libfmkv.so so both share torch's HIP runtime
@@ -198,7 +199,8 @@ def layout_bytes(desc: CacheDesc) -> tuple[int, int]:
 
 def set_blocks_per_split(bps: int) -> None:
     """Blocks per split-K work-group for decode attention (0: the plan's);
-    a paged sequence's first split takes 4 x bps blocks."""
+    a paged sequence's first split takes 4 x bps blocks when the grid holds
+    at least four work-groups per CU."""
     _check(load_library().fmkv_set_blocks_per_split(bps))
 
 
@@ -365,6 +367,75 @@ class KVCache:
                                  f"{tuple(t.shape)} {t.dtype}")
         if keys.shape != values.shape:
             raise ValueError("keys and values differ in shape")
+
+
+@dataclass(frozen=True)
+class LayerCacheSpec:
+    """One layer's cache shape as Model::make_cache derives it
+    (src/model/mod.rs:375-396 with the per-layer dims of :448-465)."""
+    is_full: bool     # layer_types[i] == "full_attention"
+    use_k_eq_v: bool  # attention_k_eq_v && is_full
+    head_dim: int     # global_head_dim on full layers, else head_dim
+    n_kv_heads: int   # num_global_key_value_heads on K==V layers
+    window: int       # sliding_window on layers that are not K==V, else 0
+    bits: int
+
+
+def layer_cache_specs(layer_types, head_dim: int, n_kv_heads: int, *,
+                      global_head_dim: int | None = None, n_global_kv_heads: int | None = None,
+                      sliding_window: int | None = None, attention_k_eq_v: bool = False,
+                      kv_quant_bits: int = 3, global_kv_quant_bits: int | None = None):
+    """Per-layer cache shapes of a Gemma-4 stack, the choices of
+    Model::make_cache (src/model/mod.rs:375-396) and the layer constructor
+    (:448-465): a layer is full iff its type is "full_attention"; K==V
+    layers are the full ones when attention_k_eq_v; only layers that are
+    not K==V get the sliding window (so with attention_k_eq_v false every
+    layer does, as in the reference); full layers use global_head_dim
+    (default head_dim); K==V layers use n_global_kv_heads (default
+    n_kv_heads). kv_quant_bits applies to every layer unless
+    global_kv_quant_bits overrides it on full layers (a mixed 4/8-bit
+    stack)."""
+    specs = []
+    for t in layer_types:
+        is_full = t == "full_attention"
+        k_eq_v = bool(attention_k_eq_v and is_full)
+        specs.append(LayerCacheSpec(
+            is_full, k_eq_v,
+            (global_head_dim or head_dim) if is_full else head_dim,
+            (n_global_kv_heads or n_kv_heads) if k_eq_v else n_kv_heads,
+            0 if k_eq_v or not sliding_window else int(sliding_window),
+            global_kv_quant_bits if (is_full and global_kv_quant_bits) else kv_quant_bits))
+    return specs
+
+
+def make_cache(layer_types, head_dim: int, n_kv_heads: int, *, capacity: int,
+               global_head_dim: int | None = None, n_global_kv_heads: int | None = None,
+               sliding_window: int | None = None, attention_k_eq_v: bool = False,
+               kv_quant_bits: int | None = 3, global_kv_quant_bits: int | None = None,
+               mode: int = MODE_CODEBOOK, sign_seed: int = 42) -> list:
+    """One cache per layer, as Model::make_cache (src/model/mod.rs:375-396)
+    builds them with KVCache::new_quantized_with_window(layer.kv_head_dim(),
+    bits, window). The reference's quantized cache is the TurboQuant
+    codebook (default 3 bits, src/main.rs:82-84), hence mode's default;
+    MODE_AFFINE gives the 4/8-bit affine caches. `capacity` bounds the
+    positions of the linear (window 0) caches, whose arenas are
+    preallocated. kv_quant_bits None (the reference's plain bf16 caches,
+    --no-kv-quant) has no quantized layout here and raises."""
+    if kv_quant_bits is None:
+        raise Exception_(FMKV_ERR_UNSUPPORTED, "plain (unquantized) caches are not provided; "
+                                               "pass kv_quant_bits")
+    specs = layer_cache_specs(layer_types, head_dim, n_kv_heads, global_head_dim=global_head_dim,
+                              n_global_kv_heads=n_global_kv_heads, sliding_window=sliding_window,
+                              attention_k_eq_v=attention_k_eq_v, kv_quant_bits=kv_quant_bits,
+                              global_kv_quant_bits=global_kv_quant_bits)
+    caches = []
+    for sp in specs:
+        c = KVCache.new_quantized_with_window(sp.head_dim, sp.bits, sp.window or None, sp.n_kv_heads,
+                                              capacity=0 if sp.window else capacity, mode=mode,
+                                              sign_seed=sign_seed)
+        c.spec = sp
+        caches.append(c)
+    return caches
 
 
 class PagedPool:

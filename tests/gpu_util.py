@@ -54,3 +54,61 @@ def check_attention(out, ref, what=""):
     assert np.all(err <= allow), f"{what}: max err {err.max():.3e} at {worst} (ref {r[worst]:.4f})"
     assert err.mean() <= 2e-3, f"{what}: mean err {err.mean():.3e}"
     return err.max(), err.mean()
+
+
+def _randn(seed: int, shape):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g, dtype=torch.float32)
+
+
+def _bf16_bits(x) -> np.ndarray:
+    import torch
+
+    return x.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)  # RNE
+
+
+def _outlier_gain(ch, H: int, D: int):
+    import torch
+
+    g = torch.ones((H, D), dtype=torch.float32)
+    for h in range(H):
+        g[h, torch.from_numpy(ch[h])] = 20.0
+    return g
+
+
+def fast_kv(seed: int, n: int, H: int, D: int, dist: str = "normal", outliers: bool = True) -> np.ndarray:
+    """bf16 bits [n, H, D] for config-sized tests: torch's CPU normals
+    (Student-t(3) as Z / sqrt(chi2_3 / 3) for dist="t3"), with 4 outlier
+    channels per head x20 when asked (synth's channel choice)."""
+    x = _randn(seed, (n, H, D))
+    if dist == "t3":
+        chi = _randn(seed + 1000003, (3, n, H, D))
+        x /= ((chi * chi).sum(0) / 3.0).sqrt()
+    if outliers:
+        x *= _outlier_gain(synth.outlier_channels(seed, H, D), H, D)
+    return _bf16_bits(x)
+
+
+def fast_q(seed: int, n: int, Hq: int, Hkv: int, D: int, outliers: bool = True) -> np.ndarray:
+    """bf16 bits [n, Hq, D]; q head h shares the outlier channels of KV head
+    h / (Hq / Hkv) (the K/V made by fast_kv with the same seed)."""
+    x = _randn(seed + 7919, (n, Hq, D))
+    if outliers:
+        g = _outlier_gain(synth.outlier_channels(seed, Hkv, D), Hkv, D)
+        x *= g.repeat_interleave(Hq // Hkv, dim=0)
+    return _bf16_bits(x)
+
+
+def check_codes(codes, meta, oc, slots=None, what=""):
+    """Device codes/meta (read_codes) bit-exact against an OracleCache, over
+    `slots` (default: all)."""
+    c = host_u32(codes)
+    m = host_u16(meta)
+    if slots is None:
+        slots = np.arange(oc.codes.shape[0])
+    bad = np.nonzero(np.any(c[slots] != oc.codes[slots], axis=(1, 2, 3)))[0]
+    assert bad.size == 0, f"{what}: codes differ at {bad.size} slots, first {slots[bad[0]]}"
+    bad = np.nonzero(np.any(m[slots] != oc.meta[slots], axis=(1, 2, 3)))[0]
+    assert bad.size == 0, f"{what}: scale/bias differ at {bad.size} slots, first {slots[bad[0]]}"
