@@ -420,14 +420,23 @@ int prepare_paged_attention(fmkv_pool* p, const void* q, const int32_t* block_ta
   // Ragged lengths: the bound counts every sequence at max_seq_len, so the
   // plan aims at several work-groups per CU (the dispatcher balances their
   // uneven sizes), but at least 64 blocks each (a work-group's prologue and
-  // epilogue cost about as much as a dozen blocks). Each sequence's first
-  // split is four times larger: the big work-groups start first and the
-  // small ones fill the tail. Six per CU measured best for 32 sequences of
-  // 512..16384 tokens (bps 171: 197 us; four per CU with equal splits:
-  // 207 us).
-  return prepare_attention_common(p, pool_store(p, block_tables, max_blocks),
-                                  n_seqs > 0 ? n_seqs : 1, nblk, q, n_q_heads, scale, tau, out,
-                                  out_dtype, 6 * fmkv::kAttnWgPerCu, 64, 4, new_col, a);
+  // epilogue cost about as much as a dozen blocks) -- unless that would
+  // leave CUs idle: the floor never exceeds one CU's share of all blocks,
+  // so a small batch at long context still spreads over every CU. When the
+  // grid holds at least four work-groups per CU, each sequence's first split
+  // is four times larger: the big work-groups start first and the small
+  // ones fill the tail (32 sequences of 512..16384 tokens: bps 171, 197 us;
+  // equal splits at four per CU: 207 us). A grid of fewer work-groups has
+  // no tail to fill, and a larger first split would only end last.
+  const int n_s = n_seqs > 0 ? n_seqs : 1;
+  const int64_t total = nblk * p->desc.n_kv_heads * n_s;
+  const int64_t share = (total + p->cus - 1) / p->cus;
+  const int min_bps = (int)std::min<int64_t>(64, std::max<int64_t>(share, 1));
+  const int64_t bps = choose_bps(total, p->cus, 6 * fmkv::kAttnWgPerCu, 0, min_bps);
+  const int first_mult = total >= 4 * (int64_t)p->cus * bps ? 4 : 1;
+  return prepare_attention_common(p, pool_store(p, block_tables, max_blocks), n_s, nblk, q,
+                                  n_q_heads, scale, tau, out, out_dtype, 6 * fmkv::kAttnWgPerCu,
+                                  min_bps, first_mult, new_col, a);
 }
 
 }  // namespace

@@ -19,6 +19,12 @@
  *  - A handle is used by one host thread at a time (no internal locks).
  *  - Descriptor validation runs before any HIP call, so invalid input is
  *    reported on machines without a GPU too.
+ *  - Magnitude bound of the affine attention read: the softmax weight times
+ *    a V group's scale travels as an f16 pair (high part + residual, at most
+ *    about 1.3e5) with weights up to 2^8, so a V group's f16 scale must stay
+ *    below 511 -- a rotated V group spanning less than 511 * (2^bits - 1),
+ *    about 7.6e3 at 4 bits and 1.3e5 at 8 bits. v_norm'd V (unit RMS) is
+ *    four orders of magnitude inside; raw V rows beyond it lose accuracy.
  */
 #ifndef FMKV_H
 #define FMKV_H
@@ -242,7 +248,8 @@ int fmkv_pool_read_codes(const fmkv_pool* pool, void* codes, void* meta, void* s
 /* ---------------------------------------------------------------------- */
 
 /* Blocks per split-K work-group for decode attention (0 = automatic). In a
- * paged pool each sequence's first split takes 4 x that many blocks. */
+ * paged pool each sequence's first split takes 4 x that many blocks when the
+ * grid holds at least four work-groups per CU. */
 int fmkv_set_blocks_per_split(int32_t blocks_per_split);
 
 /* Kernel timing (profiling aid, no reference counterpart): while enabled,

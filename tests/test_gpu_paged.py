@@ -13,9 +13,11 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize("D,bits,Hkv,Hq", [(256, 4, 8, 16), (512, 8, 2, 16)])
 @pytest.mark.parametrize("bps", [0, 1, 3, 8])
 def test_paged_ragged_decode(gpu, ora, D, bits, Hkv, Hq, bps):
-    """bps: blocks per split (0: the plan's); a paged sequence's first split
-    takes 4 x bps blocks, so 1, 3 and 8 give several splits of both sizes
-    (8: single-wave streams at 4-bit D=256)."""
+    """bps: blocks per split (0: the plan's); 1, 3 and 8 give several splits
+    per sequence (8: single-wave streams at 4-bit D=256). A paged
+    sequence's first split takes 4 x bps blocks when the grid holds at least
+    four work-groups per CU: here bps 1 on the 8-head shape (both split
+    sizes), equal splits otherwise."""
     import torch
 
     lens = [5, 40, 100, 17, 1, 64, 300, 700]

@@ -111,8 +111,8 @@ def test_step_validation_leaves_cache_unchanged(gpu):
 @pytest.mark.parametrize("D,bits,Hkv,Hq", [(256, 4, 8, 16), (512, 8, 2, 16)])
 @pytest.mark.parametrize("bps", [0, 2, 8])
 def test_paged_step_matches_oracle_and_two_calls(gpu, ora, D, bits, Hkv, Hq, bps):
-    """bps: blocks per split (0: the plan's; 2 and 8 give several splits,
-    the first of 4 x bps blocks)."""
+    """bps: blocks per split (0: the plan's; 2 and 8 give several splits
+    per sequence)."""
     import torch
 
     lens = [3, 40, 129, 16, 1, 250]
