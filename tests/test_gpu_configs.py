@@ -10,7 +10,7 @@ checked to spread over many keys.
       checked at steps around every wrap;
   C3  global layer, Hq 16, Hkv 2, head_dim 512, 8-bit: 32768 tokens in
       2048-token chunks with Student-t(3) K, then 8 decode steps under the
-      default split plan (about 120 splits of 17 blocks);
+      default split plan (about 120 splits of 17 blocks), soft scale 0.01;
   C4  32 ragged sequences (the benchmark's seeded lengths in [512, 16384]) in a
       paged pool on shuffled blocks, one batched decode step, each sequence
       against its own oracle;
@@ -129,12 +129,12 @@ def test_c3_global_32k_decode_steps(gpu, ora):
     q = fast_q(393, steps, Hq, Hkv, D, outliers=False)
     outs = []
     for i in range(steps):
-        scale = 1.0 if i % 2 == 0 else 0.02
+        scale = 1.0 if i % 2 == 0 else 0.01
         dt = torch.float32 if (i // 2) % 2 == 0 else torch.bfloat16
         outs.append((scale, cache.decode_step(dev_bf16(k1[i:i + 1]), dev_bf16(v1[i:i + 1]),
                                               dev_bf16(q[i]), scale, dtype=dt)))
     # the attention entry point on the same state (split columns only)
-    read = cache.attention(dev_bf16(q[0]), 0.02, dtype=torch.float32)
+    read = cache.attention(dev_bf16(q[0]), 0.01, dtype=torch.float32)
     codes, meta = cache.read_codes()
     torch.cuda.synchronize()
     for i in range(steps):
@@ -144,7 +144,7 @@ def test_c3_global_32k_decode_steps(gpu, ora):
             softmax_spread(oc, q[i], scale)
         check_attention(out, oc.attention(q[i], scale), f"C3 step {i} (T={T0 + i + 1}) scale {scale}")
     check_codes(codes, meta, oc, slots=np.arange(T0 - 64, T0 + steps), what="C3 after the steps")
-    check_attention(read, oc.attention(q[0], 0.02), "C3 attention read")
+    check_attention(read, oc.attention(q[0], 0.01), "C3 attention read")
 
 
 def c4_lengths():
