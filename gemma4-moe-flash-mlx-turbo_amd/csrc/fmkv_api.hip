@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -129,6 +130,13 @@ void sign_bits_of(const fmkv_cache_desc& d, uint32_t out[16]) {
   for (int i = 0; i < d.head_dim; i++)
     if (s[i] < 0.0f) out[i >> 5] |= 1u << (i & 31);
 }
+
+// Caller-provided device memory standing in for a handle's workspace (the
+// no-allocation decode step); ptr null: the handle's own workspace.
+struct ExtWorkspace {
+  float* ptr = nullptr;
+  size_t bytes = 0;
+};
 
 struct Workspace {
   float* ptr = nullptr;
@@ -317,7 +325,7 @@ template <typename Owner>
 int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, int64_t nblk,
                              const void* q, int32_t n_q_heads, float scale, float tau, void* out,
                              int32_t out_dtype, int wg_per_cu, int min_bps, int first_mult,
-                             int new_col, fmkv::AttnArgs* a) {
+                             int new_col, fmkv::AttnArgs* a, ExtWorkspace ext = {}) {
   int rc = check_attn_args(o->desc, q, n_q_heads, tau, out, out_dtype);
   if (rc) return rc;
   const int H = o->desc.n_kv_heads, D = o->desc.head_dim;
@@ -352,17 +360,28 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   a->out_f32 = out_dtype == FMKV_DTYPE_F32;
   const size_t n_rows = a->direct ? 0 : (size_t)n_seqs * a->part_stride * n_q_heads;
   const size_t n_stats = tau > 0.0f ? 3 * (size_t)n_seqs * n_q_heads : 0;
-  rc = o->ws.ensure((n_rows * (D + 2) + n_stats) * sizeof(float));
-  if (rc) return rc;
-  a->part_o = n_rows ? o->ws.ptr : nullptr;
-  a->part_ml = n_rows ? o->ws.ptr + n_rows * D : nullptr;
-  a->tau_stats = n_stats ? o->ws.ptr + n_rows * (D + 2) : nullptr;
+  const size_t need = (n_rows * (D + 2) + n_stats) * sizeof(float);
+  float* ws = ext.ptr;
+  if (ws) {
+    if (need > ext.bytes)
+      return fail(FMKV_ERR_CAPACITY, "this call needs " + std::to_string(need) +
+                                         " bytes of split partials; the no-allocation scratch "
+                                         "holds " + std::to_string(ext.bytes));
+  } else {
+    rc = o->ws.ensure(need);
+    if (rc) return rc;
+    ws = o->ws.ptr;
+  }
+  a->part_o = n_rows ? ws : nullptr;
+  a->part_ml = n_rows ? ws + n_rows * D : nullptr;
+  a->tau_stats = n_stats ? ws + n_rows * (D + 2) : nullptr;
   return FMKV_OK;
 }
 
 // Decode attention over the first T positions of a cache.
 int prepare_attention(fmkv_cache* c, int64_t T, const void* q, int32_t n_q_heads, float scale,
-                      float tau, void* out, int32_t out_dtype, int new_col, fmkv::AttnArgs* a) {
+                      float tau, void* out, int32_t out_dtype, int new_col, fmkv::AttnArgs* a,
+                      ExtWorkspace ext = {}) {
   const int64_t W = c->desc.window;
   a->seq_lens = nullptr;
   a->seq_len = T;
@@ -373,7 +392,7 @@ int prepare_attention(fmkv_cache* c, int64_t T, const void* q, int32_t n_q_heads
   const int64_t nblk =
       (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
   return prepare_attention_common(c, cache_store(c), 1, nblk, q, n_q_heads, scale, tau, out,
-                                  out_dtype, fmkv::kAttnWgPerCu, 1, 1, new_col, a);
+                                  out_dtype, fmkv::kAttnWgPerCu, 1, 1, new_col, a, ext);
 }
 
 int prepare_paged_append(const fmkv_pool* p, const void* k, const void* v,
@@ -437,6 +456,46 @@ int prepare_paged_attention(fmkv_pool* p, const void* q, const int32_t* block_ta
   return prepare_attention_common(p, pool_store(p, block_tables, max_blocks), n_s, nblk, q,
                                   n_q_heads, scale, tau, out, out_dtype, 6 * fmkv::kAttnWgPerCu,
                                   min_bps, first_mult, new_col, a);
+}
+
+int decode_step_impl(fmkv_cache* c, const void* k, const void* v, int64_t n, const void* q,
+                     int32_t n_q_heads, float scale, float tau, void* out, int32_t out_dtype,
+                     void* stream, ExtWorkspace ext);
+
+}  // namespace
+
+// Device memory of fmkv_decode_step_noalloc: the split partials (and
+// sparse-V statistics) of one decode step, as the handle's workspace holds
+// them for fmkv_decode_step. Every GPU holds its own copy for the life of the
+// process; in host code the name only stands in for it, so the library takes
+// each device's address once (noalloc_scratch) and passes that address on.
+// Calls on one GPU share it: every call writes what it reads before reading
+// it, and calls that overlap in time on one GPU race.
+static __device__ __align__(256) uint8_t scratch[FMKV_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// This device's address of `scratch`, looked up once per device with the
+// device current (hipGetSymbolAddress allocates nothing).
+int noalloc_scratch(ExtWorkspace* out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(FMKV_ERR_UNSUPPORTED, "device index beyond 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    g_scratch_dev[dev] = p;
+  }
+  out->ptr = static_cast<float*>(g_scratch_dev[dev]);
+  out->bytes = FMKV_NOALLOC_SCRATCH_BYTES;
+  return FMKV_OK;
 }
 
 }  // namespace
@@ -627,6 +686,26 @@ int fmkv_prefill_step(fmkv_cache* c, const void* k, const void* v, int64_t n, co
 int fmkv_decode_step(fmkv_cache* c, const void* k, const void* v, int64_t n, const void* q,
                      int32_t n_q_heads, float scale, float tau, void* out, int32_t out_dtype,
                      void* stream) {
+  return decode_step_impl(c, k, v, n, q, n_q_heads, scale, tau, out, out_dtype, stream, {});
+}
+
+int fmkv_decode_step_noalloc(fmkv_cache* c, const void* k, const void* v, int64_t n,
+                             const void* q, int32_t n_q_heads, float scale, float tau, void* out,
+                             int32_t out_dtype, void* stream) {
+  if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
+  ExtWorkspace ext;
+  int rc = noalloc_scratch(&ext);
+  if (rc) return rc;
+  return decode_step_impl(c, k, v, n, q, n_q_heads, scale, tau, out, out_dtype, stream, ext);
+}
+
+}  // extern "C"
+
+namespace {
+
+int decode_step_impl(fmkv_cache* c, const void* k, const void* v, int64_t n, const void* q,
+                     int32_t n_q_heads, float scale, float tau, void* out, int32_t out_dtype,
+                     void* stream, ExtWorkspace ext) {
   if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
   if (n < 1) return fail(FMKV_ERR_INVALID_ARG, "a decode step appends at least one token");
   fmkv::AppendArgs ap;
@@ -637,7 +716,7 @@ int fmkv_decode_step(fmkv_cache* c, const void* k, const void* v, int64_t n, con
   // column); sparse-V attention runs after a separate append
   const int fused = n == 1 && tau == 0.0f ? 1 : 0;
   fmkv::AttnArgs at;
-  rc = prepare_attention(c, c->offset + n, q, n_q_heads, scale, tau, out, out_dtype, fused, &at);
+  rc = prepare_attention(c, c->offset + n, q, n_q_heads, scale, tau, out, out_dtype, fused, &at, ext);
   if (rc) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
@@ -656,6 +735,10 @@ int fmkv_decode_step(fmkv_cache* c, const void* k, const void* v, int64_t n, con
   if (fused) c->offset += n;
   return FMKV_OK;
 }
+
+}  // namespace
+
+extern "C" {
 
 int fmkv_cache_trim(fmkv_cache* c, int64_t keep_last) {
   if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");

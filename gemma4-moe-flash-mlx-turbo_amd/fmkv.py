@@ -46,7 +46,7 @@ EXPORTED = (
     "fmkv_cache_append_projected", "fmkv_paged_append_projected",
     "fmkv_pool_read_codes", "fmkv_set_blocks_per_split", "fmkv_cache_decode_splits",
     "fmkv_profile_enable", "fmkv_profile_collect", "fmkv_decode_step", "fmkv_paged_decode_step",
-    "fmkv_prefill_step", "fmkv_paged_prefill_step",
+    "fmkv_prefill_step", "fmkv_paged_prefill_step", "fmkv_decode_step_noalloc",
 )
 
 
@@ -146,6 +146,8 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         "fmkv_profile_collect": ([P(ctypes.c_double), P(i32)], ctypes.c_int),
         "fmkv_decode_step": ([vp, vp, vp, i64, vp, i32, ctypes.c_float, ctypes.c_float, vp, i32,
                               vp], ctypes.c_int),
+        "fmkv_decode_step_noalloc": ([vp, vp, vp, i64, vp, i32, ctypes.c_float, ctypes.c_float, vp,
+                                      i32, vp], ctypes.c_int),
         "fmkv_prefill_step": ([vp, vp, vp, i64, vp, i32, ctypes.c_float, vp, i32, vp], ctypes.c_int),
         "fmkv_paged_prefill_step": ([vp, vp, vp, vp, i32, vp, i32, i32, vp, i32, ctypes.c_float, vp,
                                      i32, vp], ctypes.c_int),

@@ -148,6 +148,24 @@ int fmkv_decode_step(fmkv_cache* cache, const void* k_bf16, const void* v_bf16, 
                      const void* q_bf16, int32_t n_q_heads, float scale, float sparse_v_tau,
                      void* out, int32_t out_dtype, void* stream);
 
+/* Bytes of device scratch behind fmkv_decode_step_noalloc (per GPU). */
+#define FMKV_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+
+/* fmkv_decode_step with no device allocation: no counterpart in the
+ * reference; for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The same
+ * kernels run, with the split partials in a fixed per-GPU scratch of
+ * FMKV_NOALLOC_SCRATCH_BYTES held until the process ends instead of the
+ * handle's growable workspace: (splits + 1) * n_q_heads * (head_dim + 2) * 4
+ * bytes (plus 12 * n_q_heads with sparse_v_tau > 0) must fit, else
+ * FMKV_ERR_CAPACITY and nothing is launched (a 32K-token head_dim-512 layer
+ * with 16 q heads needs about 4 MiB). All calls on one GPU share that
+ * scratch: calls that overlap in time on one GPU (other streams, other
+ * threads) race. */
+int fmkv_decode_step_noalloc(fmkv_cache* cache, const void* k_bf16, const void* v_bf16,
+                             int64_t n_tokens, const void* q_bf16, int32_t n_q_heads, float scale,
+                             float sparse_v_tau, void* out, int32_t out_dtype, void* stream);
+
 /* One prefill (chunked-prefill) pass of an attention layer, as
  * Gemma4Attention::forward runs it for L = n_tokens > 1
  * (src/model/gemma4_attention.rs:84-104): cache.update_and_fetch(k, v) of the

@@ -89,6 +89,8 @@ def test_entry_points_reject_null_handles_before_hip():
                                  fmkv.DTYPE_BF16, None) == fmkv.FMKV_ERR_INVALID_ARG
     assert lib.fmkv_decode_step(None, None, None, 1, None, 8, 1.0, 0.0, None,
                                 fmkv.DTYPE_BF16, None) == fmkv.FMKV_ERR_INVALID_ARG
+    assert lib.fmkv_decode_step_noalloc(None, None, None, 1, None, 8, 1.0, 0.0, None,
+                                        fmkv.DTYPE_BF16, None) == fmkv.FMKV_ERR_INVALID_ARG
     pro = fmkv.KvPrologue(None, 1e-6, 128, 1e4, 0)
     assert lib.fmkv_cache_append_projected(None, None, None, 1, pro, None) == fmkv.FMKV_ERR_INVALID_ARG
     assert b"null" in lib.fmkv_last_error()
