@@ -50,8 +50,11 @@ def dev_bf16(bits: np.ndarray):
     return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
 
 
-def bytes_per_token_head(D: int, bits: int) -> int:
-    """K+V codes plus f16 scale and bias per 64-dim group, one token, one KV head."""
+def bytes_per_token_head(D: int, bits: int, codebook: bool = False) -> int:
+    """K+V codes plus f16 scale and bias per 64-dim group (affine) or one f16
+    norm per row (codebook), one token, one KV head."""
+    if codebook:
+        return 2 * (D * bits // 8 + 2)
     return 2 * (D * bits // 8 + 4 * (D // 64))
 
 
@@ -61,10 +64,14 @@ def run_c3(args) -> dict:
     import fmkv
     import synth
 
-    Hq, Hkv, D, bits, T0 = 16, 2, 512, 8, args.context
-    per_tok = bytes_per_token_head(D, bits)
+    cb = args.mode == "codebook"
+    Hq, Hkv, D, T0 = 16, 2, 512, args.context
+    bits = args.bits or (3 if cb else 8)
+    mode = fmkv.MODE_CODEBOOK if cb else fmkv.MODE_AFFINE
+    per_tok = bytes_per_token_head(D, bits, cb)
     n_dec = args.warmup + 2 * args.steps + 1
-    cache = fmkv.KVCache.new_quantized(D, bits, Hkv, capacity=T0 + n_dec + args.graph_steps + 16)
+    cache = fmkv.KVCache.new_quantized(D, bits, Hkv, capacity=T0 + n_dec + args.graph_steps + 16,
+                                       mode=mode)
 
     # ---- prefill: chunked appends of 2048 tokens (timed separately) ----
     chunk = 2048
@@ -84,9 +91,10 @@ def run_c3(args) -> dict:
     w = dev_bf16(synth.f32_to_bf16_bits((1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)))
     pro = fmkv.make_prologue(w, 1e-6, 128, 1e6, v_from_k=True)
     # one untimed chunk through each path first (first-launch costs)
-    warm = fmkv.KVCache.new_quantized(D, bits, Hkv, capacity=2 * chunk)
+    warm = fmkv.KVCache.new_quantized(D, bits, Hkv, capacity=2 * chunk, mode=mode)
     warm.append(dk[0], dv[0])
-    warm.append_projected(dk[0], None, pro)
+    if not cb:
+        warm.append_projected(dk[0], None, pro)
     torch.cuda.synchronize()
     del warm
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -99,17 +107,20 @@ def run_c3(args) -> dict:
     append_prefill_tps = T0 / (prefill_ms / 1e3)
     log(f"prefill {T0} tokens in {prefill_ms:.2f} ms ({append_prefill_tps/1e6:.2f} M tokens/s)")
 
-    # the same chunks as raw projections through the prologue
-    pcache = fmkv.KVCache.new_quantized(D, bits, Hkv, capacity=T0)
-    torch.cuda.synchronize()
-    ev0.record()
-    for k in dk:
-        pcache.append_projected(k, None, pro)
-    ev1.record()
-    torch.cuda.synchronize()
-    prologue_tps = T0 / (ev0.elapsed_time(ev1) / 1e3)
-    log(f"prefill with prologue (K==V): {prologue_tps/1e6:.2f} M tokens/s")
-    del dk, dv, pcache
+    # the same chunks as raw projections through the prologue (affine caches)
+    prologue_tps = None
+    if not cb:
+        pcache = fmkv.KVCache.new_quantized(D, bits, Hkv, capacity=T0)
+        torch.cuda.synchronize()
+        ev0.record()
+        for k in dk:
+            pcache.append_projected(k, None, pro)
+        ev1.record()
+        torch.cuda.synchronize()
+        prologue_tps = T0 / (ev0.elapsed_time(ev1) / 1e3)
+        log(f"prefill with prologue (K==V): {prologue_tps/1e6:.2f} M tokens/s")
+        del pcache
+    del dk, dv
 
     # ---- decode inputs resident on the device; raw pointers per step ----
     kd = dev_bf16(synth.kv_rows(41, n_dec, Hkv, D, None, dist="t3"))
@@ -224,14 +235,17 @@ def run_c3(args) -> dict:
         "dtype": "u8",
         "data": "synthetic (seeded SplitMix64: K Student-t(3), V and q N(0,1))",
         "config": {
-            "workload": "gemma4-global-layer decode at 32K: Hq 16, Hkv 2, head_dim 512, "
-                        "8-bit group-64 affine, f16 scale/bias, 1 token append + attention per step",
+            "workload": (f"gemma4-global-layer decode at {T0 // 1024}K: Hq 16, Hkv 2, head_dim 512, "
+                         + (f"{bits}-bit TurboQuant codebook, f16 norm per row" if cb else
+                            f"{bits}-bit group-64 affine, f16 scale/bias")
+                         + ", 1 token append + attention per step"),
             "context": T0, "batch": 1, "n_q_heads": Hq, "n_kv_heads": Hkv, "head_dim": D,
-            "bits": bits, "group": 64, "sparse_v_tau": tau,
+            "bits": bits, "mode": args.mode, "group": 64, "sparse_v_tau": tau,
         },
         "hbm_frac_of_value": round(value / HBM_PEAK_GBS, 4),
         "append_tokens_per_s": {"chunked_prefill_2048": round(append_prefill_tps, 1),
-                                "chunked_prefill_2048_prologue_k_eq_v": round(prologue_tps, 1)},
+                                "chunked_prefill_2048_prologue_k_eq_v":
+                                    None if prologue_tps is None else round(prologue_tps, 1)},
         "graph_step_us": None if graph_us is None else round(graph_us, 3),
         "roofline": {
             "bound": "hbm",
@@ -239,9 +253,9 @@ def run_c3(args) -> dict:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": TRAFFIC_BYTES_PER_LAUNCH,
-            "traffic_source": TRAFFIC_SOURCE,
-            "kernel": "decode_attn_kernel<512, 8, 0>",
+            "traffic": None if (cb or bits != 8) else TRAFFIC_BYTES_PER_LAUNCH,
+            "traffic_source": None if (cb or bits != 8) else TRAFFIC_SOURCE,
+            "kernel": f"cb_decode_kernel<512, {bits}>" if cb else f"decode_attn_kernel<512, {bits}, 0>",
             "avg_kernel_us": round(kern_s * 1e6, 3),
             "bytes_per_launch": int(launch_bytes),
         },
@@ -761,6 +775,10 @@ def main(argv=None) -> int:
     ap.add_argument("--prefill-sliding", action="store_true",
                     help="prefill workload on the sliding-layer shape (ring W 1024)")
     ap.add_argument("--c5-context", type=int, default=131072)
+    ap.add_argument("--mode", choices=["affine", "codebook"], default="affine",
+                    help="c3: cache mode (codebook = the reference's TurboQuant indices + norm)")
+    ap.add_argument("--bits", type=int, default=0,
+                    help="c3: code bits (0: 8 for affine, 3 for codebook, the reference's default)")
     ap.add_argument("--c4-seqs", type=int, default=0,
                     help="c4: a uniform batch of this many sequences of --c4-len tokens instead")
     ap.add_argument("--c4-len", type=int, default=32768)

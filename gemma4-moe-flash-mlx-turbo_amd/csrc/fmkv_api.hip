@@ -239,8 +239,8 @@ int make_signs(const fmkv_cache_desc& d, float** out) {
 int check_attn_args(const fmkv_cache_desc& d, const void* q, int32_t n_q_heads, float tau,
                     const void* out, int32_t out_dtype) {
   if (!q || !out) return fail(FMKV_ERR_INVALID_ARG, "q/out must be device pointers");
-  if (d.mode != FMKV_MODE_AFFINE)
-    return fail(FMKV_ERR_UNSUPPORTED, "decode attention reads affine-mode caches");
+  if (d.mode == FMKV_MODE_CODEBOOK && tau != 0.0f)
+    return fail(FMKV_ERR_UNSUPPORTED, "sparse-V attention reads affine-mode caches");
   if (n_q_heads < d.n_kv_heads || n_q_heads % d.n_kv_heads != 0)
     return fail(FMKV_ERR_INVALID_ARG, "n_q_heads must be a multiple of n_kv_heads");
   if (n_q_heads / d.n_kv_heads > 8)
@@ -391,8 +391,10 @@ int prepare_attention(fmkv_cache* c, int64_t T, const void* q, int32_t n_q_heads
   const int64_t vb = W > 0 ? 0 : c->vis_begin;
   const int64_t nblk =
       (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
+  // codebook work-groups are half as large in LDS: two per CU
+  const int wg_per_cu = c->desc.mode == FMKV_MODE_CODEBOOK ? 2 : fmkv::kAttnWgPerCu;
   return prepare_attention_common(c, cache_store(c), 1, nblk, q, n_q_heads, scale, tau, out,
-                                  out_dtype, fmkv::kAttnWgPerCu, 1, 1, new_col, a, ext);
+                                  out_dtype, wg_per_cu, 1, 1, new_col, a, ext);
 }
 
 int prepare_paged_append(const fmkv_pool* p, const void* k, const void* v,
@@ -461,6 +463,14 @@ int prepare_paged_attention(fmkv_pool* p, const void* q, const int32_t* block_ta
 int decode_step_impl(fmkv_cache* c, const void* k, const void* v, int64_t n, const void* q,
                      int32_t n_q_heads, float scale, float tau, void* out, int32_t out_dtype,
                      void* stream, ExtWorkspace ext);
+
+// The decode attention kernel of the cache's mode (and the split combine).
+hipError_t launch_attention(const fmkv::AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
+                            hipEvent_t e0, hipEvent_t e1) {
+  if (a.st.layout.mode == fmkv::kCodebook)
+    return fmkv::launch_cb_decode_attention(a, n_seqs, n_kv_heads, s, e0, e1);
+  return fmkv::launch_decode_attention(a, n_seqs, n_kv_heads, s, e0, e1);
+}
 
 }  // namespace
 
@@ -608,6 +618,8 @@ int fmkv_prefill_step(fmkv_cache* c, const void* k, const void* v, int64_t n, co
                       int32_t n_q_heads, float scale, void* out, int32_t out_dtype, void* stream) {
   if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
   if (n < 1) return fail(FMKV_ERR_INVALID_ARG, "a prefill step appends at least one token");
+  if (c->desc.mode != FMKV_MODE_AFFINE)
+    return fail(FMKV_ERR_UNSUPPORTED, "prefill attention reads affine-mode caches");
   int rc = check_attn_args(c->desc, q, n_q_heads, 0.0f, out, out_dtype);
   if (rc) return rc;
   if (!std::isfinite(scale)) return fail(FMKV_ERR_INVALID_ARG, "scale must be finite");
@@ -714,7 +726,7 @@ int decode_step_impl(fmkv_cache* c, const void* k, const void* v, int64_t n, con
   if (rc) return rc;
   // one new token: the attention launch appends it itself (new-token
   // column); sparse-V attention runs after a separate append
-  const int fused = n == 1 && tau == 0.0f ? 1 : 0;
+  const int fused = n == 1 && tau == 0.0f && c->desc.mode == FMKV_MODE_AFFINE ? 1 : 0;
   fmkv::AttnArgs at;
   rc = prepare_attention(c, c->offset + n, q, n_q_heads, scale, tau, out, out_dtype, fused, &at, ext);
   if (rc) return rc;
@@ -730,7 +742,7 @@ int decode_step_impl(fmkv_cache* c, const void* k, const void* v, int64_t n, con
   }
   hipEvent_t e0, e1;
   next_events(&e0, &e1);
-  e = fmkv::launch_decode_attention(at, 1, c->desc.n_kv_heads, s, e0, e1);
+  e = launch_attention(at, 1, c->desc.n_kv_heads, s, e0, e1);
   if (e != hipSuccess) return hip_fail(e, "decode attention launch");
   if (fused) c->offset += n;
   return FMKV_OK;
@@ -757,7 +769,7 @@ int fmkv_decode_attention(fmkv_cache* c, const void* q, int32_t n_q_heads, float
   const hipStream_t s = static_cast<hipStream_t>(stream);
   hipEvent_t e0, e1;
   next_events(&e0, &e1);
-  hipError_t e = fmkv::launch_decode_attention(a, 1, c->desc.n_kv_heads, s, e0, e1);
+  hipError_t e = launch_attention(a, 1, c->desc.n_kv_heads, s, e0, e1);
   if (e != hipSuccess) return hip_fail(e, "decode attention launch");
   return FMKV_OK;
 }
@@ -768,7 +780,8 @@ int fmkv_cache_decode_splits(const fmkv_cache* c, int32_t* n_splits) {
   int64_t vb = c->desc.window > 0 ? 0 : c->vis_begin;
   int64_t nblk = (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
   if (nblk < 1) nblk = 1;
-  const int32_t bps = choose_bps(nblk * c->desc.n_kv_heads, c->cus, fmkv::kAttnWgPerCu);
+  const int wg_per_cu = c->desc.mode == FMKV_MODE_CODEBOOK ? 2 : fmkv::kAttnWgPerCu;
+  const int32_t bps = choose_bps(nblk * c->desc.n_kv_heads, c->cus, wg_per_cu);
   *n_splits = (int32_t)((nblk + bps - 1) / bps);
   return FMKV_OK;
 }
@@ -868,6 +881,8 @@ int fmkv_paged_prefill_step(fmkv_pool* p, const void* k, const void* v,
   if (!p) return fail(FMKV_ERR_INVALID_ARG, "pool is null");
   if (n_seqs < 1 || n_new < 1)
     return fail(FMKV_ERR_INVALID_ARG, "a prefill step needs n_seqs >= 1 and n_new >= 1");
+  if (p->desc.mode != FMKV_MODE_AFFINE)
+    return fail(FMKV_ERR_UNSUPPORTED, "prefill attention reads affine-mode caches");
   int rc = check_attn_args(p->desc, q, n_q_heads, 0.0f, out, out_dtype);
   if (rc) return rc;
   if (!std::isfinite(scale)) return fail(FMKV_ERR_INVALID_ARG, "scale must be finite");
@@ -949,7 +964,7 @@ int fmkv_paged_decode_attention(fmkv_pool* p, const void* q, const int32_t* bloc
   const hipStream_t s = static_cast<hipStream_t>(stream);
   hipEvent_t e0, e1;
   next_events(&e0, &e1);
-  hipError_t e = fmkv::launch_decode_attention(a, n_seqs, p->desc.n_kv_heads, s, e0, e1);
+  hipError_t e = launch_attention(a, n_seqs, p->desc.n_kv_heads, s, e0, e1);
   if (e != hipSuccess) return hip_fail(e, "paged decode attention launch");
   return FMKV_OK;
 }
@@ -968,7 +983,7 @@ int fmkv_paged_decode_step(fmkv_pool* p, const void* k, const void* v,
   if (rc) return rc;
   // one new token per sequence: the attention launch appends it itself, at
   // position seq_lens[s] - 1 (= start_pos[s])
-  const int fused = n_new == 1 && tau == 0.0f ? 1 : 0;
+  const int fused = n_new == 1 && tau == 0.0f && p->desc.mode == FMKV_MODE_AFFINE ? 1 : 0;
   fmkv::AttnArgs at;
   rc = prepare_paged_attention(p, q, block_tables, max_blocks, seq_lens, n_seqs, max_seq_len,
                                n_q_heads, scale, tau, out, out_dtype, fused, &at);
@@ -984,7 +999,7 @@ int fmkv_paged_decode_step(fmkv_pool* p, const void* k, const void* v,
   }
   hipEvent_t e0, e1;
   next_events(&e0, &e1);
-  e = fmkv::launch_decode_attention(at, n_seqs, p->desc.n_kv_heads, s, e0, e1);
+  e = launch_attention(at, n_seqs, p->desc.n_kv_heads, s, e0, e1);
   if (e != hipSuccess) return hip_fail(e, "paged decode attention launch");
   return FMKV_OK;
 }

@@ -980,12 +980,24 @@ hipError_t launch_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s
     e = launch_split<D, BITS, kDense>(a, grid, s, ev0, ev1);
   }
   if (e != hipSuccess || a.direct) return e;
-  dim3 cgrid(D / 64, a.n_q_heads, n_seqs);
-  hipLaunchKernelGGL((combine_kernel<D>), cgrid, dim3(256), 0, s, a);
-  return hipGetLastError();
+  return launch_combine(a, n_seqs, s);
 }
 
 }  // namespace
+
+hipError_t launch_combine(const AttnArgs& a, int n_seqs, hipStream_t s) {
+  const int D = a.st.layout.head_dim;
+  dim3 cgrid(D / 64, a.n_q_heads, n_seqs);
+  if (D == 128)
+    hipLaunchKernelGGL((combine_kernel<128>), cgrid, dim3(256), 0, s, a);
+  else if (D == 256)
+    hipLaunchKernelGGL((combine_kernel<256>), cgrid, dim3(256), 0, s, a);
+  else if (D == 512)
+    hipLaunchKernelGGL((combine_kernel<512>), cgrid, dim3(256), 0, s, a);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
 
 hipError_t launch_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                                    hipEvent_t e0, hipEvent_t e1) {

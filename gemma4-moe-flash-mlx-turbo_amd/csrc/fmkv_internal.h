@@ -141,6 +141,13 @@ hipError_t launch_append(const AppendArgs& a, int n_seqs, int max_tasks, hipStre
 // kernel's dispatch: the start and end of its execution.
 hipError_t launch_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                                    hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr);
+// Decode attention over a codebook (TurboQuant) cache; one split of blocks per
+// work-group as launch_decode_attention plans it (no new-token column, no
+// sparse-V).
+hipError_t launch_cb_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
+                                      hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr);
+// The split merge of either decode kernel: out = LSE merge of the partials.
+hipError_t launch_combine(const AttnArgs& a, int n_seqs, hipStream_t s);
 hipError_t launch_prefill_attention(const PrefillArgs& a, hipStream_t s);
 hipError_t launch_read_codes(const ReadArgs& a, hipStream_t s);
 hipError_t launch_fetch(const FetchArgs& a, hipStream_t s);

@@ -106,11 +106,15 @@ int fmkv_cache_trim(fmkv_cache* cache, int64_t keep_last);
  * at src/model/gemma4_attention.rs:94-103 for L == 1 (Gemma-4: scale 1.0).
  * The current position attends to its own quantized K/V, as in the
  * reference where the round trip precedes the concat (src/cache.rs:295-298).
+ * Affine and codebook caches: a codebook (TurboQuant) cache is read as
+ * stored -- centroid[idx] * norm / sqrt(D) in the rotated domain -- with no
+ * bf16 round trip (src/cache.rs:94-129).
  * sparse_v_tau > 0 is the reference's sparse-V decode
  * (src/model/gemma4_attention.rs:196-234): softmax weights below tau are
  * zeroed without renormalisation. It reads the keys twice (a statistics
- * pass, then the gated pass); 0 is plain softmax attention. Negative or
- * non-finite tau returns FMKV_ERR_INVALID_ARG. */
+ * pass, then the gated pass); 0 is plain softmax attention; affine caches
+ * only (FMKV_ERR_UNSUPPORTED for codebook caches). Negative or non-finite
+ * tau returns FMKV_ERR_INVALID_ARG. */
 int fmkv_decode_attention(fmkv_cache* cache, const void* q_bf16, int32_t n_q_heads, float scale,
                           float sparse_v_tau, void* out, int32_t out_dtype, void* stream);
 
@@ -140,9 +144,9 @@ int fmkv_cache_append_projected(fmkv_cache* cache, const void* k_proj_bf16,
 /* One decode step of an attention layer, as Gemma4Attention::forward runs it
  * (src/model/gemma4_attention.rs:84-103): cache.update_and_fetch(k, v) for
  * n_tokens new positions, then attention of q over every visible position --
- * fmkv_cache_append followed by fmkv_decode_attention. With one new token
- * and sparse_v_tau == 0 this is a single attention launch (plus the split
- * combine) that also appends the token. Arguments and errors as those two
+ * fmkv_cache_append followed by fmkv_decode_attention. With one new token,
+ * sparse_v_tau == 0 and an affine cache this is a single attention launch
+ * (plus the split combine) that also appends the token. Arguments and errors as those two
  * calls; nothing is launched or changed when validation fails. */
 int fmkv_decode_step(fmkv_cache* cache, const void* k_bf16, const void* v_bf16, int64_t n_tokens,
                      const void* q_bf16, int32_t n_q_heads, float scale, float sparse_v_tau,
