@@ -19,6 +19,7 @@ Prints ONE JSON line:
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -69,7 +70,8 @@ def run_c3(args) -> dict:
     bits = args.bits or (3 if cb else 8)
     mode = fmkv.MODE_CODEBOOK if cb else fmkv.MODE_AFFINE
     per_tok = bytes_per_token_head(D, bits, cb)
-    n_dec = args.warmup + 2 * args.steps + 1
+    # steps: warmup, timed, event-timed, then warmup + timed projected steps
+    n_dec = 2 * args.warmup + 3 * args.steps + 1
     cache = fmkv.KVCache.new_quantized(D, bits, Hkv, capacity=T0 + n_dec + args.graph_steps + 16,
                                        mode=mode)
 
@@ -221,6 +223,31 @@ def run_c3(args) -> dict:
             graph_us = gev0.elapsed_time(gev1) * 1e3 / (reps * args.graph_steps)
             log(f"graph: {graph_us:.2f} us/step over {reps} replays of {args.graph_steps} steps")
 
+    # The integrated step from raw projections (K==V global layer: k_norm +
+    # RoPE on K, v_norm of the raw K as V, quantize, store, attend) in the
+    # same single attention launch plus combine. Informational, eager.
+    proj_us = None
+    if not cb and tau == 0.0:
+        pro_ref = ctypes.byref(pro)
+
+        def proj_step():
+            nonlocal i
+            rc = lib.fmkv_decode_step_projected(h, kp[i], None, 1, pro_ref, qp[i], Hq, 1.0, 0.0,
+                                                outp, fmkv.DTYPE_BF16, stream)
+            if rc:
+                raise RuntimeError(lib.fmkv_last_error().decode())
+            i += 1
+
+        for _ in range(args.warmup):
+            proj_step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            proj_step()
+        torch.cuda.synchronize()
+        proj_us = (time.perf_counter() - t0) / args.steps * 1e6
+        log(f"projected step (prologue in the new-token column): {proj_us:.1f} us")
+
     res = {
         "metric": "decode-attn GB/s & % HBM peak over quantized KV at 32K ctx; append tokens/s",
         "value": round(value, 2),
@@ -247,6 +274,7 @@ def run_c3(args) -> dict:
                                 "chunked_prefill_2048_prologue_k_eq_v":
                                     None if prologue_tps is None else round(prologue_tps, 1)},
         "graph_step_us": None if graph_us is None else round(graph_us, 3),
+        "projected_step_us": None if proj_us is None else round(proj_us, 3),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),

@@ -462,7 +462,15 @@ int prepare_paged_attention(fmkv_pool* p, const void* q, const int32_t* block_ta
 
 int decode_step_impl(fmkv_cache* c, const void* k, const void* v, int64_t n, const void* q,
                      int32_t n_q_heads, float scale, float tau, void* out, int32_t out_dtype,
-                     void* stream, ExtWorkspace ext);
+                     void* stream, ExtWorkspace ext, const fmkv_kv_prologue* pro = nullptr);
+
+// The prologue on the decode step's new-token column (a fused step).
+void set_prologue(const fmkv_kv_prologue* pro, fmkv::AttnArgs* a) {
+  a->k_norm_w = static_cast<const uint16_t*>(pro->k_norm_weight);
+  a->eps = pro->eps;
+  a->rope_dims = pro->rope_dims;
+  a->rope_theta = pro->rope_theta;
+}
 
 // The decode attention kernel of the cache's mode (and the split combine).
 hipError_t launch_attention(const fmkv::AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
@@ -701,6 +709,14 @@ int fmkv_decode_step(fmkv_cache* c, const void* k, const void* v, int64_t n, con
   return decode_step_impl(c, k, v, n, q, n_q_heads, scale, tau, out, out_dtype, stream, {});
 }
 
+int fmkv_decode_step_projected(fmkv_cache* c, const void* k_proj, const void* v_proj, int64_t n,
+                               const fmkv_kv_prologue* pro, const void* q, int32_t n_q_heads,
+                               float scale, float tau, void* out, int32_t out_dtype, void* stream) {
+  if (!pro) return fail(FMKV_ERR_INVALID_ARG, "prologue is null");
+  return decode_step_impl(c, k_proj, v_proj, n, q, n_q_heads, scale, tau, out, out_dtype, stream,
+                          {}, pro);
+}
+
 int fmkv_decode_step_noalloc(fmkv_cache* c, const void* k, const void* v, int64_t n,
                              const void* q, int32_t n_q_heads, float scale, float tau, void* out,
                              int32_t out_dtype, void* stream) {
@@ -717,13 +733,16 @@ namespace {
 
 int decode_step_impl(fmkv_cache* c, const void* k, const void* v, int64_t n, const void* q,
                      int32_t n_q_heads, float scale, float tau, void* out, int32_t out_dtype,
-                     void* stream, ExtWorkspace ext) {
+                     void* stream, ExtWorkspace ext, const fmkv_kv_prologue* pro) {
   if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
   if (n < 1) return fail(FMKV_ERR_INVALID_ARG, "a decode step appends at least one token");
+  int rc;
+  if (pro && (rc = check_prologue(c->desc, pro))) return rc;
   fmkv::AppendArgs ap;
   int64_t tasks = 0;
-  int rc = prepare_append(c, k, v, n, &ap, &tasks);
+  rc = prepare_append(c, k, pro && pro->v_from_k ? k : v, n, &ap, &tasks);
   if (rc) return rc;
+  if (pro) set_prologue(pro, &ap);
   // one new token: the attention launch appends it itself (new-token
   // column); sparse-V attention runs after a separate append
   const int fused = n == 1 && tau == 0.0f && c->desc.mode == FMKV_MODE_AFFINE ? 1 : 0;
@@ -735,6 +754,7 @@ int decode_step_impl(fmkv_cache* c, const void* k, const void* v, int64_t n, con
   if (fused) {
     at.k_new = ap.k;
     at.v_new = ap.v;
+    if (pro) set_prologue(pro, &at);
   } else {
     e = fmkv::launch_append(ap, 1, (int)tasks, s);
     if (e != hipSuccess) return hip_fail(e, "append launch");
@@ -969,18 +989,26 @@ int fmkv_paged_decode_attention(fmkv_pool* p, const void* q, const int32_t* bloc
   return FMKV_OK;
 }
 
-int fmkv_paged_decode_step(fmkv_pool* p, const void* k, const void* v,
+}  // extern "C"
+
+namespace {
+
+int paged_decode_step_impl(fmkv_pool* p, const void* k, const void* v,
                            const int32_t* block_tables, int32_t max_blocks,
                            const int32_t* start_pos, const int32_t* seq_lens, int32_t n_seqs,
                            int32_t n_new, int32_t max_seq_len, const void* q, int32_t n_q_heads,
-                           float scale, float tau, void* out, int32_t out_dtype, void* stream) {
+                           float scale, float tau, void* out, int32_t out_dtype, void* stream,
+                           const fmkv_kv_prologue* pro) {
   if (!p) return fail(FMKV_ERR_INVALID_ARG, "pool is null");
   if (n_new < 1) return fail(FMKV_ERR_INVALID_ARG, "a decode step appends at least one token");
+  int rc;
+  if (pro && (rc = check_prologue(p->desc, pro))) return rc;
   fmkv::AppendArgs ap;
   int tasks = 0;
-  int rc = prepare_paged_append(p, k, v, block_tables, max_blocks, start_pos, n_seqs, n_new, &ap,
-                                &tasks);
+  rc = prepare_paged_append(p, k, pro && pro->v_from_k ? k : v, block_tables, max_blocks,
+                            start_pos, n_seqs, n_new, &ap, &tasks);
   if (rc) return rc;
+  if (pro) set_prologue(pro, &ap);
   // one new token per sequence: the attention launch appends it itself, at
   // position seq_lens[s] - 1 (= start_pos[s])
   const int fused = n_new == 1 && tau == 0.0f && p->desc.mode == FMKV_MODE_AFFINE ? 1 : 0;
@@ -993,6 +1021,7 @@ int fmkv_paged_decode_step(fmkv_pool* p, const void* k, const void* v,
   if (fused) {
     at.k_new = ap.k;
     at.v_new = ap.v;
+    if (pro) set_prologue(pro, &at);
   } else {
     e = fmkv::launch_append(ap, n_seqs, tasks, s);
     if (e != hipSuccess) return hip_fail(e, "paged append launch");
@@ -1002,6 +1031,33 @@ int fmkv_paged_decode_step(fmkv_pool* p, const void* k, const void* v,
   e = launch_attention(at, n_seqs, p->desc.n_kv_heads, s, e0, e1);
   if (e != hipSuccess) return hip_fail(e, "paged decode attention launch");
   return FMKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fmkv_paged_decode_step(fmkv_pool* p, const void* k, const void* v,
+                           const int32_t* block_tables, int32_t max_blocks,
+                           const int32_t* start_pos, const int32_t* seq_lens, int32_t n_seqs,
+                           int32_t n_new, int32_t max_seq_len, const void* q, int32_t n_q_heads,
+                           float scale, float tau, void* out, int32_t out_dtype, void* stream) {
+  return paged_decode_step_impl(p, k, v, block_tables, max_blocks, start_pos, seq_lens, n_seqs,
+                                n_new, max_seq_len, q, n_q_heads, scale, tau, out, out_dtype,
+                                stream, nullptr);
+}
+
+int fmkv_paged_decode_step_projected(fmkv_pool* p, const void* k_proj, const void* v_proj,
+                                     const int32_t* block_tables, int32_t max_blocks,
+                                     const int32_t* start_pos, const int32_t* seq_lens,
+                                     int32_t n_seqs, int32_t n_new, int32_t max_seq_len,
+                                     const fmkv_kv_prologue* pro, const void* q,
+                                     int32_t n_q_heads, float scale, float tau, void* out,
+                                     int32_t out_dtype, void* stream) {
+  if (!pro) return fail(FMKV_ERR_INVALID_ARG, "prologue is null");
+  return paged_decode_step_impl(p, k_proj, v_proj, block_tables, max_blocks, start_pos, seq_lens,
+                                n_seqs, n_new, max_seq_len, q, n_q_heads, scale, tau, out,
+                                out_dtype, stream, pro);
 }
 
 int fmkv_pool_read_codes(const fmkv_pool* p, void* codes, void* meta, void* stream) {

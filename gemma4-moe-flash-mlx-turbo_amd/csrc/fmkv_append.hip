@@ -17,6 +17,7 @@
 // with -ffp-contract=off, so codes and scales are bit-identical to it.
 #include "fmkv_device.h"
 #include "fmkv_internal.h"
+#include "fmkv_prologue.h"
 #include "fmkv_quant.h"
 
 namespace fmkv {
@@ -29,21 +30,6 @@ __constant__ float kCbBounds3[7] = {-1.748f, -1.050f, -0.501f, 0.0f, 0.501f, 1.0
 __constant__ float kCbBounds4[15] = {-2.401f, -1.844f, -1.437f, -1.099f, -0.800f,
                                      -0.522f, -0.258f, 0.0f,    0.258f,  0.522f,
                                      0.800f,  1.099f,  1.437f,  1.844f,  2.401f};
-
-// Sum of squares in the oracle's order: per-lane left to right, then a
-// xor-butterfly over all 64 lanes.
-template <int E>
-__device__ inline float canonical_sumsq(const float (&x)[E], int lane) {
-  float acc = x[0] * x[0];
-#pragma unroll
-  for (int i = 1; i < E; i++) {
-    float sq = x[i] * x[i];
-    acc = acc + sq;
-  }
-  return group_sum<64>(acc, lane);
-}
-
-__device__ inline float bf16_round(float v) { return __uint_as_float((uint32_t)f32_to_bf16(v) << 16); }
 
 __device__ inline int cb_index(float z, int bits) {
   int idx = 0;
@@ -75,12 +61,6 @@ __device__ inline uint32_t v_clear_mask(int w, const int* cov) {
       if (cov[4 * q + 2 * (p & 1) + (p >> 2)] >= 0) m |= 0xfu << (4 * p);
   }
   return m;
-}
-
-// Position of a lane's pair partner for RoPE, and its value: lane ^ m via
-// the LDS crossbar (m = rope_dims / 2 / E is known only at run time).
-__device__ inline float lane_xor_value(float v, int m, int lane) {
-  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ m) << 2, __float_as_int(v)));
 }
 
 // One work-group per (touched head-block, KV head, sequence), 8 waves: wave
@@ -169,7 +149,7 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
   if (tid < kBlockTokens) cov_row[tid] = row_of(tid);
   if constexpr (PRO) {
     for (int i = tid; i < half; i += kAppendThreads)
-      rope_f[i] = (float)pow((double)a.rope_theta, -2.0 * (double)i / (double)a.rope_dims);
+      rope_f[i] = rope_inv_freq(i, a.rope_dims, a.rope_theta);
   }
   __syncthreads();
 
@@ -190,70 +170,25 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
 
   if constexpr (PRO) {
     if (!isv) {
-      // (cos, sin) of every (row, angle) pair once, spread over the lanes;
-      // angle a = f32(pos) * f32(theta^(-2i/rope_dims)), cos/sin in double
+      // (cos, sin) of every (row, angle) pair once, spread over the lanes
       for (int j = lane; j < half; j += 64) {
         const float f = rope_f[j];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-          const float ang = (float)(pos0 + (rows[r] < 0 ? 0 : rows[r])) * f;
-          double sn, cs;
-          sincos((double)ang, &sn, &cs);
-          rope_cs[quad][r][j] = make_float2((float)cs, (float)sn);
-        }
+        for (int r = 0; r < R; r++) rope_cs[quad][r][j] = rope_cos_sin(pos0 + (rows[r] < 0 ? 0 : rows[r]), f);
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      // k_norm (src/model/gemma4_attention.rs:63): r = 1 / sqrt(sum(x^2) / D
-      // + eps) with the canonical sum, x * r * w rounded to bf16
       float w[E];
       load_row<E>(a.k_norm_w + lane * E, w);
-      float rn[R];
+#pragma unroll
+      for (int r = 0; r < R; r++) k_norm_row<E>(x[r], w, a.eps, lane);
 #pragma unroll
       for (int r = 0; r < R; r++)
-        rn[r] = 1.0f / sqrtf(canonical_sumsq<E>(x[r], lane) / (float)D + a.eps);
-#pragma unroll
-      for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int i = 0; i < E; i++) x[r][i] = bf16_round((x[r][i] * rn[r]) * w[i]);
-      // RoPE (non-traditional, :78-81): pair (d, d + rope_dims/2); the
-      // partner of lane l's dims sits in lane l ^ (rope_dims / 2 / E)
-      const int m = half / E;
-      float p[R][E];
-#pragma unroll
-      for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int i = 0; i < E; i++) p[r][i] = lane_xor_value(x[r][i], m, lane);
-      if (lane * E < a.rope_dims) {
-        const bool lower = lane * E < half;
-        const int f0 = lower ? lane * E : lane * E - half;
-#pragma unroll
-        for (int r = 0; r < R; r++)
-#pragma unroll
-          for (int i = 0; i < E; i++) {
-            const float2 cs = rope_cs[quad][r][f0 + i];
-            x[r][i] = lower ? bf16_round((x[r][i] * cs.x) - (p[r][i] * cs.y))
-                            : bf16_round((p[r][i] * cs.y) + (x[r][i] * cs.x));
-          }
-      }
+        rope_row<E>(x[r], a.rope_dims, lane, [&](int j) { return rope_cs[quad][r][j]; });
     } else {
-      // v_norm (src/model/norm.rs:16-29): x2 = bf16(x * x); mean =
-      // bf16(sum(x2) / D) (canonical sum); out = x * (1 / sqrt(mean + eps))
-      float acc[R];
 #pragma unroll
-      for (int r = 0; r < R; r++) {
-        acc[r] = bf16_round(x[r][0] * x[r][0]);
-#pragma unroll
-        for (int i = 1; i < E; i++) acc[r] = acc[r] + bf16_round(x[r][i] * x[r][i]);
-      }
-#pragma unroll
-      for (int r = 0; r < R; r++) {
-        const float mean = bf16_round(group_sum<64>(acc[r], lane) / (float)D);
-        const float rms = 1.0f / sqrtf(mean + a.eps);
-#pragma unroll
-        for (int i = 0; i < E; i++) x[r][i] = x[r][i] * rms;
-      }
+      for (int r = 0; r < R; r++) v_norm_row<E>(x[r], a.eps, lane);
     }
   }
 

@@ -58,6 +58,7 @@
 
 #include "fmkv_device.h"
 #include "fmkv_internal.h"
+#include "fmkv_prologue.h"
 #include "fmkv_quant.h"
 #include "fmkv_attn_common.h"
 
@@ -279,14 +280,23 @@ __device__ inline void store_v_codes(uint8_t* vbase, int t, int d0, const uint32
 // reference's current token attends to its own quantized K/V
 // (src/cache.rs:295-298) -- contributes partial slot n_splits: m = q_rot .
 // k_deq (base 2), l = 1, o = v_deq . R^T, the same row for every head of the
-// group. Wave 0 handles K, wave 1 V.
-template <int D, int BITS>
-__device__ void new_token_column(const AttnArgs& a, uint8_t* tab, int64_t T, int n_splits,
-                                 int kvh, int seq, int wave, int lane) {
+// group. Wave 0 handles K, wave 1 V. With a.k_norm_w the layer's prologue
+// runs on the raw projections first, exactly as the append kernel runs it;
+// the RoPE (cos, sin) table of position T - 1 is built by every thread of the
+// work-group into `rope` (LDS, rope_dims / 2 float2) before the q table's
+// barriers. NT: threads of the work-group.
+template <int D, int BITS, int NT>
+__device__ void new_token_column(const AttnArgs& a, uint8_t* tab, float2* rope, int64_t T,
+                                 int n_splits, int kvh, int seq, int wave, int lane) {
   constexpr BlockLayout L = make_layout(D, BITS, kAffine);
   constexpr int E = D / 64, LPG = 64 / E;
   const int G = a.group;
+  const bool pro = a.k_norm_w != nullptr;
   copy_q_row<D>(a, tab, seq, kvh, wave, lane);
+  if (pro && T >= 1) {
+    for (int j = wave * 64 + lane; j < (a.rope_dims >> 1); j += NT)
+      rope[j] = rope_cos_sin(T - 1, rope_inv_freq(j, a.rope_dims, a.rope_theta));
+  }
   wait_vmcnt<0>();
   const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
   build_q_table<D, BITS>(a, tab, wave, lane, sbits);
@@ -310,6 +320,16 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, int64_t T, int
 
   float x[E];
   load_row<E>((isv ? a.v_new : a.k_new) + ((int64_t)seq * a.st.n_kv_heads + kvh) * D + d0, x);
+  if (pro) {  // the rope table is complete: build_q_table's barriers passed
+    if (!isv) {
+      float w[E];
+      load_row<E>(a.k_norm_w + d0, w);
+      k_norm_row<E>(x, w, a.eps, lane);
+      rope_row<E>(x, a.rope_dims, lane, [&](int j) { return rope[j]; });
+    } else {
+      v_norm_row<E>(x, a.eps, lane);
+    }
+  }
   wave_fwht_signed<E>(x, lane);
   const float cs = fwht_lane_sign(lane) * a.c;
 #pragma unroll
@@ -415,9 +435,11 @@ void decode_attn_kernel(AttnArgs a) {
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
   const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits);
+  static_assert(P::kStageRegion >= D / 2 * (int)sizeof(float2), "rope table fits the staging");
   if constexpr (MODE == kDense) {
     if (a.new_col && split == (int)gridDim.z - 1) {
-      new_token_column<D, BITS>(a, scratch, T, n_splits, kvh, seq, wave, lane);
+      new_token_column<D, BITS, P::kWaves * 64>(a, scratch, reinterpret_cast<float2*>(stage), T,
+                                                n_splits, kvh, seq, wave, lane);
       return;
     }
   }

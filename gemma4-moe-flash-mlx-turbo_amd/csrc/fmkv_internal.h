@@ -80,6 +80,13 @@ struct AttnArgs {
   int32_t new_col;
   const uint16_t* k_new;  // bf16 [n_seqs][n_kv_heads][D]
   const uint16_t* v_new;
+  // The layer's prologue on the new token first (k_norm and RoPE at
+  // position seq_len - 1 on K, v_norm on V, as AppendArgs); null: the rows
+  // are stored as given.
+  const uint16_t* k_norm_w = nullptr;  // bf16 [D]
+  float eps = 0.0f;
+  int32_t rope_dims = 0;
+  float rope_theta = 0.0f;
   // Sparse-V threshold (0: dense). With tau > 0 a stats pass writes, per
   // (sequence, q head), the base-2 score threshold theta = M + log2(tau * L)
   // and the full softmax max M and sum L: tau_stats = [theta | M | L], each

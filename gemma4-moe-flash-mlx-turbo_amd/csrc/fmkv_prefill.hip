@@ -127,7 +127,7 @@ void prefill_attn_kernel(PrefillArgs a) {
   };
   // this lane's row = column c of its pair
   const int row = pair * 16 + c;
-  const int rq = row / G, rh = row - rq * G;
+  const int rq = row / G;
   const bool row_valid = rq < nq;
   const int64_t p_row = p0 + qi0 + rq;
   const int64_t row_lo = lo_of(p_row);

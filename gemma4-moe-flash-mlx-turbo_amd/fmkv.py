@@ -47,6 +47,7 @@ EXPORTED = (
     "fmkv_pool_read_codes", "fmkv_set_blocks_per_split", "fmkv_cache_decode_splits",
     "fmkv_profile_enable", "fmkv_profile_collect", "fmkv_decode_step", "fmkv_paged_decode_step",
     "fmkv_prefill_step", "fmkv_paged_prefill_step", "fmkv_decode_step_noalloc",
+    "fmkv_decode_step_projected", "fmkv_paged_decode_step_projected",
 )
 
 
@@ -153,6 +154,11 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
                                      i32, vp], ctypes.c_int),
         "fmkv_paged_decode_step": ([vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, vp, i32,
                                     ctypes.c_float, ctypes.c_float, vp, i32, vp], ctypes.c_int),
+        "fmkv_decode_step_projected": ([vp, vp, vp, i64, P(KvPrologue), vp, i32, ctypes.c_float,
+                                        ctypes.c_float, vp, i32, vp], ctypes.c_int),
+        "fmkv_paged_decode_step_projected": ([vp, vp, vp, vp, i32, vp, vp, i32, i32, i32,
+                                              P(KvPrologue), vp, i32, ctypes.c_float,
+                                              ctypes.c_float, vp, i32, vp], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -328,6 +334,26 @@ class KVCache:
         _check(self._lib.fmkv_decode_step(self._h, _ptr(keys), _ptr(values), keys.shape[0],
                                           _ptr(q), q.shape[0], scale, sparse_v_tau, _ptr(out),
                                           _dtype_code(out.dtype), _stream(stream)))
+        return out
+
+    def decode_step_projected(self, keys: torch.Tensor, values: torch.Tensor | None,
+                              prologue: KvPrologue, q: torch.Tensor, scale: float = 1.0,
+                              sparse_v_tau: float = 0.0, out: torch.Tensor | None = None,
+                              dtype=torch.bfloat16, stream=None) -> torch.Tensor:
+        """decode_step() of raw k_proj / v_proj rows through the layer's
+        prologue (src/model/gemma4_attention.rs:50-104 after the projections;
+        values None with prologue.v_from_k)."""
+        if values is None:
+            values = keys
+        self._check_kv(keys, values)
+        _check_prologue_weight(prologue, self.desc.head_dim)
+        if q.dtype != torch.bfloat16 or q.dim() != 2 or q.shape[1] != self.desc.head_dim:
+            raise ValueError("q must be bf16 [n_q_heads, head_dim]")
+        if out is None:
+            out = torch.empty(q.shape, dtype=dtype, device=q.device)
+        _check(self._lib.fmkv_decode_step_projected(
+            self._h, _ptr(keys), _ptr(values), keys.shape[0], ctypes.byref(prologue), _ptr(q),
+            q.shape[0], scale, sparse_v_tau, _ptr(out), _dtype_code(out.dtype), _stream(stream)))
         return out
 
     def prefill_step(self, keys: torch.Tensor, values: torch.Tensor, q: torch.Tensor,
@@ -518,6 +544,24 @@ class PagedPool:
             self._h, _ptr(keys), _ptr(values), _ptr(block_tables), block_tables.shape[1],
             _ptr(start_pos), _ptr(seq_lens), keys.shape[0], keys.shape[1], max_seq_len, _ptr(q),
             q.shape[1], scale, sparse_v_tau, _ptr(out), _dtype_code(out.dtype), _stream(stream)))
+        return out
+
+    def decode_step_projected(self, keys, values, block_tables, start_pos, seq_lens,
+                              max_seq_len: int, prologue: KvPrologue, q, scale: float = 1.0,
+                              sparse_v_tau: float = 0.0, out=None, dtype=torch.bfloat16,
+                              stream=None):
+        """decode_step() of raw projections through the layer's prologue
+        (RoPE positions from start_pos; values None with prologue.v_from_k)."""
+        if values is None:
+            values = keys
+        _check_prologue_weight(prologue, self.desc.head_dim)
+        if out is None:
+            out = torch.empty(q.shape, dtype=dtype, device=q.device)
+        _check(self._lib.fmkv_paged_decode_step_projected(
+            self._h, _ptr(keys), _ptr(values), _ptr(block_tables), block_tables.shape[1],
+            _ptr(start_pos), _ptr(seq_lens), keys.shape[0], keys.shape[1], max_seq_len,
+            ctypes.byref(prologue), _ptr(q), q.shape[1], scale, sparse_v_tau, _ptr(out),
+            _dtype_code(out.dtype), _stream(stream)))
         return out
 
     def read_codes(self, stream=None):

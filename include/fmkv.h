@@ -152,6 +152,21 @@ int fmkv_decode_step(fmkv_cache* cache, const void* k_bf16, const void* v_bf16, 
                      const void* q_bf16, int32_t n_q_heads, float scale, float sparse_v_tau,
                      void* out, int32_t out_dtype, void* stream);
 
+/* fmkv_decode_step of raw projections: the layer's prologue (see
+ * fmkv_kv_prologue) on the n_tokens new rows at positions offset ..
+ * offset + n_tokens - 1, their store, then the attention read -- the whole
+ * of Gemma4Attention::forward after the q/k/v projections for L == n_tokens
+ * (src/model/gemma4_attention.rs:50-104; q arrives normed and roped). With
+ * one new token and sparse_v_tau == 0 the prologue, quantization and store
+ * run inside the attention launch's new-token column (one launch plus the
+ * split combine); otherwise fmkv_cache_append_projected, then
+ * fmkv_decode_attention. Affine-mode caches; errors as those calls. */
+int fmkv_decode_step_projected(fmkv_cache* cache, const void* k_proj_bf16,
+                               const void* v_proj_bf16, int64_t n_tokens,
+                               const fmkv_kv_prologue* prologue, const void* q_bf16,
+                               int32_t n_q_heads, float scale, float sparse_v_tau, void* out,
+                               int32_t out_dtype, void* stream);
+
 /* Bytes of device scratch behind fmkv_decode_step_noalloc (per GPU). */
 #define FMKV_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
 
@@ -248,6 +263,17 @@ int fmkv_paged_decode_step(fmkv_pool* pool, const void* k_bf16, const void* v_bf
                            int32_t n_new, int32_t max_seq_len, const void* q_bf16,
                            int32_t n_q_heads, float scale, float sparse_v_tau, void* out,
                            int32_t out_dtype, void* stream);
+
+/* fmkv_paged_decode_step of raw projections through the layer's prologue
+ * (see fmkv_decode_step_projected); RoPE positions start at start_pos. */
+int fmkv_paged_decode_step_projected(fmkv_pool* pool, const void* k_proj_bf16,
+                                     const void* v_proj_bf16, const int32_t* block_tables,
+                                     int32_t max_blocks, const int32_t* start_pos,
+                                     const int32_t* seq_lens, int32_t n_seqs, int32_t n_new,
+                                     int32_t max_seq_len, const fmkv_kv_prologue* prologue,
+                                     const void* q_bf16, int32_t n_q_heads, float scale,
+                                     float sparse_v_tau, void* out, int32_t out_dtype,
+                                     void* stream);
 
 /* Batched chunked prefill: fmkv_paged_append of n_new tokens per sequence at
  * start_pos, then each sequence's causal attention of those n_new queries
