@@ -51,9 +51,12 @@ def dev_bf16(bits: np.ndarray):
     return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
 
 
-def bytes_per_token_head(D: int, bits: int, codebook: bool = False) -> int:
-    """K+V codes plus f16 scale and bias per 64-dim group (affine) or one f16
-    norm per row (codebook), one token, one KV head."""
+def bytes_per_token_head(D: int, bits: int, codebook: bool = False, plain: bool = False) -> int:
+    """K+V codes plus f16 scale and bias per 64-dim group (affine), one f16
+    norm per row (codebook) or the bf16 rows alone (plain), one token, one KV
+    head."""
+    if plain:
+        return 2 * D * 2
     if codebook:
         return 2 * (D * bits // 8 + 2)
     return 2 * (D * bits // 8 + 4 * (D // 64))
@@ -66,10 +69,12 @@ def run_c3(args) -> dict:
     import synth
 
     cb = args.mode == "codebook"
+    plain = args.mode == "plain"
+    quant = not (cb or plain)  # affine
     Hq, Hkv, D, T0 = 16, 2, 512, args.context
-    bits = args.bits or (3 if cb else 8)
-    mode = fmkv.MODE_CODEBOOK if cb else fmkv.MODE_AFFINE
-    per_tok = bytes_per_token_head(D, bits, cb)
+    bits = 16 if plain else (args.bits or (3 if cb else 8))
+    mode = fmkv.MODE_CODEBOOK if cb else fmkv.MODE_PLAIN if plain else fmkv.MODE_AFFINE
+    per_tok = bytes_per_token_head(D, bits, cb, plain)
     # steps: warmup, timed, event-timed, then warmup + timed projected steps
     n_dec = 2 * args.warmup + 3 * args.steps + 1
     cache = fmkv.KVCache.new_quantized(D, bits, Hkv, capacity=T0 + n_dec + args.graph_steps + 16,
@@ -95,7 +100,7 @@ def run_c3(args) -> dict:
     # one untimed chunk through each path first (first-launch costs)
     warm = fmkv.KVCache.new_quantized(D, bits, Hkv, capacity=2 * chunk, mode=mode)
     warm.append(dk[0], dv[0])
-    if not cb:
+    if quant:
         warm.append_projected(dk[0], None, pro)
     torch.cuda.synchronize()
     del warm
@@ -111,7 +116,7 @@ def run_c3(args) -> dict:
 
     # the same chunks as raw projections through the prologue (affine caches)
     prologue_tps = None
-    if not cb:
+    if quant:
         pcache = fmkv.KVCache.new_quantized(D, bits, Hkv, capacity=T0)
         torch.cuda.synchronize()
         ev0.record()
@@ -227,7 +232,7 @@ def run_c3(args) -> dict:
     # RoPE on K, v_norm of the raw K as V, quantize, store, attend) in the
     # same single attention launch plus combine. Informational, eager.
     proj_us = None
-    if not cb and tau == 0.0:
+    if quant and tau == 0.0:
         pro_ref = ctypes.byref(pro)
 
         def proj_step():
@@ -264,6 +269,7 @@ def run_c3(args) -> dict:
         "config": {
             "workload": (f"gemma4-global-layer decode at {T0 // 1024}K: Hq 16, Hkv 2, head_dim 512, "
                          + (f"{bits}-bit TurboQuant codebook, f16 norm per row" if cb else
+                            "plain bf16 rows (no quantization)" if plain else
                             f"{bits}-bit group-64 affine, f16 scale/bias")
                          + ", 1 token append + attention per step"),
             "context": T0, "batch": 1, "n_q_heads": Hq, "n_kv_heads": Hkv, "head_dim": D,
@@ -281,9 +287,10 @@ def run_c3(args) -> dict:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None if (cb or bits != 8) else TRAFFIC_BYTES_PER_LAUNCH,
-            "traffic_source": None if (cb or bits != 8) else TRAFFIC_SOURCE,
-            "kernel": f"cb_decode_kernel<512, {bits}>" if cb else f"decode_attn_kernel<512, {bits}, 0>",
+            "traffic": None if (not quant or bits != 8) else TRAFFIC_BYTES_PER_LAUNCH,
+            "traffic_source": None if (not quant or bits != 8) else TRAFFIC_SOURCE,
+            "kernel": (f"cb_decode_kernel<512, {bits}>" if cb else "plain_decode_kernel<512>" if plain
+                       else f"decode_attn_kernel<512, {bits}, 0>"),
             "avg_kernel_us": round(kern_s * 1e6, 3),
             "bytes_per_launch": int(launch_bytes),
         },
@@ -803,8 +810,9 @@ def main(argv=None) -> int:
     ap.add_argument("--prefill-sliding", action="store_true",
                     help="prefill workload on the sliding-layer shape (ring W 1024)")
     ap.add_argument("--c5-context", type=int, default=131072)
-    ap.add_argument("--mode", choices=["affine", "codebook"], default="affine",
-                    help="c3: cache mode (codebook = the reference's TurboQuant indices + norm)")
+    ap.add_argument("--mode", choices=["affine", "codebook", "plain"], default="affine",
+                    help="c3: cache mode (codebook = the reference's TurboQuant indices + norm; "
+                         "plain = unquantized bf16 rows)")
     ap.add_argument("--bits", type=int, default=0,
                     help="c3: code bits (0: 8 for affine, 3 for codebook, the reference's default)")
     ap.add_argument("--c4-seqs", type=int, default=0,

@@ -80,6 +80,8 @@ int check_desc(const fmkv_cache_desc* d) {
   } else if (d->mode == FMKV_MODE_CODEBOOK) {
     if (d->bits < 2 || d->bits > 4)
       return fail(FMKV_ERR_UNSUPPORTED, "codebook mode supports 2, 3 or 4 bits");
+  } else if (d->mode == FMKV_MODE_PLAIN) {
+    if (d->bits != 16) return fail(FMKV_ERR_UNSUPPORTED, "plain (bf16) mode has bits = 16");
   } else {
     return fail(FMKV_ERR_UNSUPPORTED, "unknown mode");
   }
@@ -105,6 +107,13 @@ int device_cus() {
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     return 256;
   return cus;
+}
+
+// Decode work-groups per CU the split plan aims at: the affine kernel's LDS
+// staging fills a CU; the codebook and plain kernels' work-groups are about
+// half as large (two per CU).
+int attn_wg_per_cu(const fmkv_cache_desc& d) {
+  return d.mode == FMKV_MODE_AFFINE ? fmkv::kAttnWgPerCu : 2;
 }
 
 // Split-K plan: blocks per split such that the grid has about `wg_per_cu`
@@ -239,7 +248,7 @@ int make_signs(const fmkv_cache_desc& d, float** out) {
 int check_attn_args(const fmkv_cache_desc& d, const void* q, int32_t n_q_heads, float tau,
                     const void* out, int32_t out_dtype) {
   if (!q || !out) return fail(FMKV_ERR_INVALID_ARG, "q/out must be device pointers");
-  if (d.mode == FMKV_MODE_CODEBOOK && tau != 0.0f)
+  if (d.mode != FMKV_MODE_AFFINE && tau != 0.0f)
     return fail(FMKV_ERR_UNSUPPORTED, "sparse-V attention reads affine-mode caches");
   if (n_q_heads < d.n_kv_heads || n_q_heads % d.n_kv_heads != 0)
     return fail(FMKV_ERR_INVALID_ARG, "n_q_heads must be a multiple of n_kv_heads");
@@ -391,8 +400,7 @@ int prepare_attention(fmkv_cache* c, int64_t T, const void* q, int32_t n_q_heads
   const int64_t vb = W > 0 ? 0 : c->vis_begin;
   const int64_t nblk =
       (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
-  // codebook work-groups are half as large in LDS: two per CU
-  const int wg_per_cu = c->desc.mode == FMKV_MODE_CODEBOOK ? 2 : fmkv::kAttnWgPerCu;
+  const int wg_per_cu = attn_wg_per_cu(c->desc);
   return prepare_attention_common(c, cache_store(c), 1, nblk, q, n_q_heads, scale, tau, out,
                                   out_dtype, wg_per_cu, 1, 1, new_col, a, ext);
 }
@@ -477,6 +485,8 @@ hipError_t launch_attention(const fmkv::AttnArgs& a, int n_seqs, int n_kv_heads,
                             hipEvent_t e0, hipEvent_t e1) {
   if (a.st.layout.mode == fmkv::kCodebook)
     return fmkv::launch_cb_decode_attention(a, n_seqs, n_kv_heads, s, e0, e1);
+  if (a.st.layout.mode == fmkv::kPlain)
+    return fmkv::launch_plain_decode_attention(a, n_seqs, n_kv_heads, s, e0, e1);
   return fmkv::launch_decode_attention(a, n_seqs, n_kv_heads, s, e0, e1);
 }
 
@@ -800,8 +810,7 @@ int fmkv_cache_decode_splits(const fmkv_cache* c, int32_t* n_splits) {
   int64_t vb = c->desc.window > 0 ? 0 : c->vis_begin;
   int64_t nblk = (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
   if (nblk < 1) nblk = 1;
-  const int wg_per_cu = c->desc.mode == FMKV_MODE_CODEBOOK ? 2 : fmkv::kAttnWgPerCu;
-  const int32_t bps = choose_bps(nblk * c->desc.n_kv_heads, c->cus, wg_per_cu);
+  const int32_t bps = choose_bps(nblk * c->desc.n_kv_heads, c->cus, attn_wg_per_cu(c->desc));
   *n_splits = (int32_t)((nblk + bps - 1) / bps);
   return FMKV_OK;
 }
@@ -829,7 +838,8 @@ int fmkv_cache_fetch(const fmkv_cache* c, void* k_out, void* v_out, int32_t out_
 
 int fmkv_cache_read_codes(const fmkv_cache* c, void* codes, void* meta, void* stream) {
   if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
-  if (!codes || !meta) return fail(FMKV_ERR_INVALID_ARG, "codes/meta must be device pointers");
+  if (!codes || (!meta && c->desc.mode != FMKV_MODE_PLAIN))
+    return fail(FMKV_ERR_INVALID_ARG, "codes/meta must be device pointers");
   fmkv::ReadArgs a;
   a.st = cache_store(c);
   a.n_slots = c->desc.window > 0 ? c->desc.window : c->desc.capacity;
@@ -1062,7 +1072,8 @@ int fmkv_paged_decode_step_projected(fmkv_pool* p, const void* k_proj, const voi
 
 int fmkv_pool_read_codes(const fmkv_pool* p, void* codes, void* meta, void* stream) {
   if (!p) return fail(FMKV_ERR_INVALID_ARG, "pool is null");
-  if (!codes || !meta) return fail(FMKV_ERR_INVALID_ARG, "codes/meta must be device pointers");
+  if (!codes || (!meta && p->desc.mode != FMKV_MODE_PLAIN))
+    return fail(FMKV_ERR_INVALID_ARG, "codes/meta must be device pointers");
   fmkv::ReadArgs a;
   a.st = pool_store(p, nullptr, 0);
   a.n_slots = p->n_blocks * fmkv::kBlockTokens;

@@ -8,6 +8,8 @@
 //    then lane exchanges), then * (1/sqrt D) and the LCG sign;
 //  - affine mode: MLX group-64 affine quantization (4/8-bit, f16 scale/bias);
 //  - codebook mode: the reference's own TurboQuant Lloyd-Max binning;
+//  - plain mode: the bf16 rows as given (KVCacheInner::Plain,
+//    src/cache.rs:274-288), K token-major and V dim-major;
 //  - slot write: ring slot pos % W for sliding layers, pos for global layers,
 //    block table for paged pools;
 //  - optionally, the layer's prologue first (src/model/gemma4_attention.rs
@@ -163,6 +165,10 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
       const uint32_t old =
           all_cov ? 0u : reinterpret_cast<const uint32_t*>(blk + L.v_codes)[w];
       vst[w] = old & ~v_clear_mask<BITS>(w, cov_row);
+    } else if constexpr (MODE == kPlain) {
+      // a dim's word holds two tokens: start from the stored block, the
+      // covered tokens' halves are overwritten below
+      vst[w] = all_cov ? 0u : reinterpret_cast<const uint32_t*>(blk + L.v_codes)[w];
     } else {
       vst[w] = 0u;
     }
@@ -204,7 +210,14 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
 
   uint32_t code[R][E];
   uint32_t meta[R];
-  if constexpr (MODE == kAffine) {
+  if constexpr (MODE == kPlain) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      meta[r] = 0u;
+#pragma unroll
+      for (int i = 0; i < E; i++) code[r][i] = (uint32_t)f32_to_bf16(x[r][i]);  // exact
+    }
+  } else if constexpr (MODE == kAffine) {
 #pragma unroll
     for (int r = 0; r < R; r++) wave_fwht_signed<E>(x[r], lane);
 #pragma unroll
@@ -237,7 +250,19 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
 
   if (any) {
     uint32_t* stage = isv ? vst : kst;
-    if constexpr (MODE == kAffine) {
+    if constexpr (MODE == kPlain) {
+      uint16_t* st16 = reinterpret_cast<uint16_t*>(stage);
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        if (rows[r] < 0) continue;
+        const int t = quad * R + r;
+#pragma unroll
+        for (int i = 0; i < E; i++) {
+          const int d = lane * E + i;
+          st16[(isv ? plain_v_pos(t, d) : plain_k_pos(D, t, d)) >> 1] = (uint16_t)code[r][i];
+        }
+      }
+    } else if constexpr (MODE == kAffine) {
       if (!isv) {
         // G consecutive elements of a lane fall into one K word
         constexpr int G = E < 32 / BITS ? E : 32 / BITS;
@@ -307,7 +332,8 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
   }
   __syncthreads();
 
-  // 16-byte copy-out; K (and codebook V) chunks belong to one token each
+  // 16-byte copy-out; K (and codebook V) chunks belong to one token each,
+  // affine and plain V chunks are whole (merged with the stored block above)
   uint4* kdst = reinterpret_cast<uint4*>(blk + L.k_codes);
   uint4* vdst = reinterpret_cast<uint4*>(blk + L.v_codes);
   const uint4* ks = reinterpret_cast<const uint4*>(kst);
@@ -316,6 +342,9 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
     int tk;
     if constexpr (MODE == kAffine) {
       tk = c & 15;
+      vdst[c] = vs[c];
+    } else if constexpr (MODE == kPlain) {
+      tk = (int)((int64_t)c * 16 / (L.code_bytes / kBlockTokens));
       vdst[c] = vs[c];
     } else {
       tk = (int)((int64_t)c * 16 / (L.code_bytes / kBlockTokens));
@@ -352,6 +381,12 @@ hipError_t launch_append(const AppendArgs& a, int n_seqs, int max_tasks, hipStre
       case 256 * 16 + 8: return launch_t<256, 8, kAffine>(a, n_seqs, max_tasks, s);
       case 512 * 16 + 4: return launch_t<512, 4, kAffine>(a, n_seqs, max_tasks, s);
       case 512 * 16 + 8: return launch_t<512, 8, kAffine>(a, n_seqs, max_tasks, s);
+    }
+  } else if (L.mode == kPlain) {
+    switch (L.head_dim) {
+      case 128: return launch_t<128, 16, kPlain>(a, n_seqs, max_tasks, s);
+      case 256: return launch_t<256, 16, kPlain>(a, n_seqs, max_tasks, s);
+      case 512: return launch_t<512, 16, kPlain>(a, n_seqs, max_tasks, s);
     }
   } else {
     switch (L.head_dim * 16 + L.bits) {

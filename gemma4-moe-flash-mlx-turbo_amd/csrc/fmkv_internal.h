@@ -153,7 +153,11 @@ hipError_t launch_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads
 // sparse-V).
 hipError_t launch_cb_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                                       hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr);
-// The split merge of either decode kernel: out = LSE merge of the partials.
+// Decode attention over a plain (bf16) cache, planned as the codebook kernel.
+hipError_t launch_plain_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads,
+                                         hipStream_t s, hipEvent_t ev_begin = nullptr,
+                                         hipEvent_t ev_end = nullptr);
+// The split merge of every decode kernel: out = LSE merge of the partials.
 hipError_t launch_combine(const AttnArgs& a, int n_seqs, hipStream_t s);
 hipError_t launch_prefill_attention(const PrefillArgs& a, hipStream_t s);
 hipError_t launch_read_codes(const ReadArgs& a, hipStream_t s);

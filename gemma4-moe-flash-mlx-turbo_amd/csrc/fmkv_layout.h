@@ -5,6 +5,7 @@
 //
 //   [K codes][V codes][K scale/bias][V scale/bias]            (affine mode)
 //   [K codes][V codes][K norms][V norms]                      (codebook mode)
+//   [K rows][V columns]                                       (plain mode)
 //
 // Affine mode (4- or 8-bit codes, 64-element groups along head_dim, f16
 // scale and bias per group per token) arranges codes for the decode kernel's
@@ -30,6 +31,12 @@
 // little-endian bit stream (index j at bit j*bits), plus one f16 L2 norm per
 // token row.
 //
+// Plain mode (unquantized bf16, bits = 16) keeps K token-major -- row t is
+// head_dim bf16 at t * head_dim * 2 -- and V dim-major -- dim d holds the 16
+// tokens' bf16 at d * 32 -- so that a lane's 16-byte K load is an operand of
+// v_mfma_f32_16x16x32_bf16 (8 consecutive dims of one token) and its 8-byte
+// V load one of v_mfma_f32_16x16x16_bf16 (4 consecutive tokens of one dim).
+//
 // Head-block address: base + phys_block * block_stride + head * head_stride,
 // with phys_block = block_table[logical block] for a paged pool and the
 // logical block itself otherwise.
@@ -47,7 +54,7 @@ namespace fmkv {
 constexpr int kBlockTokens = 16;
 constexpr int kGroup = 64;
 
-enum Mode : int { kAffine = 0, kCodebook = 1 };
+enum Mode : int { kAffine = 0, kCodebook = 1, kPlain = 2 };
 
 struct BlockLayout {
   int head_dim;
@@ -72,8 +79,9 @@ FMKV_HD constexpr BlockLayout make_layout(int head_dim, int bits, int mode) {
   L.k_codes = 0;
   L.v_codes = L.code_bytes;
   L.k_meta = 2 * L.code_bytes;
-  int64_t meta = (mode == kAffine) ? (int64_t)(head_dim / kGroup) * kBlockTokens * 4
-                                   : (int64_t)kBlockTokens * 2;
+  int64_t meta = (mode == kAffine)     ? (int64_t)(head_dim / kGroup) * kBlockTokens * 4
+                 : (mode == kCodebook) ? (int64_t)kBlockTokens * 2
+                                       : 0;
   L.v_meta = L.k_meta + round_up(meta, 64);
   L.block_bytes = round_up(L.v_meta + round_up(meta, 64), 256);
   return L;
@@ -113,6 +121,10 @@ FMKV_HD void v_code_pos(int bits, int t, int d, int64_t* word_off, int* shift) {
 
 // Offset of the {f16 scale, f16 bias} pair of group g, token t (affine).
 FMKV_HD int64_t scale_pos(int g, int t) { return (int64_t)(g * kBlockTokens + t) * 4; }
+
+// Plain mode: byte offsets of K dim d of token t and of V dim d of token t.
+FMKV_HD int64_t plain_k_pos(int head_dim, int t, int d) { return ((int64_t)t * head_dim + d) * 2; }
+FMKV_HD int64_t plain_v_pos(int t, int d) { return ((int64_t)d * kBlockTokens + t) * 2; }
 
 // Codebook mode: byte offset of token t's row and of its norm.
 FMKV_HD int64_t cb_row_bytes(int head_dim, int bits) { return (int64_t)head_dim * bits / 8; }

@@ -5,7 +5,7 @@
 //    chronological order -- what KVCache::update_and_fetch returns and
 //    KVCache::peek_kv reads (src/cache.rs:247-310). In codebook mode this is
 //    the reference's round trip output (src/cache.rs:119-125) computed from
-//    the stored indices and f16 norm.
+//    the stored indices and f16 norm; in plain mode the stored bf16 rows.
 #include "fmkv_device.h"
 #include "fmkv_internal.h"
 
@@ -30,9 +30,12 @@ __device__ inline uint32_t get_bits(const uint32_t* words, int64_t bit, int bits
   return (uint32_t)(v & ((1u << bits) - 1u));
 }
 
-// Code of dim d, token t, of a head-block (affine or codebook).
+// Code of dim d, token t, of a head-block (plain: the bf16 bits).
 __device__ inline uint32_t stored_code(const uint8_t* blk, const BlockLayout& L, int isv, int t,
                                        int d) {
+  if (L.mode == kPlain)
+    return *reinterpret_cast<const uint16_t*>(
+        blk + (isv ? L.v_codes + plain_v_pos(t, d) : L.k_codes + plain_k_pos(L.head_dim, t, d)));
   if (L.mode == kAffine) {
     int64_t off;
     int sh;
@@ -81,7 +84,7 @@ __global__ void read_codes_kernel(ReadArgs a) {
     }
     a.codes[row * words + wi] = out;
   }
-  const int n_meta = L.mode == kAffine ? 2 * (D / kGroup) : 1;
+  const int n_meta = L.mode == kAffine ? 2 * (D / kGroup) : L.mode == kCodebook ? 1 : 0;
   const uint8_t* meta = blk + (isv ? L.v_meta : L.k_meta);
   for (int mi = threadIdx.x; mi < n_meta; mi += blockDim.x) {
     uint16_t v;
@@ -112,6 +115,19 @@ __global__ __launch_bounds__(64) void fetch_kernel(FetchArgs a) {
   const uint8_t* blk = a.st.base + blk_i * a.st.block_stride + (int64_t)h * a.st.head_stride;
   float x[E];
   float norm = 1.0f;
+  void* dst = isv ? a.v_out : a.k_out;
+  const int64_t base = (i * H + h) * D + lane * E;
+  if (L.mode == kPlain) {  // the stored rows, no rotation
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+      const uint32_t b = stored_code(blk, L, isv, t, lane * E + e);
+      if (a.out_f32)
+        reinterpret_cast<float*>(dst)[base + e] = __uint_as_float(b << 16);
+      else
+        reinterpret_cast<uint16_t*>(dst)[base + e] = (uint16_t)b;
+    }
+    return;
+  }
   if (L.mode == kAffine) {
 #pragma unroll
     for (int e = 0; e < E; e++) {
@@ -132,8 +148,6 @@ __global__ __launch_bounds__(64) void fetch_kernel(FetchArgs a) {
     }
   }
   wave_fwht<E>(x, lane);  // true values: the output is compared bit for bit
-  void* dst = isv ? a.v_out : a.k_out;
-  const int64_t base = (i * H + h) * D + lane * E;
 #pragma unroll
   for (int e = 0; e < E; e++) {
     const float v = (L.mode == kAffine) ? x[e] * a.c : (x[e] * a.c) * norm;

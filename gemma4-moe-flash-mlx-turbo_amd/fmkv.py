@@ -34,6 +34,8 @@ FMKV_ERR_HIP = 4
 FMKV_ERR_CAPACITY = 5
 MODE_AFFINE = 0
 MODE_CODEBOOK = 1
+MODE_PLAIN = 2  # unquantized bf16 rows (bits 16): KVCacheInner::Plain, src/cache.rs:174-178
+PLAIN_BITS = 16
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
 BLOCK_TOKENS = 16
@@ -225,7 +227,8 @@ def profile_collect() -> tuple[float, int]:
 
 
 class KVCache:
-    """Quantized KV cache of one attention layer (src/cache.rs:166-172)."""
+    """KV cache of one attention layer (src/cache.rs:166-172): quantized
+    (affine or codebook) or plain bf16."""
 
     def __init__(self, desc: CacheDesc):
         self.desc = desc
@@ -246,6 +249,17 @@ class KVCache:
     def new_quantized(cls, head_dim: int, bits: int, n_kv_heads: int, capacity: int,
                       mode: int = MODE_AFFINE) -> "KVCache":
         return cls.new_quantized_with_window(head_dim, bits, None, n_kv_heads, capacity, mode)
+
+    @classmethod
+    def new_with_window(cls, head_dim: int, window: int | None, n_kv_heads: int,
+                        capacity: int = 0) -> "KVCache":
+        """The plain bf16 cache (KVCache::new_with_window, src/cache.rs:191-199)."""
+        return cls(make_desc(n_kv_heads, head_dim, PLAIN_BITS, window or 0, capacity, MODE_PLAIN))
+
+    @classmethod
+    def new(cls, head_dim: int, n_kv_heads: int, capacity: int) -> "KVCache":
+        """KVCache::new (src/cache.rs:187-189): plain, no window."""
+        return cls.new_with_window(head_dim, None, n_kv_heads, capacity)
 
     def close(self) -> None:
         if getattr(self, "_h", None):
@@ -447,20 +461,23 @@ def make_cache(layer_types, head_dim: int, n_kv_heads: int, *, capacity: int,
     codebook (default 3 bits, src/main.rs:82-84), hence mode's default;
     MODE_AFFINE gives the 4/8-bit affine caches. `capacity` bounds the
     positions of the linear (window 0) caches, whose arenas are
-    preallocated. kv_quant_bits None (the reference's plain bf16 caches,
-    --no-kv-quant) has no quantized layout here and raises."""
-    if kv_quant_bits is None:
-        raise Exception_(FMKV_ERR_UNSUPPORTED, "plain (unquantized) caches are not provided; "
-                                               "pass kv_quant_bits")
+    preallocated. kv_quant_bits None gives the reference's plain bf16
+    caches (KVCache::new_with_window, --no-kv-quant) on every layer."""
+    plain = kv_quant_bits is None
     specs = layer_cache_specs(layer_types, head_dim, n_kv_heads, global_head_dim=global_head_dim,
                               n_global_kv_heads=n_global_kv_heads, sliding_window=sliding_window,
-                              attention_k_eq_v=attention_k_eq_v, kv_quant_bits=kv_quant_bits,
-                              global_kv_quant_bits=global_kv_quant_bits)
+                              attention_k_eq_v=attention_k_eq_v,
+                              kv_quant_bits=PLAIN_BITS if plain else kv_quant_bits,
+                              global_kv_quant_bits=None if plain else global_kv_quant_bits)
     caches = []
     for sp in specs:
-        c = KVCache.new_quantized_with_window(sp.head_dim, sp.bits, sp.window or None, sp.n_kv_heads,
-                                              capacity=0 if sp.window else capacity, mode=mode,
-                                              sign_seed=sign_seed)
+        if plain:
+            c = KVCache.new_with_window(sp.head_dim, sp.window or None, sp.n_kv_heads,
+                                        capacity=0 if sp.window else capacity)
+        else:
+            c = KVCache.new_quantized_with_window(sp.head_dim, sp.bits, sp.window or None,
+                                                  sp.n_kv_heads, capacity=0 if sp.window else capacity,
+                                                  mode=mode, sign_seed=sign_seed)
         c.spec = sp
         caches.append(c)
     return caches
@@ -582,6 +599,8 @@ def words_per_row(desc: CacheDesc) -> int:
 
 
 def meta_per_row(desc: CacheDesc) -> int:
+    if desc.mode == MODE_PLAIN:
+        return 0
     return 2 * (desc.head_dim // 64) if desc.mode == MODE_AFFINE else 1
 
 

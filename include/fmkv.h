@@ -47,6 +47,8 @@ extern "C" {
 /* cache modes */
 #define FMKV_MODE_AFFINE 0   /* rotated, group-64 affine 4/8-bit codes + f16 scale/bias */
 #define FMKV_MODE_CODEBOOK 1 /* rotated TurboQuant Lloyd-Max 2/3/4-bit indices + f16 norm */
+#define FMKV_MODE_PLAIN 2    /* unquantized bf16 rows (bits = 16): KVCacheInner::Plain,
+                                src/cache.rs:174-178, :274-288; --no-kv-quant */
 
 /* output dtypes */
 #define FMKV_DTYPE_BF16 0
@@ -58,7 +60,7 @@ extern "C" {
 typedef struct fmkv_cache_desc {
   int32_t n_kv_heads; /* >= 1 */
   int32_t head_dim;   /* 128, 256 or 512 */
-  int32_t bits;       /* affine: 4 or 8; codebook: 2, 3 or 4 (src/cache.rs:67-89) */
+  int32_t bits;       /* affine: 4 or 8; codebook: 2, 3 or 4 (src/cache.rs:67-89); plain: 16 */
   int32_t group_size; /* 64 */
   int32_t mode;       /* FMKV_MODE_* */
   int32_t window;     /* 0: global layer, linear growth; W > 0: ring of W slots (W % 16 == 0) */
@@ -106,15 +108,15 @@ int fmkv_cache_trim(fmkv_cache* cache, int64_t keep_last);
  * at src/model/gemma4_attention.rs:94-103 for L == 1 (Gemma-4: scale 1.0).
  * The current position attends to its own quantized K/V, as in the
  * reference where the round trip precedes the concat (src/cache.rs:295-298).
- * Affine and codebook caches: a codebook (TurboQuant) cache is read as
- * stored -- centroid[idx] * norm / sqrt(D) in the rotated domain -- with no
- * bf16 round trip (src/cache.rs:94-129).
+ * All modes: a codebook (TurboQuant) cache is read as stored --
+ * centroid[idx] * norm / sqrt(D) in the rotated domain -- with no bf16 round
+ * trip (src/cache.rs:94-129); a plain cache is the bf16 rows themselves.
  * sparse_v_tau > 0 is the reference's sparse-V decode
  * (src/model/gemma4_attention.rs:196-234): softmax weights below tau are
  * zeroed without renormalisation. It reads the keys twice (a statistics
  * pass, then the gated pass); 0 is plain softmax attention; affine caches
- * only (FMKV_ERR_UNSUPPORTED for codebook caches). Negative or non-finite
- * tau returns FMKV_ERR_INVALID_ARG. */
+ * only (FMKV_ERR_UNSUPPORTED for codebook and plain caches). Negative or
+ * non-finite tau returns FMKV_ERR_INVALID_ARG. */
 int fmkv_decode_attention(fmkv_cache* cache, const void* q_bf16, int32_t n_q_heads, float scale,
                           float sparse_v_tau, void* out, int32_t out_dtype, void* stream);
 
@@ -203,7 +205,8 @@ int fmkv_prefill_step(fmkv_cache* cache, const void* k_bf16, const void* v_bf16,
 
 /* The fetch half of update_and_fetch and KVCache::peek_kv (src/cache.rs:247-257):
  * dequantized, un-rotated K and V of the visible positions in chronological
- * order, [stored_len][n_kv_heads][head_dim] in out_dtype. */
+ * order, [stored_len][n_kv_heads][head_dim] in out_dtype (plain caches: the
+ * stored bf16 rows). */
 int fmkv_cache_fetch(const fmkv_cache* cache, void* k_out, void* v_out, int32_t out_dtype,
                      void* stream);
 
@@ -211,8 +214,10 @@ int fmkv_cache_fetch(const fmkv_cache* cache, void* k_out, void* v_out, int32_t 
  * rings, pos for linear caches), for bit-exact checks:
  *   codes  uint32 [n_slots][2][n_kv_heads][words]   (K = 0, V = 1; LE bit stream)
  *   meta   uint16 [n_slots][2][n_kv_heads][n_meta]  (affine: scale g, bias g
- *          interleaved, n_meta = 2*head_dim/64; codebook: norm, n_meta = 1)
- * n_slots = window for rings, capacity for linear caches. */
+ *          interleaved, n_meta = 2*head_dim/64; codebook: norm, n_meta = 1;
+ *          plain: n_meta = 0 and meta may be NULL)
+ * Plain caches: words = head_dim / 2, the bf16 row (dim 2w in the low half
+ * of word w). n_slots = window for rings, capacity for linear caches. */
 int fmkv_cache_read_codes(const fmkv_cache* cache, void* codes, void* meta, void* stream);
 
 /* ---------------------------------------------------------------------- */

@@ -368,14 +368,19 @@ class OracleCache:
         self.n_slots = window if window > 0 else capacity
         self.sgn = signs(head_dim, seed)
         self.words = (head_dim * bits + 31) // 32
-        self.n_meta = 2 * (head_dim // 64) if mode == 0 else 1
+        self.n_meta = 2 * (head_dim // 64) if mode == 0 else (1 if mode == 1 else 0)
         self.codes = np.zeros((self.n_slots, 2, self.H, self.words), np.uint32)
         self.meta = np.zeros((self.n_slots, 2, self.H, self.n_meta), np.uint16)
         self.offset = 0
         self.vis_begin = 0
 
     def quantize_rows(self, x_bf16):
-        """[..., D] bf16 rows -> (packed, meta [..., n_meta])."""
+        """[..., D] bf16 rows -> (packed, meta [..., n_meta]). Plain mode
+        (mode 2, src/cache.rs:274-288) stores the rows as given: the bf16 bits,
+        dim 2w in the low half of word w, and no meta."""
+        if self.mode == 2:
+            x = np.ascontiguousarray(np.asarray(x_bf16, np.uint16))
+            return x.view(np.uint32).copy(), np.zeros(x.shape[:-1] + (0,), np.uint16)
         if self.mode == 0:
             y = rotate_rows(x_bf16, self.sgn)
             packed, sc, bi = affine_quantize(y, self.bits)
@@ -405,6 +410,8 @@ class OracleCache:
                          theta: float) -> None:
         """append() of raw k_proj / v_proj rows through the layer's prologue
         (kv_prologue at the cache offset); v_bf16 None: a K==V layer."""
+        if self.mode != 0:
+            raise ValueError("the fused prologue is modelled for affine caches")
         k, v = kv_prologue(k_bf16, v_bf16, self.offset, w_bf16, eps, rope_dims, theta)
         kp, km = self.quantize_rows(k)
         vp, vm = self.quantize_rows_f32(v)
@@ -421,8 +428,15 @@ class OracleCache:
             self.codes[s, 1], self.meta[s, 1] = vp[i], vm[i]
         self.offset += n
 
+    def _plain_rows(self, packed) -> np.ndarray:
+        """f64 values of stored plain rows (packed bf16 words)."""
+        u = np.ascontiguousarray(packed).view(np.uint16)
+        return bf16_to_f32(u).astype(np.float64)
+
     def _dequant_rows(self, packed, meta) -> np.ndarray:
         """Un-rotated f64 rows of quantized rows (packed, meta)."""
+        if self.mode == 2:
+            return self._plain_rows(packed)
         if self.mode == 0:
             y = affine_dequantize(packed, np.ascontiguousarray(meta[..., 0::2]),
                                   np.ascontiguousarray(meta[..., 1::2]), self.D, self.bits)
@@ -474,7 +488,10 @@ class OracleCache:
         return pos % self.W if self.W > 0 else pos
 
     def rotated_kv(self, positions=None):
-        """Dequantized rotated-domain K, V (f64) [n, H, D] for positions."""
+        """Dequantized rotated-domain K, V (f64) [n, H, D] for positions
+        (quantized modes)."""
+        if self.mode == 2:
+            raise ValueError("a plain cache has no rotated domain")
         pos = self.visible_positions() if positions is None else np.asarray(positions)
         sl = self.slots_of(pos)
         out = []
@@ -490,7 +507,12 @@ class OracleCache:
         return out[0], out[1]
 
     def dequant_kv(self, positions=None):
-        """Dequantized, un-rotated K, V (f64) [n, H, D] in chronological order."""
+        """Dequantized, un-rotated K, V (f64) [n, H, D] in chronological order
+        (plain mode: the stored bf16 values)."""
+        if self.mode == 2:
+            pos = self.visible_positions() if positions is None else np.asarray(positions)
+            sl = self.slots_of(pos)
+            return self._plain_rows(self.codes[sl, 0]), self._plain_rows(self.codes[sl, 1])
         yk, yv = self.rotated_kv(positions)
         return unrotate_rows_f64(yk, self.sgn), unrotate_rows_f64(yv, self.sgn)
 

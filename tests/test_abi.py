@@ -39,6 +39,10 @@ def test_library_exports_header_symbols():
         (dict(n_kv_heads=8, head_dim=256, bits=4, capacity=1 << 31), fmkv.FMKV_ERR_INVALID_ARG),
         (dict(n_kv_heads=8, head_dim=256, bits=4, group_size=32, capacity=16), fmkv.FMKV_ERR_UNSUPPORTED),
         (dict(n_kv_heads=8, head_dim=256, bits=4, mode=7, capacity=16), fmkv.FMKV_ERR_UNSUPPORTED),
+        (dict(n_kv_heads=8, head_dim=256, bits=8, mode=fmkv.MODE_PLAIN, capacity=16),
+         fmkv.FMKV_ERR_UNSUPPORTED),
+        (dict(n_kv_heads=8, head_dim=96, bits=16, mode=fmkv.MODE_PLAIN, capacity=16),
+         fmkv.FMKV_ERR_UNSUPPORTED),
     ],
 )
 def test_invalid_descriptors_rejected_before_hip(kw, code):
@@ -56,7 +60,8 @@ def test_invalid_descriptors_rejected_before_hip(kw, code):
     "D,bits,mode,block",
     [(512, 8, 0, 16 * (2 * 512 + 8 * 4 * 2) // 2 * 1),  # 17408
      (256, 4, 0, 4608), (256, 8, 0, 8704), (512, 4, 0, 9216), (128, 4, 0, 2304),
-     (256, 3, 1, 3328), (512, 2, 1, 4352)],
+     (256, 3, 1, 3328), (512, 2, 1, 4352),
+     (128, 16, 2, 8192), (256, 16, 2, 16384), (512, 16, 2, 32768)],
 )
 def test_layout_bytes(D, bits, mode, block):
     if D == 512 and bits == 8:
@@ -93,4 +98,18 @@ def test_entry_points_reject_null_handles_before_hip():
                                         fmkv.DTYPE_BF16, None) == fmkv.FMKV_ERR_INVALID_ARG
     pro = fmkv.KvPrologue(None, 1e-6, 128, 1e4, 0)
     assert lib.fmkv_cache_append_projected(None, None, None, 1, pro, None) == fmkv.FMKV_ERR_INVALID_ARG
+    assert lib.fmkv_decode_step_projected(None, None, None, 1, pro, None, 8, 1.0, 0.0, None,
+                                          fmkv.DTYPE_BF16, None) == fmkv.FMKV_ERR_INVALID_ARG
     assert b"null" in lib.fmkv_last_error()
+
+
+def test_plain_descriptor_and_layout():
+    """Plain (bf16) caches: bits 16, no meta, K rows then V columns; a
+    head-block is 16 tokens x head_dim x 2 bytes x 2 (KVCacheInner::Plain,
+    src/cache.rs:174-178)."""
+    d = fmkv.make_desc(2, 512, 16, capacity=32768, mode=fmkv.MODE_PLAIN)
+    fmkv.validate(d)
+    b, a = fmkv.layout_bytes(d)
+    assert b == 16 * 512 * 2 * 2
+    assert a == 2 * 32768 * 512 * 2 * 2
+    assert fmkv.meta_per_row(d) == 0 and fmkv.words_per_row(d) == 256

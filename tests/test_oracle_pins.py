@@ -583,3 +583,34 @@ def test_prefill_equals_token_by_token_decode(ora, W, keep):
         assert np.allclose(got[i], want, rtol=1e-10, atol=1e-12), i
     assert np.array_equal(a.codes, b.codes) and np.array_equal(a.meta, b.meta)
     assert a.offset == b.offset
+
+
+# ------------------------------------------------------------ plain caches
+def test_oracle_plain_cache_stores_rows_as_given(ora):
+    """Plain mode (src/cache.rs:274-288: concatenate, then keep the last W on
+    a ring): the stored words are the input bf16 bits, dequant_kv returns the
+    rows in chronological order, and attention equals a numpy softmax over
+    the visible rows."""
+    rng = np.random.default_rng(12)
+    D, H, W = 128, 2, 32
+    c = ora.OracleCache(H, D, 16, W, 0, mode=2)
+    rows = []
+    for n in (5, 30, 1, 40):
+        k = synth.f32_to_bf16_bits(rng.standard_normal((n, H, D)).astype(np.float32))
+        v = synth.f32_to_bf16_bits(rng.standard_normal((n, H, D)).astype(np.float32))
+        c.append(k, v)
+        rows += list(zip(k, v))
+    assert c.meta.shape[-1] == 0 and c.words == D // 2
+    pos = c.visible_positions()
+    assert list(pos) == list(range(76 - W, 76))
+    k_all = np.stack([r[0] for r in rows])
+    v_all = np.stack([r[1] for r in rows])
+    slot = pos[0] % W
+    assert np.array_equal(c.codes[slot, 0].view(np.uint16), k_all[pos[0]])
+    kf, vf = c.dequant_kv()
+    want_k = ora.bf16_to_f32(k_all[pos]).astype(np.float64)
+    want_v = ora.bf16_to_f32(v_all[pos]).astype(np.float64)
+    assert np.array_equal(kf, want_k) and np.array_equal(vf, want_v)
+    q = synth.f32_to_bf16_bits(rng.standard_normal((4, D)).astype(np.float32))
+    qf = ora.bf16_to_f32(q).astype(np.float64)
+    assert np.allclose(c.attention(q, 0.1), np_attention(qf, want_k, want_v, 0.1, 0.0), atol=1e-12)
