@@ -554,6 +554,74 @@ def run_prefill(args) -> dict:
     }
 
 
+def run_append(args) -> dict:
+    """The global layer's chunked prefill store at the C3 shape: 2048-token
+    chunks of K and V rows (Hkv 2, head_dim 512, 8-bit) appended into a
+    32K cache -- rotate, quantize, write (src/cache.rs:266-310) -- and the
+    same chunks as raw K projections through the K==V layer prologue
+    (src/model/gemma4_attention.rs:52-81). One step = one chunk; the append
+    kernel's duration comes from HIP events recorded by its own dispatches."""
+    import torch
+
+    import fmkv
+    import synth
+
+    Hkv, D, bits, chunk = 2, 512, 8, 2048
+    n_chunks = max(1, args.context // chunk)
+    per_tok = bytes_per_token_head(D, bits)
+    k = dev_bf16(synth.kv_rows(31, chunk, Hkv, D, None, dist="t3"))
+    v = dev_bf16(synth.kv_rows(32, chunk, Hkv, D, None))
+    rng = np.random.default_rng(33)
+    w = dev_bf16(synth.f32_to_bf16_bits((1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)))
+    pro = fmkv.make_prologue(w, 1e-6, 128, 1e6, v_from_k=True)
+    # algorithmic bytes per chunk: bf16 K and V rows in, codes + scale/bias out
+    in_bytes = {"plain": 2 * chunk * Hkv * D * 2, "prologue_k_eq_v": chunk * Hkv * D * 2}
+    out_bytes = chunk * Hkv * per_tok
+    res_rows = {}
+    for kind in ("plain", "prologue_k_eq_v"):
+        cache = fmkv.KVCache.new_quantized(D, bits, Hkv, capacity=n_chunks * chunk)
+
+        def step():
+            if kind == "plain":
+                cache.append(k, v)
+            else:
+                cache.append_projected(k, None, pro)
+
+        for _ in range(min(args.warmup, n_chunks)):  # untimed, into a cache dropped after
+            step()
+        cache = fmkv.KVCache.new_quantized(D, bits, Hkv, capacity=n_chunks * chunk)
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(n_chunks):
+            step()
+        ev1.record()
+        torch.cuda.synchronize()
+        us = ev0.elapsed_time(ev1) * 1e3 / n_chunks
+        res_rows[kind] = {"us_per_chunk": round(us, 3), "tokens_per_s": round(chunk / (us * 1e-6), 1),
+                          "algorithmic_GBps": round((in_bytes[kind] + out_bytes) / (us * 1e-6) / 1e9, 1)}
+        log(f"append {kind}: {us:.2f} us per {chunk}-token chunk (stream time), "
+            f"{chunk / us:.1f} M tokens/s")
+    main = res_rows["plain"]
+    achieved = main["algorithmic_GBps"]
+    return {
+        "metric": "append tokens/s (2048-token chunked prefill into the quantized cache)",
+        "value": main["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": n_chunks,
+        "warmup": args.warmup, "ms_per_step": round(main["us_per_chunk"] / 1e3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
+        "data": "synthetic (seeded SplitMix64: K Student-t(3), V N(0,1))",
+        "config": {"workload": "gemma4-global-layer chunked prefill store: 2048-token chunks, Hkv 2, "
+                               "head_dim 512, 8-bit group-64 affine, into a 32K cache",
+                   "chunk": chunk, "n_kv_heads": Hkv, "head_dim": D, "bits": bits},
+        "append": res_rows,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "append_kernel<512, 8, 0, false>",
+                     "bytes_per_launch": in_bytes["plain"] + out_bytes,
+                     "note": "stream time per chunk (launch gaps included)"},
+    }
+
+
 def run_c5(args) -> dict:
     """Decode-step cache traffic of a 30-layer Gemma-4-26B-A4B-shaped stack:
     25 sliding layers (ring of 1024, Hkv 8, head_dim 256, 4-bit) and 5 global
@@ -803,10 +871,11 @@ def main(argv=None) -> int:
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 8 device-to-device copies of MIB MiB (the reference kernel "
                          "for scaling HBM byte counters) and exit")
-    ap.add_argument("--workload", choices=["c3", "c2", "c4", "c5", "prefill"], default="c3",
+    ap.add_argument("--workload", choices=["c3", "c2", "c4", "c5", "prefill", "append"], default="c3",
                     help="c3 (default): global layer at 32K; c2: sliding ring, 8192 steps; "
                          "c4: 32 ragged paged sequences; c5: 30-layer stack; prefill: "
-                         "2048-token chunked-prefill attention after --context tokens")
+                         "2048-token chunked-prefill attention after --context tokens; append: "
+                         "the C3 chunked-prefill store alone")
     ap.add_argument("--prefill-sliding", action="store_true",
                     help="prefill workload on the sliding-layer shape (ring W 1024)")
     ap.add_argument("--c5-context", type=int, default=131072)
@@ -837,7 +906,7 @@ def main(argv=None) -> int:
 
         fmkv.set_blocks_per_split(args.bps)
     res = {"c3": run_c3, "c2": run_c2, "c4": run_c4, "c5": run_c5,
-           "prefill": run_prefill}[args.workload](args)
+           "prefill": run_prefill, "append": run_append}[args.workload](args)
     print(json.dumps(res), flush=True)
     return 0
 

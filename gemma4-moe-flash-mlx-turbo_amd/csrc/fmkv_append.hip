@@ -25,7 +25,14 @@
 namespace fmkv {
 namespace {
 
-constexpr int kAppendThreads = 512;
+#ifndef FMKV_APPEND_ROWS
+#define FMKV_APPEND_ROWS 2
+#endif
+// Rows per wave: each half (K, V) of a work-group's 16 tokens takes 16 / R
+// waves, so a 2048-token chunk of two KV heads runs 4096 waves at R = 2
+// (four per SIMD), whose latencies (lane exchanges, divisions) overlap.
+constexpr int kAppendRows = FMKV_APPEND_ROWS;
+constexpr int kAppendThreads = 2 * (16 / kAppendRows) * 64;
 
 __constant__ float kCbBounds2[3] = {-0.982f, 0.0f, 0.982f};
 __constant__ float kCbBounds3[7] = {-1.748f, -1.050f, -0.501f, 0.0f, 0.501f, 1.050f, 1.748f};
@@ -65,17 +72,18 @@ __device__ inline uint32_t v_clear_mask(int w, const int* cov) {
   return m;
 }
 
-// One work-group per (touched head-block, KV head, sequence), 8 waves: wave
-// w handles the K (w < 4) or V (w >= 4) rows of the four tokens 4q..4q+3,
-// q = w & 3, all four rows in lockstep (independent chains for the
-// scheduler). Codes are combined in registers (the elements of one K word;
-// the four tokens that share a V word) before one LDS atomic per word; the
-// block is then copied out with 16-byte stores. PRO: the layer's prologue
-// (k_norm + RoPE on K, v_norm on V) runs on the rows first.
+// One work-group per (touched head-block, KV head, sequence), 2 x 16 / R
+// waves: wave w handles the K (w < 16 / R) or V rows of the R tokens
+// R q .. R q + R - 1, q = w mod 16 / R, all R rows in lockstep (independent
+// chains for the scheduler). Codes are combined in registers (the elements
+// of one K word; the wave's tokens of a V word) before one LDS atomic per
+// word; the block is then copied out with 16-byte stores. PRO: the layer's
+// prologue (k_norm + RoPE on K, v_norm on V) runs on the rows first.
 template <int D, int BITS, int MODE, bool PRO>
 __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
   constexpr int E = D / 64;
-  constexpr int R = 4;  // rows per wave
+  constexpr int R = kAppendRows;  // rows per wave
+  constexpr int NWH = 16 / R;      // waves per half (K or V)
   constexpr BlockLayout L = make_layout(D, BITS, MODE);
   constexpr int kWords = (int)(L.code_bytes / 4);
   constexpr int kHalfMax = PRO ? D / 2 : 1;
@@ -83,11 +91,11 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
   __shared__ __align__(16) uint32_t vst[kWords];
   __shared__ int cov_row[kBlockTokens];
   __shared__ float rope_f[kHalfMax];              // f32 theta^(-2i/rope_dims)
-  __shared__ float2 rope_cs[R][R][kHalfMax];      // per K wave: (cos, sin) per row, angle
+  __shared__ float2 rope_cs[NWH][R][kHalfMax];    // per K wave: (cos, sin) per row, angle
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int isv = wv >> 2, quad = wv & 3;
+  const int isv = wv / NWH, quad = wv % NWH;
   const int h = blockIdx.y, seq = blockIdx.z, bx = blockIdx.x;
   const int64_t pos0 = a.start_pos ? (int64_t)a.start_pos[seq] : a.start_scalar;
   const int64_t end = pos0 + a.n_new;
@@ -135,13 +143,13 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
   // the wave's four rows (rows not written here re-read row 0, unused)
   const int H = a.st.n_kv_heads;
   int rows[R];
-  bool any = false, all4 = true;
+  bool any = false, allr = true;
   float x[R][E];
 #pragma unroll
   for (int r = 0; r < R; r++) {
     rows[r] = row_of(quad * R + r);
     any = any || rows[r] >= 0;
-    all4 = all4 && rows[r] >= 0;
+    allr = allr && rows[r] >= 0;
     const int row = rows[r] < 0 ? 0 : rows[r];
     const uint16_t* src = (isv && !a.v_from_k ? a.v : a.k) +
                           (((int64_t)seq * a.n_new + row) * H + h) * D + lane * E;
@@ -283,7 +291,8 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
           }
         }
       } else {
-        // the four tokens of the quad share each V word
+        // the tokens of a quad 4q .. 4q+3 share each V word; this wave's
+        // R of them are or-ed in here
 #pragma unroll
         for (int i = 0; i < E; i++) {
           int64_t off = 0;
@@ -301,8 +310,13 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
         const int g = lane / (64 / E);
         uint32_t* mp = reinterpret_cast<uint32_t*>(blk + (isv ? L.v_meta : L.k_meta) +
                                                    scale_pos(g, quad * R));
-        if (all4) {
-          *reinterpret_cast<uint4*>(mp) = make_uint4(meta[0], meta[1], meta[2], meta[3]);
+        if (allr) {
+          if constexpr (R == 4)
+            *reinterpret_cast<uint4*>(mp) = make_uint4(meta[0], meta[1], meta[2], meta[3]);
+          else if constexpr (R == 2)
+            *reinterpret_cast<uint2*>(mp) = make_uint2(meta[0], meta[1]);
+          else
+            mp[0] = meta[0];
         } else {
 #pragma unroll
           for (int r = 0; r < R; r++)
