@@ -109,11 +109,11 @@ int device_cus() {
   return cus;
 }
 
-// Decode work-groups per CU the split plan aims at: the affine kernel's LDS
-// staging fills a CU; the codebook and plain kernels' work-groups are about
+// Decode work-groups per CU the split plan aims at: the affine and codebook
+// kernels' LDS staging fills a CU; the plain kernel's work-groups are about
 // half as large (two per CU).
 int attn_wg_per_cu(const fmkv_cache_desc& d) {
-  return d.mode == FMKV_MODE_AFFINE ? fmkv::kAttnWgPerCu : 2;
+  return d.mode == FMKV_MODE_PLAIN ? 2 : fmkv::kAttnWgPerCu;
 }
 
 // Split-K plan: blocks per split such that the grid has about `wg_per_cu`

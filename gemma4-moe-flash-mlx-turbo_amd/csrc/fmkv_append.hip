@@ -178,7 +178,18 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
       // covered tokens' halves are overwritten below
       vst[w] = all_cov ? 0u : reinterpret_cast<const uint32_t*>(blk + L.v_codes)[w];
     } else {
-      vst[w] = 0u;
+      // codebook: a word may hold bits of several tokens; the covered tokens'
+      // bits are cleared and set below, the others keep the stored ones
+      uint32_t keep_k = 0u, keep_v = 0u;
+      if (!all_cov) {
+        for (int k = 0; k < 32; k++) {
+          const int64_t bit = (int64_t)w * 32 + k;
+          if (cov_row[cb_k_token_of_bit(D, BITS, bit)] < 0) keep_k |= 1u << k;
+          if (cov_row[cb_v_token_of_bit(BITS, bit)] < 0) keep_v |= 1u << k;
+        }
+      }
+      kst[w] = keep_k ? reinterpret_cast<const uint32_t*>(blk + L.k_codes)[w] & keep_k : 0u;
+      vst[w] = keep_v ? reinterpret_cast<const uint32_t*>(blk + L.v_codes)[w] & keep_v : 0u;
     }
   }
 
@@ -324,20 +335,31 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
         }
       }
     } else {
-      // token row = bit stream, index j at bit j * bits: the lane's E
-      // indices are E * bits consecutive bits
-      constexpr int64_t row_bits = (int64_t)D * BITS;
+      // K: the lane's E indices are E * bits consecutive bits of the token's
+      // half row; V: each index goes to its dim's token run (fmkv_layout.h)
 #pragma unroll
       for (int r = 0; r < R; r++) {
         if (rows[r] < 0) continue;
-        uint64_t v = 0;
+        const int t = quad * R + r;
+        if (!isv) {
+          uint64_t v = 0;
 #pragma unroll
-        for (int i = 0; i < E; i++) v |= (uint64_t)code[r][i] << (i * BITS);
-        const int64_t bit = (quad * R + r) * row_bits + (int64_t)lane * E * BITS;
-        const int wi = (int)(bit >> 5), off = (int)(bit & 31);
-        v <<= off;
-        atomicOr(&stage[wi], (uint32_t)v);
-        if (off + E * BITS > 32) atomicOr(&stage[wi + 1], (uint32_t)(v >> 32));
+          for (int i = 0; i < E; i++) v |= (uint64_t)code[r][i] << (i * BITS);
+          const int64_t bit = cb_k_bit(D, BITS, t, lane * E);
+          const int wi = (int)(bit >> 5), off = (int)(bit & 31);
+          v <<= off;
+          atomicOr(&stage[wi], (uint32_t)v);
+          if (off + E * BITS > 32) atomicOr(&stage[wi + 1], (uint32_t)(v >> 32));
+        } else {
+#pragma unroll
+          for (int i = 0; i < E; i++) {
+            const int64_t bit = cb_v_bit(BITS, t, lane * E + i);
+            const int wi = (int)(bit >> 5), off = (int)(bit & 31);
+            const uint64_t v = (uint64_t)code[r][i] << off;
+            atomicOr(&stage[wi], (uint32_t)v);
+            if (off + BITS > 32) atomicOr(&stage[wi + 1], (uint32_t)(v >> 32));
+          }
+        }
         if (lane == 0)
           *reinterpret_cast<uint16_t*>(blk + (isv ? L.v_meta : L.k_meta) + (quad * R + r) * 2) =
               (uint16_t)meta[r];
@@ -346,8 +368,8 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
   }
   __syncthreads();
 
-  // 16-byte copy-out; K (and codebook V) chunks belong to one token each,
-  // affine and plain V chunks are whole (merged with the stored block above)
+  // 16-byte copy-out; affine K chunks belong to one token each, the other
+  // regions are whole (merged with the stored block above)
   uint4* kdst = reinterpret_cast<uint4*>(blk + L.k_codes);
   uint4* vdst = reinterpret_cast<uint4*>(blk + L.v_codes);
   const uint4* ks = reinterpret_cast<const uint4*>(kst);
@@ -361,8 +383,9 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
       tk = (int)((int64_t)c * 16 / (L.code_bytes / kBlockTokens));
       vdst[c] = vs[c];
     } else {
-      tk = (int)((int64_t)c * 16 / (L.code_bytes / kBlockTokens));
-      if (cov_row[tk] >= 0) vdst[c] = vs[c];
+      kdst[c] = ks[c];
+      vdst[c] = vs[c];
+      continue;
     }
     if (cov_row[tk] >= 0) kdst[c] = ks[c];
   }

@@ -105,10 +105,15 @@ struct AttnPlan {
   static constexpr int GH = NG / kWPS;  // groups per wave
   static constexpr int kCodeChunks = (int)(L.code_bytes / kChunk);  // per K or V region
   // code chunks a wave copies per region: its groups' chunks (at 4 bits one
-  // chunk holds two groups; at head_dim 128 both waves copy the one chunk)
+  // chunk holds two groups)
   static constexpr int kWaveChunks = BITS == 8 ? GH : (GH >= 2 ? GH / 2 : 1);
+  // head_dim 128 at 4 bits: the pair's two groups share the block's one
+  // chunk, and each wave keeps its own copy of it in the stage, so that a
+  // wave refilling a stage never overwrites a chunk its partner still reads
+  static constexpr bool kSharedChunk = !kSolo && BITS == 4 && GH == 1;
+  static constexpr int kCodeSlots = kSharedChunk ? 2 : kCodeChunks;  // chunk slots per region
   static constexpr int kMetaHalf = GH * 64;  // one wave's K (or V) scale/bias bytes
-  static constexpr int kMetaOff = 2 * kCodeChunks * kChunk;
+  static constexpr int kMetaOff = 2 * kCodeSlots * kChunk;
   static constexpr int kStageBytes = kMetaOff + 2 * kWPS * kMetaHalf;
   static constexpr int kCopies = 2 * kWaveChunks + 1;  // copy instructions per wave per block
   static constexpr int kFit = ((kSolo ? 144 : 136) * 1024) / (kStreams * kStageBytes);
@@ -474,7 +479,8 @@ void decode_attn_kernel(AttnArgs a) {
   // This wave's part of block lb into stage st: its groups' K and V code
   // chunks, then one partial instruction moving its groups' K and V
   // scale/bias (lanes < 4 GH: K, the next 4 GH: V) to its meta area.
-  const int kc0 = BITS == 8 ? g0 : (GH >= 2 ? g0 / 2 : 0);  // first code chunk
+  const int kc0 = BITS == 8 ? g0 : (GH >= 2 ? g0 / 2 : 0);  // first code chunk in HBM
+  const int ks0 = P::kSharedChunk ? half : kc0;               // its first chunk slot
   const int mlane = lane < 4 * GH ? lane : lane - 4 * GH;
   const int meta_voff = (lane < 4 * GH ? (int)L.k_meta : (int)L.v_meta) + g0 * 64 + mlane * 16;
   auto copy_block = [&](int st, int64_t lb) {
@@ -483,10 +489,10 @@ void decode_attn_kernel(AttnArgs a) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of this stage are done
 #pragma unroll
     for (int k = 0; k < P::kWaveChunks; k++) {
-      const int ch = kc0 + k;
-      dma16(sl + (int)L.k_codes + ch * kChunk, (int)L.k_codes + ch * kChunk + lane * 16, rs);
+      const int ch = kc0 + k, slot = ks0 + k;
+      dma16(sl + slot * kChunk, (int)L.k_codes + ch * kChunk + lane * 16, rs);
       if constexpr (MODE != kStats)
-        dma16(sl + (int)L.v_codes + ch * kChunk, (int)L.v_codes + ch * kChunk + lane * 16, rs);
+        dma16(sl + (P::kCodeSlots + slot) * kChunk, (int)L.v_codes + ch * kChunk + lane * 16, rs);
     }
     if (lane < 8 * GH) dma16(sl + P::kMetaOff + half * 2 * MH, meta_voff, rs);
   };
@@ -576,9 +582,11 @@ void decode_attn_kernel(AttnArgs a) {
 
   // LDS operands, read one group ahead of their use so that the read
   // latency overlaps the previous group's MFMAs
+  // region 0: K codes, 1: V codes
   auto codes = [&](const uint8_t* sp, int region, int gi) {
     const int g = g0 + gi;
-    return lds16(sp + region + (BITS == 8 ? g : g / 2) * kChunk + lane * 16);
+    const int slot = P::kSharedChunk ? half : (BITS == 8 ? g : g / 2);
+    return lds16(sp + (region * P::kCodeSlots + slot) * kChunk + lane * 16);
   };
   auto kmeta = [&](const uint8_t* sp, int gi) {
     return lds16(sp + P::kMetaOff + half * 2 * MH + gi * 64 + j * 16);
@@ -592,12 +600,12 @@ void decode_attn_kernel(AttnArgs a) {
     float4_t sv = (float4_t){0.f, 0.f, 0.f, 0.f};
     // (pair waves keep each group's MFMA chain in program order; a solo
     // wave's four independent groups interleave, 2% faster on 4-bit D=256)
-    u32x4 kw = codes(sp, (int)L.k_codes, 0), km = kmeta(sp, 0);
+    u32x4 kw = codes(sp, 0, 0), km = kmeta(sp, 0);
 #pragma unroll
     for (int gi = 0; gi < GH; gi++) {
       const u32x4 kw_g = kw, km_g = km;
       if (gi + 1 < GH) {
-        if (BITS == 8 || ((g0 + gi + 1) & 1) == 0) kw = codes(sp, (int)L.k_codes, gi + 1);
+        if (BITS == 8 || ((g0 + gi + 1) & 1) == 0) kw = codes(sp, 0, gi + 1);
         km = kmeta(sp, gi + 1);
       }
       const int g = g0 + gi;
@@ -611,7 +619,7 @@ void decode_attn_kernel(AttnArgs a) {
     }
     u32x4 vw, vm;
     if constexpr (MODE != kStats) {
-      vw = codes(sp, (int)L.v_codes, 0);  // in flight during the softmax
+      vw = codes(sp, 1, 0);  // in flight during the softmax
       vm = vmeta(sp, 0);
     }
 
@@ -697,7 +705,7 @@ void decode_attn_kernel(AttnArgs a) {
     for (int gi = 0; gi < GH; gi++) {
       const u32x4 vw_g = vw, vm_g = vm;
       if (gi + 1 < GH) {
-        if (BITS == 8 || ((g0 + gi + 1) & 1) == 0) vw = codes(sp, (int)L.v_codes, gi + 1);
+        if (BITS == 8 || ((g0 + gi + 1) & 1) == 0) vw = codes(sp, 1, gi + 1);
         vm = vmeta(sp, gi + 1);
       }
       float x[4];

@@ -10,21 +10,34 @@
 //   out     = (sum_t w_t (norm_t / sqrt D) centroid[idx_t]) . R^T.
 // The cache is read as stored, with no bf16 round trip.
 //
-// One work-group of four waves per (KV head, sequence, split of consecutive
-// 16-token blocks). Per block the waves:
-//  1. dequantize the block from its LDS copy into f16 matrix-core operand
-//     tiles of centroid high and residual parts (a product then keeps ~22
-//     bits of the centroid; one f16 alone is off by up to 2^-12 of the
-//     value), V laid out for v_mfma_f32_16x16x16f16 with the tokens as the
-//     reduction dimension;
-//  2. compute S^T = K . q_rot^T on v_mfma_f32_16x16x32_f16, each wave a
-//     quarter of head_dim, summed through LDS in a fixed order;
-//  3. run the same base-2 online softmax as the affine kernel;
-//  4. accumulate O^T += V^T . P'^T with P' = p * norm / sqrt D split into f16
-//     high and residual columns, each wave a quarter of head_dim.
-// The block's raw bytes for the next block are loaded into registers while
-// the current one is processed. The epilogue applies R^T and writes the final
-// output (one split) or a split partial for the shared combine kernel.
+// One work-group = one (split of consecutive 16-token blocks, KV head,
+// sequence) with four wave pairs, as in the affine kernel: pair p streams the
+// head-blocks b_begin + p, b_begin + p + 4, ...; wave h of a pair owns half h
+// of head_dim, which the layout keeps contiguous for K and V alike
+// (fmkv_layout.h), copies that half of each block HBM -> LDS with
+// buffer_load_dwordx4 ... lds several stages ahead, exchanges its partial
+// scores with its partner through LDS and runs the same online softmax.
+//
+// Dequantization happens in registers on the way to the matrix cores: an LDS
+// table holds, for every pair of indices (two dims of a K row, or two tokens
+// of a V dim), the two centroids as f16 high parts and as f16 residuals
+// (cent - high), so one 8-byte lookup yields both operands' words for two
+// elements (4-bit codes: one 4-byte lookup per element, paired by v_perm). The
+// table is replicated 32 times, entry e of copy l at (e * 32 + l) * 8, so the
+// lanes of a half-wave never hit one bank twice. Per block, per 32-dim slice
+// and per 16-dim tile of the wave's half:
+//   QK   S^T[16 tok x 16 col] += K[16 x 32] . Q^T[32 x 16]
+//        (v_mfma_f32_16x16x32_f16), once with the high and once with the
+//        residual parts of the centroids (a product then keeps ~22 bits of
+//        the centroid; one f16 alone is off by up to 2^-12 of the value).
+//        Column c = q head c & 7, c < 8 the f16 high part of q_rot and
+//        c >= 8 its residual; the columns fold with DPP row_ror:8.
+//   PV   O^T[16 dim x 16 col] += V^T[16 dim x 16 tok] . P'^T[16 tok x 16 col]
+//        (v_mfma_f32_16x16x16f16, high and residual centroid parts), with
+//        P' = p * norm_t / sqrt D split hi/lo in the same columns.
+// Epilogue: the pairs' (m, l, O) merge in LDS, the inverse rotation
+// o . R^T = c * FWHT(o o s) follows, and the result is the final output (one
+// split) or a split partial for the shared combine kernel.
 #include <hip/hip_ext.h>
 
 #include "fmkv_device.h"
@@ -41,70 +54,164 @@ __constant__ float kCbCent4[16] = {-2.733f, -2.069f, -1.618f, -1.256f, -0.942f, 
                                    -0.388f, -0.128f, 0.128f,  0.388f,  0.657f,  0.942f,
                                    1.256f,  1.618f,  2.069f,  2.733f};
 
-constexpr int kCbWaves = 4;
-constexpr int kCbThreads = kCbWaves * 64;
+constexpr int kCbWaves = 8;  // four wave pairs, two waves per SIMD
+constexpr int kCbStreams = kCbWaves / 2;
+constexpr int kLutCopies = 32;
 
 template <int D, int BITS>
 struct CbPlan {
   static constexpr BlockLayout L = make_layout(D, BITS, kCodebook);
-  static constexpr int kRow = D * BITS / 8;               // code bytes of one token row
-  static constexpr int kSlices = D / 32;                  // QK MFMAs (32 dims each)
-  static constexpr int kTiles = D / 16;                   // PV column tiles (16 dims each)
-  static constexpr int kRawChunks = (int)(L.block_bytes / 16);  // the whole head-block
-  static constexpr int kLoads = (kRawChunks + kCbThreads - 1) / kCbThreads;  // 16-B loads per thread
-  static_assert(kSlices % kCbWaves == 0 && kTiles % kCbWaves == 0, "head_dim split over four waves");
-  static constexpr int kSlicesW = kSlices / kCbWaves;
-  static constexpr int kTilesW = kTiles / kCbWaves;
-  // LDS: q operand table (later the V residual tile), K high / residual
-  // tiles, V high tile, raw block, score exchange
-  static constexpr int kQTab = kSlices * 1024;
-  static constexpr int kKTile = kSlices * 1024;
-  static constexpr int kVTile = kTiles * 512;
-  static_assert(kVTile <= kQTab, "the V residual tile reuses the q table");
-  static constexpr int kXch = kCbWaves * 64 * 16;
+  static constexpr int kHalfBytes = D * BITS;  // one half of K (or V) codes: 16 x D/2 x BITS bits
+  static constexpr int kHalfPieces = kHalfBytes / 16;
+  static constexpr int kHalfCopies = (kHalfPieces + 63) / 64;  // copy instructions per half
+  static constexpr int kNSW = D / 64;                        // 32-dim QK slices per wave
+  static constexpr int kNTW = D / 32;                        // 16-dim PV tiles per wave
+  // a stage: [K half 0][K half 1][V half 0][V half 1][wave 0 norms][wave 1 norms],
+  // codes at their head-block offsets; a wave's norms are K then V (32 B each)
+  static constexpr int kNormOff = 4 * kHalfBytes;
+  static constexpr int kStageBytes = kNormOff + 2 * 64;
+  static constexpr int kCopies = 2 * kHalfCopies + 1;  // per wave per block
+  // index pairs (2 and 3 bits; 16 or 64 entries of 8 bytes) or single
+  // indices (4 bits; 16 entries of 4 bytes)
+  static constexpr bool kPairs = BITS <= 3;
+  static constexpr int kLutEntries = kPairs ? (1 << (2 * BITS)) : 16;
+  static constexpr int kLutStride = kPairs ? 8 : 4;
+  static constexpr int kLutBytes = kLutEntries * kLutCopies * kLutStride;
+  // q table (the QK B operands, one KiB per slice), then the score exchange
+  static constexpr int kTabBytes = (D / 32) * 1024;
+  static constexpr int kXBytes = kCbWaves * 2 * 64 * 16;
+  static constexpr int kScratch = cmax(cmax(kTabBytes, kXBytes), 8 * D * 2);
+  static constexpr int kQS = D + 4;  // merge-row stride (floats)
+  static constexpr int kFit =
+      (160 * 1024 - 2048 - kLutBytes - kScratch) / (kCbStreams * kStageBytes);
+  static constexpr int kStagesA = kFit > 8 ? 8 : kFit;
+  static constexpr int kStages = kStagesA * kCopies <= 63 ? kStagesA : 63 / kCopies;
+  static constexpr int kStageRegion = kCbStreams * kStages * kStageBytes;
+  static_assert(kHalfBytes % 16 == 0, "halves are whole copy pieces");
+  static_assert(kStages >= 2, "two stages per stream fit");
+  static_assert(8 * kQS * 4 <= kStages * kStageBytes, "merge rows fit in a stream's stages");
 };
 
-// Codes of 8 consecutive dims of one row: bits [bit0, bit0 + 8 BITS) of the
-// row's little-endian bit stream (index j at bit j * BITS), row 4-byte
-// aligned in LDS.
-template <int BITS>
-__device__ inline uint64_t codes8(const uint8_t* row, int bit0) {
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(row) + (bit0 >> 5);
-  uint64_t v = (uint64_t)w[0];
-  if ((bit0 & 31) + 8 * BITS > 32) v |= (uint64_t)w[1] << 32;
-  return v >> (bit0 & 31);
+// The raw bf16 q row of GQA head `wave` to LDS at dst + wave * D * 2, copied
+// by that wave (lanes < D / 8).
+template <int D>
+__device__ inline void cb_copy_q_row(const AttnArgs& a, uint8_t* dst, int seq, int kvh, int wave,
+                                     int lane) {
+  if (wave < a.group && lane < D / 8) {
+    const uint16_t* qh =
+        a.q + ((int64_t)seq * a.n_q_heads + (int64_t)kvh * a.group + wave) * D;
+    dma16(lds_addr(dst + wave * D * 2), lane * 16, buffer_rsrc(qh, (uint32_t)(D * 2)));
+  }
 }
 
-// The code of one dim (bits [bit, bit + BITS) of a row's bit stream).
+// q_rot = (FWHT(q * qscale) * c) o s of head `wave` (every wave whose raw
+// row has landed), written over the raw rows as the QK B operands: slice k
+// (dims 32k .. 32k + 31) at k KiB, lane (jj, c) = (lane / 16, lane % 16):
+// 8 f16 of head c & 7, dims 32k + 8jj .. + 7 -- the f16 high part of q_rot
+// for c < 8, the residual for c >= 8, zero past the group. Every thread of
+// the work-group calls it (it holds two barriers).
+template <int D>
+__device__ void cb_build_q_table(const AttnArgs& a, uint8_t* tab, int wave, int lane,
+                                 uint32_t sbits) {
+  constexpr int E = D / 64;
+  float x[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) x[i] = 0.0f;
+  if (wave < a.group) {
+    const uint32_t* raw = reinterpret_cast<const uint32_t*>(tab + (wave * D + lane * E) * 2);
+#pragma unroll
+    for (int k = 0; k < E / 2; k++) {
+      const uint32_t w = raw[k];
+      x[2 * k] = __uint_as_float(w << 16) * a.qscale;
+      x[2 * k + 1] = __uint_as_float(w & 0xffff0000u) * a.qscale;
+    }
+    wave_fwht_signed<E>(x, lane);
+    const float cs = fwht_lane_sign(lane) * a.c;
+#pragma unroll
+    for (int i = 0; i < E; i++) x[i] = apply_sign(x[i] * cs, sbits, i);
+  }
+  _Float16 hv[E], lv[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) {
+    hv[i] = (_Float16)x[i];
+    lv[i] = (_Float16)(x[i] - (float)hv[i]);
+  }
+  __syncthreads();  // every raw row is read before the table replaces them
+  if (wave < 8) {
+    const int d0 = lane * E, k = d0 >> 5, jj = (d0 & 31) >> 3, i0 = d0 & 7;
+    uint8_t* ent = tab + k * 1024 + i0 * 2;
+    store_halves<E>(ent + (jj * 16 + wave) * 16, hv);
+    store_halves<E>(ent + (jj * 16 + wave + 8) * 16, lv);
+  }
+  __syncthreads();
+}
+
+// Centroid i as {f16 high part, f16 residual}.
 template <int BITS>
-__device__ inline uint32_t code1(const uint8_t* row, int bit) {
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(row) + (bit >> 5);
-  uint32_t v = w[0] >> (bit & 31);
-  if ((bit & 31) + BITS > 32) v |= w[1] << (32 - (bit & 31));
-  return v & ((1u << BITS) - 1u);
+__device__ inline uint32_t cent_hl(int i) {
+  const float cv = BITS == 2 ? kCbCent2[i] : BITS == 3 ? kCbCent3[i] : kCbCent4[i];
+  const _Float16 h = (_Float16)cv;
+  const _Float16 r = (_Float16)(cv - (float)h);
+  return (uint32_t)__builtin_bit_cast(uint16_t, h) | ((uint32_t)__builtin_bit_cast(uint16_t, r) << 16);
+}
+
+// The 32 bits from bit offset `bit` on of an LDS region (4-byte aligned;
+// the word after the first one is read too, and lies inside the LDS
+// staging: the K halves are followed by the V halves, the V halves by the
+// norms).
+__device__ inline uint32_t lds_bits(const uint8_t* region, int bit) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(region) + (bit >> 5);
+  return __builtin_amdgcn_alignbit(w[1], w[0], (uint32_t)(bit & 31));
+}
+
+// High and residual f16 operand words of two consecutive elements of a
+// field (the field's elements 2p and 2p + 1, element e at bits e * BITS).
+template <int BITS>
+__device__ inline void cb_pair(const uint8_t* lut, uint32_t field, int p, int lut_lane,
+                               uint32_t& hw, uint32_t& lw) {
+  if constexpr (BITS <= 3) {
+    const uint32_t idx = (field >> (2 * p * BITS)) & ((1u << (2 * BITS)) - 1u);
+    const uint2 e = *reinterpret_cast<const uint2*>(lut + (idx * kLutCopies + lut_lane) * 8);
+    hw = e.x;
+    lw = e.y;
+  } else {
+    const uint32_t i0 = (field >> (8 * p)) & 15u, i1 = (field >> (8 * p + 4)) & 15u;
+    const uint32_t e0 = *reinterpret_cast<const uint32_t*>(lut + (i0 * kLutCopies + lut_lane) * 4);
+    const uint32_t e1 = *reinterpret_cast<const uint32_t*>(lut + (i1 * kLutCopies + lut_lane) * 4);
+    hw = __builtin_amdgcn_perm(e1, e0, 0x05040100u);  // the high parts
+    lw = __builtin_amdgcn_perm(e1, e0, 0x07060302u);  // the residuals
+  }
 }
 
 template <int D, int BITS>
-__global__ __launch_bounds__(kCbThreads) void cb_decode_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kCbWaves * 64)
+__attribute__((amdgpu_waves_per_eu(2, 2)))
+void cb_decode_kernel(AttnArgs a) {
   using P = CbPlan<D, BITS>;
   constexpr BlockLayout L = P::L;
-  constexpr int E = D / 64;  // dims per lane in a row-wise (FWHT) layout
-  constexpr int NC = 1 << BITS;
-  __shared__ __align__(16) uint8_t qtab[P::kQTab];
-  __shared__ __align__(16) uint8_t khi[P::kKTile];
-  __shared__ __align__(16) uint8_t klo[P::kKTile];
-  __shared__ __align__(16) uint8_t vt[P::kVTile];
-  uint8_t* const vlo = qtab;  // once each wave holds its q operands
-  __shared__ __align__(16) uint8_t raw[P::kLoads * kCbThreads * 16];
-  __shared__ __align__(16) float4_t xch[kCbWaves][64];
-  __shared__ uint32_t lut[NC];  // centroid as {f16 high, f16 residual}
-  __shared__ float ml_s[8][2];
+  constexpr int E = D / 64;
+  constexpr int NSW = P::kNSW, NTW = P::kNTW;
+  constexpr int NST = P::kStages, SB = P::kStageBytes, CP = P::kCopies;
+  constexpr int HB = P::kHalfBytes;
+  constexpr int QS = P::kQS;
+  constexpr int NS = kCbStreams;
+
+  __shared__ __align__(16) uint8_t stage[P::kStageRegion];
+  __shared__ __align__(16) uint8_t scratch[P::kScratch];  // q rows, q table, then score exchange
+  __shared__ __align__(16) uint8_t lut[P::kLutBytes];
+  __shared__ float ml_s[NS][8][2];
+  __shared__ int xflag[kCbWaves];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int j = lane >> 4, c = lane & 15, head = c & 7;
-  const bool hi_col = c < 8;
+  const int stream = wave >> 1, half = wave & 1;
+  const int j = lane >> 4, c = lane & 15;
+  const int head = c & 7;
+  const bool hi = c < 8;
   const int G = a.group;
+  const bool col_valid = head < G;
+  const int lut_lane = lane & (kLutCopies - 1);
+  // grid (KV head, sequence, split column), as the affine kernel
   const int kvh = blockIdx.x, seq = blockIdx.y, split = blockIdx.z;
 
   const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
@@ -115,10 +222,14 @@ __global__ __launch_bounds__(kCbThreads) void cb_decode_kernel(AttnArgs a) {
   const int64_t b_begin = geo.blk_lo + (split == 0 ? 0 : a.bps0 + (int64_t)(split - 1) * a.bps);
   int64_t b_end = b_begin + (split == 0 ? a.bps0 : a.bps);
   if (b_end > geo.blk_hi) b_end = geo.blk_hi;
-  const int nb = (int)(b_end - b_begin);
 
-  const int32_t* table =
-      a.st.block_table ? a.st.block_table + (int64_t)seq * a.st.table_stride : nullptr;
+  // table entries through the constant address space: a uniform index then
+  // becomes a scalar load, which never waits for the copies in flight
+  typedef const int32_t __attribute__((address_space(4)))* table_ptr;
+  const table_ptr table =
+      a.st.block_table
+          ? (table_ptr)(uintptr_t)(a.st.block_table + (int64_t)seq * a.st.table_stride)
+          : nullptr;
   const uint8_t* hbase = a.st.base + (int64_t)kvh * a.st.head_stride;
   auto blk_ptr = [&](int64_t lb) -> const uint8_t* {
     int64_t phys = table ? (int64_t)table[lb] : lb;
@@ -126,71 +237,67 @@ __global__ __launch_bounds__(kCbThreads) void cb_decode_kernel(AttnArgs a) {
     phys = phys < 0 ? 0 : (phys >= a.st.n_blocks ? a.st.n_blocks - 1 : phys);
     return hbase + phys * a.st.block_stride;
   };
-  // the raw block in 16-byte pieces, kLoads per thread (past the block: zero)
-  u32x4 pre[P::kLoads];
-  auto load_raw = [&](int64_t lb) {
-    const uint8_t* p = blk_ptr(lb);
-#pragma unroll
-    for (int k = 0; k < P::kLoads; k++) {
-      const int ch = k * kCbThreads + tid;
-      pre[k] = ch * 16 < (int)L.block_bytes ? *reinterpret_cast<const u32x4*>(p + ch * 16)
-                                            : (u32x4){0u, 0u, 0u, 0u};
-    }
-  };
-  auto store_raw = [&]() {
-#pragma unroll
-    for (int k = 0; k < P::kLoads; k++)
-      *reinterpret_cast<u32x4*>(raw + (k * kCbThreads + tid) * 16) = pre[k];
-  };
-  if (nb > 0) load_raw(b_begin);
 
-  // ---- prologue: centroid table, q_rot as QK B operands ----
-  if (tid < NC) {
-    const float cv = BITS == 2 ? kCbCent2[tid] : BITS == 3 ? kCbCent3[tid] : kCbCent4[tid];
-    const _Float16 h = (_Float16)cv;
-    const _Float16 r = (_Float16)(cv - (float)h);
-    lut[tid] = (uint32_t)__builtin_bit_cast(uint16_t, h) |
-               ((uint32_t)__builtin_bit_cast(uint16_t, r) << 16);
+  const int64_t pb0 = b_begin + stream;
+  const int nb = pb0 < b_end ? (int)((b_end - pb0 + NS - 1) / NS) : 0;
+  uint8_t* const pstage = stage + stream * NST * SB;
+  const uint32_t pstage_lds = lds_addr(pstage);
+
+  // This wave's half of block lb into stage st: its K half, its V half, and
+  // with one partial instruction (lanes 0..3) the block's K and V norms.
+  auto copy_block = [&](int st, int64_t lb) {
+    const u32x4 rs = buffer_rsrc(blk_ptr(lb), (uint32_t)L.block_bytes);
+    const uint32_t sl = pstage_lds + st * SB;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of this stage are done
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int off = (int)(r == 0 ? L.k_codes : L.v_codes) + half * HB;
+#pragma unroll
+      for (int k = 0; k < P::kHalfCopies; k++) {
+        if (P::kHalfPieces % 64 == 0 || k * 64 + lane < P::kHalfPieces)
+          dma16(sl + off + k * 1024, off + k * 1024 + lane * 16, rs);
+      }
+    }
+    if (lane < 4)
+      dma16(sl + P::kNormOff + half * 64, (int)(lane < 2 ? L.k_meta : L.v_meta) + (lane & 1) * 16, rs);
+  };
+
+  // ---- prologue: LUT, copies, q table ----
+  for (int e = tid; e < P::kLutEntries * kLutCopies; e += kCbWaves * 64) {
+    const int idx = e / kLutCopies;
+    if constexpr (P::kPairs) {
+      const uint32_t c0 = cent_hl<BITS>(idx & ((1 << BITS) - 1)), c1 = cent_hl<BITS>(idx >> BITS);
+      *reinterpret_cast<uint2*>(lut + e * 8) =
+          make_uint2((c0 & 0xffffu) | (c1 << 16), (c0 >> 16) | (c1 & 0xffff0000u));
+    } else {
+      *reinterpret_cast<uint32_t*>(lut + e * 4) = cent_hl<BITS>(idx);
+    }
   }
+  if (lane == 0) xflag[wave] = 0;
+  constexpr int NQ = (NST + 1) / 2;
+  cb_copy_q_row<D>(a, scratch, seq, kvh, wave, lane);
+#pragma unroll
+  for (int s = 0; s < NQ; s++)
+    if (s < nb) copy_block(s, pb0 + (int64_t)NS * s);
+  wait_copies<CP, NQ>(nb < NQ ? nb : NQ);  // the q copy preceded every block
   const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
-  // wave w rotates q heads w and w + 4: q_rot = (FWHT(q * qscale) * c) o s;
-  // lane l holds dims l E .. l E + E - 1, which in the operand table are
-  // slice k = l E / 32, k-group (l E % 32) / 8, element (l E) % 8
+  cb_build_q_table<D>(a, scratch, wave, lane, sbits);
 #pragma unroll
-  for (int r = 0; r < 2; r++) {
-    const int h = wave + 4 * r;
-    float x[E];
+  for (int s = NQ; s < NST; s++)
+    if (s < nb) copy_block(s, pb0 + (int64_t)NS * s);
+  half8_t bq[NSW];
 #pragma unroll
-    for (int i = 0; i < E; i++) x[i] = 0.0f;
-    if (h < G) {
-      const uint16_t* qh = a.q + ((int64_t)seq * a.n_q_heads + (int64_t)kvh * G + h) * D + lane * E;
-      load_row<E>(qh, x);
-#pragma unroll
-      for (int i = 0; i < E; i++) x[i] *= a.qscale;
-      wave_fwht_signed<E>(x, lane);
-      const float cs = fwht_lane_sign(lane) * a.c;
-#pragma unroll
-      for (int i = 0; i < E; i++) x[i] = apply_sign(x[i] * cs, sbits, i);
-    }
-    _Float16 hv[E], lv[E];
-#pragma unroll
-    for (int i = 0; i < E; i++) {
-      hv[i] = (_Float16)x[i];
-      lv[i] = (_Float16)(x[i] - (float)hv[i]);
-    }
-    const int d0 = lane * E, k = d0 >> 5, jj = (d0 & 31) >> 3, i0 = d0 & 7;
-    uint8_t* ent = qtab + k * 1024 + i0 * 2;
-    store_halves<E>(ent + (jj * 16 + h) * 16, hv);
-    store_halves<E>(ent + (jj * 16 + h + 8) * 16, lv);
-  }
+  for (int s = 0; s < NSW; s++)
+    bq[s] = *reinterpret_cast<const half8_t*>(scratch + (half * NSW + s) * 1024 + lane * 16);
+  __syncthreads();  // the table is consumed: the region becomes the score exchange
+  float4_t* const xs = reinterpret_cast<float4_t*>(scratch);  // [wave][parity][lane]
 
-  __syncthreads();
-  // this wave's B operands (its quarter of head_dim); the table's memory then
-  // holds the V residual tile
-  half8_t bq[P::kSlicesW];
+  float4_t o[NTW];
 #pragma unroll
-  for (int s = 0; s < P::kSlicesW; s++)
-    bq[s] = *reinterpret_cast<const half8_t*>(qtab + (wave * P::kSlicesW + s) * 1024 + lane * 16);
+  for (int i = 0; i < NTW; i++) o[i] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  float m_run = -1e30f, l_run = 0.0f;
+  const float lo_sel = hi ? 0.0f : 1.0f;
+  const float inv_sd = a.c;  // 1 / sqrt(D): the codebook's value scale
 
   // visible slots: linear [vis_lo, vis_hi); ring [0, min(T, W)), unless a
   // trim hides older positions (then each slot's position is computed)
@@ -198,102 +305,69 @@ __global__ __launch_bounds__(kCbThreads) void cb_decode_kernel(AttnArgs a) {
   const int64_t vis_hi = a.window > 0 ? (T < a.window ? T : a.window) : T;
   const bool ring_trim = a.window > 0 && a.vis_begin > T - a.window;
 
-  float4_t o[P::kTilesW];
-#pragma unroll
-  for (int i = 0; i < P::kTilesW; i++) o[i] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  float m_run = -1e30f, l_run = 0.0f;
-  const float lo_sel = hi_col ? 0.0f : 1.0f;
-  const float inv_sd = a.c;  // 1 / sqrt(D): the codebook's value scale
+  // this lane's fields: QK slice s, token t = c of the MFMA A rows:
+  // 8 indices at bit (t D/2 + 32 s + 8 j) BITS of the K half;
+  // PV tile n, dim 16 n + c, tokens 4 j .. 4 j + 3: 4 indices at bit
+  // ((16 n + c) 16 + 4 j) BITS of the V half
+  const int kbit0 = (c * (D / 2) + 8 * j) * BITS;
+  const int vbit0 = (c * 16 + 4 * j) * BITS;
 
-  for (int i = 0; i < nb; i++) {
-    const int64_t b = b_begin + i;
-    __syncthreads();  // the tiles of the previous block are consumed (and the table written)
-    store_raw();
-    if (i + 1 < nb) load_raw(b + 1);
-    __syncthreads();
-
-    // -- dequantize: K tiles (slice k, lane (jj, t): dims 32k + 8jj .. + 7 of
-    // token t) and the V tile (column tile ct, lane (q, n): dim 16ct + n of
-    // tokens 4q .. 4q + 3, as 4 halves) --
-    const uint8_t* kraw = raw + L.k_codes;
-    const uint8_t* vraw = raw + L.v_codes;
-#pragma unroll
-    for (int it = 0; it < P::kSlices * 64 / kCbThreads; it++) {
-      const int item = it * kCbThreads + tid;
-      const int k = item >> 6, ln = item & 63, jj = ln >> 4, t = ln & 15;
-      const uint64_t cw = codes8<BITS>(kraw + t * P::kRow, (32 * k + 8 * jj) * BITS);
-      uint32_t hw[4], lw[4];
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const uint32_t a0 = lut[(cw >> (2 * e * BITS)) & (NC - 1)];
-        const uint32_t a1 = lut[(cw >> ((2 * e + 1) * BITS)) & (NC - 1)];
-        hw[e] = (a0 & 0xffffu) | (a1 << 16);
-        lw[e] = (a0 >> 16) | (a1 & 0xffff0000u);
-      }
-      *reinterpret_cast<u32x4*>(khi + k * 1024 + ln * 16) = (u32x4){hw[0], hw[1], hw[2], hw[3]};
-      *reinterpret_cast<u32x4*>(klo + k * 1024 + ln * 16) = (u32x4){lw[0], lw[1], lw[2], lw[3]};
-    }
-#pragma unroll
-    for (int it = 0; it < P::kTiles * 64 / kCbThreads; it++) {
-      const int item = it * kCbThreads + tid;
-      const int ct = item >> 6, ln = item & 63, q4 = ln >> 4, n = ln & 15;
-      const int d = ct * 16 + n;
-      uint32_t h4[2], l4[2];
-#pragma unroll
-      for (int r = 0; r < 4; r += 2) {
-        const uint8_t* r0 = vraw + (4 * q4 + r) * P::kRow;
-        const uint32_t a0 = lut[code1<BITS>(r0, d * BITS)];
-        const uint32_t a1 = lut[code1<BITS>(r0 + P::kRow, d * BITS)];
-        h4[r >> 1] = (a0 & 0xffffu) | (a1 << 16);
-        l4[r >> 1] = (a0 >> 16) | (a1 & 0xffff0000u);
-      }
-      *reinterpret_cast<uint2*>(vt + ct * 512 + ln * 8) = make_uint2(h4[0], h4[1]);
-      *reinterpret_cast<uint2*>(vlo + ct * 512 + ln * 8) = make_uint2(l4[0], l4[1]);
-    }
-    __syncthreads();
-
-    // -- S^T over this wave's quarter of head_dim, summed over the waves --
+  auto process = [&](const uint8_t* sp, int64_t b, int it) {
+    const uint8_t* kh = sp + (int)L.k_codes + half * HB;
+    const uint8_t* vh = sp + (int)L.v_codes + half * HB;
+    // this half's S^T = K . q_rot^T (high + residual centroid parts)
     float4_t acc = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < P::kSlicesW; s++) {
-      const int k = wave * P::kSlicesW + s;
-      const half8_t ah = *reinterpret_cast<const half8_t*>(khi + k * 1024 + lane * 16);
-      const half8_t al = *reinterpret_cast<const half8_t*>(klo + k * 1024 + lane * 16);
+    for (int s = 0; s < NSW; s++) {
+      const uint32_t f = lds_bits(kh, kbit0 + 32 * s * BITS);
+      uint32_t h4[4], l4[4];
+#pragma unroll
+      for (int p = 0; p < 4; p++) cb_pair<BITS>(lut, f, p, lut_lane, h4[p], l4[p]);
+      const half8_t ah = __builtin_bit_cast(half8_t, (u32x4){h4[0], h4[1], h4[2], h4[3]});
+      const half8_t al = __builtin_bit_cast(half8_t, (u32x4){l4[0], l4[1], l4[2], l4[3]});
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[s], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq[s], acc, 0, 0, 0);
     }
-    xch[wave][lane] = acc;
-    __syncthreads();
-    float4_t st = xch[0][lane];
-#pragma unroll
-    for (int w = 1; w < kCbWaves; w++) st += xch[w][lane];
-    // per-token value scale norm / sqrt D (f16 norms follow the codes)
-    const uint2 kn = *reinterpret_cast<const uint2*>(raw + L.k_meta + 8 * j);
-    const uint2 vn = *reinterpret_cast<const uint2*>(raw + L.v_meta + 8 * j);
+    // the tokens' norms: lane (j, c) holds tokens 4j .. 4j + 3
+    const uint2 kn = *reinterpret_cast<const uint2*>(sp + P::kNormOff + half * 64 + 8 * j);
+    const uint2 vn = *reinterpret_cast<const uint2*>(sp + P::kNormOff + half * 64 + 32 + 8 * j);
+
+    // exchange the half scores with the partner wave (release orders the
+    // data before the flag); both waves add the halves in the same order
+    const int par = it & 1;
+    xs[(wave * 2 + par) * 64 + lane] = acc;
+    __hip_atomic_store(&xflag[wave], it + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    while (__hip_atomic_load(&xflag[wave ^ 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+           it + 1)
+      __builtin_amdgcn_s_sleep(1);
+    const float4_t other = xs[((wave ^ 1) * 2 + par) * 64 + lane];
+    const float4_t s0 = half == 0 ? acc : other;
+    const float4_t s1 = half == 0 ? other : acc;
     const float kscale[4] = {lo16(kn.x) * inv_sd, hi16(kn.x) * inv_sd, lo16(kn.y) * inv_sd,
                              hi16(kn.y) * inv_sd};
     const float vscale[4] = {lo16(vn.x) * inv_sd, hi16(vn.x) * inv_sd, lo16(vn.y) * inv_sd,
                              hi16(vn.y) * inv_sd};
-    float s4[4];
+    float sc[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const float tv = st[r] + row_ror8(st[r]);  // high + residual columns of q
-      s4[r] = (G > head) ? tv * kscale[r] : -INFINITY;
+    for (int i = 0; i < 4; i++) {
+      const float t = s0[i] + s1[i];
+      sc[i] = col_valid ? (t + row_ror8(t)) * kscale[i] : -INFINITY;
     }
     // visibility: whole block in the common case, per token at the edges
     const int64_t t0 = b * kBlockTokens;
     const bool full = t0 >= vis_lo && t0 + kBlockTokens <= vis_hi && !ring_trim;
     if (!full) {
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int64_t slot = t0 + 4 * j + r;
+      for (int i = 0; i < 4; i++) {
+        const int64_t slot = t0 + 4 * j + i;
         bool vis = slot >= vis_lo && slot < vis_hi;
         if (ring_trim) vis = vis && slot_position(slot, T, a.window) >= a.vis_begin;
-        if (!vis) s4[r] = -INFINITY;
+        if (!vis) sc[i] = -INFINITY;
       }
     }
-    // -- online softmax in base 2 (as the affine kernel) --
-    float mb = fmaxf(fmaxf(s4[0], s4[1]), fmaxf(s4[2], s4[3]));
+    // online softmax in base 2 (the affine kernel's rule: the reference max
+    // moves only on jumps above kRescaleSlack)
+    float mb = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
     mb = xor16_max(mb);
     mb = xor32_max(mb);
     const float m_new = fmaxf(m_run, mb);
@@ -301,85 +375,121 @@ __global__ __launch_bounds__(kCbThreads) void cb_decode_kernel(AttnArgs a) {
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       if (__any(l_run > 0.0f)) {
 #pragma unroll
-        for (int tI = 0; tI < P::kTilesW; tI++) o[tI] *= alpha;
+        for (int i = 0; i < NTW; i++) o[i] *= alpha;
       }
       l_run *= alpha;
       m_run = m_new;
     }
     float p[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++) p[r] = __builtin_amdgcn_exp2f(s4[r] - m_run);
+    for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(sc[i] - m_run);
     l_run += (p[0] + p[1]) + (p[2] + p[3]);
-    // -- O^T += V^T . P'^T, P' = p * norm / sqrt D as f16 high / residual columns --
+
+    // O^T += V^T . P'^T, P' = p * norm / sqrt D as f16 high (c < 8) and
+    // residual (c >= 8) columns
     float x[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++) x[r] = p[r] * vscale[r];
+    for (int i = 0; i < 4; i++) x[i] = p[i] * vscale[i];
     const half2_t h01 = pkrtz(x[0], x[1]);
     const half2_t h23 = pkrtz(x[2], x[3]);
     const half2_t b01 = pkrtz(fmaf(-lo_sel, (float)h01[0], x[0]), fmaf(-lo_sel, (float)h01[1], x[1]));
     const half2_t b23 = pkrtz(fmaf(-lo_sel, (float)h23[0], x[2]), fmaf(-lo_sel, (float)h23[1], x[3]));
     const half4_t bp = cat4(b01, b23);
 #pragma unroll
-    for (int tI = 0; tI < P::kTilesW; tI++) {
-      const int ct = wave * P::kTilesW + tI;
-      const half4_t av = *reinterpret_cast<const half4_t*>(vt + ct * 512 + lane * 8);
-      const half4_t al = *reinterpret_cast<const half4_t*>(vlo + ct * 512 + lane * 8);
-      o[tI] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bp, o[tI], 0, 0, 0);
-      o[tI] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bp, o[tI], 0, 0, 0);
+    for (int n = 0; n < NTW; n++) {
+      const uint32_t f = lds_bits(vh, vbit0 + 256 * n * BITS);
+      uint32_t h2[2], l2[2];
+#pragma unroll
+      for (int q = 0; q < 2; q++) cb_pair<BITS>(lut, f, q, lut_lane, h2[q], l2[q]);
+      const half4_t ah = __builtin_bit_cast(half4_t, make_uint2(h2[0], h2[1]));
+      const half4_t al = __builtin_bit_cast(half4_t, make_uint2(l2[0], l2[1]));
+      o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bp, o[n], 0, 0, 0);
+      o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bp, o[n], 0, 0, 0);
     }
+  };
+
+  // stage st holds block i; before reading it, wait until only the copies
+  // issued after it (the next min(NST - 1, nb - 1 - i) blocks) are pending;
+  // once read, the stage is refilled with block i + NST
+  int st = 0;
+  for (int i = 0; i < nb; i++) {
+    const int rest = nb - 1 - i;
+    wait_copies<CP, NST - 1>(rest < NST - 1 ? rest : NST - 1);
+    process(pstage + st * SB, pb0 + (int64_t)NS * i, i);
+    if (i + NST < nb) copy_block(st, pb0 + (int64_t)NS * (i + NST));
+    st = st + 1 == NST ? 0 : st + 1;
   }
 
-  // ---- epilogue: rows [head][D] in LDS, inverse rotation, store ----
+  // ---- epilogue: merge the four pairs, inverse rotation, store ----
   l_run = xor16_sum(l_run);
   l_run = xor32_sum(l_run);
-  __syncthreads();  // every wave is done with the tiles
-  float* rows = reinterpret_cast<float*>(khi);  // [8][D] f32
-  static_assert(P::kKTile >= 8 * D * 4, "epilogue rows fit in the K tile");
+  // fold the residual columns (c >= 8) into the high-part columns (c < 8)
 #pragma unroll
-  for (int tI = 0; tI < P::kTilesW; tI++)
+  for (int n = 0; n < NTW; n++)
 #pragma unroll
-    for (int r = 0; r < 4; r++) o[tI][r] = o[tI][r] + row_ror8(o[tI][r]);
-  if (hi_col) {
+    for (int i = 0; i < 4; i++) o[n][i] = o[n][i] + row_ror8(o[n][i]);
+  // the stream's own stages become its merge rows [head][QS] once both of
+  // its waves are done with them
+  __hip_atomic_store(&xflag[wave], nb + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  while (__hip_atomic_load(&xflag[wave ^ 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+         nb + 1)
+    __builtin_amdgcn_s_sleep(1);
+  float* const Rp = reinterpret_cast<float*>(pstage);
+  if (hi && col_valid) {
 #pragma unroll
-    for (int tI = 0; tI < P::kTilesW; tI++) {
-      const int ct = wave * P::kTilesW + tI;
-      *reinterpret_cast<float4_t*>(&rows[head * D + ct * 16 + 4 * j]) = o[tI];
+    for (int n = 0; n < NTW; n++) {
+      const int d = half * (D / 2) + n * 16 + 4 * j;
+      *reinterpret_cast<float4_t*>(&Rp[head * QS + d]) = o[n];
     }
-    // every wave holds the same softmax state; wave 0 publishes it per head
-    if (wave == 0 && j == 0) {
-      ml_s[head][0] = m_run;
-      ml_s[head][1] = l_run;
+    if (half == 0 && j == 0) {
+      ml_s[stream][head][0] = m_run;
+      ml_s[stream][head][1] = l_run;
     }
   }
-  __syncthreads();
-  const int64_t qh0 = (int64_t)seq * a.n_q_heads + (int64_t)kvh * G;
+  __syncthreads();  // every stream's rows are written
+
+  if (wave < G) {  // head w on wave w
+    const int hh = wave;
+    float M = ml_s[0][hh][0];
 #pragma unroll
-  for (int r = 0; r < 2; r++) {
-    const int hh = wave + 4 * r;
-    if (hh >= G) continue;
+    for (int q = 1; q < NS; q++) M = fmaxf(M, ml_s[q][hh][0]);
+    float wgt[NS], Lsum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NS; q++) {
+      wgt[q] = __builtin_amdgcn_exp2f(ml_s[q][hh][0] - M);
+      Lsum = fmaf(wgt[q], ml_s[q][hh][1], Lsum);
+    }
     float x[E];
 #pragma unroll
-    for (int i = 0; i < E; i++) x[i] = apply_sign(rows[hh * D + lane * E + i], sbits, i);
+    for (int i = 0; i < E; i++) {
+      float v = 0.0f;
+#pragma unroll
+      for (int q = 0; q < NS; q++)
+        v = fmaf(wgt[q], reinterpret_cast<const float*>(stage + q * NST * SB)[hh * QS + lane * E + i],
+                 v);
+      x[i] = apply_sign(v, sbits, i);
+    }
     wave_fwht_signed<E>(x, lane);
     const float cs = fwht_lane_sign(lane) * a.c;
-    const float Mh = ml_s[hh][0], Lh = ml_s[hh][1];
+    const int64_t qh0 = (int64_t)seq * a.n_q_heads + (int64_t)kvh * G;
     if (a.direct) {
       const int64_t o_idx = (qh0 + hh) * D + lane * E;
 #pragma unroll
       for (int i = 0; i < E; i++) {
-        const float v = Lh > 0.0f ? (x[i] * cs) / Lh : 0.0f;
+        const float v = Lsum > 0.0f ? (x[i] * cs) / Lsum : 0.0f;
         if (a.out_f32)
           reinterpret_cast<float*>(a.out)[o_idx + i] = v;
         else
           reinterpret_cast<uint16_t*>(a.out)[o_idx + i] = f32_to_bf16(v);
       }
     } else {
-      const int64_t pb = ((int64_t)seq * a.part_stride + split) * a.n_q_heads + (int64_t)kvh * G + hh;
+      const int64_t pbase = ((int64_t)seq * a.part_stride + split) * a.n_q_heads + (int64_t)kvh * G;
+      float* dst = a.part_o + (pbase + hh) * D + lane * E;
 #pragma unroll
-      for (int i = 0; i < E; i++) a.part_o[pb * D + lane * E + i] = x[i] * cs;
+      for (int i = 0; i < E; i++) dst[i] = x[i] * cs;
       if (lane == 0) {
-        a.part_ml[pb * 2 + 0] = Mh;
-        a.part_ml[pb * 2 + 1] = Lh;
+        a.part_ml[(pbase + hh) * 2 + 0] = M;
+        a.part_ml[(pbase + hh) * 2 + 1] = Lsum;
       }
     }
   }
@@ -390,9 +500,9 @@ hipError_t launch_cb_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_
                        hipEvent_t ev1) {
   dim3 grid(n_kv_heads, n_seqs, a.max_splits);
   if (ev0 && ev1)
-    hipExtLaunchKernelGGL((cb_decode_kernel<D, BITS>), grid, dim3(kCbThreads), 0, s, ev0, ev1, 0, a);
+    hipExtLaunchKernelGGL((cb_decode_kernel<D, BITS>), grid, dim3(kCbWaves * 64), 0, s, ev0, ev1, 0, a);
   else
-    hipLaunchKernelGGL((cb_decode_kernel<D, BITS>), grid, dim3(kCbThreads), 0, s, a);
+    hipLaunchKernelGGL((cb_decode_kernel<D, BITS>), grid, dim3(kCbWaves * 64), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.direct) return e;
   return launch_combine(a, n_seqs, s);

@@ -27,9 +27,18 @@
 //  Scale/bias: per group g, 16 tokens x {f16 scale, f16 bias} = 64 bytes;
 //    the four tokens 4q..4q+3 of a group are one 16-byte load.
 //
-// Codebook mode (TurboQuant indices, 2/3/4 bits) stores each token's row as a
-// little-endian bit stream (index j at bit j*bits), plus one f16 L2 norm per
-// token row.
+// Codebook mode (TurboQuant indices, 2/3/4 bits, index of dim d of token t
+// written idx(t, d)) keeps bit streams (little-endian: bit i of the stream is
+// bit i & 7 of byte i >> 3) laid out for the decode kernel, whose wave pairs
+// each own one half of head_dim:
+//  K codes: two halves of D*bits bytes, half h holding dims h*D/2 .. h*D/2 +
+//    D/2 - 1; in it token t's D/2 indices follow each other: idx(t, d) at bit
+//    (t*D/2 + d - h*D/2) * bits. Eight consecutive dims of a token are
+//    8*bits consecutive bits (one matrix-core operand).
+//  V codes: dim-major, idx(t, d) at bit (d*16 + t) * bits, so the tokens of
+//    one dim are consecutive (four of them are one operand) and each half of
+//    head_dim is one contiguous range of D*bits bytes.
+//  One f16 L2 norm per token row, for K and for V.
 //
 // Plain mode (unquantized bf16, bits = 16) keeps K token-major -- row t is
 // head_dim bf16 at t * head_dim * 2 -- and V dim-major -- dim d holds the 16
@@ -126,8 +135,20 @@ FMKV_HD int64_t scale_pos(int g, int t) { return (int64_t)(g * kBlockTokens + t)
 FMKV_HD int64_t plain_k_pos(int head_dim, int t, int d) { return ((int64_t)t * head_dim + d) * 2; }
 FMKV_HD int64_t plain_v_pos(int t, int d) { return ((int64_t)d * kBlockTokens + t) * 2; }
 
-// Codebook mode: byte offset of token t's row and of its norm.
-FMKV_HD int64_t cb_row_bytes(int head_dim, int bits) { return (int64_t)head_dim * bits / 8; }
+// Codebook mode: bit offsets of idx(t, d) in the K and V code regions.
+FMKV_HD int64_t cb_k_bit(int head_dim, int bits, int t, int d) {
+  const int hd = head_dim / 2, h = d >= hd ? 1 : 0;
+  return ((int64_t)h * kBlockTokens * hd + (int64_t)t * hd + (d - h * hd)) * bits;
+}
+FMKV_HD int64_t cb_v_bit(int bits, int t, int d) { return ((int64_t)d * kBlockTokens + t) * bits; }
+// Codebook mode: the token owning bit `bit` of the K or V code region.
+FMKV_HD int cb_k_token_of_bit(int head_dim, int bits, int64_t bit) {
+  const int64_t half_bits = (int64_t)kBlockTokens * (head_dim / 2) * bits;
+  return (int)((bit % half_bits) / ((int64_t)(head_dim / 2) * bits));
+}
+FMKV_HD int cb_v_token_of_bit(int bits, int64_t bit) {
+  return (int)((bit % ((int64_t)kBlockTokens * bits)) / bits);
+}
 
 // Position held by `slot` after `offset` appends (ring of `window` slots, or
 // linear when window == 0); -1 when the slot is empty.

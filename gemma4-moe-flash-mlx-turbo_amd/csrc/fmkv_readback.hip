@@ -46,9 +46,8 @@ __device__ inline uint32_t stored_code(const uint8_t* blk, const BlockLayout& L,
     const uint32_t w = *reinterpret_cast<const uint32_t*>(blk + (isv ? L.v_codes : L.k_codes) + off);
     return (w >> sh) & ((1u << L.bits) - 1u);
   }
-  const uint32_t* row = reinterpret_cast<const uint32_t*>(blk + (isv ? L.v_codes : L.k_codes) +
-                                                          t * cb_row_bytes(L.head_dim, L.bits));
-  return get_bits(row, (int64_t)d * L.bits, L.bits);
+  const uint32_t* region = reinterpret_cast<const uint32_t*>(blk + (isv ? L.v_codes : L.k_codes));
+  return get_bits(region, isv ? cb_v_bit(L.bits, t, d) : cb_k_bit(L.head_dim, L.bits, t, d), L.bits);
 }
 
 // One thread per canonical output word; grid.x over slots, grid.y = K/V x heads.
