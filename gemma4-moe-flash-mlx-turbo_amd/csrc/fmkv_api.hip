@@ -345,6 +345,7 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   a->qscale = scale * 1.4426950408889634f;
   std::memcpy(a->sign_bits, o->sign_bits, sizeof(a->sign_bits));
   a->c = o->c;
+  a->sqrt_d = o->sqrt_d;
   if (nblk < 1) nblk = 1;
   // one sequence: the new-token column takes CUs of its own; many sequences:
   // the dispatcher fills CUs as work-groups finish
@@ -755,7 +756,7 @@ int decode_step_impl(fmkv_cache* c, const void* k, const void* v, int64_t n, con
   if (pro) set_prologue(pro, &ap);
   // one new token: the attention launch appends it itself (new-token
   // column); sparse-V attention runs after a separate append
-  const int fused = n == 1 && tau == 0.0f && c->desc.mode == FMKV_MODE_AFFINE ? 1 : 0;
+  const int fused = n == 1 && tau == 0.0f && c->desc.mode != FMKV_MODE_PLAIN ? 1 : 0;
   fmkv::AttnArgs at;
   rc = prepare_attention(c, c->offset + n, q, n_q_heads, scale, tau, out, out_dtype, fused, &at, ext);
   if (rc) return rc;
@@ -1021,7 +1022,7 @@ int paged_decode_step_impl(fmkv_pool* p, const void* k, const void* v,
   if (pro) set_prologue(pro, &ap);
   // one new token per sequence: the attention launch appends it itself, at
   // position seq_lens[s] - 1 (= start_pos[s])
-  const int fused = n_new == 1 && tau == 0.0f && p->desc.mode == FMKV_MODE_AFFINE ? 1 : 0;
+  const int fused = n_new == 1 && tau == 0.0f && p->desc.mode != FMKV_MODE_PLAIN ? 1 : 0;
   fmkv::AttnArgs at;
   rc = prepare_paged_attention(p, q, block_tables, max_blocks, seq_lens, n_seqs, max_seq_len,
                                n_q_heads, scale, tau, out, out_dtype, fused, &at);

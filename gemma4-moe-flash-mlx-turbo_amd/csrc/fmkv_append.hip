@@ -34,27 +34,6 @@ namespace {
 constexpr int kAppendRows = FMKV_APPEND_ROWS;
 constexpr int kAppendThreads = 2 * (16 / kAppendRows) * 64;
 
-__constant__ float kCbBounds2[3] = {-0.982f, 0.0f, 0.982f};
-__constant__ float kCbBounds3[7] = {-1.748f, -1.050f, -0.501f, 0.0f, 0.501f, 1.050f, 1.748f};
-__constant__ float kCbBounds4[15] = {-2.401f, -1.844f, -1.437f, -1.099f, -0.800f,
-                                     -0.522f, -0.258f, 0.0f,    0.258f,  0.522f,
-                                     0.800f,  1.099f,  1.437f,  1.844f,  2.401f};
-
-__device__ inline int cb_index(float z, int bits) {
-  int idx = 0;
-  if (bits == 2) {
-#pragma unroll
-    for (int b = 0; b < 3; b++) idx += (z >= kCbBounds2[b]) ? 1 : 0;
-  } else if (bits == 3) {
-#pragma unroll
-    for (int b = 0; b < 7; b++) idx += (z >= kCbBounds3[b]) ? 1 : 0;
-  } else {
-#pragma unroll
-    for (int b = 0; b < 15; b++) idx += (z >= kCbBounds4[b]) ? 1 : 0;
-  }
-  return idx;
-}
-
 // Token owning 32-bit word w of an affine V-code region, for byte/nibble k.
 template <int BITS>
 __device__ inline uint32_t v_clear_mask(int w, const int* cov) {

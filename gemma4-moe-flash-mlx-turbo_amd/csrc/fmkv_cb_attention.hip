@@ -20,11 +20,13 @@
 //
 // Dequantization happens in registers on the way to the matrix cores: an LDS
 // table holds, for every pair of indices (two dims of a K row, or two tokens
-// of a V dim), the two centroids as f16 high parts and as f16 residuals
-// (cent - high), so one 8-byte lookup yields both operands' words for two
-// elements (4-bit codes: one 4-byte lookup per element, paired by v_perm). The
-// table is replicated 32 times, entry e of copy l at (e * 32 + l) * 8, so the
-// lanes of a half-wave never hit one bank twice. Per block, per 32-dim slice
+// of a V dim), the two centroids' f16 high parts as one word and, in a second
+// table at a fixed offset, their f16 residuals (cent - high), so two 4-byte
+// lookups at one address give the high and residual operand words of two
+// elements straight into the operand registers (4-bit codes: one lookup of
+// {high, residual} per element, paired by v_perm). Each table is replicated
+// 32 times, entry e of copy l at (e * 32 + l) * 4, so the lanes of a
+// half-wave never hit one bank twice. Per block, per 32-dim slice
 // and per 16-dim tile of the wave's half:
 //   QK   S^T[16 tok x 16 col] += K[16 x 32] . Q^T[32 x 16]
 //        (v_mfma_f32_16x16x32_f16), once with the high and once with the
@@ -38,10 +40,17 @@
 // Epilogue: the pairs' (m, l, O) merge in LDS, the inverse rotation
 // o . R^T = c * FWHT(o o s) follows, and the result is the final output (one
 // split) or a split partial for the shared combine kernel.
+//
+// Decode step (a.new_col): one more grid column appends the step's new token
+// (the append kernel's codebook arithmetic) and contributes its attention as
+// one more partial; the split columns leave its slot out. A decode step is
+// then this launch and the combine.
 #include <hip/hip_ext.h>
 
 #include "fmkv_device.h"
 #include "fmkv_internal.h"
+#include "fmkv_prologue.h"
+#include "fmkv_quant.h"
 #include "fmkv_attn_common.h"
 
 namespace fmkv {
@@ -71,12 +80,13 @@ struct CbPlan {
   static constexpr int kNormOff = 4 * kHalfBytes;
   static constexpr int kStageBytes = kNormOff + 2 * 64;
   static constexpr int kCopies = 2 * kHalfCopies + 1;  // per wave per block
-  // index pairs (2 and 3 bits; 16 or 64 entries of 8 bytes) or single
-  // indices (4 bits; 16 entries of 4 bytes)
+  // index pairs (2 and 3 bits; 16 or 64 entries, a high-part table and a
+  // residual table) or single indices (4 bits; 16 entries of {high,
+  // residual}); 4 bytes per entry and copy
   static constexpr bool kPairs = BITS <= 3;
   static constexpr int kLutEntries = kPairs ? (1 << (2 * BITS)) : 16;
-  static constexpr int kLutStride = kPairs ? 8 : 4;
-  static constexpr int kLutBytes = kLutEntries * kLutCopies * kLutStride;
+  static constexpr int kLutHalf = kLutEntries * kLutCopies * 4;  // one table
+  static constexpr int kLutBytes = kPairs ? 2 * kLutHalf : kLutHalf;
   // q table (the QK B operands, one KiB per slice), then the score exchange
   static constexpr int kTabBytes = (D / 32) * 1024;
   static constexpr int kXBytes = kCbWaves * 2 * 64 * 16;
@@ -155,31 +165,178 @@ __device__ inline uint32_t cent_hl(int i) {
   return (uint32_t)__builtin_bit_cast(uint16_t, h) | ((uint32_t)__builtin_bit_cast(uint16_t, r) << 16);
 }
 
-// The 32 bits from bit offset `bit` on of an LDS region (4-byte aligned;
-// the word after the first one is read too, and lies inside the LDS
+// A lane's field: the bits from `sh` on of word `dw` of w (and of the next
+// word at 3 bits, where fields straddle words; that word lies inside the LDS
 // staging: the K halves are followed by the V halves, the V halves by the
-// norms).
-__device__ inline uint32_t lds_bits(const uint8_t* region, int bit) {
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(region) + (bit >> 5);
-  return __builtin_amdgcn_alignbit(w[1], w[0], (uint32_t)(bit & 31));
+// norms). 2- and 4-bit fields never straddle a word.
+template <int BITS>
+__device__ inline uint32_t lds_field(const uint32_t* w, int dw, uint32_t sh) {
+  if constexpr (BITS == 3)
+    return __builtin_amdgcn_alignbit(w[dw + 1], w[dw], sh);
+  else
+    return w[dw] >> sh;
+}
+
+typedef const uint32_t __attribute__((address_space(3)))* lds_u32_ptr;
+typedef const volatile uint32_t __attribute__((address_space(3)))* lds_vu32_ptr;
+__device__ inline uint32_t lds_load(uint32_t addr) { return *(lds_u32_ptr)addr; }
+
+// Bits [OFF, OFF + W) of x (one v_bfe_u32; written out so that the index
+// and the table address stay two instructions).
+template <int OFF, int W>
+__device__ inline uint32_t bfe(uint32_t x) {
+  uint32_t r;
+  asm("v_bfe_u32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "n"(OFF), "n"(W));
+  return r;
 }
 
 // High and residual f16 operand words of two consecutive elements of a
-// field (the field's elements 2p and 2p + 1, element e at bits e * BITS).
-template <int BITS>
-__device__ inline void cb_pair(const uint8_t* lut, uint32_t field, int p, int lut_lane,
-                               uint32_t& hw, uint32_t& lw) {
+// field (the field's elements 2p and 2p + 1, element e at bits e * BITS);
+// base: LDS address of this lane's copy of entry 0 of the high-part table
+// (4-bit: of the one table). The residual is read at the same address plus
+// LUT_HALF as a volatile load, so that the two lookups stay two 4-byte loads
+// into the operand registers instead of being merged into one paired load
+// whose halves then need moving.
+template <int BITS, int LUT_HALF, int P>
+__device__ inline void cb_pair(uint32_t base, uint32_t field, uint32_t& hw, uint32_t& lw) {
   if constexpr (BITS <= 3) {
-    const uint32_t idx = (field >> (2 * p * BITS)) & ((1u << (2 * BITS)) - 1u);
-    const uint2 e = *reinterpret_cast<const uint2*>(lut + (idx * kLutCopies + lut_lane) * 8);
-    hw = e.x;
-    lw = e.y;
+    const uint32_t a = base + bfe<2 * P * BITS, 2 * BITS>(field) * (kLutCopies * 4);
+    hw = lds_load(a);
+    lw = *(lds_vu32_ptr)(a + LUT_HALF);
   } else {
-    const uint32_t i0 = (field >> (8 * p)) & 15u, i1 = (field >> (8 * p + 4)) & 15u;
-    const uint32_t e0 = *reinterpret_cast<const uint32_t*>(lut + (i0 * kLutCopies + lut_lane) * 4);
-    const uint32_t e1 = *reinterpret_cast<const uint32_t*>(lut + (i1 * kLutCopies + lut_lane) * 4);
+    const uint32_t e0 = lds_load(base + bfe<8 * P, 4>(field) * (kLutCopies * 4));
+    const uint32_t e1 = lds_load(base + bfe<8 * P + 4, 4>(field) * (kLutCopies * 4));
     hw = __builtin_amdgcn_perm(e1, e0, 0x05040100u);  // the high parts
     lw = __builtin_amdgcn_perm(e1, e0, 0x07060302u);  // the residuals
+  }
+}
+
+// The new-token column of a decode step, one work-group per (seq, kvh): the
+// token at position T - 1 is normalised, rotated and binned exactly as the
+// append kernel does it (src/cache.rs:94-129), its indices and f16 norm go to
+// its slot (ring: (T - 1) mod W; paged: through the block table) -- cleared
+// and set bit by bit with atomics, since other tokens' indices share the
+// words and the split columns may be reading them -- and, as the reference's
+// current token attends to its own round-tripped K/V (src/cache.rs:295-298),
+// it contributes partial slot n_splits: m = q_rot . k_deq (base 2), l = 1,
+// o = v_deq . R^T, the same row for every head of the group. Wave 0 handles
+// K, wave 1 V.
+template <int D, int BITS>
+__device__ void cb_new_token_column(const AttnArgs& a, uint8_t* tab, int64_t T, int n_splits,
+                                    int kvh, int seq, int wave, int lane) {
+  constexpr BlockLayout L = make_layout(D, BITS, kCodebook);
+  constexpr int E = D / 64;
+  const int G = a.group;
+  cb_copy_q_row<D>(a, tab, seq, kvh, wave, lane);
+  wait_vmcnt<0>();
+  const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
+  cb_build_q_table<D>(a, tab, wave, lane, sbits);
+  if (wave >= 2) return;  // no barrier follows
+
+  const bool isv = wave == 1;
+  const int d0 = lane * E;
+  const int64_t pbase = ((int64_t)seq * a.part_stride + n_splits) * a.n_q_heads + (int64_t)kvh * G;
+  if (T < 1) {  // no token: an empty partial
+    for (int h = 0; h < G; h++) {
+      if (isv) {
+#pragma unroll
+        for (int i = 0; i < E; i++) a.part_o[(pbase + h) * D + d0 + i] = 0.0f;
+      } else if (lane == 0) {
+        a.part_ml[(pbase + h) * 2 + 0] = -1e30f;
+        a.part_ml[(pbase + h) * 2 + 1] = 0.0f;
+      }
+    }
+    return;
+  }
+
+  float x[E];
+  load_row<E>((isv ? a.v_new : a.k_new) + ((int64_t)seq * a.st.n_kv_heads + kvh) * D + d0, x);
+  const float norm = sqrtf(canonical_sumsq<E>(x, lane));
+  const float den = norm + 1e-8f;
+#pragma unroll
+  for (int i = 0; i < E; i++) x[i] = x[i] / den;
+  wave_fwht_signed<E>(x, lane);
+  const float cl = fwht_lane_sign(lane) * a.c;
+  uint32_t code[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) {
+    const float sc = ((sbits >> i) & 1u) ? -cl : cl;
+    code[i] = (uint32_t)cb_index((x[i] * sc) * a.sqrt_d, BITS);
+  }
+  const uint16_t n16 = f32_to_f16_bits(norm);
+
+  // slot write (a bad block-table entry skips it; the token still attends)
+  const int64_t pos = T - 1;
+  const int64_t slot = a.window > 0 ? pos % a.window : pos;
+  const int64_t lb = slot / kBlockTokens;
+  const int t = (int)(slot % kBlockTokens);
+  int64_t phys = lb;
+  bool ok = true;
+  if (a.st.block_table) {
+    ok = lb < a.st.table_stride;
+    phys = ok ? (int64_t)a.st.block_table[(int64_t)seq * a.st.table_stride + lb] : -1;
+  }
+  ok = ok && phys >= 0 && phys < a.st.n_blocks;
+  if (ok) {
+    uint8_t* blk = a.st.base + phys * a.st.block_stride + (int64_t)kvh * a.st.head_stride;
+    uint32_t* w = reinterpret_cast<uint32_t*>(blk + (isv ? L.v_codes : L.k_codes));
+    // bits [bit, bit + n) of the region := v
+    auto put = [&](int64_t bit, uint64_t v, int n) {
+      const int wi = (int)(bit >> 5), off = (int)(bit & 31);
+      const uint64_t m = (((uint64_t)1 << n) - 1) << off;
+      v <<= off;
+      atomicAnd(&w[wi], ~(uint32_t)m);
+      atomicOr(&w[wi], (uint32_t)v);
+      if (off + n > 32) {
+        atomicAnd(&w[wi + 1], ~(uint32_t)(m >> 32));
+        atomicOr(&w[wi + 1], (uint32_t)(v >> 32));
+      }
+    };
+    if (!isv) {
+      // the lane's E dims are E * BITS consecutive bits of the half row
+      uint64_t v = 0;
+#pragma unroll
+      for (int i = 0; i < E; i++) v |= (uint64_t)code[i] << (i * BITS);
+      put(cb_k_bit(D, BITS, t, d0), v, E * BITS);
+    } else {
+#pragma unroll
+      for (int i = 0; i < E; i++) put(cb_v_bit(BITS, t, d0 + i), code[i], BITS);
+    }
+    if (lane == 0) *reinterpret_cast<uint16_t*>(blk + (isv ? L.v_meta : L.k_meta) + t * 2) = n16;
+  }
+
+  // the stored row in the rotated domain, as the split columns read it:
+  // centroid * norm / sqrt(D), the norm as stored
+  const float vs = f16_bits_to_f32(n16) * a.c;
+  float y[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) {
+    const uint32_t ci = code[i];
+    y[i] = BITS == 2 ? kCbCent2[ci] : BITS == 3 ? kCbCent3[ci] : kCbCent4[ci];
+  }
+  if (!isv) {
+    const int k = d0 >> 5, jj = (d0 & 31) >> 3, i0 = d0 & 7;
+    const uint8_t* ent = tab + k * 1024 + i0 * 2;
+    for (int h = 0; h < G; h++) {
+      const _Float16* qh = reinterpret_cast<const _Float16*>(ent + (jj * 16 + h) * 16);
+      const _Float16* ql = reinterpret_cast<const _Float16*>(ent + (jj * 16 + h + 8) * 16);
+      float p = 0.0f;
+#pragma unroll
+      for (int i = 0; i < E; i++) p += ((float)qh[i] + (float)ql[i]) * y[i];
+      p = group_sum<64>(p, lane);
+      if (lane == 0) {
+        a.part_ml[(pbase + h) * 2 + 0] = p * vs;
+        a.part_ml[(pbase + h) * 2 + 1] = 1.0f;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < E; i++) y[i] = apply_sign(y[i] * vs, sbits, i);
+    wave_fwht_signed<E>(y, lane);
+    const float cs = fwht_lane_sign(lane) * a.c;
+    for (int h = 0; h < G; h++)
+#pragma unroll
+      for (int i = 0; i < E; i++) a.part_o[(pbase + h) * D + d0 + i] = y[i] * cs;
   }
 }
 
@@ -210,7 +367,8 @@ void cb_decode_kernel(AttnArgs a) {
   const bool hi = c < 8;
   const int G = a.group;
   const bool col_valid = head < G;
-  const int lut_lane = lane & (kLutCopies - 1);
+  // this lane's copy of the tables
+  const uint32_t lut_l = lds_addr(lut) + (lane & (kLutCopies - 1)) * 4;
   // grid (KV head, sequence, split column), as the affine kernel
   const int kvh = blockIdx.x, seq = blockIdx.y, split = blockIdx.z;
 
@@ -218,6 +376,10 @@ void cb_decode_kernel(AttnArgs a) {
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
   const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits);
+  if (a.new_col && split == (int)gridDim.z - 1) {
+    cb_new_token_column<D, BITS>(a, scratch, T, n_splits, kvh, seq, wave, lane);
+    return;
+  }
   if (split >= n_splits) return;
   const int64_t b_begin = geo.blk_lo + (split == 0 ? 0 : a.bps0 + (int64_t)(split - 1) * a.bps);
   int64_t b_end = b_begin + (split == 0 ? a.bps0 : a.bps);
@@ -267,8 +429,8 @@ void cb_decode_kernel(AttnArgs a) {
     const int idx = e / kLutCopies;
     if constexpr (P::kPairs) {
       const uint32_t c0 = cent_hl<BITS>(idx & ((1 << BITS) - 1)), c1 = cent_hl<BITS>(idx >> BITS);
-      *reinterpret_cast<uint2*>(lut + e * 8) =
-          make_uint2((c0 & 0xffffu) | (c1 << 16), (c0 >> 16) | (c1 & 0xffff0000u));
+      *reinterpret_cast<uint32_t*>(lut + e * 4) = (c0 & 0xffffu) | (c1 << 16);
+      *reinterpret_cast<uint32_t*>(lut + P::kLutHalf + e * 4) = (c0 >> 16) | (c1 & 0xffff0000u);
     } else {
       *reinterpret_cast<uint32_t*>(lut + e * 4) = cent_hl<BITS>(idx);
     }
@@ -304,6 +466,10 @@ void cb_decode_kernel(AttnArgs a) {
   const int64_t vis_lo = a.window > 0 ? 0 : a.vis_begin;
   const int64_t vis_hi = a.window > 0 ? (T < a.window ? T : a.window) : T;
   const bool ring_trim = a.window > 0 && a.vis_begin > T - a.window;
+  // a decode step's new token is the new-token column's (its slot may still
+  // hold the position it replaces, or be written meanwhile)
+  int64_t ex_slot = -1;
+  if (a.new_col && T > 0) ex_slot = a.window > 0 ? (T - 1) % a.window : T - 1;
 
   // this lane's fields: QK slice s, token t = c of the MFMA A rows:
   // 8 indices at bit (t D/2 + 32 s + 8 j) BITS of the K half;
@@ -312,17 +478,24 @@ void cb_decode_kernel(AttnArgs a) {
   const int kbit0 = (c * (D / 2) + 8 * j) * BITS;
   const int vbit0 = (c * 16 + 4 * j) * BITS;
 
+  // slice s moves the K field by 32 BITS bits (a whole number of words),
+  // tile n the V field by 256 BITS bits, so a lane's shift stays put
+  const uint32_t ksh = kbit0 & 31, vsh = vbit0 & 31;
   auto process = [&](const uint8_t* sp, int64_t b, int it) {
-    const uint8_t* kh = sp + (int)L.k_codes + half * HB;
-    const uint8_t* vh = sp + (int)L.v_codes + half * HB;
+    const uint32_t* kw =
+        reinterpret_cast<const uint32_t*>(sp + (int)L.k_codes + half * HB) + (kbit0 >> 5);
+    const uint32_t* vw =
+        reinterpret_cast<const uint32_t*>(sp + (int)L.v_codes + half * HB) + (vbit0 >> 5);
     // this half's S^T = K . q_rot^T (high + residual centroid parts)
     float4_t acc = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < NSW; s++) {
-      const uint32_t f = lds_bits(kh, kbit0 + 32 * s * BITS);
+      const uint32_t f = lds_field<BITS>(kw, s * BITS, ksh);
       uint32_t h4[4], l4[4];
-#pragma unroll
-      for (int p = 0; p < 4; p++) cb_pair<BITS>(lut, f, p, lut_lane, h4[p], l4[p]);
+      cb_pair<BITS, P::kLutHalf, 0>(lut_l, f, h4[0], l4[0]);
+      cb_pair<BITS, P::kLutHalf, 1>(lut_l, f, h4[1], l4[1]);
+      cb_pair<BITS, P::kLutHalf, 2>(lut_l, f, h4[2], l4[2]);
+      cb_pair<BITS, P::kLutHalf, 3>(lut_l, f, h4[3], l4[3]);
       const half8_t ah = __builtin_bit_cast(half8_t, (u32x4){h4[0], h4[1], h4[2], h4[3]});
       const half8_t al = __builtin_bit_cast(half8_t, (u32x4){l4[0], l4[1], l4[2], l4[3]});
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[s], acc, 0, 0, 0);
@@ -355,12 +528,13 @@ void cb_decode_kernel(AttnArgs a) {
     }
     // visibility: whole block in the common case, per token at the edges
     const int64_t t0 = b * kBlockTokens;
-    const bool full = t0 >= vis_lo && t0 + kBlockTokens <= vis_hi && !ring_trim;
+    const bool full = t0 >= vis_lo && t0 + kBlockTokens <= vis_hi && !ring_trim &&
+                      (uint64_t)(ex_slot - t0) >= (uint64_t)kBlockTokens;
     if (!full) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int64_t slot = t0 + 4 * j + i;
-        bool vis = slot >= vis_lo && slot < vis_hi;
+        bool vis = slot >= vis_lo && slot < vis_hi && slot != ex_slot;
         if (ring_trim) vis = vis && slot_position(slot, T, a.window) >= a.vis_begin;
         if (!vis) sc[i] = -INFINITY;
       }
@@ -397,10 +571,10 @@ void cb_decode_kernel(AttnArgs a) {
     const half4_t bp = cat4(b01, b23);
 #pragma unroll
     for (int n = 0; n < NTW; n++) {
-      const uint32_t f = lds_bits(vh, vbit0 + 256 * n * BITS);
+      const uint32_t f = lds_field<BITS>(vw, n * 8 * BITS, vsh);
       uint32_t h2[2], l2[2];
-#pragma unroll
-      for (int q = 0; q < 2; q++) cb_pair<BITS>(lut, f, q, lut_lane, h2[q], l2[q]);
+      cb_pair<BITS, P::kLutHalf, 0>(lut_l, f, h2[0], l2[0]);
+      cb_pair<BITS, P::kLutHalf, 1>(lut_l, f, h2[1], l2[1]);
       const half4_t ah = __builtin_bit_cast(half4_t, make_uint2(h2[0], h2[1]));
       const half4_t al = __builtin_bit_cast(half4_t, make_uint2(l2[0], l2[1]));
       o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bp, o[n], 0, 0, 0);
@@ -498,7 +672,7 @@ void cb_decode_kernel(AttnArgs a) {
 template <int D, int BITS>
 hipError_t launch_cb_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s, hipEvent_t ev0,
                        hipEvent_t ev1) {
-  dim3 grid(n_kv_heads, n_seqs, a.max_splits);
+  dim3 grid(n_kv_heads, n_seqs, a.max_splits + a.new_col);
   if (ev0 && ev1)
     hipExtLaunchKernelGGL((cb_decode_kernel<D, BITS>), grid, dim3(kCbWaves * 64), 0, s, ev0, ev1, 0, a);
   else

@@ -65,6 +65,7 @@ struct AttnArgs {
   float qscale;       // softmax scale * log2(e)
   uint32_t sign_bits[16];  // RHT signs of dims 0..D-1, bit d set = -1
   float c;            // 1/sqrt(D)
+  float sqrt_d;       // sqrt(D) (f32): binning scale of a codebook decode step's new token
   int32_t bps0;       // blocks of split 0 (>= bps)
   int32_t bps;        // blocks of every later split
   int32_t max_splits; // split columns of the grid

@@ -72,4 +72,32 @@ __device__ inline void affine_quant(const float (&y)[E], uint32_t (&code)[E], fl
   bias_o = bias;
 }
 
+namespace {
+
+// Lloyd-Max bin of a rotated, normalised value scaled by sqrt(D)
+// (src/cache.rs:67-89 boundaries; a value on a boundary goes to the upper
+// bin), as the reference's round trip bins it (src/cache.rs:94-129).
+__constant__ float kCbBounds2[3] = {-0.982f, 0.0f, 0.982f};
+__constant__ float kCbBounds3[7] = {-1.748f, -1.050f, -0.501f, 0.0f, 0.501f, 1.050f, 1.748f};
+__constant__ float kCbBounds4[15] = {-2.401f, -1.844f, -1.437f, -1.099f, -0.800f,
+                                     -0.522f, -0.258f, 0.0f,    0.258f,  0.522f,
+                                     0.800f,  1.099f,  1.437f,  1.844f,  2.401f};
+
+__device__ inline int cb_index(float z, int bits) {
+  int idx = 0;
+  if (bits == 2) {
+#pragma unroll
+    for (int b = 0; b < 3; b++) idx += (z >= kCbBounds2[b]) ? 1 : 0;
+  } else if (bits == 3) {
+#pragma unroll
+    for (int b = 0; b < 7; b++) idx += (z >= kCbBounds3[b]) ? 1 : 0;
+  } else {
+#pragma unroll
+    for (int b = 0; b < 15; b++) idx += (z >= kCbBounds4[b]) ? 1 : 0;
+  }
+  return idx;
+}
+
+}  // namespace
+
 }  // namespace fmkv

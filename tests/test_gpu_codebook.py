@@ -2,13 +2,14 @@
 oracle: exact f64 softmax attention over the oracle's codebook dequantization
 (centroid[idx] * norm / sqrt(D), un-rotated; src/cache.rs:94-129 without the
 bf16 round trip). Tolerance: max-abs 2e-2, mean-abs 2e-3 (bf16 outputs also
-allow one bf16 ulp of the reference). Codes are checked bit-exact by
-test_gpu_append.py; here the read is."""
+allow one bf16 ulp of the reference). Codes written by appends are checked
+bit-exact by test_gpu_append.py, those written by decode steps' new-token
+column here."""
 import numpy as np
 import pytest
 
 import synth
-from gpu_util import check_attention, dev_bf16, fast_kv, fast_q, kv_batch
+from gpu_util import check_attention, dev_bf16, fast_kv, fast_q, host_u16, host_u32, kv_batch
 
 pytestmark = pytest.mark.gpu
 CB = 1  # MODE_CODEBOOK
@@ -96,6 +97,40 @@ def test_codebook_ring_steps_through_wraps(gpu, ora, D, bits, W):
             torch.cuda.synchronize()
             check_attention(out, oc.attention(q[i], 0.02), f"ring W={W} step {i}")
     assert cache.stored_len() == W
+
+
+@pytest.mark.parametrize("D,bits,W", [(256, 3, 0), (512, 3, 0), (512, 2, 48), (256, 4, 32), (128, 3, 16)])
+def test_codebook_decode_steps_store_append_codes(gpu, ora, D, bits, W):
+    """Decode steps append their token in the attention launch's new-token
+    column: after a prefill and single-token steps (linear, or a ring through
+    wraps) every stored index and norm equals the oracle's round trip, and
+    every step's output is within the path tolerance."""
+    import torch
+
+    Hkv, Hq = (8, 16) if D == 256 else (2, 16)
+    n0, n = 37, (3 * W + 5 if W else 70)
+    cache = gpu.KVCache.new_quantized_with_window(D, bits, W, Hkv, 0 if W else n0 + n + 16, mode=CB)
+    oc = ora.OracleCache(Hkv, D, bits, W, 0 if W else n0 + n + 16, mode=CB)
+    k0, v0 = kv_batch(61, n0, Hkv, D), kv_batch(62, n0, Hkv, D)
+    cache.append(dev_bf16(k0), dev_bf16(v0))
+    oc.append(k0, v0)
+    k, v = kv_batch(63, n, Hkv, D), kv_batch(64, n, Hkv, D)
+    q = fast_q(65, n, Hq, Hkv, D)
+    kd, vd = dev_bf16(k), dev_bf16(v)
+    for i in range(n):
+        out = cache.decode_step(kd[i:i + 1], vd[i:i + 1], dev_bf16(q[i]), 0.02, dtype=torch.float32)
+        oc.append(k[i:i + 1], v[i:i + 1])
+        if i % 9 == 0 or i == n - 1:
+            torch.cuda.synchronize()
+            check_attention(out, oc.attention(q[i], 0.02), f"step {i}")
+    torch.cuda.synchronize()
+    assert cache.offset() == n0 + n
+    codes, meta = cache.read_codes()
+    c, m = host_u32(codes), host_u16(meta)
+    bad = np.argwhere((c != oc.codes).any(-1))
+    assert bad.size == 0, f"index mismatch at (slot, kv, head) {bad[:5].tolist()} of {len(bad)}"
+    badm = np.argwhere((m != oc.meta).any(-1))
+    assert badm.size == 0, f"norm mismatch at {badm[:5].tolist()}"
 
 
 def test_codebook_trim_and_empty(gpu, ora):
