@@ -755,8 +755,10 @@ int decode_step_impl(fmkv_cache* c, const void* k, const void* v, int64_t n, con
   if (rc) return rc;
   if (pro) set_prologue(pro, &ap);
   // one new token: the attention launch appends it itself (new-token
-  // column); sparse-V attention runs after a separate append
-  const int fused = n == 1 && tau == 0.0f && c->desc.mode != FMKV_MODE_PLAIN ? 1 : 0;
+  // column; with sparse-V the statistics pass does); plain caches, codebook
+  // caches with sparse-V (which they reject) and chunks append first
+  const int fused = n == 1 && c->desc.mode != FMKV_MODE_PLAIN &&
+                            (tau == 0.0f || c->desc.mode == FMKV_MODE_AFFINE) ? 1 : 0;
   fmkv::AttnArgs at;
   rc = prepare_attention(c, c->offset + n, q, n_q_heads, scale, tau, out, out_dtype, fused, &at, ext);
   if (rc) return rc;
@@ -1022,7 +1024,8 @@ int paged_decode_step_impl(fmkv_pool* p, const void* k, const void* v,
   if (pro) set_prologue(pro, &ap);
   // one new token per sequence: the attention launch appends it itself, at
   // position seq_lens[s] - 1 (= start_pos[s])
-  const int fused = n_new == 1 && tau == 0.0f && p->desc.mode != FMKV_MODE_PLAIN ? 1 : 0;
+  const int fused = n_new == 1 && p->desc.mode != FMKV_MODE_PLAIN &&
+                            (tau == 0.0f || p->desc.mode == FMKV_MODE_AFFINE) ? 1 : 0;
   fmkv::AttnArgs at;
   rc = prepare_paged_attention(p, q, block_tables, max_blocks, seq_lens, n_seqs, max_seq_len,
                                n_q_heads, scale, tau, out, out_dtype, fused, &at);

@@ -441,7 +441,9 @@ void decode_attn_kernel(AttnArgs a) {
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
   const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits);
   static_assert(P::kStageRegion >= D / 2 * (int)sizeof(float2), "rope table fits the staging");
-  if constexpr (MODE == kDense) {
+  // decode step: the new token's column (dense mode, or the statistics pass
+  // of a sparse-V step, whose gated pass then reads the stored token)
+  if constexpr (MODE != kGated) {
     if (a.new_col && split == (int)gridDim.z - 1) {
       new_token_column<D, BITS, P::kWaves * 64>(a, scratch, reinterpret_cast<float2*>(stage), T,
                                                 n_splits, kvh, seq, wave, lane);
@@ -696,6 +698,12 @@ void decode_attn_kernel(AttnArgs a) {
     for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(s[i] - m_run);
     l_run += (p[0] + p[1]) + (p[2] + p[3]);
     if constexpr (MODE == kStats) return;
+    // sparse-V: a block whose weights are all below tau adds nothing to O
+    // (no renormalisation), so its V dequantisation and products are
+    // skipped (the pair's waves hold the same scores: a uniform branch)
+    if constexpr (MODE == kGated) {
+      if (!__any((p[0] + p[1]) + (p[2] + p[3]) > 0.0f)) return;
+    }
 
     // O^T += V^T . P'^T with P' = p * v_scale as f16 hi (c < 8) / residual
     // (c >= 8): x = p * v_scale in f32, hi = f16(x), residual = f16(x - hi),
@@ -955,7 +963,8 @@ __global__ __launch_bounds__(64) void tau_threshold_kernel(AttnArgs a) {
   const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
-  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits);
+  // the statistics pass's splits and its new-token column
+  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits) + a.new_col;
   const int64_t base = (int64_t)seq * a.part_stride * a.n_q_heads + h;
   float M = -INFINITY, L = 0.0f;
   for (int sp = lane; sp < n_splits; sp += 64) {
@@ -1001,14 +1010,21 @@ hipError_t launch_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s
                     hipEvent_t ev0, hipEvent_t ev1) {
   dim3 grid(n_kv_heads, n_seqs, a.max_splits + a.new_col);
   hipError_t e;
-  if (a.tau > 0.0f) {  // sparse-V: stats pass, thresholds, gated pass, combine
+  if (a.tau > 0.0f) {
+    // sparse-V: the stats pass (with a decode step's new-token column, which
+    // appends the token), the thresholds, the gated pass over every stored
+    // token (the new one included) and the combine of its splits
     if ((e = launch_split<D, BITS, kStats>(a, grid, s, nullptr, nullptr)) != hipSuccess) return e;
     hipLaunchKernelGGL(tau_threshold_kernel, dim3(a.n_q_heads, n_seqs), dim3(64), 0, s, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    e = launch_split<D, BITS, kGated>(a, grid, s, ev0, ev1);
-  } else {
-    e = launch_split<D, BITS, kDense>(a, grid, s, ev0, ev1);
+    AttnArgs g = a;
+    g.new_col = 0;
+    if ((e = launch_split<D, BITS, kGated>(g, dim3(n_kv_heads, n_seqs, a.max_splits), s, ev0, ev1)) !=
+        hipSuccess)
+      return e;
+    return a.direct ? hipSuccess : launch_combine(g, n_seqs, s);
   }
+  e = launch_split<D, BITS, kDense>(a, grid, s, ev0, ev1);
   if (e != hipSuccess || a.direct) return e;
   return launch_combine(a, n_seqs, s);
 }

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import synth
-from gpu_util import check_attention, dev_bf16, kv_batch
+from gpu_util import check_attention, dev_bf16, host_u16, host_u32, kv_batch
 
 pytestmark = pytest.mark.gpu
 
@@ -111,7 +111,9 @@ def test_sparse_v_split_counts_agree(gpu, ora, bps):
 @pytest.mark.parametrize("D,bits", [(256, 4), (256, 8)])
 def test_sparse_v_ring_steps(gpu, ora, D, bits):
     """Sliding layer W = 64: decode steps through two wraps with tau > 0 (the
-    step appends, then runs both passes)."""
+    statistics pass's new-token column appends the token, the gated pass
+    reads it back): every checked output within tolerance, and the stored
+    codes and scale/bias bit-exact with the oracle's at the end."""
     import torch
 
     Hkv, Hq, W = 8, 16, 64
@@ -130,6 +132,9 @@ def test_sparse_v_ring_steps(gpu, ora, D, bits):
         torch.cuda.synchronize()
         if step % 9 == 0 or step > 90:
             check_attention(out, oc.attention(q, 0.05, 0.01), f"step {step}")
+    codes, meta = cache.read_codes()
+    assert np.array_equal(host_u32(codes), oc.codes), "codes written by sparse-V steps"
+    assert np.array_equal(host_u16(meta), oc.meta), "scale/bias written by sparse-V steps"
 
 
 def test_sparse_v_paged(gpu, ora):
