@@ -181,15 +181,19 @@ def run_c3(args) -> dict:
     tb = cache.offset()
     for _ in range(args.steps):
         step()
-    kernel_ms, n_rec = fmkv.profile_collect()
+    each_ms = fmkv.profile_collect_each(args.steps)
     fmkv.profile_enable(0)
+    n_rec = len(each_ms)
     te = cache.offset()
     avg_T = (tb + te + 1) / 2.0
-    kern_s = kernel_ms / n_rec / 1e3
+    kern_s = sum(each_ms) / n_rec / 1e3
+    each_us = sorted(m * 1e3 for m in each_ms)
+    kern_pct = {q: round(each_us[min(n_rec - 1, int(q / 100 * n_rec))], 3) for q in (10, 50, 90)}
     launch_bytes = avg_T * Hkv * per_tok + 2 * Hq * D * 2
     achieved = launch_bytes / kern_s / 1e9
     log(f"step {ms_per_step*1e3:.1f} us, split kernel {kern_s*1e6:.2f} us over {n_rec} launches, "
-        f"{achieved:.0f} GB/s, splits={cache.decode_splits()}")
+        f"{achieved:.0f} GB/s, splits={cache.decode_splits()}; per launch p10/p50/p90 "
+        f"{kern_pct[10]:.2f}/{kern_pct[50]:.2f}/{kern_pct[90]:.2f} us")
 
     # The next graph_steps steps captured into a HIP graph and replayed: a
     # replay repeats the same appends (the same codes into the same slots)
@@ -292,6 +296,7 @@ def run_c3(args) -> dict:
             "kernel": (f"cb_decode_kernel<512, {bits}>" if cb else "plain_decode_kernel<512>" if plain
                        else f"decode_attn_kernel<512, {bits}, 0>"),
             "avg_kernel_us": round(kern_s * 1e6, 3),
+            "kernel_us_p10_p50_p90": [kern_pct[10], kern_pct[50], kern_pct[90]],
             "bytes_per_launch": int(launch_bytes),
         },
     }

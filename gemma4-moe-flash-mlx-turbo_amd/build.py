@@ -4,8 +4,15 @@ Usage: python gemma4-moe-flash-mlx-turbo_amd/build.py [--jobs N]
 
 Every .hip file under csrc/ is compiled by hipcc for gfx950 and linked into
 one shared library next to this file. Compile flags:
-  -ffp-contract=off          the append kernel reproduces the oracle's rounding
-                             op by op, so no implicit FMA contraction anywhere;
+  -ffp-contract=off          the append and readback kernels reproduce the
+                             oracle's rounding op by op: no implicit FMA
+                             contraction there;
+  -ffp-contract=fast-honor-pragmas
+                             the attention sources (CONTRACT_SOURCES) let the
+                             compiler fuse multiply-adds in their loops; the
+                             quantization helpers and new-token columns they
+                             share with the append turn contraction off in
+                             their bodies (#pragma clang fp contract(off));
   -packed-fp32-ops disabled  no packed FP32 instructions are generated;
   -amdgpu-mfma-vgpr-form=1   MFMA accumulators in VGPRs (see HIP_FLAGS).
 """
@@ -45,6 +52,11 @@ HIP_FLAGS = [
 ]
 
 
+# attention sources: contraction on, except where a pragma turns it off
+CONTRACT_SOURCES = {"fmkv_attention.hip", "fmkv_cb_attention.hip", "fmkv_plain_attention.hip",
+                    "fmkv_prefill.hip"}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -53,7 +65,11 @@ def hipcc() -> str:
 
 
 def _compile(src: Path, obj: Path) -> tuple[Path, str]:
-    cmd = [hipcc(), *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    flags = HIP_FLAGS
+    if src.name in CONTRACT_SOURCES:
+        flags = ["-ffp-contract=fast-honor-pragmas" if f == "-ffp-contract=off" else f
+                 for f in HIP_FLAGS]
+    cmd = [hipcc(), *flags, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     out = (res.stdout + res.stderr)
     # the host pass does not know the packed-fp32 feature; that note is noise

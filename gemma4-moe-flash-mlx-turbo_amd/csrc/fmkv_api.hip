@@ -328,6 +328,45 @@ int prepare_append(const fmkv_cache* c, const void* k, const void* v, int64_t n,
   return FMKV_OK;
 }
 
+// Split-K plan of one decode attention launch: blocks per split (bps, bps0
+// for split 0), split columns per sequence and the XCD-aware skew.
+void plan_splits(int cus, int H, int32_t n_seqs, int64_t nblk, int wg_per_cu, int min_bps,
+                 int first_mult, int new_col, float tau, bool paged, fmkv::AttnArgs* a) {
+  if (nblk < 1) nblk = 1;
+  // one sequence: the new-token column takes CUs of its own; many sequences:
+  // the dispatcher fills CUs as work-groups finish
+  const int64_t reserved = n_seqs == 1 ? (int64_t)new_col * H : 0;
+  a->bps = choose_bps(nblk * H * n_seqs, cus, wg_per_cu, reserved, min_bps);
+  // the split columns are the grid's z dimension (at most 65535)
+  if ((nblk + a->bps - 1) / a->bps + new_col > 65535)
+    a->bps = (int32_t)((nblk + 65534 - new_col) / (65535 - new_col));
+  // split 0 of each sequence takes first_mult x bps blocks
+  const int64_t bps0 = (int64_t)a->bps * first_mult;
+  a->bps0 = (int32_t)(bps0 < nblk ? bps0 : nblk);
+  if (a->bps0 < a->bps) a->bps0 = a->bps;
+  a->max_splits = (int32_t)(nblk <= a->bps0 ? 1 : 1 + (nblk - a->bps0 + a->bps - 1) / a->bps);
+  a->skew_p = a->skew_extra = 0;
+  // XCD-aware plan for one sequence over two KV heads at one work-group per
+  // CU: the work-groups (KV head h, split s) go round-robin to the 8 XCDs by
+  // linear id h + 2 s, so the splits s = 0 mod 4 land on XCDs 0 and 1, which
+  // start first (the others start 1.4 to 4.4 us later). Every CU gets a split
+  // of bps blocks (a multiple of the 4 block streams when bps is) and the
+  // blocks left over go one each to those early splits, instead of bps + 1
+  // blocks for every work-group and some CUs left idle.
+  if (n_seqs == 1 && H == 2 && wg_per_cu == 1 && tau == 0.0f && !paged &&
+      g_bps_override <= 0) {
+    const int64_t n_s = (cus - (int64_t)new_col * H) / H;
+    const int64_t b = n_s > 0 ? nblk / n_s : 0;
+    const int64_t extra = nblk - n_s * b;
+    if (n_s >= 8 && b >= fmkv::kAttnPlanMinSkewBlocks && extra <= (n_s + 3) / 4) {
+      a->bps = a->bps0 = (int32_t)b;
+      a->max_splits = (int32_t)n_s;
+      a->skew_p = 4;
+      a->skew_extra = (int32_t)extra;
+    }
+  }
+}
+
 // Split-K plan, workspace ([part_o | part_ml]) and launch arguments of
 // decode attention; new_col adds the decode step's new-token column.
 template <typename Owner>
@@ -346,19 +385,8 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   std::memcpy(a->sign_bits, o->sign_bits, sizeof(a->sign_bits));
   a->c = o->c;
   a->sqrt_d = o->sqrt_d;
-  if (nblk < 1) nblk = 1;
-  // one sequence: the new-token column takes CUs of its own; many sequences:
-  // the dispatcher fills CUs as work-groups finish
-  const int64_t reserved = n_seqs == 1 ? (int64_t)new_col * H : 0;
-  a->bps = choose_bps(nblk * H * n_seqs, o->cus, wg_per_cu, reserved, min_bps);
-  // the split columns are the grid's z dimension (at most 65535)
-  if ((nblk + a->bps - 1) / a->bps + new_col > 65535)
-    a->bps = (int32_t)((nblk + 65534 - new_col) / (65535 - new_col));
-  // split 0 of each sequence takes first_mult x bps blocks
-  const int64_t bps0 = (int64_t)a->bps * first_mult;
-  a->bps0 = (int32_t)(bps0 < nblk ? bps0 : nblk);
-  if (a->bps0 < a->bps) a->bps0 = a->bps;
-  a->max_splits = (int32_t)(nblk <= a->bps0 ? 1 : 1 + (nblk - a->bps0 + a->bps - 1) / a->bps);
+  plan_splits(o->cus, H, n_seqs, nblk, wg_per_cu, min_bps, first_mult, new_col, tau,
+              st.block_table != nullptr, a);
   a->new_col = new_col;
   a->part_stride = a->max_splits + new_col;
   // sparse-V (tau > 0) always goes through the split partials and the
@@ -781,6 +809,16 @@ int decode_step_impl(fmkv_cache* c, const void* k, const void* v, int64_t n, con
   return FMKV_OK;
 }
 
+// Elapsed milliseconds of recorded pair i (waits for it).
+int profile_pair_ms(int32_t i, float* ms) {
+  hipError_t e = hipEventSynchronize(g_prof.ev[2 * (size_t)i + 1]);
+  if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+  *ms = 0.0f;
+  e = hipEventElapsedTime(ms, g_prof.ev[2 * (size_t)i], g_prof.ev[2 * (size_t)i + 1]);
+  if (e != hipSuccess) return hip_fail(e, "hipEventElapsedTime");
+  return FMKV_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -813,8 +851,10 @@ int fmkv_cache_decode_splits(const fmkv_cache* c, int32_t* n_splits) {
   int64_t vb = c->desc.window > 0 ? 0 : c->vis_begin;
   int64_t nblk = (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
   if (nblk < 1) nblk = 1;
-  const int32_t bps = choose_bps(nblk * c->desc.n_kv_heads, c->cus, attn_wg_per_cu(c->desc));
-  *n_splits = (int32_t)((nblk + bps - 1) / bps);
+  fmkv::AttnArgs a;
+  plan_splits(c->cus, c->desc.n_kv_heads, 1, nblk, attn_wg_per_cu(c->desc), 1, 1, 0, 0.0f, false,
+              &a);
+  *n_splits = a.max_splits;
   return FMKV_OK;
 }
 
@@ -1117,14 +1157,26 @@ int fmkv_profile_collect(double* total_ms, int32_t* n_records) {
   if (!total_ms || !n_records) return fail(FMKV_ERR_INVALID_ARG, "null argument");
   double sum = 0.0;
   for (int32_t i = 0; i < g_prof.used; i++) {
-    hipError_t e = hipEventSynchronize(g_prof.ev[2 * (size_t)i + 1]);
-    if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
-    float ms = 0.0f;
-    e = hipEventElapsedTime(&ms, g_prof.ev[2 * (size_t)i], g_prof.ev[2 * (size_t)i + 1]);
-    if (e != hipSuccess) return hip_fail(e, "hipEventElapsedTime");
+    float ms;
+    int rc = profile_pair_ms(i, &ms);
+    if (rc) return rc;
     sum += ms;
   }
   *total_ms = sum;
+  *n_records = g_prof.used;
+  g_prof.used = 0;
+  return FMKV_OK;
+}
+
+int fmkv_profile_collect_each(float* ms_out, int32_t capacity, int32_t* n_records) {
+  if (!ms_out || !n_records) return fail(FMKV_ERR_INVALID_ARG, "null argument");
+  if (capacity < g_prof.used)
+    return fail(FMKV_ERR_CAPACITY, std::to_string(g_prof.used) + " records need a buffer of as "
+                                   "many floats; capacity is " + std::to_string(capacity));
+  for (int32_t i = 0; i < g_prof.used; i++) {
+    int rc = profile_pair_ms(i, &ms_out[i]);
+    if (rc) return rc;
+  }
   *n_records = g_prof.used;
   g_prof.used = 0;
   return FMKV_OK;

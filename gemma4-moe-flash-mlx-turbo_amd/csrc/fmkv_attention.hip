@@ -293,6 +293,7 @@ __device__ inline void store_v_codes(uint8_t* vbase, int t, int d0, const uint32
 template <int D, int BITS, int NT>
 __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, float2* rope, int64_t T,
                                  int n_splits, int kvh, int seq, int wave, int lane) {
+#pragma clang fp contract(off)
   constexpr BlockLayout L = make_layout(D, BITS, kAffine);
   constexpr int E = D / 64, LPG = 64 / E;
   const int G = a.group;
@@ -439,7 +440,7 @@ void decode_attn_kernel(AttnArgs a) {
   const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
-  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits);
+  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits, a.skew_p);
   static_assert(P::kStageRegion >= D / 2 * (int)sizeof(float2), "rope table fits the staging");
   // decode step: the new token's column (dense mode, or the statistics pass
   // of a sparse-V step, whose gated pass then reads the stored token)
@@ -451,10 +452,8 @@ void decode_attn_kernel(AttnArgs a) {
     }
   }
   if (split >= n_splits) return;
-  const int64_t b_begin =
-      geo.blk_lo + (split == 0 ? 0 : a.bps0 + (int64_t)(split - 1) * a.bps);
-  int64_t b_end = b_begin + (split == 0 ? a.bps0 : a.bps);
-  if (b_end > geo.blk_hi) b_end = geo.blk_hi;
+  int64_t b_begin, b_end;
+  split_range(geo, split, a.bps0, a.bps, a.skew_p, a.skew_extra, &b_begin, &b_end);
 
   // Table entries are read through the constant address space: a uniform
   // index then becomes a scalar load, which never waits for the copies in
@@ -893,7 +892,7 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
   const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
-  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits) + a.new_col;
+  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits, a.skew_p) + a.new_col;
   const int64_t stride = (int64_t)a.n_q_heads;
   const int64_t base = (int64_t)seq * a.part_stride * stride + h;
 
@@ -964,7 +963,7 @@ __global__ __launch_bounds__(64) void tau_threshold_kernel(AttnArgs a) {
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
   // the statistics pass's splits and its new-token column
-  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits) + a.new_col;
+  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits, a.skew_p) + a.new_col;
   const int64_t base = (int64_t)seq * a.part_stride * a.n_q_heads + h;
   float M = -INFINITY, L = 0.0f;
   for (int sp = lane; sp < n_splits; sp += 64) {

@@ -179,7 +179,7 @@ __device__ inline uint32_t lds_field(const uint32_t* w, int dw, uint32_t sh) {
 
 typedef const uint32_t __attribute__((address_space(3)))* lds_u32_ptr;
 typedef const volatile uint32_t __attribute__((address_space(3)))* lds_vu32_ptr;
-__device__ inline uint32_t lds_load(uint32_t addr) { return *(lds_u32_ptr)addr; }
+__device__ inline uint32_t lds_load(uint32_t addr) { return *(lds_u32_ptr)(size_t)addr; }
 
 // Bits [OFF, OFF + W) of x (one v_bfe_u32; written out so that the index
 // and the table address stay two instructions).
@@ -202,7 +202,7 @@ __device__ inline void cb_pair(uint32_t base, uint32_t field, uint32_t& hw, uint
   if constexpr (BITS <= 3) {
     const uint32_t a = base + bfe<2 * P * BITS, 2 * BITS>(field) * (kLutCopies * 4);
     hw = lds_load(a);
-    lw = *(lds_vu32_ptr)(a + LUT_HALF);
+    lw = *(lds_vu32_ptr)(size_t)(a + LUT_HALF);
   } else {
     const uint32_t e0 = lds_load(base + bfe<8 * P, 4>(field) * (kLutCopies * 4));
     const uint32_t e1 = lds_load(base + bfe<8 * P + 4, 4>(field) * (kLutCopies * 4));
@@ -224,6 +224,7 @@ __device__ inline void cb_pair(uint32_t base, uint32_t field, uint32_t& hw, uint
 template <int D, int BITS>
 __device__ void cb_new_token_column(const AttnArgs& a, uint8_t* tab, int64_t T, int n_splits,
                                     int kvh, int seq, int wave, int lane) {
+#pragma clang fp contract(off)
   constexpr BlockLayout L = make_layout(D, BITS, kCodebook);
   constexpr int E = D / 64;
   const int G = a.group;
@@ -375,15 +376,14 @@ void cb_decode_kernel(AttnArgs a) {
   const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
-  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits);
+  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits, a.skew_p);
   if (a.new_col && split == (int)gridDim.z - 1) {
     cb_new_token_column<D, BITS>(a, scratch, T, n_splits, kvh, seq, wave, lane);
     return;
   }
   if (split >= n_splits) return;
-  const int64_t b_begin = geo.blk_lo + (split == 0 ? 0 : a.bps0 + (int64_t)(split - 1) * a.bps);
-  int64_t b_end = b_begin + (split == 0 ? a.bps0 : a.bps);
-  if (b_end > geo.blk_hi) b_end = geo.blk_hi;
+  int64_t b_begin, b_end;
+  split_range(geo, split, a.bps0, a.bps, a.skew_p, a.skew_extra, &b_begin, &b_end);
 
   // table entries through the constant address space: a uniform index then
   // becomes a scalar load, which never waits for the copies in flight

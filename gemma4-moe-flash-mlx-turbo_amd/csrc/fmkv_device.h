@@ -331,12 +331,35 @@ __device__ inline SeqGeom seq_geometry(int64_t T, int64_t window, int64_t vis_be
 // sequence's first work-group is its largest, so the dispatcher, which
 // takes the grid's split columns in order, starts the big work first and
 // fills the tail with small work-groups.
-__device__ inline int n_splits_for(const SeqGeom& g, int bps0, int bps, int max_splits) {
+// An XCD-aware plan (skew_p > 0, one sequence) sizes the grid to the
+// sequence exactly: every one of its max_splits splits is used.
+__device__ inline int n_splits_for(const SeqGeom& g, int bps0, int bps, int max_splits,
+                                   int skew_p = 0) {
+  if (skew_p > 0) return max_splits;
   // block counts stay below 2^31 / 16: a 32-bit division suffices
   const uint32_t nb = (uint32_t)(g.blk_hi - g.blk_lo);
   int64_t ns = nb <= (uint32_t)bps0 ? 1 : 1 + (nb - (uint32_t)bps0 + (uint32_t)bps - 1u) / (uint32_t)bps;
   if (ns > max_splits) ns = max_splits;
   return (int)ns;
+}
+
+// Blocks [*b_begin, *b_end) of split `split`. Default plan: split 0 has bps0
+// blocks, every later one bps. XCD-aware plan (skew_p > 0): every split has
+// bps blocks and the first skew_extra splits whose index is a multiple of
+// skew_p one more -- the launch puts those on the XCDs that start first.
+__device__ inline void split_range(const SeqGeom& g, int split, int bps0, int bps, int skew_p,
+                                   int skew_extra, int64_t* b_begin, int64_t* b_end) {
+  int64_t first, count;
+  if (skew_p > 0) {
+    const int before = (split + skew_p - 1) / skew_p;  // skewed splits ahead of this one
+    first = (int64_t)split * bps + (before < skew_extra ? before : skew_extra);
+    count = bps + ((split % skew_p == 0 && split / skew_p < skew_extra) ? 1 : 0);
+  } else {
+    first = split == 0 ? 0 : bps0 + (int64_t)(split - 1) * bps;
+    count = split == 0 ? bps0 : bps;
+  }
+  *b_begin = g.blk_lo + first < g.blk_hi ? g.blk_lo + first : g.blk_hi;
+  *b_end = *b_begin + count < g.blk_hi ? *b_begin + count : g.blk_hi;
 }
 
 }  // namespace fmkv

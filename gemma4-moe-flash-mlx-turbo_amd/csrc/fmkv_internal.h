@@ -30,6 +30,9 @@ constexpr int kAttnWaves = 2 * kAttnPairs;
 #define FMKV_ATTN_WG_PER_CU 1
 #endif
 constexpr int kAttnWgPerCu = FMKV_ATTN_WG_PER_CU;
+// The XCD-aware single-sequence plan needs at least one block per stream in
+// every split.
+constexpr int kAttnPlanMinSkewBlocks = kAttnPairs;
 
 struct AppendArgs {
   Store st;
@@ -67,6 +70,8 @@ struct AttnArgs {
   float c;            // 1/sqrt(D)
   float sqrt_d;       // sqrt(D) (f32): binning scale of a codebook decode step's new token
   int32_t bps0;       // blocks of split 0 (>= bps)
+  int32_t skew_p = 0;      // XCD-aware plan (split_range): period of the larger splits, 0 = off
+  int32_t skew_extra = 0;  // number of splits with bps + 1 blocks
   int32_t bps;        // blocks of every later split
   int32_t max_splits; // split columns of the grid
   int32_t part_stride;  // partial slots per sequence: max_splits + new_col

@@ -77,11 +77,10 @@ __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
   const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
-  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits);
+  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits, a.skew_p);
   if (split >= n_splits) return;
-  const int64_t b_begin = geo.blk_lo + (split == 0 ? 0 : a.bps0 + (int64_t)(split - 1) * a.bps);
-  int64_t b_end = b_begin + (split == 0 ? a.bps0 : a.bps);
-  if (b_end > geo.blk_hi) b_end = geo.blk_hi;
+  int64_t b_begin, b_end;
+  split_range(geo, split, a.bps0, a.bps, a.skew_p, a.skew_extra, &b_begin, &b_end);
   const int nb = (int)(b_end - b_begin);
 
   const int32_t* table =

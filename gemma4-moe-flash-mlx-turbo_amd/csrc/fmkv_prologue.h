@@ -3,10 +3,11 @@
 // row layout (lane l holds dims l*E .. l*E+E-1 of a D = 64*E row):
 //   K = RoPE(k_norm(k_proj)), each rounded to bf16;
 //   V = v_norm(v_proj) in f32 (or v_norm of the raw K on K==V layers).
-// Every float op is written out in the oracle's order (the sources are built
-// with -ffp-contract=off), so the append kernel and the decode step's
-// new-token column, which both use these helpers, store the same codes as the
-// oracle does.
+// Every float op is written out in the oracle's order, with FMA contraction
+// off in each helper's body (also in the attention sources, which are built
+// with contraction on), so the append kernel and the decode step's new-token
+// column, which both use these helpers, store the same codes as the oracle
+// does.
 #pragma once
 #include "fmkv_device.h"
 
@@ -17,6 +18,7 @@ namespace {
 // xor-butterfly over all 64 lanes.
 template <int E>
 __device__ inline float canonical_sumsq(const float (&x)[E], int lane) {
+#pragma clang fp contract(off)
   float acc = x[0] * x[0];
 #pragma unroll
   for (int i = 1; i < E; i++) {
@@ -52,6 +54,7 @@ __device__ inline float2 rope_cos_sin(int64_t pos, float f) {
 // x = bf16((x * (1 / sqrt(sum(x^2) / D + eps))) * w), the canonical sum.
 template <int E>
 __device__ inline void k_norm_row(float (&x)[E], const float (&w)[E], float eps, int lane) {
+#pragma clang fp contract(off)
   constexpr int D = 64 * E;
   const float rn = 1.0f / sqrtf(canonical_sumsq<E>(x, lane) / (float)D + eps);
 #pragma unroll
@@ -64,6 +67,7 @@ __device__ inline void k_norm_row(float (&x)[E], const float (&w)[E], float eps,
 // at or past rope_dims are left as they are. Every lane must call it.
 template <int E, typename CS>
 __device__ inline void rope_row(float (&x)[E], int rope_dims, int lane, CS cs) {
+#pragma clang fp contract(off)
   const int half = rope_dims >> 1;
   const int m = half / E;
   float p[E];
@@ -84,6 +88,7 @@ __device__ inline void rope_row(float (&x)[E], int rope_dims, int lane, CS cs) {
 // mean = bf16(sum(x2) / D) (canonical sum); x = x * (1 / sqrt(mean + eps)).
 template <int E>
 __device__ inline void v_norm_row(float (&x)[E], float eps, int lane) {
+#pragma clang fp contract(off)
   constexpr int D = 64 * E;
   float acc = bf16_round(x[0] * x[0]);
 #pragma unroll

@@ -10,8 +10,8 @@
 // becomes edge / q0 and the bias the edge itself, else the bias is 0; codes
 // are clip(rint((y - bias) / scale), 0, 2^b - 1) with the f32 scale and
 // bias, which are then stored as f16. rint rounds half to even. Every
-// operation is written in the oracle's order (the build disables FMA
-// contraction).
+// operation is written in the oracle's order, with FMA contraction off (the
+// pragma in the function body holds in sources built with contraction on).
 #pragma once
 #include "fmkv_device.h"
 
@@ -22,6 +22,7 @@ namespace fmkv {
 template <int E, int BITS>
 __device__ inline void affine_quant(const float (&y)[E], uint32_t (&code)[E], float& scale_o,
                                     float& bias_o, int lane) {
+#pragma clang fp contract(off)
   constexpr int kLanesPerGroup = 64 / E;
   float mx = y[0], mn = y[0];
 #pragma unroll

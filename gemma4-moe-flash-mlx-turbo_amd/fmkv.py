@@ -47,7 +47,8 @@ EXPORTED = (
     "fmkv_pool_create", "fmkv_pool_destroy", "fmkv_paged_append", "fmkv_paged_decode_attention",
     "fmkv_cache_append_projected", "fmkv_paged_append_projected",
     "fmkv_pool_read_codes", "fmkv_set_blocks_per_split", "fmkv_cache_decode_splits",
-    "fmkv_profile_enable", "fmkv_profile_collect", "fmkv_decode_step", "fmkv_paged_decode_step",
+    "fmkv_profile_enable", "fmkv_profile_collect", "fmkv_profile_collect_each",
+    "fmkv_decode_step", "fmkv_paged_decode_step",
     "fmkv_prefill_step", "fmkv_paged_prefill_step", "fmkv_decode_step_noalloc",
     "fmkv_decode_step_projected", "fmkv_paged_decode_step_projected",
 )
@@ -147,6 +148,7 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         "fmkv_cache_decode_splits": ([vp, P(i32)], ctypes.c_int),
         "fmkv_profile_enable": ([i32], ctypes.c_int),
         "fmkv_profile_collect": ([P(ctypes.c_double), P(i32)], ctypes.c_int),
+        "fmkv_profile_collect_each": ([P(ctypes.c_float), i32, P(i32)], ctypes.c_int),
         "fmkv_decode_step": ([vp, vp, vp, i64, vp, i32, ctypes.c_float, ctypes.c_float, vp, i32,
                               vp], ctypes.c_int),
         "fmkv_decode_step_noalloc": ([vp, vp, vp, i64, vp, i32, ctypes.c_float, ctypes.c_float, vp,
@@ -224,6 +226,13 @@ def profile_collect() -> tuple[float, int]:
     ms, n = ctypes.c_double(), ctypes.c_int32()
     _check(load_library().fmkv_profile_collect(ctypes.byref(ms), ctypes.byref(n)))
     return ms.value, n.value
+
+
+def profile_collect_each(capacity: int) -> list[float]:
+    """Kernel milliseconds of each launch timed since the last collect."""
+    buf, n = (ctypes.c_float * max(capacity, 1))(), ctypes.c_int32()
+    _check(load_library().fmkv_profile_collect_each(buf, capacity, ctypes.byref(n)))
+    return [buf[i] for i in range(n.value)]
 
 
 class KVCache:

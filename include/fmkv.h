@@ -313,7 +313,13 @@ int fmkv_set_blocks_per_split(int32_t blocks_per_split);
  * clears the records. */
 int fmkv_profile_enable(int32_t max_records);
 int fmkv_profile_collect(double* total_ms, int32_t* n_records);
-/* Split count the next decode call on `cache` will use (for profiling). */
+/* As fmkv_profile_collect, but writes each recorded launch's kernel time in
+ * milliseconds to ms_out[0 .. *n_records) (FMKV_ERR_CAPACITY when capacity
+ * is smaller than the number of records). */
+int fmkv_profile_collect_each(float* ms_out, int32_t capacity, int32_t* n_records);
+/* Split columns per KV head that the next fmkv_decode_attention call on
+ * `cache` will launch (for profiling; the decode step adds its new-token
+ * column to these and plans around it). */
 int fmkv_cache_decode_splits(const fmkv_cache* cache, int32_t* n_splits);
 
 #ifdef __cplusplus
