@@ -350,18 +350,21 @@ void plan_splits(int cus, int H, int32_t n_seqs, int64_t nblk, int wg_per_cu, in
   // CU: the work-groups (KV head h, split s) go round-robin to the 8 XCDs by
   // linear id h + 2 s, so the splits s = 0 mod 4 land on XCDs 0 and 1, which
   // start first (the others start 1.4 to 4.4 us later). Every CU gets a split
-  // of bps blocks (a multiple of the 4 block streams when bps is) and the
-  // blocks left over go one each to those early splits, instead of bps + 1
-  // blocks for every work-group and some CUs left idle.
+  // of bps blocks and the blocks left over go one each to the splits
+  // s = 0 mod p, p = 4 when they fit there (else 2, else 1: the first
+  // splits), instead of bps + 1 blocks for every work-group and some CUs
+  // left idle.
   if (n_seqs == 1 && H == 2 && wg_per_cu == 1 && tau == 0.0f && !paged &&
       g_bps_override <= 0) {
     const int64_t n_s = (cus - (int64_t)new_col * H) / H;
     const int64_t b = n_s > 0 ? nblk / n_s : 0;
     const int64_t extra = nblk - n_s * b;
-    if (n_s >= 8 && b >= fmkv::kAttnPlanMinSkewBlocks && extra <= (n_s + 3) / 4) {
+    if (n_s >= 8 && b >= fmkv::kAttnPlanMinSkewBlocks) {
+      int p = 4;
+      while (p > 1 && extra > (n_s + p - 1) / p) p >>= 1;
       a->bps = a->bps0 = (int32_t)b;
       a->max_splits = (int32_t)n_s;
-      a->skew_p = 4;
+      a->skew_p = p;
       a->skew_extra = (int32_t)extra;
     }
   }
