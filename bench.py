@@ -201,7 +201,7 @@ def run_c3(args) -> dict:
     # without the per-launch cost of eager submission. Informational; the
     # headline value above is eager.
     graph_us = None
-    if args.graph_steps > 0 and tau == 0.0:
+    if args.graph_steps > 0:
         gs = torch.cuda.Stream()
         gs.wait_stream(torch.cuda.current_stream())
         torch.cuda.synchronize()

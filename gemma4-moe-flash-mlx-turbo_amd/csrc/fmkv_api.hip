@@ -374,7 +374,7 @@ void plan_splits(int cus, int H, int32_t n_seqs, int64_t nblk, int wg_per_cu, in
 // decode attention; new_col adds the decode step's new-token column.
 template <typename Owner>
 int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, int64_t nblk,
-                             const void* q, int32_t n_q_heads, float scale, float tau, void* out,
+                             int64_t blk_cap, const void* q, int32_t n_q_heads, float scale, float tau, void* out,
                              int32_t out_dtype, int wg_per_cu, int min_bps, int first_mult,
                              int new_col, fmkv::AttnArgs* a, ExtWorkspace ext = {}) {
   int rc = check_attn_args(o->desc, q, n_q_heads, tau, out, out_dtype);
@@ -401,7 +401,14 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   a->out_f32 = out_dtype == FMKV_DTYPE_F32;
   const size_t n_rows = a->direct ? 0 : (size_t)n_seqs * a->part_stride * n_q_heads;
   const size_t n_stats = tau > 0.0f ? 3 * (size_t)n_seqs * n_q_heads : 0;
-  const size_t need = (n_rows * (D + 2) + n_stats) * sizeof(float);
+  // sparse-V block maxima, 16-byte aligned (read as float4)
+  const size_t blk_off = (n_rows * (D + 2) + n_stats + 3) & ~(size_t)3;
+  // (rows sized for the most blocks a sequence can hold, so that the
+  // library's workspace does not grow as the context does; a caller's
+  // scratch holds the call's blocks only)
+  a->blk_stride = (int32_t)std::max<int64_t>(std::max<int64_t>(nblk, ext.ptr ? 0 : blk_cap), 1);
+  const size_t n_blk = tau > 0.0f ? (size_t)n_seqs * H * a->blk_stride * 8 : 0;
+  const size_t need = (n_blk ? blk_off + n_blk : n_rows * (D + 2) + n_stats) * sizeof(float);
   float* ws = ext.ptr;
   if (ws) {
     if (need > ext.bytes)
@@ -416,6 +423,7 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   a->part_o = n_rows ? ws : nullptr;
   a->part_ml = n_rows ? ws + n_rows * D : nullptr;
   a->tau_stats = n_stats ? ws + n_rows * (D + 2) : nullptr;
+  a->blk_max = n_blk ? ws + blk_off : nullptr;
   return FMKV_OK;
 }
 
@@ -433,8 +441,9 @@ int prepare_attention(fmkv_cache* c, int64_t T, const void* q, int32_t n_q_heads
   const int64_t nblk =
       (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
   const int wg_per_cu = attn_wg_per_cu(c->desc);
-  return prepare_attention_common(c, cache_store(c), 1, nblk, q, n_q_heads, scale, tau, out,
-                                  out_dtype, wg_per_cu, 1, 1, new_col, a, ext);
+  const int64_t blk_cap = n_slots_of(c->desc) / fmkv::kBlockTokens;
+  return prepare_attention_common(c, cache_store(c), 1, nblk, blk_cap, q, n_q_heads, scale, tau,
+                                  out, out_dtype, wg_per_cu, 1, 1, new_col, a, ext);
 }
 
 int prepare_paged_append(const fmkv_pool* p, const void* k, const void* v,
@@ -495,7 +504,8 @@ int prepare_paged_attention(fmkv_pool* p, const void* q, const int32_t* block_ta
   const int min_bps = (int)std::min<int64_t>(64, std::max<int64_t>(share, 1));
   const int64_t bps = choose_bps(total, p->cus, 6 * fmkv::kAttnWgPerCu, 0, min_bps);
   const int first_mult = total >= 4 * (int64_t)p->cus * bps ? 4 : 1;
-  return prepare_attention_common(p, pool_store(p, block_tables, max_blocks), n_s, nblk, q,
+  return prepare_attention_common(p, pool_store(p, block_tables, max_blocks), n_s, nblk,
+                                  max_blocks, q,
                                   n_q_heads, scale, tau, out, out_dtype, 6 * fmkv::kAttnWgPerCu,
                                   min_bps, first_mult, new_col, a);
 }

@@ -68,10 +68,27 @@ namespace {
 // Kernel modes. Dense: softmax attention. Sparse-V (src/model/
 // gemma4_attention.rs:196-234, weights below tau zeroed without
 // renormalisation) takes two passes over the cache: kStats streams only the
-// keys and writes each split's (m, l); kGated is the dense pass with every
-// score below its head's threshold theta = M + log2(tau * L) dropped, and the
-// combine divides by the full L of the stats pass.
+// keys and writes each split's (m, l) and each block's largest score per
+// head; kGated derives every head's threshold theta = M + log2(tau * L)
+// from those, visits only the blocks that hold a score at or above it and
+// is the dense pass with every score below theta dropped; the combine
+// divides by the full L of the stats pass.
 constexpr int kDense = 0, kStats = 1, kGated = 2;
+
+// A stream's visiting order in the gated pass: the set bits of `mask` in
+// increasing order, then next, next + 1, ... below n (scalar values).
+struct BlockList {
+  uint64_t mask;
+  int next, n;
+  __device__ int pop() {
+    if (mask) {
+      const int i = __builtin_ctzll(mask);
+      mask &= mask - 1;
+      return i;
+    }
+    return next < n ? next++ : n;
+  }
+};
 
 // Staging plan of one (head_dim, bits, stream kind). A block stream is a
 // wave pair (each wave owns half the 64-dim groups, SOLO false) or a single
@@ -420,6 +437,7 @@ void decode_attn_kernel(AttnArgs a) {
   __shared__ __align__(16) uint8_t scratch[P::kScratch];  // q-prep table, then score exchange
   __shared__ float ml_s[P::kStreams][8][2];
   __shared__ int xflag[P::kWaves];
+  __shared__ float th_s[8];  // sparse-V gated pass: the group's thresholds
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -474,6 +492,72 @@ void decode_attn_kernel(AttnArgs a) {
   // this stream's blocks: pb0 + NS i, i < nb
   const int64_t pb0 = b_begin + stream;
   const int nb = pb0 < b_end ? (int)((b_end - pb0 + NS - 1) / NS) : 0;
+  const int64_t blk_row = ((int64_t)seq * a.st.n_kv_heads + kvh) * a.blk_stride;
+  // Sparse-V gated pass: the stream visits only the blocks in which some
+  // head's largest score (from the stats pass) reaches its theta, plus the
+  // block of the newest token (which the stats pass's split columns leave
+  // out when its new-token column attends it); a block whose weights are
+  // all below tau adds nothing to O. Lane i tests block i (i < 64; any
+  // blocks beyond are always visited); the visits pop the mask's bits in
+  // order, as scalars.
+  BlockList blist{0ull, 0, nb};
+  int nbx = nb;  // blocks visited
+  if constexpr (MODE == kGated) {
+    // The thresholds from the stats pass's split statistics (its split
+    // columns and new-token column): wave w < G merges q head kvh * G + w,
+    // lane i splits i, i + 64, ..., the lanes meeting in a butterfly, into
+    // the full softmax max M and sum L; theta = M + log2(tau * L), so that a
+    // weight 2^(s - M) / L >= tau exactly when its base-2 score s >= theta
+    // (no visible token: +inf). Split column 0 stores theta, M and L for the
+    // combine.
+    if (wave < G) {
+      const int n_stat = n_splits + a.stats_new_col;
+      const int64_t base = (int64_t)seq * a.part_stride * a.n_q_heads + kvh * G + wave;
+      float M = -INFINITY, Ls = 0.0f;
+      for (int sp = lane; sp < n_stat; sp += 64) {
+        const float2 ml =
+            *reinterpret_cast<const float2*>(a.part_ml + (base + (int64_t)sp * a.n_q_heads) * 2);
+        const float mn = fmaxf(M, ml.x);
+        Ls = fmaf(ml.y, exp2f(ml.x - mn), Ls * exp2f(M - mn));
+        M = mn;
+      }
+      const float Mw = group_max<64>(M, lane);
+      Ls = group_sum<64>(Ls > 0.0f ? Ls * exp2f(M - Mw) : 0.0f, lane);
+      const float th = Ls > 0.0f ? Mw + log2f(a.tau * Ls) : INFINITY;
+      if (lane == 0) {
+        th_s[wave] = th;
+        if (split == 0) {
+          const int64_t nh = (int64_t)gridDim.y * a.n_q_heads;
+          const int64_t r = (int64_t)seq * a.n_q_heads + kvh * G + wave;
+          a.tau_stats[r] = th;
+          a.tau_stats[nh + r] = Mw;
+          a.tau_stats[2 * nh + r] = Ls;
+        }
+      }
+    }
+    __syncthreads();
+    float thk[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) thk[k] = k < G ? th_s[k] : INFINITY;
+    const int64_t last_blk =
+        T > 0 ? (a.window > 0 ? (T - 1) % a.window : T - 1) / kBlockTokens : -1;
+    bool need = false;
+    if (lane < nb) {
+      const int64_t bl = pb0 + (int64_t)NS * lane, rb = bl - geo.blk_lo;
+      need = bl == last_blk || rb >= a.blk_stride;
+      if (!need) {
+        const float4_t m0 = *reinterpret_cast<const float4_t*>(a.blk_max + (blk_row + rb) * 8);
+        const float4_t m1 = *reinterpret_cast<const float4_t*>(a.blk_max + (blk_row + rb) * 8 + 4);
+#pragma unroll
+        for (int k = 0; k < 4; k++) need = need || m0[k] >= thk[k] || m1[k] >= thk[k + 4];
+      }
+    }
+    const uint64_t mask = __ballot(need);
+    blist.mask = mask;
+    blist.next = 64;
+    nbx = __builtin_popcountll(mask) + (nb > 64 ? nb - 64 : 0);
+  }
+  BlockList bcopy = blist;  // the copies run ahead of the visits on the same list
   uint8_t* const pstage = stage + stream * NST * SB;
   const uint32_t pstage_lds = lds_addr(pstage);
 
@@ -509,14 +593,14 @@ void decode_attn_kernel(AttnArgs a) {
   copy_q_row<D>(a, scratch, seq, kvh, wave, lane);
 #pragma unroll
   for (int s = 0; s < NQ; s++)
-    if (s < nb) copy_block(s, pb0 + (int64_t)NS * s);
-  wait_copies<CP, NQ>(nb < NQ ? nb : NQ);  // the q copy preceded every block
+    if (s < nbx) copy_block(s, pb0 + (int64_t)NS * (MODE == kGated ? bcopy.pop() : s));
+  wait_copies<CP, NQ>(nbx < NQ ? nbx : NQ);  // the q copy preceded every block
   // this lane's RHT signs, for the q rotation and the inverse rotation
   const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
   build_q_table<D, BITS>(a, scratch, wave, lane, sbits);
 #pragma unroll
   for (int s = NQ; s < NST; s++)
-    if (s < nb) copy_block(s, pb0 + (int64_t)NS * s);
+    if (s < nbx) copy_block(s, pb0 + (int64_t)NS * (MODE == kGated ? bcopy.pop() : s));
 
   // B operands of this wave's groups (hi / residual halves of q_rot) and
   // their q sums for the bias term
@@ -569,17 +653,9 @@ void decode_attn_kernel(AttnArgs a) {
   // hold the position it replaces, or be written meanwhile)
   int64_t ex_slot = -1;
   if (a.new_col && T > 0) ex_slot = a.window > 0 ? (T - 1) % a.window : T - 1;
-  // sparse-V: this column's score threshold (scalar loads of the group's
-  // thresholds, then a per-lane select)
+  // sparse-V: this column's score threshold
   float theta = -INFINITY;
-  if constexpr (MODE == kGated) {
-    typedef const float __attribute__((address_space(4)))* cfloat_ptr;
-    const cfloat_ptr th = (cfloat_ptr)(uintptr_t)(a.tau_stats + (int64_t)seq * a.n_q_heads + kvh * G);
-#pragma unroll
-    for (int k = 0; k < 8; k++)
-      if (k < G) theta = head == k ? th[k] : theta;
-    if (!col_valid) theta = -INFINITY;
-  }
+  if constexpr (MODE == kGated) theta = col_valid ? th_s[head] : -INFINITY;
 
   // LDS operands, read one group ahead of their use so that the read
   // latency overlaps the previous group's MFMAs
@@ -670,6 +746,12 @@ void decode_attn_kernel(AttnArgs a) {
     float mb = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     mb = xor16_max(mb);
     mb = xor32_max(mb);
+    if constexpr (MODE == kStats) {
+      // the block's largest score per head, for the gated pass's block skip
+      const int64_t rb = b - geo.blk_lo;
+      if (half == 0 && j == 0 && hi && rb < a.blk_stride)
+        a.blk_max[(blk_row + rb) * 8 + head] = col_valid ? mb : -INFINITY;
+    }
     // The reference max moves only when a score exceeds it by more than
     // kRescaleSlack (base 2): O, l and the bias sums are then rescaled, which
     // costs a multiply per accumulator; below that, p = 2^(s - m_run) stays
@@ -742,11 +824,11 @@ void decode_attn_kernel(AttnArgs a) {
   // issued after it (the next min(NST - 1, nb - 1 - i) blocks) are pending;
   // once read, the stage is refilled with block i + NST
   int st = 0;
-  for (int i = 0; i < nb; i++) {
-    const int rest = nb - 1 - i;
+  for (int i = 0; i < nbx; i++) {
+    const int rest = nbx - 1 - i;
     wait_copies<CP, NST - 1>(rest < NST - 1 ? rest : NST - 1);
-    process(pstage + st * SB, pb0 + (int64_t)NS * i, i);
-    if (i + NST < nb) copy_block(st, pb0 + (int64_t)NS * (i + NST));
+    process(pstage + st * SB, pb0 + (int64_t)NS * (MODE == kGated ? blist.pop() : i), i);
+    if (i + NST < nbx) copy_block(st, pb0 + (int64_t)NS * (MODE == kGated ? bcopy.pop() : i + NST));
     st = st + 1 == NST ? 0 : st + 1;
   }
 
@@ -952,36 +1034,6 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
   }
 }
 
-// Sparse-V thresholds from the stats pass, one wave per (q head, sequence):
-// the full softmax max M and sum L over the splits' (m, l) (lane i merges
-// splits i, i + 64, ...; the lanes meet in a butterfly), and
-// theta = M + log2(tau * L), so that a weight 2^(s - M) / L >= tau exactly
-// when its base-2 score s >= theta. No visible token: theta = +inf.
-__global__ __launch_bounds__(64) void tau_threshold_kernel(AttnArgs a) {
-  const int h = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
-  const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
-  const SeqGeom geo =
-      seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
-  // the statistics pass's splits and its new-token column
-  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits, a.skew_p) + a.new_col;
-  const int64_t base = (int64_t)seq * a.part_stride * a.n_q_heads + h;
-  float M = -INFINITY, L = 0.0f;
-  for (int sp = lane; sp < n_splits; sp += 64) {
-    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (base + (int64_t)sp * a.n_q_heads) * 2);
-    const float mn = fmaxf(M, ml.x);
-    L = fmaf(ml.y, exp2f(ml.x - mn), L * exp2f(M - mn));
-    M = mn;
-  }
-  const float Mw = group_max<64>(M, lane);
-  L = group_sum<64>(L > 0.0f ? L * exp2f(M - Mw) : 0.0f, lane);
-  if (lane == 0) {
-    const int64_t nh = (int64_t)gridDim.y * a.n_q_heads, r = (int64_t)seq * a.n_q_heads + h;
-    a.tau_stats[r] = L > 0.0f ? Mw + log2f(a.tau * L) : INFINITY;
-    a.tau_stats[nh + r] = Mw;
-    a.tau_stats[2 * nh + r] = L;
-  }
-}
-
 // The split kernel of one mode; with events, they are recorded by the
 // dispatch itself (start and end of the kernel's execution, as a kernel
 // trace times it), else a plain launch.
@@ -1011,13 +1063,13 @@ hipError_t launch_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s
   hipError_t e;
   if (a.tau > 0.0f) {
     // sparse-V: the stats pass (with a decode step's new-token column, which
-    // appends the token), the thresholds, the gated pass over every stored
-    // token (the new one included) and the combine of its splits
+    // appends the token), the gated pass over every stored token (the new
+    // one included; it derives the thresholds from the stats pass's
+    // partials) and the combine of its splits
     if ((e = launch_split<D, BITS, kStats>(a, grid, s, nullptr, nullptr)) != hipSuccess) return e;
-    hipLaunchKernelGGL(tau_threshold_kernel, dim3(a.n_q_heads, n_seqs), dim3(64), 0, s, a);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
     AttnArgs g = a;
     g.new_col = 0;
+    g.stats_new_col = a.new_col;
     if ((e = launch_split<D, BITS, kGated>(g, dim3(n_kv_heads, n_seqs, a.max_splits), s, ev0, ev1)) !=
         hipSuccess)
       return e;

@@ -93,12 +93,20 @@ struct AttnArgs {
   float eps = 0.0f;
   int32_t rope_dims = 0;
   float rope_theta = 0.0f;
-  // Sparse-V threshold (0: dense). With tau > 0 a stats pass writes, per
+  // Sparse-V threshold (0: dense). With tau > 0 the gated pass writes, per
   // (sequence, q head), the base-2 score threshold theta = M + log2(tau * L)
-  // and the full softmax max M and sum L: tau_stats = [theta | M | L], each
-  // [n_seqs][n_q_heads].
+  // and the full softmax max M and sum L of the stats pass: tau_stats =
+  // [theta | M | L], each [n_seqs][n_q_heads], for the combine.
   float tau;
   float* tau_stats;
+  // Sparse-V: the stats pass's largest base-2 score per (sequence, KV head,
+  // block) and q head of the group, [n_seqs][n_kv_heads][blk_stride][8]
+  // (-inf for heads beyond the group; block index relative to the first
+  // visible block); the gated pass skips the blocks in which no head has a
+  // score at or above its theta.
+  float* blk_max = nullptr;
+  int32_t blk_stride = 0;
+  int32_t stats_new_col = 0;  // gated pass: the stats pass had a new-token column
 };
 
 // Prefill (chunked) attention: n_q queries at positions p0 .. p0 + n_q - 1,

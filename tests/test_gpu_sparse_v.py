@@ -108,6 +108,66 @@ def test_sparse_v_split_counts_agree(gpu, ora, bps):
     check_attention(out, ref, f"bps={bps}")
 
 
+@pytest.mark.parametrize("bps", [40, 300])
+@pytest.mark.parametrize("scale,tau", [(1.0, 1e-3), (0.05, 1.0 / 12000)])
+def test_sparse_v_block_skip_long_splits(gpu, ora, bps, scale, tau):
+    """The gated pass visits only the blocks in which some head's largest
+    score reaches its threshold (each of a work-group's four block streams
+    tests up to 64 of its blocks at once; bps 300 gives streams of 75 blocks,
+    whose blocks past the 64th are always visited): peaked weights (most
+    blocks skipped) and soft ones, both within tolerance."""
+    import torch
+
+    D, bits, Hkv, Hq, T = 512, 8, 2, 16, 6000
+    cache, oc = filled(gpu, ora, D, bits, Hkv, T, seed=12)
+    q = q_batch(13, Hq, Hkv, D)
+    ref = oc.attention(q, scale, tau)
+    gpu.set_blocks_per_split(bps)
+    try:
+        out = cache.attention(dev_bf16(q), scale, sparse_v_tau=tau, dtype=torch.float32)
+        torch.cuda.synchronize()
+    finally:
+        gpu.set_blocks_per_split(0)
+    check_attention(out, ref, f"bps={bps} scale={scale} tau={tau}")
+
+
+def test_sparse_v_32k_decode_steps(gpu, ora):
+    """Global-layer shape at 32K context (Hq 16, Hkv 2, head_dim 512, 8-bit):
+    decode steps with tau 1e-3 at scale 1.0 and at a soft scale whose tau is
+    the weights' 99.9th percentile, against the oracle; the codes the steps
+    stored bit-exact."""
+    import torch
+    from gpu_util import check_codes, fast_kv, fast_q
+
+    Hq, Hkv, D, bits, T0, L, steps = 16, 2, 512, 8, 32768, 2048, 4
+    cap = T0 + 16
+    cache = gpu.KVCache.new_quantized(D, bits, Hkv, capacity=cap)
+    oc = ora.OracleCache(Hkv, D, bits, 0, cap)
+    for c0 in range(0, T0, L):
+        k = fast_kv(600 + c0, L, Hkv, D, dist="t3", outliers=False)
+        v = fast_kv(100600 + c0, L, Hkv, D, outliers=False)
+        cache.append(dev_bf16(k), dev_bf16(v))
+        oc.append(k, v)
+    k1 = fast_kv(691, steps, Hkv, D, dist="t3", outliers=False)
+    v1 = fast_kv(692, steps, Hkv, D, outliers=False)
+    q = fast_q(693, steps, Hq, Hkv, D, outliers=False)
+    soft = 0.01
+    outs = []
+    for i in range(steps):
+        oc.append(k1[i:i + 1], v1[i:i + 1])
+        scale = 1.0 if i % 2 == 0 else soft
+        tau = 1e-3 if i % 2 == 0 else float(np.quantile(oc.attention_weights(q[i], soft), 0.999))
+        ref = oc.attention(q[i], scale, tau)
+        out = cache.decode_step(dev_bf16(k1[i:i + 1]), dev_bf16(v1[i:i + 1]), dev_bf16(q[i]),
+                                scale, sparse_v_tau=tau, dtype=torch.float32)
+        outs.append((out, ref, scale, tau))
+    codes, meta = cache.read_codes()
+    torch.cuda.synchronize()
+    for i, (out, ref, scale, tau) in enumerate(outs):
+        check_attention(out, ref, f"step {i} scale {scale} tau {tau:.3g}")
+    check_codes(codes, meta, oc, slots=np.arange(T0 - 16, T0 + steps), what="32K sparse-V steps")
+
+
 @pytest.mark.parametrize("D,bits", [(256, 4), (256, 8)])
 def test_sparse_v_ring_steps(gpu, ora, D, bits):
     """Sliding layer W = 64: decode steps through two wraps with tau > 0 (the
