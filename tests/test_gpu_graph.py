@@ -10,7 +10,7 @@ second pass on, every slot holds what the previous pass wrote). The
 workspace is sized by an eager step before the capture (nothing may
 allocate inside it), and the steps stay inside one split plan. Each replay
 is followed by unrelated eager work and a synchronisation, and every
-replay is checked."""
+replay is checked; the same for sparse-V steps (tau > 0)."""
 import pytest
 
 from gpu_util import dev_bf16, kv_batch
@@ -19,11 +19,12 @@ import synth
 pytestmark = pytest.mark.gpu
 
 
+@pytest.mark.parametrize("tau", [0.0, 0.01])  # dense; sparse-V (stats, gated, combine)
 @pytest.mark.parametrize("D,bits,Hkv,Hq,W,T0", [
     (512, 8, 2, 16, 0, 295),   # global layer: positions 296..304 stay in 19 blocks
     (256, 4, 8, 16, 64, 200),  # sliding ring: 4 blocks once full
 ])
-def test_graph_replays_match_eager(gpu, D, bits, Hkv, Hq, W, T0):
+def test_graph_replays_match_eager(gpu, D, bits, Hkv, Hq, W, T0, tau):
     import torch
 
     cap = 0 if W else T0 + 32
@@ -35,11 +36,12 @@ def test_graph_replays_match_eager(gpu, D, bits, Hkv, Hq, W, T0):
     qs = [dev_bf16(synth.q_rows(70 + j, Hq, Hkv, D, None)) for j in range(n + 1)]
     for c in caches:
         c.append(k0, v0)
-        c.decode_step(ks[0], vs[0], qs[0], 1.0, dtype=torch.float32)  # sizes the workspace
+        # sizes the workspace
+        c.decode_step(ks[0], vs[0], qs[0], 1.0, sparse_v_tau=tau, dtype=torch.float32)
     eager, graphed = caches
     passes = 3 if W else 1
-    want = [[eager.decode_step(ks[j], vs[j], qs[j], 1.0, dtype=torch.float32) for j in range(1, n + 1)]
-            for _ in range(passes)]
+    want = [[eager.decode_step(ks[j], vs[j], qs[j], 1.0, sparse_v_tau=tau, dtype=torch.float32)
+             for j in range(1, n + 1)] for _ in range(passes)]
     torch.cuda.synchronize()
 
     outs = [torch.empty((Hq, D), dtype=torch.float32, device="cuda") for _ in range(n)]
@@ -48,7 +50,8 @@ def test_graph_replays_match_eager(gpu, D, bits, Hkv, Hq, W, T0):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
         for j in range(n):
-            graphed.decode_step(ks[j + 1], vs[j + 1], qs[j + 1], 1.0, out=outs[j], stream=s)
+            graphed.decode_step(ks[j + 1], vs[j + 1], qs[j + 1], 1.0, sparse_v_tau=tau, out=outs[j],
+                                stream=s)
     for rep in range(3):
         for o in outs:
             o.fill_(float("nan"))
