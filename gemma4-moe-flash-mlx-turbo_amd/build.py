@@ -14,7 +14,10 @@ one shared library next to this file. Compile flags:
                              share with the append turn contraction off in
                              their bodies (#pragma clang fp contract(off));
   -packed-fp32-ops disabled  no packed FP32 instructions are generated;
-  -amdgpu-mfma-vgpr-form=1   MFMA accumulators in VGPRs (see HIP_FLAGS).
+  -amdgpu-mfma-vgpr-form=1   MFMA accumulators in VGPRs (see HIP_FLAGS);
+  -amdgpu-kernarg-preload-count=14
+                             PRELOAD_SOURCES: the leading scalar kernel
+                             arguments arrive in SGPRs with the dispatch.
 """
 from __future__ import annotations
 
@@ -55,6 +58,9 @@ HIP_FLAGS = [
 # attention sources: contraction on, except where a pragma turns it off
 CONTRACT_SOURCES = {"fmkv_attention.hip", "fmkv_cb_attention.hip", "fmkv_plain_attention.hip",
                     "fmkv_prefill.hip"}
+# sources whose kernels take their first 14 argument dwords as scalars that
+# the dispatch preloads into SGPRs
+PRELOAD_SOURCES = {"fmkv_attention.hip"}
 
 
 def hipcc() -> str:
@@ -69,6 +75,8 @@ def _compile(src: Path, obj: Path) -> tuple[Path, str]:
     if src.name in CONTRACT_SOURCES:
         flags = ["-ffp-contract=fast-honor-pragmas" if f == "-ffp-contract=off" else f
                  for f in HIP_FLAGS]
+    if src.name in PRELOAD_SOURCES:
+        flags = [*flags, "-mllvm", "-amdgpu-kernarg-preload-count=14"]
     cmd = [hipcc(), *flags, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     out = (res.stdout + res.stderr)

@@ -154,13 +154,17 @@ struct AttnPlan {
 // Raw bf16 q row of GQA head `wave` of (seq, kvh) (D * 2 bytes) to LDS at
 // dst + wave * D * 2, copied by that wave itself (lanes < D / 8).
 template <int D>
-__device__ inline void copy_q_row(const AttnArgs& a, uint8_t* dst, int seq, int kvh, int wave,
-                                  int lane) {
-  if (wave < a.group && lane < D / 8) {
-    const uint16_t* qh =
-        a.q + ((int64_t)seq * a.n_q_heads + (int64_t)kvh * a.group + wave) * D;
+__device__ inline void copy_q_row(const uint16_t* q, int n_q_heads, int group, uint8_t* dst,
+                                  int seq, int kvh, int wave, int lane) {
+  if (wave < group && lane < D / 8) {
+    const uint16_t* qh = q + ((int64_t)seq * n_q_heads + (int64_t)kvh * group + wave) * D;
     dma16(lds_addr(dst + wave * D * 2), lane * 16, buffer_rsrc(qh, (uint32_t)(D * 2)));
   }
+}
+template <int D>
+__device__ inline void copy_q_row(const AttnArgs& a, uint8_t* dst, int seq, int kvh, int wave,
+                                  int lane) {
+  copy_q_row<D>(a.q, a.n_q_heads, a.group, dst, seq, kvh, wave, lane);
 }
 
 // q_rot = (FWHT(q * qscale) * c) o s of the work-group's GQA heads (q . R,
@@ -418,11 +422,26 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, float2* rope, 
 
 // Pair work-groups: 8 waves, two per SIMD (register budget <= 256 each);
 // solo work-groups: 12 waves, three per SIMD (<= 168).
-template <int D, int BITS, int MODE, bool SOLO>
+// Arguments: what a work-group needs before its first copies comes first,
+// as 14 dwords of scalars, which the build preloads into SGPRs with the
+// dispatch (a scalar load from the argument struct waits 1.5-2 us at a
+// work-group's start); the struct follows. geo_len and geo_vis_begin give
+// the block range (the visible length, at most the window on a ring; the
+// first visible position, 0 on a ring); skew = skew_p | skew_extra << 8;
+// flags: bit 2 new-token column, bits 4-7 q heads per KV head, bits 8-31 q
+// heads. A linear or ring cache's dense or stats pass needs no struct field
+// for its first copies; a paged pool's (PAGED: block table, per-sequence
+// lengths) needs the struct from the start. (Measured: C3 step 23.4 -> 23.2
+// us, 24.0 -> 23.5 us in a HIP graph; the compiler still hoists some of the
+// struct's loads above the first copies.)
+template <int D, int BITS, int MODE, bool SOLO, bool PAGED>
 __global__ __launch_bounds__((AttnPlan<D, BITS, SOLO>::kWaves * 64))
 __attribute__((amdgpu_waves_per_eu(AttnPlan<D, BITS, SOLO>::kWavesPerSimd,
                                    AttnPlan<D, BITS, SOLO>::kWavesPerSimd)))
-void decode_attn_kernel(AttnArgs a) {
+void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
+                        int32_t geo_vis_begin, int32_t window, int32_t bps0, int32_t bps,
+                        int32_t max_splits, uint32_t skew, int32_t block_stride,
+                        int32_t head_stride, uint32_t flags, AttnArgs a) {
   using P = AttnPlan<D, BITS, SOLO>;
   constexpr BlockLayout L = P::L;
   constexpr int NG = P::NG, GH = P::GH;
@@ -446,8 +465,9 @@ void decode_attn_kernel(AttnArgs a) {
   const int j = lane >> 4, c = lane & 15;
   const int head = c & 7;
   const bool hi = c < 8;
-  const int G = a.group;
+  const int G = (int)((flags >> 4) & 15u);
   const bool col_valid = head < G;
+  const int skew_p = (int)(skew & 255u), skew_extra = (int)(skew >> 8);
   // grid (KV head, sequence, split column): consecutive work-groups, which
   // the dispatcher deals round-robin to the XCDs, are the KV heads of one
   // split and then the sequences, so each XCD gets a like share of the work;
@@ -455,44 +475,57 @@ void decode_attn_kernel(AttnArgs a) {
   const int kvh = blockIdx.x, seq = blockIdx.y, split = blockIdx.z;
   const int g0 = half * GH;  // this wave's first group
 
-  const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
-  const SeqGeom geo =
-      seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
-  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits, a.skew_p);
+  // the block range from the preloaded arguments (paged: the sequence's
+  // length, bounded by the table width)
+  int64_t Tg = geo_len;
+  if constexpr (PAGED) Tg = a.seq_lens[seq];
+  SeqGeom geo = seq_geometry(Tg, window, geo_vis_begin);
+  if constexpr (PAGED) {
+    if (geo.blk_hi > a.st.table_stride) geo.blk_hi = a.st.table_stride;
+    if (geo.blk_hi < geo.blk_lo) geo.blk_hi = geo.blk_lo;
+  }
+  const int n_splits = n_splits_for(geo, bps0, bps, max_splits, skew_p);
   static_assert(P::kStageRegion >= D / 2 * (int)sizeof(float2), "rope table fits the staging");
   // decode step: the new token's column (dense mode, or the statistics pass
-  // of a sparse-V step, whose gated pass then reads the stored token)
+  // of a sparse-V step, whose gated pass then reads the stored token), the
+  // grid's last split column
   if constexpr (MODE != kGated) {
-    if (a.new_col && split == (int)gridDim.z - 1) {
-      new_token_column<D, BITS, P::kWaves * 64>(a, scratch, reinterpret_cast<float2*>(stage), T,
-                                                n_splits, kvh, seq, wave, lane);
+    if ((flags & 4u) && split == max_splits) {
+      new_token_column<D, BITS, P::kWaves * 64>(a, scratch, reinterpret_cast<float2*>(stage),
+                                                PAGED ? Tg : a.seq_len, n_splits, kvh, seq, wave,
+                                                lane);
       return;
     }
   }
   if (split >= n_splits) return;
   int64_t b_begin, b_end;
-  split_range(geo, split, a.bps0, a.bps, a.skew_p, a.skew_extra, &b_begin, &b_end);
+  split_range(geo, split, bps0, bps, skew_p, skew_extra, &b_begin, &b_end);
 
   // Table entries are read through the constant address space: a uniform
   // index then becomes a scalar load, which never waits for the copies in
   // flight.
   typedef const int32_t __attribute__((address_space(4)))* table_ptr;
-  const table_ptr table =
-      a.st.block_table
-          ? (table_ptr)(uintptr_t)(a.st.block_table + (int64_t)seq * a.st.table_stride)
-          : nullptr;
-  const uint8_t* hbase = a.st.base + (int64_t)kvh * a.st.head_stride;
+  table_ptr table = nullptr;
+  if constexpr (PAGED)
+    table = (table_ptr)(uintptr_t)(a.st.block_table + (int64_t)seq * a.st.table_stride);
+  const uint8_t* hbase = base + (int64_t)kvh * head_stride;
   auto blk_ptr = [&](int64_t lb) -> const uint8_t* {
-    int64_t phys = table ? (int64_t)table[lb] : lb;
-    // a bad table entry reads a valid block rather than faulting
-    phys = phys < 0 ? 0 : (phys >= a.st.n_blocks ? a.st.n_blocks - 1 : phys);
-    return hbase + phys * a.st.block_stride;
+    if constexpr (!PAGED) {
+      return hbase + lb * block_stride;  // linear or ring: lb is a valid slot block
+    } else {
+      int64_t phys = (int64_t)table[lb];
+      // a bad table entry reads a valid block rather than faulting
+      phys = phys < 0 ? 0 : (phys >= a.st.n_blocks ? a.st.n_blocks - 1 : phys);
+      return hbase + phys * block_stride;
+    }
   };
 
   // this stream's blocks: pb0 + NS i, i < nb
   const int64_t pb0 = b_begin + stream;
   const int nb = pb0 < b_end ? (int)((b_end - pb0 + NS - 1) / NS) : 0;
-  const int64_t blk_row = ((int64_t)seq * a.st.n_kv_heads + kvh) * a.blk_stride;
+  // sparse-V: this (sequence, KV head)'s row of block maxima
+  int64_t blk_row = 0;
+  if constexpr (MODE == kGated) blk_row = ((int64_t)seq * a.st.n_kv_heads + kvh) * a.blk_stride;
   // Sparse-V gated pass: the stream visits only the blocks in which some
   // head's largest score (from the stats pass) reaches its theta, plus the
   // block of the newest token (which the stats pass's split columns leave
@@ -512,11 +545,11 @@ void decode_attn_kernel(AttnArgs a) {
     // combine.
     if (wave < G) {
       const int n_stat = n_splits + a.stats_new_col;
-      const int64_t base = (int64_t)seq * a.part_stride * a.n_q_heads + kvh * G + wave;
+      const int64_t rbase = (int64_t)seq * a.part_stride * a.n_q_heads + kvh * G + wave;
       float M = -INFINITY, Ls = 0.0f;
       for (int sp = lane; sp < n_stat; sp += 64) {
         const float2 ml =
-            *reinterpret_cast<const float2*>(a.part_ml + (base + (int64_t)sp * a.n_q_heads) * 2);
+            *reinterpret_cast<const float2*>(a.part_ml + (rbase + (int64_t)sp * a.n_q_heads) * 2);
         const float mn = fmaxf(M, ml.x);
         Ls = fmaf(ml.y, exp2f(ml.x - mn), Ls * exp2f(M - mn));
         M = mn;
@@ -539,8 +572,9 @@ void decode_attn_kernel(AttnArgs a) {
     float thk[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) thk[k] = k < G ? th_s[k] : INFINITY;
+    const int64_t Tl = PAGED ? Tg : a.seq_len;
     const int64_t last_blk =
-        T > 0 ? (a.window > 0 ? (T - 1) % a.window : T - 1) / kBlockTokens : -1;
+        Tl > 0 ? (a.window > 0 ? (Tl - 1) % a.window : Tl - 1) / kBlockTokens : -1;
     bool need = false;
     if (lane < nb) {
       const int64_t bl = pb0 + (int64_t)NS * lane, rb = bl - geo.blk_lo;
@@ -568,10 +602,12 @@ void decode_attn_kernel(AttnArgs a) {
   const int ks0 = P::kSharedChunk ? half : kc0;               // its first chunk slot
   const int mlane = lane < 4 * GH ? lane : lane - 4 * GH;
   const int meta_voff = (lane < 4 * GH ? (int)L.k_meta : (int)L.v_meta) + g0 * 64 + mlane * 16;
-  auto copy_block = [&](int st, int64_t lb) {
+  // (a stage's first fill follows no reads of it: no wait, so that the
+  // first copies do not wait for the argument struct's scalar loads)
+  auto copy_block = [&](int st, int64_t lb, bool refill) {
     const u32x4 rs = buffer_rsrc(blk_ptr(lb), (uint32_t)L.block_bytes);
     const uint32_t sl = pstage_lds + st * SB;
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of this stage are done
+    if (refill) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of this stage are done
 #pragma unroll
     for (int k = 0; k < P::kWaveChunks; k++) {
       const int ch = kc0 + k, slot = ks0 + k;
@@ -590,17 +626,19 @@ void decode_attn_kernel(AttnArgs a) {
   // rotation's first barrier then waits for less copy issue, which stalls
   // while the whole chip's first requests queue up.
   constexpr int NQ = (NST + 1) / 2;
-  copy_q_row<D>(a, scratch, seq, kvh, wave, lane);
+  copy_q_row<D>(q, (int)(flags >> 8), G, scratch, seq, kvh, wave, lane);
 #pragma unroll
   for (int s = 0; s < NQ; s++)
-    if (s < nbx) copy_block(s, pb0 + (int64_t)NS * (MODE == kGated ? bcopy.pop() : s));
+    if (s < nbx) copy_block(s, pb0 + (int64_t)NS * (MODE == kGated ? bcopy.pop() : s), false);
+  const int64_t T = PAGED ? Tg : a.seq_len;
+  if constexpr (MODE == kStats) blk_row = ((int64_t)seq * a.st.n_kv_heads + kvh) * a.blk_stride;
   wait_copies<CP, NQ>(nbx < NQ ? nbx : NQ);  // the q copy preceded every block
   // this lane's RHT signs, for the q rotation and the inverse rotation
   const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
   build_q_table<D, BITS>(a, scratch, wave, lane, sbits);
 #pragma unroll
   for (int s = NQ; s < NST; s++)
-    if (s < nbx) copy_block(s, pb0 + (int64_t)NS * (MODE == kGated ? bcopy.pop() : s));
+    if (s < nbx) copy_block(s, pb0 + (int64_t)NS * (MODE == kGated ? bcopy.pop() : s), false);
 
   // B operands of this wave's groups (hi / residual halves of q_rot) and
   // their q sums for the bias term
@@ -828,7 +866,8 @@ void decode_attn_kernel(AttnArgs a) {
     const int rest = nbx - 1 - i;
     wait_copies<CP, NST - 1>(rest < NST - 1 ? rest : NST - 1);
     process(pstage + st * SB, pb0 + (int64_t)NS * (MODE == kGated ? blist.pop() : i), i);
-    if (i + NST < nbx) copy_block(st, pb0 + (int64_t)NS * (MODE == kGated ? bcopy.pop() : i + NST));
+    if (i + NST < nbx)
+      copy_block(st, pb0 + (int64_t)NS * (MODE == kGated ? bcopy.pop() : i + NST), true);
     st = st + 1 == NST ? 0 : st + 1;
   }
 
@@ -1037,23 +1076,47 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
 // The split kernel of one mode; with events, they are recorded by the
 // dispatch itself (start and end of the kernel's execution, as a kernel
 // trace times it), else a plain launch.
-template <int D, int BITS, int MODE, bool SOLO>
+template <int D, int BITS, int MODE, bool SOLO, bool PAGED>
 hipError_t launch_kind(const AttnArgs& a, dim3 grid, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
+  const bool ring = a.window > 0;
+  const int64_t geo_len = ring ? std::min<int64_t>(a.seq_len, a.window) : a.seq_len;
+  if (geo_len > INT32_MAX || (!ring && a.vis_begin > INT32_MAX) || a.window > INT32_MAX ||
+      a.st.block_stride > INT32_MAX || a.st.head_stride > INT32_MAX || a.n_q_heads >= (1 << 24) ||
+      a.skew_extra >= (1 << 24) || a.skew_p > 255)
+    return hipErrorInvalidValue;
+  const uint32_t flags =
+      (a.new_col ? 4u : 0u) | ((uint32_t)a.group << 4) | ((uint32_t)a.n_q_heads << 8);
+  const uint32_t skew = (uint32_t)a.skew_p | ((uint32_t)a.skew_extra << 8);
+  const dim3 block(AttnPlan<D, BITS, SOLO>::kWaves * 64);
+  const uint8_t* base = a.st.base;
+  const int32_t gl = (int32_t)geo_len, gvb = ring ? 0 : (int32_t)a.vis_begin;
+  const int32_t w = (int32_t)a.window, bs = (int32_t)a.st.block_stride;
+  const int32_t hs = (int32_t)a.st.head_stride;
   if (ev0 && ev1)
-    hipExtLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SOLO>), grid,
-                          dim3(AttnPlan<D, BITS, SOLO>::kWaves * 64), 0, s, ev0, ev1, 0, a);
+    hipExtLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SOLO, PAGED>), grid, block, 0, s, ev0,
+                          ev1, 0, base, a.q, gl, gvb, w, a.bps0, a.bps, a.max_splits, skew, bs, hs,
+                          flags, a);
   else
-    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SOLO>), grid,
-                       dim3(AttnPlan<D, BITS, SOLO>::kWaves * 64), 0, s, a);
+    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SOLO, PAGED>), grid, block, 0, s, base,
+                       a.q, gl, gvb, w, a.bps0, a.bps, a.max_splits, skew, bs, hs, flags, a);
   return hipGetLastError();
+}
+
+template <int D, int BITS, int MODE, bool SOLO>
+hipError_t launch_paged(const AttnArgs& a, dim3 grid, hipStream_t s, hipEvent_t ev0,
+                        hipEvent_t ev1) {
+  // a paged pool has per-sequence lengths; a cache has neither
+  if ((a.st.block_table != nullptr) != (a.seq_lens != nullptr)) return hipErrorInvalidValue;
+  return a.st.block_table ? launch_kind<D, BITS, MODE, SOLO, true>(a, grid, s, ev0, ev1)
+                          : launch_kind<D, BITS, MODE, SOLO, false>(a, grid, s, ev0, ev1);
 }
 
 template <int D, int BITS, int MODE>
 hipError_t launch_split(const AttnArgs& a, dim3 grid, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   if constexpr (kSoloCapable<D, BITS>) {
-    if (a.bps >= kSoloMinBlocks) return launch_kind<D, BITS, MODE, true>(a, grid, s, ev0, ev1);
+    if (a.bps >= kSoloMinBlocks) return launch_paged<D, BITS, MODE, true>(a, grid, s, ev0, ev1);
   }
-  return launch_kind<D, BITS, MODE, false>(a, grid, s, ev0, ev1);
+  return launch_paged<D, BITS, MODE, false>(a, grid, s, ev0, ev1);
 }
 
 template <int D, int BITS>
