@@ -1002,20 +1002,32 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
 // One work-group per (64 dims, q head, sequence); thread (sl, dq) owns dims
 // d0 + 4*dq .. +3 and splits sl, sl + 16, ..., merged in one pass with a
 // running maximum; the 16 partial merges meet in LDS.
+// Arguments: as the split kernel's, what the kernel needs first comes as
+// leading scalars (preloaded into SGPRs with the dispatch), the struct last.
+// n_cols: split partials per sequence (splits and new-token column), or -1
+// for per-sequence counts from the struct (a paged batch); flags: bit 0 f32
+// output, bit 1 sparse-V, bits 8-31 q heads.
 template <int D>
-__global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) void combine_kernel(const float* part_o, const float* part_ml,
+                                                      void* out, int32_t n_cols,
+                                                      int32_t part_stride, uint32_t flags,
+                                                      AttnArgs a) {
   __shared__ float4_t red_o[16][16];
   __shared__ float red_m[16][16];
   __shared__ float red_l[16][16];
   const int seq = blockIdx.z, h = blockIdx.y, tid = threadIdx.x;
   const int dq = tid & 15, sl = tid >> 4;
   const int d0 = blockIdx.x * 64 + dq * 4;
-  const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
-  const SeqGeom geo =
-      seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
-  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits, a.skew_p) + a.new_col;
-  const int64_t stride = (int64_t)a.n_q_heads;
-  const int64_t base = (int64_t)seq * a.part_stride * stride + h;
+  const int nqh = (int)(flags >> 8);
+  int n_splits = n_cols;
+  if (n_cols < 0) {
+    const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
+    const SeqGeom geo =
+        seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
+    n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits, a.skew_p) + a.new_col;
+  }
+  const int64_t stride = (int64_t)nqh;
+  const int64_t base = (int64_t)seq * part_stride * stride + h;
 
   // split maxima are finite (the split kernel starts from -1e30): the first
   // merge scales the empty state by exp2(-inf) = 0
@@ -1024,8 +1036,8 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
 #pragma unroll 4
   for (int s = sl; s < n_splits; s += 16) {
     const int64_t r = base + s * stride;
-    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + r * 2);
-    const float4_t ov = *reinterpret_cast<const float4_t*>(a.part_o + r * D + d0);
+    const float2 ml = *reinterpret_cast<const float2*>(part_ml + r * 2);
+    const float4_t ov = *reinterpret_cast<const float4_t*>(part_o + r * D + d0);
     const float mn = fmaxf(M, ml.x);
     const float alpha = exp2f(M - mn);
     const float w = exp2f(ml.x - mn);
@@ -1052,23 +1064,24 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
         L = fmaf(w, red_l[k][tid], L);
       }
     }
-    const int64_t o_idx = ((int64_t)seq * a.n_q_heads + h) * D + blockIdx.x * 64 + tid * 4;
+    const int64_t o_idx = ((int64_t)seq * nqh + h) * D + blockIdx.x * 64 + tid * 4;
     // sparse-V: the kept weights are normalised by the full sum L of the
     // stats pass (no renormalisation, gemma4_attention.rs:226-232), taken at
     // its max M
+    const bool sparse = (flags & 2u) != 0;
     float gated = 0.0f;
-    if (a.tau > 0.0f) {
-      const int64_t nh = (int64_t)gridDim.z * a.n_q_heads, r = (int64_t)seq * a.n_q_heads + h;
+    if (sparse) {
+      const int64_t nh = (int64_t)gridDim.z * nqh, r = (int64_t)seq * nqh + h;
       const float Mf = a.tau_stats[nh + r], Lf = a.tau_stats[2 * nh + r];
       gated = (Lf > 0.0f && Mx != -INFINITY) ? exp2f(Mx - Mf) / Lf : 0.0f;
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const float v = a.tau > 0.0f ? s[i] * gated : (L > 0.0f ? s[i] / L : 0.0f);
-      if (a.out_f32)
-        reinterpret_cast<float*>(a.out)[o_idx + i] = v;
+      const float v = sparse ? s[i] * gated : (L > 0.0f ? s[i] / L : 0.0f);
+      if (flags & 1u)
+        reinterpret_cast<float*>(out)[o_idx + i] = v;
       else
-        reinterpret_cast<uint16_t*>(a.out)[o_idx + i] = f32_to_bf16(v);
+        reinterpret_cast<uint16_t*>(out)[o_idx + i] = f32_to_bf16(v);
     }
   }
 }
@@ -1148,12 +1161,26 @@ hipError_t launch_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s
 hipError_t launch_combine(const AttnArgs& a, int n_seqs, hipStream_t s) {
   const int D = a.st.layout.head_dim;
   dim3 cgrid(D / 64, a.n_q_heads, n_seqs);
+  // one cache: the partial count from the plan, as the split kernel sees it
+  int32_t n_cols = -1;
+  if (!a.seq_lens && !a.st.block_table && n_seqs == 1) {
+    const SeqGeom geo = seq_geometry(a.seq_len, a.window, a.vis_begin);
+    n_cols = n_splits_for(geo, a.bps0, a.bps, a.max_splits, a.skew_p) + a.new_col;
+  }
+  if (a.n_q_heads >= (1 << 24)) return hipErrorInvalidValue;
+  const uint32_t flags =
+      (a.out_f32 ? 1u : 0u) | (a.tau > 0.0f ? 2u : 0u) | ((uint32_t)a.n_q_heads << 8);
+  const float* po = a.part_o;
+  const float* pm = a.part_ml;
   if (D == 128)
-    hipLaunchKernelGGL((combine_kernel<128>), cgrid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((combine_kernel<128>), cgrid, dim3(256), 0, s, po, pm, a.out, n_cols,
+                       a.part_stride, flags, a);
   else if (D == 256)
-    hipLaunchKernelGGL((combine_kernel<256>), cgrid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((combine_kernel<256>), cgrid, dim3(256), 0, s, po, pm, a.out, n_cols,
+                       a.part_stride, flags, a);
   else if (D == 512)
-    hipLaunchKernelGGL((combine_kernel<512>), cgrid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((combine_kernel<512>), cgrid, dim3(256), 0, s, po, pm, a.out, n_cols,
+                       a.part_stride, flags, a);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -301,7 +301,7 @@ struct SeqGeom {
   int64_t blk_lo, blk_hi;  // logical blocks to scan
 };
 
-__device__ inline SeqGeom seq_geometry(int64_t T, int64_t window, int64_t vis_begin) {
+__host__ __device__ inline SeqGeom seq_geometry(int64_t T, int64_t window, int64_t vis_begin) {
   SeqGeom g;
   if (window > 0) {
     int64_t filled = T < window ? T : window;
@@ -317,8 +317,8 @@ __device__ inline SeqGeom seq_geometry(int64_t T, int64_t window, int64_t vis_be
 }
 
 // Blocks to scan for one sequence; paged tables bound it by their width.
-__device__ inline SeqGeom seq_geometry(int64_t T, int64_t window, int64_t vis_begin,
-                                       int32_t table_stride, bool paged) {
+__host__ __device__ inline SeqGeom seq_geometry(int64_t T, int64_t window, int64_t vis_begin,
+                                                int32_t table_stride, bool paged) {
   SeqGeom g = seq_geometry(T, window, vis_begin);
   if (paged && g.blk_hi > table_stride) g.blk_hi = table_stride;
   if (g.blk_hi < g.blk_lo) g.blk_hi = g.blk_lo;
@@ -333,8 +333,8 @@ __device__ inline SeqGeom seq_geometry(int64_t T, int64_t window, int64_t vis_be
 // fills the tail with small work-groups.
 // An XCD-aware plan (skew_p > 0, one sequence) sizes the grid to the
 // sequence exactly: every one of its max_splits splits is used.
-__device__ inline int n_splits_for(const SeqGeom& g, int bps0, int bps, int max_splits,
-                                   int skew_p = 0) {
+__host__ __device__ inline int n_splits_for(const SeqGeom& g, int bps0, int bps, int max_splits,
+                                            int skew_p = 0) {
   if (skew_p > 0) return max_splits;
   // block counts stay below 2^31 / 16: a 32-bit division suffices
   const uint32_t nb = (uint32_t)(g.blk_hi - g.blk_lo);
