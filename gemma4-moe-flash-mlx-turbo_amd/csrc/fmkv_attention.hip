@@ -1091,27 +1091,17 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* part_o, const
 // trace times it), else a plain launch.
 template <int D, int BITS, int MODE, bool SOLO, bool PAGED>
 hipError_t launch_kind(const AttnArgs& a, dim3 grid, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
-  const bool ring = a.window > 0;
-  const int64_t geo_len = ring ? std::min<int64_t>(a.seq_len, a.window) : a.seq_len;
-  if (geo_len > INT32_MAX || (!ring && a.vis_begin > INT32_MAX) || a.window > INT32_MAX ||
-      a.st.block_stride > INT32_MAX || a.st.head_stride > INT32_MAX || a.n_q_heads >= (1 << 24) ||
-      a.skew_extra >= (1 << 24) || a.skew_p > 255)
-    return hipErrorInvalidValue;
-  const uint32_t flags =
-      (a.new_col ? 4u : 0u) | ((uint32_t)a.group << 4) | ((uint32_t)a.n_q_heads << 8);
-  const uint32_t skew = (uint32_t)a.skew_p | ((uint32_t)a.skew_extra << 8);
+  SplitPre p;
+  if (!split_pre(a, &p)) return hipErrorInvalidValue;
   const dim3 block(AttnPlan<D, BITS, SOLO>::kWaves * 64);
-  const uint8_t* base = a.st.base;
-  const int32_t gl = (int32_t)geo_len, gvb = ring ? 0 : (int32_t)a.vis_begin;
-  const int32_t w = (int32_t)a.window, bs = (int32_t)a.st.block_stride;
-  const int32_t hs = (int32_t)a.st.head_stride;
   if (ev0 && ev1)
     hipExtLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SOLO, PAGED>), grid, block, 0, s, ev0,
-                          ev1, 0, base, a.q, gl, gvb, w, a.bps0, a.bps, a.max_splits, skew, bs, hs,
-                          flags, a);
+                          ev1, 0, p.base, p.q, p.geo_len, p.geo_vis_begin, p.window, p.bps0, p.bps,
+                          p.max_splits, p.skew, p.block_stride, p.head_stride, p.flags, a);
   else
-    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SOLO, PAGED>), grid, block, 0, s, base,
-                       a.q, gl, gvb, w, a.bps0, a.bps, a.max_splits, skew, bs, hs, flags, a);
+    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SOLO, PAGED>), grid, block, 0, s, p.base,
+                       p.q, p.geo_len, p.geo_vis_begin, p.window, p.bps0, p.bps, p.max_splits,
+                       p.skew, p.block_stride, p.head_stride, p.flags, a);
   return hipGetLastError();
 }
 

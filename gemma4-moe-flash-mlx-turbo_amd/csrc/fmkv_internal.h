@@ -157,6 +157,44 @@ struct FetchArgs {
   int32_t out_f32;
 };
 
+// The leading scalar arguments of the decode split kernels, 14 dwords that
+// the dispatch preloads into SGPRs (the argument struct follows them): the
+// block range (geo_len: the visible length, at most the window on a ring;
+// geo_vis_begin: the first visible position, 0 on a ring), the split plan
+// (skew = skew_p | skew_extra << 8), the cache and q pointers and flags (bit
+// 2 new-token column, bits 4-7 q heads per KV head, bits 8-31 q heads).
+struct SplitPre {
+  const uint8_t* base;
+  const uint16_t* q;
+  int32_t geo_len, geo_vis_begin, window, bps0, bps, max_splits;
+  uint32_t skew;
+  int32_t block_stride, head_stride;
+  uint32_t flags;
+};
+
+// false when a value does not fit its 32-bit field
+inline bool split_pre(const AttnArgs& a, SplitPre* p) {
+  const bool ring = a.window > 0;
+  const int64_t geo_len = ring ? (a.seq_len < a.window ? a.seq_len : a.window) : a.seq_len;
+  if (geo_len > INT32_MAX || (!ring && a.vis_begin > INT32_MAX) || a.window > INT32_MAX ||
+      a.st.block_stride > INT32_MAX || a.st.head_stride > INT32_MAX || a.n_q_heads >= (1 << 24) ||
+      a.skew_extra >= (1 << 24) || a.skew_p > 255 || a.group > 15)
+    return false;
+  p->base = a.st.base;
+  p->q = a.q;
+  p->geo_len = (int32_t)geo_len;
+  p->geo_vis_begin = ring ? 0 : (int32_t)a.vis_begin;
+  p->window = (int32_t)a.window;
+  p->bps0 = a.bps0;
+  p->bps = a.bps;
+  p->max_splits = a.max_splits;
+  p->skew = (uint32_t)a.skew_p | ((uint32_t)a.skew_extra << 8);
+  p->block_stride = (int32_t)a.st.block_stride;
+  p->head_stride = (int32_t)a.st.head_stride;
+  p->flags = (a.new_col ? 4u : 0u) | ((uint32_t)a.group << 4) | ((uint32_t)a.n_q_heads << 8);
+  return true;
+}
+
 hipError_t launch_append(const AppendArgs& a, int n_seqs, int max_tasks, hipStream_t s);
 // ev_begin / ev_end (optional, both or neither) are recorded by the split-K
 // kernel's dispatch: the start and end of its execution.
