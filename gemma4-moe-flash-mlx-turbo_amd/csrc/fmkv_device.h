@@ -351,9 +351,12 @@ __device__ inline void split_range(const SeqGeom& g, int split, int bps0, int bp
                                    int skew_extra, int64_t* b_begin, int64_t* b_end) {
   int64_t first, count;
   if (skew_p > 0) {
-    const int before = (split + skew_p - 1) / skew_p;  // skewed splits ahead of this one
+    // skew_p is 1, 2 or 4: shifts, not divisions (this runs before a
+    // work-group's first copies)
+    const int sh = __builtin_ctz((unsigned)skew_p);
+    const int before = (split + skew_p - 1) >> sh;  // skewed splits ahead of this one
     first = (int64_t)split * bps + (before < skew_extra ? before : skew_extra);
-    count = bps + ((split % skew_p == 0 && split / skew_p < skew_extra) ? 1 : 0);
+    count = bps + (((split & (skew_p - 1)) == 0 && (split >> sh) < skew_extra) ? 1 : 0);
   } else {
     first = split == 0 ? 0 : bps0 + (int64_t)(split - 1) * bps;
     count = split == 0 ? bps0 : bps;
