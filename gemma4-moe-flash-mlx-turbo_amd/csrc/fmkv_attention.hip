@@ -484,7 +484,9 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
     if (geo.blk_hi > a.st.table_stride) geo.blk_hi = a.st.table_stride;
     if (geo.blk_hi < geo.blk_lo) geo.blk_hi = geo.blk_lo;
   }
-  const int n_splits = n_splits_for(geo, bps0, bps, max_splits, skew_p);
+  // one sequence: the host planned max_splits for exactly this block range
+  // (no division before the first copies); paged: per sequence
+  const int n_splits = PAGED ? n_splits_for(geo, bps0, bps, max_splits, skew_p) : max_splits;
   static_assert(P::kStageRegion >= D / 2 * (int)sizeof(float2), "rope table fits the staging");
   // decode step: the new token's column (dense mode, or the statistics pass
   // of a sparse-V step, whose gated pass then reads the stored token), the
