@@ -331,7 +331,7 @@ int prepare_append(const fmkv_cache* c, const void* k, const void* v, int64_t n,
 // Split-K plan of one decode attention launch: blocks per split (bps, bps0
 // for split 0), split columns per sequence and the XCD-aware skew.
 void plan_splits(int cus, int H, int32_t n_seqs, int64_t nblk, int wg_per_cu, int min_bps,
-                 int first_mult, int new_col, float tau, bool paged, fmkv::AttnArgs* a) {
+                 int first_mult, int new_col, bool paged, fmkv::AttnArgs* a) {
   if (nblk < 1) nblk = 1;
   // one sequence: the new-token column takes CUs of its own; many sequences:
   // the dispatcher fills CUs as work-groups finish
@@ -354,7 +354,7 @@ void plan_splits(int cus, int H, int32_t n_seqs, int64_t nblk, int wg_per_cu, in
   // s = 0 mod p, p = 4 when they fit there (else 2, else 1: the first
   // splits), instead of bps + 1 blocks for every work-group and some CUs
   // left idle.
-  if (n_seqs == 1 && H == 2 && wg_per_cu == 1 && tau == 0.0f && !paged &&
+  if (n_seqs == 1 && H == 2 && wg_per_cu == 1 && !paged &&
       g_bps_override <= 0) {
     const int64_t n_s = (cus - (int64_t)new_col * H) / H;
     const int64_t b = n_s > 0 ? nblk / n_s : 0;
@@ -388,7 +388,7 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   std::memcpy(a->sign_bits, o->sign_bits, sizeof(a->sign_bits));
   a->c = o->c;
   a->sqrt_d = o->sqrt_d;
-  plan_splits(o->cus, H, n_seqs, nblk, wg_per_cu, min_bps, first_mult, new_col, tau,
+  plan_splits(o->cus, H, n_seqs, nblk, wg_per_cu, min_bps, first_mult, new_col,
               st.block_table != nullptr, a);
   a->new_col = new_col;
   a->part_stride = a->max_splits + new_col;
@@ -865,8 +865,7 @@ int fmkv_cache_decode_splits(const fmkv_cache* c, int32_t* n_splits) {
   int64_t nblk = (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
   if (nblk < 1) nblk = 1;
   fmkv::AttnArgs a;
-  plan_splits(c->cus, c->desc.n_kv_heads, 1, nblk, attn_wg_per_cu(c->desc), 1, 1, 0, 0.0f, false,
-              &a);
+  plan_splits(c->cus, c->desc.n_kv_heads, 1, nblk, attn_wg_per_cu(c->desc), 1, 1, 0, false, &a);
   *n_splits = a.max_splits;
   return FMKV_OK;
 }
