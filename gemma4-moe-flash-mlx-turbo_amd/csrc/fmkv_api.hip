@@ -796,10 +796,9 @@ int decode_step_impl(fmkv_cache* c, const void* k, const void* v, int64_t n, con
   if (rc) return rc;
   if (pro) set_prologue(pro, &ap);
   // one new token: the attention launch appends it itself (new-token
-  // column; with sparse-V the statistics pass does); plain caches, codebook
+  // column; with sparse-V the statistics pass does); codebook and plain
   // caches with sparse-V (which they reject) and chunks append first
-  const int fused = n == 1 && c->desc.mode != FMKV_MODE_PLAIN &&
-                            (tau == 0.0f || c->desc.mode == FMKV_MODE_AFFINE) ? 1 : 0;
+  const int fused = n == 1 && (tau == 0.0f || c->desc.mode == FMKV_MODE_AFFINE) ? 1 : 0;
   fmkv::AttnArgs at;
   rc = prepare_attention(c, c->offset + n, q, n_q_heads, scale, tau, out, out_dtype, fused, &at, ext);
   if (rc) return rc;

@@ -57,6 +57,74 @@ __device__ inline uint32_t pack_bf16x2(float a, float b) {
 
 __device__ inline float bf16_value(float a) { return __uint_as_float((uint32_t)f32_to_bf16(a) << 16); }
 
+// Decode step's new-token column (the grid's last split column): wave 0
+// stores the step's K row, wave 1 its V row, at slot T - 1 (the rows as
+// given: a plain cache stores them unchanged), and the token's attention
+// goes out as one more partial: m = its base-2 score, l = 1, O = its V row.
+// The split columns leave that slot out.
+template <int D>
+__device__ void plain_new_token_column(const AttnArgs& a, int64_t T, int n_splits, int kvh,
+                                       int seq, int wave, int lane) {
+  constexpr BlockLayout L = make_layout(D, 16, kPlain);
+  constexpr int E = D / 64;
+  if (wave >= 2) return;
+  const bool isv = wave == 1;
+  const int G = a.group, d0 = lane * E;
+  const int64_t pbase = ((int64_t)seq * a.part_stride + n_splits) * a.n_q_heads + (int64_t)kvh * G;
+  if (T < 1) {  // no token: an empty partial
+    for (int h = 0; h < G; h++) {
+      if (isv) {
+#pragma unroll
+        for (int i = 0; i < E; i++) a.part_o[(pbase + h) * D + d0 + i] = 0.0f;
+      } else if (lane == 0) {
+        a.part_ml[(pbase + h) * 2 + 0] = -1e30f;
+        a.part_ml[(pbase + h) * 2 + 1] = 0.0f;
+      }
+    }
+    return;
+  }
+  const uint16_t* row = (isv ? a.v_new : a.k_new) + ((int64_t)seq * a.st.n_kv_heads + kvh) * D + d0;
+  float x[E];
+  load_row<E>(row, x);
+  // slot write (a bad block-table entry skips it; the token still attends)
+  const int64_t pos = T - 1;
+  const int64_t slot = a.window > 0 ? pos % a.window : pos;
+  const int64_t lb = slot / kBlockTokens;
+  const int t = (int)(slot % kBlockTokens);
+  int64_t phys = lb;
+  bool ok = true;
+  if (a.st.block_table) {
+    ok = lb < a.st.table_stride;
+    phys = ok ? (int64_t)a.st.block_table[(int64_t)seq * a.st.table_stride + lb] : -1;
+  }
+  ok = ok && phys >= 0 && phys < a.st.n_blocks;
+  if (ok) {
+    uint8_t* blk = a.st.base + phys * a.st.block_stride + (int64_t)kvh * a.st.head_stride;
+#pragma unroll
+    for (int i = 0; i < E; i++)
+      *reinterpret_cast<uint16_t*>(blk + (isv ? L.v_codes + plain_v_pos(t, d0 + i)
+                                              : L.k_codes + plain_k_pos(D, t, d0 + i))) = row[i];
+  }
+  if (!isv) {
+    for (int h = 0; h < G; h++) {
+      float qx[E];
+      load_row<E>(a.q + ((int64_t)seq * a.n_q_heads + (int64_t)kvh * G + h) * D + d0, qx);
+      float dot = 0.0f;
+#pragma unroll
+      for (int i = 0; i < E; i++) dot = fmaf(qx[i], x[i], dot);
+      dot = group_sum<64>(dot, lane);
+      if (lane == 0) {
+        a.part_ml[(pbase + h) * 2 + 0] = dot * a.qscale;
+        a.part_ml[(pbase + h) * 2 + 1] = 1.0f;
+      }
+    }
+  } else {
+    for (int h = 0; h < G; h++)
+#pragma unroll
+      for (int i = 0; i < E; i++) a.part_o[(pbase + h) * D + d0 + i] = x[i];
+  }
+}
+
 template <int D>
 __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
   using P = PlainPlan<D>;
@@ -78,6 +146,10 @@ __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
   const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits, a.skew_p);
+  if (a.new_col && split == (int)gridDim.z - 1) {
+    plain_new_token_column<D>(a, T, n_splits, kvh, seq, wave, lane);
+    return;
+  }
   if (split >= n_splits) return;
   int64_t b_begin, b_end;
   split_range(geo, split, a.bps0, a.bps, a.skew_p, a.skew_extra, &b_begin, &b_end);
@@ -122,6 +194,9 @@ __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
   const int64_t vis_lo = a.window > 0 ? 0 : a.vis_begin;
   const int64_t vis_hi = a.window > 0 ? (T < a.window ? T : a.window) : T;
   const bool ring_trim = a.window > 0 && a.vis_begin > T - a.window;
+  // a decode step's new token is the new-token column's
+  int64_t ex_slot = -1;
+  if (a.new_col && T > 0) ex_slot = a.window > 0 ? (T - 1) % a.window : T - 1;
 
   float4_t o[TW];
 #pragma unroll
@@ -151,12 +226,13 @@ __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
     for (int r = 0; r < 4; r++) s4[r] = head < G ? st[r] * a.qscale : -INFINITY;
     // visibility: whole block in the common case, per token at the edges
     const int64_t t0 = b * kBlockTokens;
-    const bool full = t0 >= vis_lo && t0 + kBlockTokens <= vis_hi && !ring_trim;
+    const bool full = t0 >= vis_lo && t0 + kBlockTokens <= vis_hi && !ring_trim &&
+                      (uint64_t)(ex_slot - t0) >= (uint64_t)kBlockTokens;
     if (!full) {
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int64_t slot = t0 + 4 * j + r;
-        bool vis = slot >= vis_lo && slot < vis_hi;
+        bool vis = slot >= vis_lo && slot < vis_hi && slot != ex_slot;
         if (ring_trim) vis = vis && slot_position(slot, T, a.window) >= a.vis_begin;
         if (!vis) s4[r] = -INFINITY;
       }
@@ -241,7 +317,7 @@ __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
 template <int D>
 hipError_t launch_plain_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                           hipEvent_t ev0, hipEvent_t ev1) {
-  dim3 grid(n_kv_heads, n_seqs, a.max_splits);
+  dim3 grid(n_kv_heads, n_seqs, a.max_splits + a.new_col);
   if (ev0 && ev1)
     hipExtLaunchKernelGGL((plain_decode_kernel<D>), grid, dim3(kPlThreads), 0, s, ev0, ev1, 0, a);
   else
@@ -255,7 +331,8 @@ hipError_t launch_plain_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStre
 
 hipError_t launch_plain_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads,
                                          hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
-  if (a.new_col || a.tau > 0.0f) return hipErrorInvalidValue;
+  if (a.tau > 0.0f || (a.new_col && (a.k_norm_w || !a.k_new || !a.v_new)))
+    return hipErrorInvalidValue;
   switch (a.st.layout.head_dim) {
     case 128: return launch_plain_t<128>(a, n_seqs, n_kv_heads, s, e0, e1);
     case 256: return launch_plain_t<256>(a, n_seqs, n_kv_heads, s, e0, e1);

@@ -224,6 +224,40 @@ def test_plain_make_cache_stack(gpu, ora):
         check_attention(out, oc.attention(q, 1.0), f"layer {li}")
 
 
+@pytest.mark.parametrize("bps", [0, 3, 40])
+def test_plain_linear_decode_steps(gpu, ora, bps):
+    """Linear cache, single-token decode steps after a 3000-token prefill
+    under the default plan and forced split sizes: the step's attention
+    launch stores the token in its new-token column and attends it there
+    (the split columns leave its slot out); rows and attention against the
+    oracle."""
+    import torch
+
+    D, Hkv, Hq, T0, n = 512, 2, 16, 3000, 6
+    cache = gpu.KVCache.new(D, Hkv, capacity=T0 + 16)
+    oc = ora.OracleCache(Hkv, D, 16, 0, T0 + 16, mode=PLAIN)
+    k0, v0 = kv_batch(41, T0, Hkv, D), kv_batch(42, T0, Hkv, D)
+    cache.append(dev_bf16(k0), dev_bf16(v0))
+    oc.append(k0, v0)
+    k, v = kv_batch(43, n, Hkv, D), kv_batch(44, n, Hkv, D)
+    q = fast_q(45, n, Hq, Hkv, D)
+    kd, vd = dev_bf16(k), dev_bf16(v)
+    gpu.set_blocks_per_split(bps)
+    try:
+        for i in range(n):
+            scale = 1.0 if i % 2 == 0 else 0.02
+            out = cache.decode_step(kd[i:i + 1], vd[i:i + 1], dev_bf16(q[i]), scale,
+                                    dtype=torch.float32)
+            oc.append(k[i:i + 1], v[i:i + 1])
+            torch.cuda.synchronize()
+            check_attention(out, oc.attention(q[i], scale), f"bps={bps} step {i}")
+    finally:
+        gpu.set_blocks_per_split(0)
+    codes, meta = cache.read_codes()
+    torch.cuda.synchronize()
+    check_codes(codes, meta, oc, None, f"bps={bps} rows")
+
+
 def test_plain_rejects_quantized_only_paths(gpu):
     """Sparse-V, prefill attention and the fused prologue read quantized
     caches only; each fails before launching anything."""
