@@ -1075,8 +1075,7 @@ int paged_decode_step_impl(fmkv_pool* p, const void* k, const void* v,
   if (pro) set_prologue(pro, &ap);
   // one new token per sequence: the attention launch appends it itself, at
   // position seq_lens[s] - 1 (= start_pos[s])
-  const int fused = n_new == 1 && p->desc.mode != FMKV_MODE_PLAIN &&
-                            (tau == 0.0f || p->desc.mode == FMKV_MODE_AFFINE) ? 1 : 0;
+  const int fused = n_new == 1 && (tau == 0.0f || p->desc.mode == FMKV_MODE_AFFINE) ? 1 : 0;
   fmkv::AttnArgs at;
   rc = prepare_paged_attention(p, q, block_tables, max_blocks, seq_lens, n_seqs, max_seq_len,
                                n_q_heads, scale, tau, out, out_dtype, fused, &at);
