@@ -157,7 +157,7 @@ struct FetchArgs {
   int32_t out_f32;
 };
 
-// The leading scalar arguments of the decode split kernels, 14 dwords that
+// The leading scalar arguments of the affine decode split kernel, 14 dwords that
 // the dispatch preloads into SGPRs (the argument struct follows them): the
 // block range (geo_len: the visible length, at most the window on a ring;
 // geo_vis_begin: the first visible position, 0 on a ring), the split plan
