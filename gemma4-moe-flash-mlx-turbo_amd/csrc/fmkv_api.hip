@@ -400,15 +400,19 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   a->out = out;
   a->out_f32 = out_dtype == FMKV_DTYPE_F32;
   const size_t n_rows = a->direct ? 0 : (size_t)n_seqs * a->part_stride * n_q_heads;
+  // sparse-V: [theta | M | L] per (sequence, q head), then the stats pass's
+  // split (m, l) in a region of their own
   const size_t n_stats = tau > 0.0f ? 3 * (size_t)n_seqs * n_q_heads : 0;
+  const size_t n_stat_ml = tau > 0.0f ? 2 * n_rows : 0;
+  const size_t stat_off = n_rows * (D + 2) + n_stats;
   // sparse-V block maxima, 16-byte aligned (read as float4)
-  const size_t blk_off = (n_rows * (D + 2) + n_stats + 3) & ~(size_t)3;
+  const size_t blk_off = (stat_off + n_stat_ml + 3) & ~(size_t)3;
   // (rows sized for the most blocks a sequence can hold, so that the
   // library's workspace does not grow as the context does; a caller's
   // scratch holds the call's blocks only)
   a->blk_stride = (int32_t)std::max<int64_t>(std::max<int64_t>(nblk, ext.ptr ? 0 : blk_cap), 1);
   const size_t n_blk = tau > 0.0f ? (size_t)n_seqs * H * a->blk_stride * 8 : 0;
-  const size_t need = (n_blk ? blk_off + n_blk : n_rows * (D + 2) + n_stats) * sizeof(float);
+  const size_t need = (n_blk ? blk_off + n_blk : stat_off + n_stat_ml) * sizeof(float);
   float* ws = ext.ptr;
   if (ws) {
     if (need > ext.bytes)
@@ -423,6 +427,7 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   a->part_o = n_rows ? ws : nullptr;
   a->part_ml = n_rows ? ws + n_rows * D : nullptr;
   a->tau_stats = n_stats ? ws + n_rows * (D + 2) : nullptr;
+  a->stat_ml = n_stat_ml ? ws + stat_off : nullptr;
   a->blk_max = n_blk ? ws + blk_off : nullptr;
   return FMKV_OK;
 }
@@ -539,8 +544,11 @@ hipError_t launch_attention(const fmkv::AttnArgs& a, int n_seqs, int n_kv_heads,
 // them for fmkv_decode_step. Every GPU holds its own copy for the life of the
 // process; in host code the name only stands in for it, so the library takes
 // each device's address once (noalloc_scratch) and passes that address on.
-// Calls on one GPU share it: every call writes what it reads before reading
-// it, and calls that overlap in time on one GPU race.
+// The lookup runs at set-up, when a cache handle is created on the device:
+// the runtime materialises the symbol's storage on the first lookup (about
+// 10 MiB of device memory on one MI355X), which the allocation-free entry
+// point must not do. Calls on one GPU share it: every call writes what it
+// reads before reading it, and calls that overlap in time on one GPU race.
 static __device__ __align__(256) uint8_t scratch[FMKV_NOALLOC_SCRATCH_BYTES];
 
 namespace {
@@ -621,6 +629,14 @@ int fmkv_cache_create(const fmkv_cache_desc* desc, fmkv_cache** out) {
   }
   sign_bits_of(*desc, c->sign_bits);
   c->cus = device_cus();
+  // set-up of the no-allocation decode step's scratch on this device (once
+  // per device; later creations find the address recorded)
+  ExtWorkspace ext;
+  rc = noalloc_scratch(&ext);
+  if (rc) {
+    (void)fmkv_cache_destroy(c);
+    return rc;
+  }
   *out = c;
   return FMKV_OK;
 }

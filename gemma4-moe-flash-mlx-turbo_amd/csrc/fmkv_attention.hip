@@ -538,39 +538,7 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
   BlockList blist{0ull, 0, nb};
   int nbx = nb;  // blocks visited
   if constexpr (MODE == kGated) {
-    // The thresholds from the stats pass's split statistics (its split
-    // columns and new-token column): wave w < G merges q head kvh * G + w,
-    // lane i splits i, i + 64, ..., the lanes meeting in a butterfly, into
-    // the full softmax max M and sum L; theta = M + log2(tau * L), so that a
-    // weight 2^(s - M) / L >= tau exactly when its base-2 score s >= theta
-    // (no visible token: +inf). Split column 0 stores theta, M and L for the
-    // combine.
-    if (wave < G) {
-      const int n_stat = n_splits + a.stats_new_col;
-      const int64_t rbase = (int64_t)seq * a.part_stride * a.n_q_heads + kvh * G + wave;
-      float M = -INFINITY, Ls = 0.0f;
-      for (int sp = lane; sp < n_stat; sp += 64) {
-        const float2 ml =
-            *reinterpret_cast<const float2*>(a.part_ml + (rbase + (int64_t)sp * a.n_q_heads) * 2);
-        const float mn = fmaxf(M, ml.x);
-        Ls = fmaf(ml.y, exp2f(ml.x - mn), Ls * exp2f(M - mn));
-        M = mn;
-      }
-      const float Mw = group_max<64>(M, lane);
-      Ls = group_sum<64>(Ls > 0.0f ? Ls * exp2f(M - Mw) : 0.0f, lane);
-      const float th = Ls > 0.0f ? Mw + log2f(a.tau * Ls) : INFINITY;
-      if (lane == 0) {
-        th_s[wave] = th;
-        if (split == 0) {
-          const int64_t nh = (int64_t)gridDim.y * a.n_q_heads;
-          const int64_t r = (int64_t)seq * a.n_q_heads + kvh * G + wave;
-          a.tau_stats[r] = th;
-          a.tau_stats[nh + r] = Mw;
-          a.tau_stats[2 * nh + r] = Ls;
-        }
-      }
-    }
-    __syncthreads();
+    gated_thresholds(a, n_splits, seq, kvh, G, split, wave, lane, th_s);
     float thk[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) thk[k] = k < G ? th_s[k] : INFINITY;
@@ -1133,8 +1101,13 @@ hipError_t launch_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s
     // sparse-V: the stats pass (with a decode step's new-token column, which
     // appends the token), the gated pass over every stored token (the new
     // one included; it derives the thresholds from the stats pass's
-    // partials) and the combine of its splits
-    if ((e = launch_split<D, BITS, kStats>(a, grid, s, nullptr, nullptr)) != hipSuccess) return e;
+    // statistics, which sit in a region of their own, stat_ml, so that no
+    // gated work-group overwrites what another still reads) and the combine
+    // of its splits
+    AttnArgs st = a;
+    st.part_ml = a.stat_ml;
+    if (!st.part_ml) return hipErrorInvalidValue;
+    if ((e = launch_split<D, BITS, kStats>(st, grid, s, nullptr, nullptr)) != hipSuccess) return e;
     AttnArgs g = a;
     g.new_col = 0;
     g.stats_new_col = a.new_col;

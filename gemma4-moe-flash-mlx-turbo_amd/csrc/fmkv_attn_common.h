@@ -4,6 +4,7 @@
 // matrix-core tiles, and the lane/dim correspondence of those tiles.
 #pragma once
 #include "fmkv_device.h"
+#include "fmkv_internal.h"
 
 namespace fmkv {
 namespace {
@@ -120,6 +121,46 @@ struct QSlot {
     i0 = o & 7;
   }
 };
+
+// Sparse-V gated pass (src/model/gemma4_attention.rs:196-234): the score
+// thresholds of the work-group's q heads from the statistics pass's split
+// (m, l) in a.stat_ml (its split columns and, with stats_new_col, its
+// new-token column). Wave w < G merges q head kvh * G + w, lane i taking
+// splits i, i + 64, ..., the lanes meeting in a butterfly, into the full
+// softmax max M and sum L; theta = M + log2(tau * L), so that a weight
+// 2^(s - M) / L >= tau exactly when its base-2 score s >= theta (no visible
+// token: +inf). Split column 0 stores theta, M and L in tau_stats for the
+// combine. The thresholds land in th_s[0 .. G) (LDS); every thread of the
+// work-group calls this (one barrier).
+__device__ inline void gated_thresholds(const AttnArgs& a, int n_splits, int seq, int kvh, int G,
+                                        int split, int wave, int lane, float* th_s) {
+  if (wave < G) {
+    const int n_stat = n_splits + a.stats_new_col;
+    const int64_t rbase = (int64_t)seq * a.part_stride * a.n_q_heads + kvh * G + wave;
+    float M = -INFINITY, Ls = 0.0f;
+    for (int sp = lane; sp < n_stat; sp += 64) {
+      const float2 ml =
+          *reinterpret_cast<const float2*>(a.stat_ml + (rbase + (int64_t)sp * a.n_q_heads) * 2);
+      const float mn = fmaxf(M, ml.x);
+      Ls = fmaf(ml.y, exp2f(ml.x - mn), Ls * exp2f(M - mn));
+      M = mn;
+    }
+    const float Mw = group_max<64>(M, lane);
+    Ls = group_sum<64>(Ls > 0.0f ? Ls * exp2f(M - Mw) : 0.0f, lane);
+    const float th = Ls > 0.0f ? Mw + log2f(a.tau * Ls) : INFINITY;
+    if (lane == 0) {
+      th_s[wave] = th;
+      if (split == 0) {
+        const int64_t nh = (int64_t)gridDim.y * a.n_q_heads;
+        const int64_t r = (int64_t)seq * a.n_q_heads + kvh * G + wave;
+        a.tau_stats[r] = th;
+        a.tau_stats[nh + r] = Mw;
+        a.tau_stats[2 * nh + r] = Ls;
+      }
+    }
+  }
+  __syncthreads();
+}
 
 template <int E>
 __device__ inline void store_halves(uint8_t* p, const _Float16 (&h)[E]) {

@@ -107,6 +107,11 @@ struct AttnArgs {
   float* blk_max = nullptr;
   int32_t blk_stride = 0;
   int32_t stats_new_col = 0;  // gated pass: the stats pass had a new-token column
+  // Sparse-V: the stats pass's split (m, l), [n_seqs][part_stride][n_q_heads][2],
+  // a region of its own: the stats launch writes it in place of part_ml and
+  // the gated pass only reads it (the gated work-groups write their own
+  // partials to part_ml while others may still be deriving thresholds).
+  float* stat_ml = nullptr;
 };
 
 // Prefill (chunked) attention: n_q queries at positions p0 .. p0 + n_q - 1,

@@ -146,9 +146,11 @@ int fmkv_cache_append_projected(fmkv_cache* cache, const void* k_proj_bf16,
 /* One decode step of an attention layer, as Gemma4Attention::forward runs it
  * (src/model/gemma4_attention.rs:84-103): cache.update_and_fetch(k, v) for
  * n_tokens new positions, then attention of q over every visible position --
- * fmkv_cache_append followed by fmkv_decode_attention. With one new token,
- * sparse_v_tau == 0 and an affine cache this is a single attention launch
- * (plus the split combine) that also appends the token. Arguments and errors as those two
+ * fmkv_cache_append followed by fmkv_decode_attention. With one new token
+ * and sparse_v_tau == 0 this is, in every mode, a single attention launch
+ * (plus the split combine) whose new-token column also appends the token;
+ * with sparse_v_tau > 0 the statistics pass's new-token column appends it
+ * (then the gated pass and the combine). Arguments and errors as those two
  * calls; nothing is launched or changed when validation fails. */
 int fmkv_decode_step(fmkv_cache* cache, const void* k_bf16, const void* v_bf16, int64_t n_tokens,
                      const void* q_bf16, int32_t n_q_heads, float scale, float sparse_v_tau,
@@ -177,10 +179,14 @@ int fmkv_decode_step_projected(fmkv_cache* cache, const void* k_proj_bf16,
  * capture, tight serving loops, harnesses that forbid hipMalloc). The same
  * kernels run, with the split partials in a fixed per-GPU scratch of
  * FMKV_NOALLOC_SCRATCH_BYTES held until the process ends instead of the
- * handle's growable workspace: (splits + 1) * n_q_heads * (head_dim + 2) * 4
- * bytes (plus 12 * n_q_heads with sparse_v_tau > 0) must fit, else
- * FMKV_ERR_CAPACITY and nothing is launched (a 32K-token head_dim-512 layer
- * with 16 q heads needs about 4 MiB). All calls on one GPU share that
+ * handle's growable workspace: P = (splits + 1) * n_q_heads rows of split
+ * partials take P * (head_dim + 2) * 4 bytes; with sparse_v_tau > 0 add
+ * 12 * n_q_heads bytes of softmax statistics, P * 8 bytes of the statistics
+ * pass's split (m, l), padding to 16 bytes, and 32 * n_kv_heads * blocks
+ * bytes of per-block score maxima (blocks = visible 16-token blocks of the
+ * call). A call needing more gets FMKV_ERR_CAPACITY and nothing is
+ * launched (a 32K-token head_dim-512 layer with 16 q heads needs about
+ * 4 MiB dense, 4.2 MiB with sparse-V). All calls on one GPU share that
  * scratch: calls that overlap in time on one GPU (other streams, other
  * threads) race. */
 int fmkv_decode_step_noalloc(fmkv_cache* cache, const void* k_bf16, const void* v_bf16,

@@ -444,14 +444,15 @@ class OracleCache:
             y = codebook_dequant_rotated(packed, np.ascontiguousarray(meta[..., 0]), self.D, self.bits)
         return unrotate_rows_f64(y, self.sgn)
 
-    def prefill(self, k_bf16, v_bf16, q_bf16, scale: float = 1.0) -> np.ndarray:
+    def prefill(self, k_bf16, v_bf16, q_bf16, scale: float = 1.0, rows=None) -> np.ndarray:
         """update_and_fetch of an L-token chunk, then the chunk's attention
         (src/model/gemma4_attention.rs:84-104 with L > 1) under the mask of
         src/model/mod.rs:682-753: query position p = offset + i sees the
         visible keys j <= p, and on a ring of W slots only j > p - W. The keys
         are the positions visible before the chunk plus the chunk's own
         quantized rows (update_and_fetch returns both before trimming,
-        src/cache.rs:266-310). Returns [L, Hq, D] f64."""
+        src/cache.rs:266-310). Returns [L, Hq, D] f64, or with `rows` (chunk
+        indices) only those queries' outputs, [len(rows), Hq, D]."""
         k_bf16, v_bf16 = np.asarray(k_bf16), np.asarray(v_bf16)
         n = k_bf16.shape[0]
         p0 = self.offset
@@ -464,12 +465,13 @@ class OracleCache:
         pos = np.concatenate([old_pos, np.arange(p0, p0 + n)])
         kk, vv = np.concatenate([ko, kn]), np.concatenate([vo, vn])
         q = bf16_to_f32(q_bf16).astype(np.float64)
-        out = np.empty(q.shape, np.float64)
-        for i in range(n):
+        sel = list(range(n)) if rows is None else [int(i) for i in rows]
+        out = np.empty((len(sel),) + q.shape[1:], np.float64)
+        for o, i in enumerate(sel):
             p = p0 + i
             lo = self.vis_begin if self.W == 0 else max(self.vis_begin, p - self.W + 1)
             valid = ((pos >= lo) & (pos <= p)).astype(np.uint8)
-            out[i] = attention_f64(q[i], kk, vv, valid, scale)
+            out[o] = attention_f64(q[i], kk, vv, valid, scale)
         return out
 
     def trim(self, keep_last: int) -> None:

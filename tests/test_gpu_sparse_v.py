@@ -235,6 +235,81 @@ def test_sparse_v_paged(gpu, ora):
         check_attention(out[s], oracles[s].attention(q[s], 0.05, tau), f"seq {s}")
 
 
+def test_sparse_v_gated_grid_beyond_resident(gpu, ora):
+    """One cache split one block per work-group (Hkv 8, 6000 tokens: 3000
+    gated work-groups, several waves of them per CU): every gated work-group
+    derives its thresholds from the statistics pass's (m, l), which no gated
+    work-group overwrites, however early its siblings finish. tau is the
+    weights' 99th percentile at a soft scale, so about 1% of the weights sit
+    above it and many near it."""
+    import torch
+
+    D, bits, Hkv, Hq, T = 256, 4, 8, 16, 6000
+    cache, oc = filled(gpu, ora, D, bits, Hkv, T, seed=31)
+    q = q_batch(31, Hq, Hkv, D)
+    for scale in (1.0, 0.003):
+        tau = 1e-3 if scale == 1.0 else float(np.quantile(oc.attention_weights(q, scale), 0.99))
+        ref = oc.attention(q, scale, tau)
+        gpu.set_blocks_per_split(1)
+        try:
+            out = cache.attention(dev_bf16(q), scale, sparse_v_tau=tau, dtype=torch.float32)
+            torch.cuda.synchronize()
+        finally:
+            gpu.set_blocks_per_split(0)
+        check_attention(out, ref, f"bps=1 scale={scale} tau={tau:.3g}")
+
+
+def test_sparse_v_paged_batch_beyond_resident(gpu, ora):
+    """Sixteen ragged sequences of 2048..6144 tokens in a paged pool (Hkv 8,
+    head_dim 256, 4-bit, shuffled blocks): the batched plan puts several
+    work-groups on every CU, so gated work-groups start after others of the
+    same sequence have finished. Sparse-V decode steps against the oracle's
+    gated attention at tau 1e-3 (scale 1.0) and at the 99th-percentile weight
+    of a soft scale."""
+    import torch
+
+    from gpu_util import fast_kv, fast_q
+
+    D, bits, Hkv, Hq, n_seqs = 256, 4, 8, 16, 16
+    lens = (2048 + np.floor(synth.uniform(41, n_seqs) * 4096)).astype(int).tolist()
+    need = [(n + 2 + 15) // 16 for n in lens]
+    max_blocks, n_blocks = max(need), sum(need)
+    perm = np.argsort(synth.splitmix64(43, n_blocks)).astype(np.int32)
+    tables = np.zeros((n_seqs, max_blocks), np.int32)
+    o = 0
+    for s, nb in enumerate(need):
+        tables[s, :nb] = perm[o:o + nb]
+        o += nb
+    pool = gpu.PagedPool(gpu.make_desc(Hkv, D, bits), n_blocks)
+    dtab = torch.from_numpy(tables).cuda()
+    oracles = []
+    for s, n in enumerate(lens):
+        oc = ora.OracleCache(Hkv, D, bits, 0, n + 2)
+        k, v = fast_kv(1000 + s, n, Hkv, D), fast_kv(2000 + s, n, Hkv, D)
+        oc.append(k, v)
+        oracles.append(oc)
+        pool.append(dev_bf16(k[None]), dev_bf16(v[None]), dtab[s:s + 1].contiguous(),
+                    torch.zeros(1, dtype=torch.int32, device="cuda"))
+    k1 = np.stack([fast_kv(3000 + s, 1, Hkv, D) for s in range(n_seqs)])
+    v1 = np.stack([fast_kv(4000 + s, 1, Hkv, D) for s in range(n_seqs)])
+    q = np.stack([fast_q(5000 + s, 1, Hq, Hkv, D)[0] for s in range(n_seqs)])
+    start = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    for s in range(n_seqs):
+        oracles[s].append(k1[s], v1[s])
+    soft = 0.003
+    taus = [float(np.quantile(oracles[s].attention_weights(q[s], soft), 0.99)) for s in range(n_seqs)]
+    tau_soft = float(np.median(taus))
+    out1 = pool.decode_step(dev_bf16(k1), dev_bf16(v1), dtab, start, start + 1, max(lens) + 1,
+                            dev_bf16(q), 1.0, sparse_v_tau=1e-3, dtype=torch.float32)
+    out2 = pool.attention(dev_bf16(q), dtab, start + 1, max(lens) + 1, soft,
+                          sparse_v_tau=tau_soft, dtype=torch.float32)
+    torch.cuda.synchronize()
+    for s in range(n_seqs):
+        check_attention(out1[s], oracles[s].attention(q[s], 1.0, 1e-3), f"seq {s} scale 1.0")
+        check_attention(out2[s], oracles[s].attention(q[s], soft, tau_soft),
+                        f"seq {s} scale {soft} tau {tau_soft:.3g}")
+
+
 def test_sparse_v_rejects_bad_tau(gpu):
     import torch
 

@@ -277,6 +277,81 @@ def test_codebook_canonical_vs_dense_reference(ora, bits, d):
     assert np.mean(err) <= 2e-3 * np.abs(dense).mean() + 1e-3
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("d", [128, 256, 512])
+def test_codebook_dequant_rotated_is_reference_dequant(ora, bits, d):
+    """ora_codebook_dequant_rotated (the rotated-domain row every codebook
+    attention check reads) composed with the f64 inverse rotation equals the
+    reference's dequantization written as src/cache.rs:119-125 does it:
+    (centroid[idx] / sqrt(d)) . R^T . norm, with the dense R^T of
+    build_rht (src/cache.rs:47-62) in f64 -- to 1e-12. The canonical f32
+    round trip from the same codes (ora_codebook_round_trip) lies within one
+    bf16 rounding of it. A row whose indices are all one value k is
+    centroid[k] * norm / sqrt(d) in every coordinate."""
+    rng = np.random.default_rng(100 * bits + d)
+    x = (rng.standard_normal((24, d)) * rng.uniform(0.1, 30, (24, 1))).astype(np.float32)
+    x[:, :4] *= 20
+    x[3] = 0.0
+    xb = synth.f32_to_bf16_bits(x)
+    s = ora.signs(d, 42)
+    packed, norms = ora.codebook_quantize(xb, bits, s)
+    y = ora.codebook_dequant_rotated(packed, norms, d, bits)
+    got = ora.unrotate_rows_f64(y, s)
+    # the reference order, dense and in f64, from the same stored codes
+    c, _ = ora.codebook(bits)
+    idx = ora.unpack_codes(packed, d, bits)
+    _, rt = ora.build_rht(d, 42)
+    nrm = ora.f16_to_f32(norms).astype(np.float64)
+    inv = np.float64(np.float32(1.0) / np.sqrt(np.float32(d)))
+    want = ((c.astype(np.float64)[idx] * inv) @ rt.astype(np.float64)) * nrm[:, None]
+    assert np.allclose(got, want, rtol=0, atol=1e-12 * max(1.0, np.abs(want).max()))
+    assert not got[3].any()  # zero row: norm 0
+    # canonical f32 round trip (bf16 output) from the same codes
+    rt_bf16 = ora.bf16_to_f32(ora.codebook_round_trip(packed, norms, d, bits, s)).astype(np.float64)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(want), 1e-30))) - 7)
+    assert np.all(np.abs(rt_bf16 - want) <= ulp * 1.01 + 1e-6 * nrm[:, None])
+    # constant indices: every rotated coordinate is centroid[k] * norm / sqrt(d)
+    for k in (0, (1 << bits) - 1, 1 << (bits - 1)):
+        row = np.zeros((1, packed.shape[1]), np.uint32)
+        for j in range(d):
+            bit = j * bits
+            row[0, bit // 32] |= np.uint32((k << (bit % 32)) & 0xFFFFFFFF)
+            if bit % 32 + bits > 32:
+                row[0, bit // 32 + 1] |= np.uint32(k >> (32 - bit % 32))
+        n16 = ora.f32_to_f16(np.array([2.5], np.float32))
+        yk = ora.codebook_dequant_rotated(row, n16, d, bits)
+        assert np.all(yk == np.float64(c[k]) * inv * 2.5)
+
+
+@pytest.mark.parametrize("d", [128, 256, 512])
+def test_rotate_rows_f32_is_x_times_r(ora, d):
+    """ora_rotate_rows_f32 (the rotation of f32 rows -- v_norm output -- behind
+    every projected-V code) is x . R (src/cache.rs:47-62, 109-112) within f32
+    FWHT rounding of the dense f64 product, bit-identical to rotate_rows on
+    bf16-representable rows and to the canonical order restated in numpy,
+    and maps the one-hot row e_k to (-1)^popcount(k & j) * c * s_j exactly."""
+    rng = np.random.default_rng(3 * d)
+    x = rng.standard_normal((16, d)).astype(np.float32)
+    x /= np.sqrt(np.mean(x * x, axis=1, keepdims=True))  # unit RMS, as v_norm leaves a row
+    x[:, 5] *= 20
+    s = ora.signs(d, 42)
+    r, _ = ora.build_rht(d, 42)
+    y = ora.rotate_rows_f32(x, s)
+    dense = ora.rotate_rows_dense_f64(x, r)
+    assert np.allclose(y, dense, rtol=0, atol=4 * math.log2(d) * 2.0 ** -24 * np.abs(x).sum(1).max())
+    c = np.float32(1.0) / np.sqrt(np.float32(d))
+    assert np.array_equal(y, ((np_fwht_f32(x) * c) * s).astype(np.float32))
+    xb = synth.f32_to_bf16_bits(x)
+    assert np.array_equal(ora.rotate_rows_f32(ora.bf16_to_f32(xb), s), ora.rotate_rows(xb, s))
+    for k in (0, 1, d // 2 + 3, d - 1):
+        e = np.zeros((1, d), np.float32)
+        e[0, k] = 1.0
+        j = np.arange(d)
+        par = np.vectorize(lambda v: bin(v).count("1") & 1)(k & j)
+        want = np.where(par == 0, c, -c).astype(np.float32) * s
+        assert np.array_equal(ora.rotate_rows_f32(e, s)[0], want)
+
+
 # --------------------------------------------------------------------------
 # cache index semantics (A8, A9, A14)
 # --------------------------------------------------------------------------

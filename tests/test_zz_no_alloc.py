@@ -48,8 +48,15 @@ def test_noalloc_step_matches_decode_step(gpu, case):
             ob = torch.full((Hq, D), float("nan"), dtype=torch.float32, device="cuda")
             ks, vs = kn[s * n:(s + 1) * n].contiguous(), vn[s * n:(s + 1) * n].contiguous()
             step(lib, lib.fmkv_decode_step, a, ks, vs, q[s], Hq, 0.05, tau, oa)
+            # the entry point's contract: no device memory is taken (b is a
+            # fresh handle that never ran fmkv_decode_step; the scratch's
+            # device address was set up when a handle was created, and the
+            # same kernels already ran for a, so nothing loads lazily either)
+            torch.cuda.synchronize()
+            free0 = torch.cuda.mem_get_info()[0]
             step(lib, lib.fmkv_decode_step_noalloc, b, ks, vs, q[s], Hq, 0.05, tau, ob)
             torch.cuda.synchronize()
+            assert torch.cuda.mem_get_info()[0] == free0, f"call {i} step {s}: device memory taken"
             assert torch.isfinite(ob).all()
             assert torch.equal(oa, ob), f"call {i} step {s}: outputs differ"
         assert a.offset() == b.offset() == T0 + 2 * n
