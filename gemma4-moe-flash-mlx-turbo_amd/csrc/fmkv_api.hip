@@ -248,8 +248,6 @@ int make_signs(const fmkv_cache_desc& d, float** out) {
 int check_attn_args(const fmkv_cache_desc& d, const void* q, int32_t n_q_heads, float tau,
                     const void* out, int32_t out_dtype) {
   if (!q || !out) return fail(FMKV_ERR_INVALID_ARG, "q/out must be device pointers");
-  if (d.mode != FMKV_MODE_AFFINE && tau != 0.0f)
-    return fail(FMKV_ERR_UNSUPPORTED, "sparse-V attention reads affine-mode caches");
   if (n_q_heads < d.n_kv_heads || n_q_heads % d.n_kv_heads != 0)
     return fail(FMKV_ERR_INVALID_ARG, "n_q_heads must be a multiple of n_kv_heads");
   if (n_q_heads / d.n_kv_heads > 8)
@@ -263,14 +261,12 @@ int check_attn_args(const fmkv_cache_desc& d, const void* q, int32_t n_q_heads, 
 
 // Validation and launch arguments of an append of n tokens at the cache's
 // offset (no state change).
-// The layer prologue's arguments (no HIP call): affine mode, a k_norm
+// The layer prologue's arguments (no HIP call): a k_norm
 // weight, positive finite eps and theta, rope_dims a power of 2 in
 // [2 * head_dim / 64, head_dim] (the rotated pairs then sit in different
 // lanes of the append kernel's row layout).
 int check_prologue(const fmkv_cache_desc& d, const fmkv_kv_prologue* pro) {
   if (!pro) return fail(FMKV_ERR_INVALID_ARG, "prologue is null");
-  if (d.mode != FMKV_MODE_AFFINE)
-    return fail(FMKV_ERR_UNSUPPORTED, "the fused prologue is for affine-mode caches");
   if (!pro->k_norm_weight) return fail(FMKV_ERR_INVALID_ARG, "k_norm_weight must be a device pointer");
   if (!(pro->eps > 0.0f) || !std::isfinite(pro->eps))
     return fail(FMKV_ERR_INVALID_ARG, "eps must be finite and > 0");
@@ -812,9 +808,8 @@ int decode_step_impl(fmkv_cache* c, const void* k, const void* v, int64_t n, con
   if (rc) return rc;
   if (pro) set_prologue(pro, &ap);
   // one new token: the attention launch appends it itself (new-token
-  // column; with sparse-V the statistics pass does); codebook and plain
-  // caches with sparse-V (which they reject) and chunks append first
-  const int fused = n == 1 && (tau == 0.0f || c->desc.mode == FMKV_MODE_AFFINE) ? 1 : 0;
+  // column; with sparse-V the statistics pass does); chunks append first
+  const int fused = n == 1 ? 1 : 0;
   fmkv::AttnArgs at;
   rc = prepare_attention(c, c->offset + n, q, n_q_heads, scale, tau, out, out_dtype, fused, &at, ext);
   if (rc) return rc;
@@ -1091,7 +1086,7 @@ int paged_decode_step_impl(fmkv_pool* p, const void* k, const void* v,
   if (pro) set_prologue(pro, &ap);
   // one new token per sequence: the attention launch appends it itself, at
   // position seq_lens[s] - 1 (= start_pos[s])
-  const int fused = n_new == 1 && (tau == 0.0f || p->desc.mode == FMKV_MODE_AFFINE) ? 1 : 0;
+  const int fused = n_new == 1 ? 1 : 0;
   fmkv::AttnArgs at;
   rc = prepare_paged_attention(p, q, block_tables, max_blocks, seq_lens, n_seqs, max_seq_len,
                                n_q_heads, scale, tau, out, out_dtype, fused, &at);

@@ -213,7 +213,9 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
     for (int r = 0; r < R; r++) {
       meta[r] = 0u;
 #pragma unroll
-      for (int i = 0; i < E; i++) code[r][i] = (uint32_t)f32_to_bf16(x[r][i]);  // exact
+      // exact for rows as given; with the prologue, V (f32 after v_norm) is
+      // rounded to the stored bf16 here (RNE)
+      for (int i = 0; i < E; i++) code[r][i] = (uint32_t)f32_to_bf16(x[r][i]);
     }
   } else if constexpr (MODE == kAffine) {
 #pragma unroll
@@ -373,11 +375,9 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendArgs a) {
 template <int D, int BITS, int MODE>
 hipError_t launch_t(const AppendArgs& a, int n_seqs, int max_tasks, hipStream_t s) {
   dim3 grid(max_tasks, a.st.n_kv_heads, n_seqs);
-  if constexpr (MODE == kAffine) {
-    if (a.k_norm_w) {
-      hipLaunchKernelGGL((append_kernel<D, BITS, MODE, true>), grid, dim3(kAppendThreads), 0, s, a);
-      return hipGetLastError();
-    }
+  if (a.k_norm_w) {
+    hipLaunchKernelGGL((append_kernel<D, BITS, MODE, true>), grid, dim3(kAppendThreads), 0, s, a);
+    return hipGetLastError();
   }
   hipLaunchKernelGGL((append_kernel<D, BITS, MODE, false>), grid, dim3(kAppendThreads), 0, s, a);
   return hipGetLastError();

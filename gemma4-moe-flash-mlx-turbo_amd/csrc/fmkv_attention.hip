@@ -65,31 +65,6 @@
 namespace fmkv {
 namespace {
 
-// Kernel modes. Dense: softmax attention. Sparse-V (src/model/
-// gemma4_attention.rs:196-234, weights below tau zeroed without
-// renormalisation) takes two passes over the cache: kStats streams only the
-// keys and writes each split's (m, l) and each block's largest score per
-// head; kGated derives every head's threshold theta = M + log2(tau * L)
-// from those, visits only the blocks that hold a score at or above it and
-// is the dense pass with every score below theta dropped; the combine
-// divides by the full L of the stats pass.
-constexpr int kDense = 0, kStats = 1, kGated = 2;
-
-// A stream's visiting order in the gated pass: the set bits of `mask` in
-// increasing order, then next, next + 1, ... below n (scalar values).
-struct BlockList {
-  uint64_t mask;
-  int next, n;
-  __device__ int pop() {
-    if (mask) {
-      const int i = __builtin_ctzll(mask);
-      mask &= mask - 1;
-      return i;
-    }
-    return next < n ? next++ : n;
-  }
-};
-
 // Staging plan of one (head_dim, bits, stream kind). A block stream is a
 // wave pair (each wave owns half the 64-dim groups, SOLO false) or a single
 // wave owning every group (SOLO true). Pairs finish one block soonest; solo
@@ -542,24 +517,8 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
     float thk[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) thk[k] = k < G ? th_s[k] : INFINITY;
-    const int64_t Tl = PAGED ? Tg : a.seq_len;
-    const int64_t last_blk =
-        Tl > 0 ? (a.window > 0 ? (Tl - 1) % a.window : Tl - 1) / kBlockTokens : -1;
-    bool need = false;
-    if (lane < nb) {
-      const int64_t bl = pb0 + (int64_t)NS * lane, rb = bl - geo.blk_lo;
-      need = bl == last_blk || rb >= a.blk_stride;
-      if (!need) {
-        const float4_t m0 = *reinterpret_cast<const float4_t*>(a.blk_max + (blk_row + rb) * 8);
-        const float4_t m1 = *reinterpret_cast<const float4_t*>(a.blk_max + (blk_row + rb) * 8 + 4);
-#pragma unroll
-        for (int k = 0; k < 4; k++) need = need || m0[k] >= thk[k] || m1[k] >= thk[k + 4];
-      }
-    }
-    const uint64_t mask = __ballot(need);
-    blist.mask = mask;
-    blist.next = 64;
-    nbx = __builtin_popcountll(mask) + (nb > 64 ? nb - 64 : 0);
+    blist = gated_block_list(a, thk, blk_row, geo.blk_lo, pb0, NS, nb, PAGED ? Tg : a.seq_len,
+                             lane, &nbx);
   }
   BlockList bcopy = blist;  // the copies run ahead of the visits on the same list
   uint8_t* const pstage = stage + stream * NST * SB;

@@ -19,6 +19,31 @@ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 // max before the accumulators are rescaled to a new one.
 constexpr float kRescaleSlack = 8.0f;
 
+// Decode kernel modes. Dense: softmax attention. Sparse-V (src/model/
+// gemma4_attention.rs:196-234, weights below tau zeroed without
+// renormalisation) takes two passes over the cache: kStats streams only the
+// keys and writes each split's (m, l) and each block's largest score per
+// head; kGated derives every head's threshold theta = M + log2(tau * L)
+// from those, visits only the blocks that hold a score at or above it and
+// is the dense pass with every score below theta dropped; the combine
+// divides by the full L of the stats pass.
+constexpr int kDense = 0, kStats = 1, kGated = 2;
+
+// A stream's visiting order in the gated pass: the set bits of `mask` in
+// increasing order, then next, next + 1, ... below n (scalar values).
+struct BlockList {
+  uint64_t mask;
+  int next, n;
+  __device__ int pop() {
+    if (mask) {
+      const int i = __builtin_ctzll(mask);
+      mask &= mask - 1;
+      return i;
+    }
+    return next < n ? next++ : n;
+  }
+};
+
 __device__ inline uint32_t lds_addr(const void* p) {
   return (uint32_t)reinterpret_cast<uintptr_t>(p);  // low half of the flat LDS address
 }
@@ -125,18 +150,19 @@ struct QSlot {
 // Sparse-V gated pass (src/model/gemma4_attention.rs:196-234): the score
 // thresholds of the work-group's q heads from the statistics pass's split
 // (m, l) in a.stat_ml (its split columns and, with stats_new_col, its
-// new-token column). Wave w < G merges q head kvh * G + w, lane i taking
-// splits i, i + 64, ..., the lanes meeting in a butterfly, into the full
-// softmax max M and sum L; theta = M + log2(tau * L), so that a weight
-// 2^(s - M) / L >= tau exactly when its base-2 score s >= theta (no visible
-// token: +inf). Split column 0 stores theta, M and L in tau_stats for the
-// combine. The thresholds land in th_s[0 .. G) (LDS); every thread of the
-// work-group calls this (one barrier).
+// new-token column). Wave w merges q heads kvh * G + h for h = w, w + n_waves,
+// ... < G, lane i taking splits i, i + 64, ..., the lanes meeting in a
+// butterfly, into the full softmax max M and sum L; theta = M + log2(tau * L),
+// so that a weight 2^(s - M) / L >= tau exactly when its base-2 score s >=
+// theta (no visible token: +inf). Split column 0 stores theta, M and L in
+// tau_stats for the combine. The thresholds land in th_s[0 .. G) (LDS);
+// every thread of the work-group calls this (one barrier).
 __device__ inline void gated_thresholds(const AttnArgs& a, int n_splits, int seq, int kvh, int G,
-                                        int split, int wave, int lane, float* th_s) {
-  if (wave < G) {
+                                        int split, int wave, int lane, float* th_s,
+                                        int n_waves = 8) {
+  for (int h = wave; h < G; h += n_waves) {
     const int n_stat = n_splits + a.stats_new_col;
-    const int64_t rbase = (int64_t)seq * a.part_stride * a.n_q_heads + kvh * G + wave;
+    const int64_t rbase = (int64_t)seq * a.part_stride * a.n_q_heads + kvh * G + h;
     float M = -INFINITY, Ls = 0.0f;
     for (int sp = lane; sp < n_stat; sp += 64) {
       const float2 ml =
@@ -149,10 +175,10 @@ __device__ inline void gated_thresholds(const AttnArgs& a, int n_splits, int seq
     Ls = group_sum<64>(Ls > 0.0f ? Ls * exp2f(M - Mw) : 0.0f, lane);
     const float th = Ls > 0.0f ? Mw + log2f(a.tau * Ls) : INFINITY;
     if (lane == 0) {
-      th_s[wave] = th;
+      th_s[h] = th;
       if (split == 0) {
         const int64_t nh = (int64_t)gridDim.y * a.n_q_heads;
-        const int64_t r = (int64_t)seq * a.n_q_heads + kvh * G + wave;
+        const int64_t r = (int64_t)seq * a.n_q_heads + kvh * G + h;
         a.tau_stats[r] = th;
         a.tau_stats[nh + r] = Mw;
         a.tau_stats[2 * nh + r] = Ls;
@@ -160,6 +186,34 @@ __device__ inline void gated_thresholds(const AttnArgs& a, int n_splits, int seq
     }
   }
   __syncthreads();
+}
+
+// Sparse-V gated pass: which of a stream's blocks pb0 + ns * i (i < nb) to
+// visit -- those in which some head's largest score from the statistics pass
+// (blk_max) reaches its threshold thk[head], plus the block holding the
+// newest token (whose statistics came from the statistics pass's new-token
+// column rather than a block row) and any block beyond the block-maxima
+// rows. Lane i tests block i (i < 64); blocks past the 64th are always
+// visited. Returns the visiting list; *n_visit is its length.
+__device__ inline BlockList gated_block_list(const AttnArgs& a, const float (&thk)[8], int64_t blk_row,
+                                             int64_t blk_lo, int64_t pb0, int ns, int nb,
+                                             int64_t T, int lane, int* n_visit) {
+  const int64_t last_blk =
+      T > 0 ? (a.window > 0 ? (T - 1) % a.window : T - 1) / kBlockTokens : -1;
+  bool need = false;
+  if (lane < nb) {
+    const int64_t bl = pb0 + (int64_t)ns * lane, rb = bl - blk_lo;
+    need = bl == last_blk || rb >= a.blk_stride;
+    if (!need) {
+      const float4_t m0 = *reinterpret_cast<const float4_t*>(a.blk_max + (blk_row + rb) * 8);
+      const float4_t m1 = *reinterpret_cast<const float4_t*>(a.blk_max + (blk_row + rb) * 8 + 4);
+#pragma unroll
+      for (int k = 0; k < 4; k++) need = need || m0[k] >= thk[k] || m1[k] >= thk[k + 4];
+    }
+  }
+  const uint64_t mask = __ballot(need);
+  *n_visit = __builtin_popcountll(mask) + (nb > 64 ? nb - 64 : 0);
+  return BlockList{mask, 64, nb};
 }
 
 template <int E>

@@ -220,15 +220,24 @@ __device__ inline void cb_pair(uint32_t base, uint32_t field, uint32_t& hw, uint
 // current token attends to its own round-tripped K/V (src/cache.rs:295-298),
 // it contributes partial slot n_splits: m = q_rot . k_deq (base 2), l = 1,
 // o = v_deq . R^T, the same row for every head of the group. Wave 0 handles
-// K, wave 1 V.
+// K, wave 1 V. With a.k_norm_w the layer's prologue runs on the raw
+// projections first, exactly as the append kernel runs it (K = RoPE(k_norm(k))
+// in bf16, V = v_norm(v) in f32); the RoPE (cos, sin) table of position T - 1
+// is built by every thread into `rope` (LDS, rope_dims / 2 float2) before the
+// q table's barriers.
 template <int D, int BITS>
-__device__ void cb_new_token_column(const AttnArgs& a, uint8_t* tab, int64_t T, int n_splits,
-                                    int kvh, int seq, int wave, int lane) {
+__device__ void cb_new_token_column(const AttnArgs& a, uint8_t* tab, float2* rope, int64_t T,
+                                    int n_splits, int kvh, int seq, int wave, int lane) {
 #pragma clang fp contract(off)
   constexpr BlockLayout L = make_layout(D, BITS, kCodebook);
   constexpr int E = D / 64;
   const int G = a.group;
+  const bool pro = a.k_norm_w != nullptr;
   cb_copy_q_row<D>(a, tab, seq, kvh, wave, lane);
+  if (pro && T >= 1) {
+    for (int j = wave * 64 + lane; j < (a.rope_dims >> 1); j += kCbWaves * 64)
+      rope[j] = rope_cos_sin(T - 1, rope_inv_freq(j, a.rope_dims, a.rope_theta));
+  }
   wait_vmcnt<0>();
   const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
   cb_build_q_table<D>(a, tab, wave, lane, sbits);
@@ -252,6 +261,16 @@ __device__ void cb_new_token_column(const AttnArgs& a, uint8_t* tab, int64_t T, 
 
   float x[E];
   load_row<E>((isv ? a.v_new : a.k_new) + ((int64_t)seq * a.st.n_kv_heads + kvh) * D + d0, x);
+  if (pro) {  // the rope table is complete: cb_build_q_table's barriers passed
+    if (!isv) {
+      float w[E];
+      load_row<E>(a.k_norm_w + d0, w);
+      k_norm_row<E>(x, w, a.eps, lane);
+      rope_row<E>(x, a.rope_dims, lane, [&](int j) { return rope[j]; });
+    } else {
+      v_norm_row<E>(x, a.eps, lane);
+    }
+  }
   const float norm = sqrtf(canonical_sumsq<E>(x, lane));
   const float den = norm + 1e-8f;
 #pragma unroll
@@ -341,7 +360,10 @@ __device__ void cb_new_token_column(const AttnArgs& a, uint8_t* tab, int64_t T, 
   }
 }
 
-template <int D, int BITS>
+// MODE: kDense, or the statistics (kStats: keys only, split (m, l) and block
+// maxima) and gated (kGated) passes of sparse-V, as the affine kernel runs
+// them.
+template <int D, int BITS, int MODE>
 __global__ __launch_bounds__(kCbWaves * 64)
 __attribute__((amdgpu_waves_per_eu(2, 2)))
 void cb_decode_kernel(AttnArgs a) {
@@ -349,7 +371,9 @@ void cb_decode_kernel(AttnArgs a) {
   constexpr BlockLayout L = P::L;
   constexpr int E = D / 64;
   constexpr int NSW = P::kNSW, NTW = P::kNTW;
-  constexpr int NST = P::kStages, SB = P::kStageBytes, CP = P::kCopies;
+  // copy instructions per wave per block (the stats pass copies no V codes)
+  constexpr int NST = P::kStages, SB = P::kStageBytes;
+  constexpr int CP = MODE == kStats ? P::kHalfCopies + 1 : P::kCopies;
   constexpr int HB = P::kHalfBytes;
   constexpr int QS = P::kQS;
   constexpr int NS = kCbStreams;
@@ -359,6 +383,7 @@ void cb_decode_kernel(AttnArgs a) {
   __shared__ __align__(16) uint8_t lut[P::kLutBytes];
   __shared__ float ml_s[NS][8][2];
   __shared__ int xflag[kCbWaves];
+  __shared__ float th_s[8];  // sparse-V gated pass: the group's thresholds
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -377,9 +402,13 @@ void cb_decode_kernel(AttnArgs a) {
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
   const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits, a.skew_p);
-  if (a.new_col && split == (int)gridDim.z - 1) {
-    cb_new_token_column<D, BITS>(a, scratch, T, n_splits, kvh, seq, wave, lane);
-    return;
+  if constexpr (MODE != kGated) {
+    if (a.new_col && split == (int)gridDim.z - 1) {
+      static_assert(P::kStageRegion >= D / 2 * (int)sizeof(float2), "rope table fits the staging");
+      cb_new_token_column<D, BITS>(a, scratch, reinterpret_cast<float2*>(stage), T, n_splits, kvh,
+                                   seq, wave, lane);
+      return;
+    }
   }
   if (split >= n_splits) return;
   int64_t b_begin, b_end;
@@ -402,6 +431,20 @@ void cb_decode_kernel(AttnArgs a) {
 
   const int64_t pb0 = b_begin + stream;
   const int nb = pb0 < b_end ? (int)((b_end - pb0 + NS - 1) / NS) : 0;
+  // sparse-V: this (sequence, KV head)'s row of block maxima; the gated pass
+  // visits only the blocks holding a score at or above a head's threshold
+  const int64_t blk_row =
+      MODE == kDense ? 0 : ((int64_t)seq * a.st.n_kv_heads + kvh) * a.blk_stride;
+  BlockList blist{0ull, 0, nb};
+  int nbx = nb;  // blocks visited
+  if constexpr (MODE == kGated) {
+    gated_thresholds(a, n_splits, seq, kvh, G, split, wave, lane, th_s);
+    float thk[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) thk[k] = k < G ? th_s[k] : INFINITY;
+    blist = gated_block_list(a, thk, blk_row, geo.blk_lo, pb0, NS, nb, T, lane, &nbx);
+  }
+  BlockList bcopy = blist;  // the copies run ahead of the visits on the same list
   uint8_t* const pstage = stage + stream * NST * SB;
   const uint32_t pstage_lds = lds_addr(pstage);
 
@@ -412,7 +455,7 @@ void cb_decode_kernel(AttnArgs a) {
     const uint32_t sl = pstage_lds + st * SB;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of this stage are done
 #pragma unroll
-    for (int r = 0; r < 2; r++) {
+    for (int r = 0; r < (MODE == kStats ? 1 : 2); r++) {
       const int off = (int)(r == 0 ? L.k_codes : L.v_codes) + half * HB;
 #pragma unroll
       for (int k = 0; k < P::kHalfCopies; k++) {
@@ -440,13 +483,13 @@ void cb_decode_kernel(AttnArgs a) {
   cb_copy_q_row<D>(a, scratch, seq, kvh, wave, lane);
 #pragma unroll
   for (int s = 0; s < NQ; s++)
-    if (s < nb) copy_block(s, pb0 + (int64_t)NS * s);
-  wait_copies<CP, NQ>(nb < NQ ? nb : NQ);  // the q copy preceded every block
+    if (s < nbx) copy_block(s, pb0 + (int64_t)NS * (MODE == kGated ? bcopy.pop() : s));
+  wait_copies<CP, NQ>(nbx < NQ ? nbx : NQ);  // the q copy preceded every block
   const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
   cb_build_q_table<D>(a, scratch, wave, lane, sbits);
 #pragma unroll
   for (int s = NQ; s < NST; s++)
-    if (s < nb) copy_block(s, pb0 + (int64_t)NS * s);
+    if (s < nbx) copy_block(s, pb0 + (int64_t)NS * (MODE == kGated ? bcopy.pop() : s));
   half8_t bq[NSW];
 #pragma unroll
   for (int s = 0; s < NSW; s++)
@@ -470,6 +513,9 @@ void cb_decode_kernel(AttnArgs a) {
   // hold the position it replaces, or be written meanwhile)
   int64_t ex_slot = -1;
   if (a.new_col && T > 0) ex_slot = a.window > 0 ? (T - 1) % a.window : T - 1;
+  // sparse-V: this column's score threshold
+  float theta = -INFINITY;
+  if constexpr (MODE == kGated) theta = col_valid ? th_s[head] : -INFINITY;
 
   // this lane's fields: QK slice s, token t = c of the MFMA A rows:
   // 8 indices at bit (t D/2 + 32 s + 8 j) BITS of the K half;
@@ -539,11 +585,21 @@ void cb_decode_kernel(AttnArgs a) {
         if (!vis) sc[i] = -INFINITY;
       }
     }
+    if constexpr (MODE == kGated) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) sc[i] = sc[i] >= theta ? sc[i] : -INFINITY;
+    }
     // online softmax in base 2 (the affine kernel's rule: the reference max
     // moves only on jumps above kRescaleSlack)
     float mb = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
     mb = xor16_max(mb);
     mb = xor32_max(mb);
+    if constexpr (MODE == kStats) {
+      // the block's largest score per head, for the gated pass's block skip
+      const int64_t rb = b - geo.blk_lo;
+      if (half == 0 && j == 0 && hi && rb < a.blk_stride)
+        a.blk_max[(blk_row + rb) * 8 + head] = col_valid ? mb : -INFINITY;
+    }
     const float m_new = fmaxf(m_run, mb);
     if (__any(m_new > m_run + kRescaleSlack)) {
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -558,6 +614,12 @@ void cb_decode_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(sc[i] - m_run);
     l_run += (p[0] + p[1]) + (p[2] + p[3]);
+    if constexpr (MODE == kStats) return;
+    // sparse-V: a block whose weights are all below tau adds nothing to O
+    // (the pair's waves hold the same scores: a uniform branch)
+    if constexpr (MODE == kGated) {
+      if (!__any((p[0] + p[1]) + (p[2] + p[3]) > 0.0f)) return;
+    }
 
     // O^T += V^T . P'^T, P' = p * norm / sqrt D as f16 high (c < 8) and
     // residual (c >= 8) columns
@@ -586,17 +648,39 @@ void cb_decode_kernel(AttnArgs a) {
   // issued after it (the next min(NST - 1, nb - 1 - i) blocks) are pending;
   // once read, the stage is refilled with block i + NST
   int st = 0;
-  for (int i = 0; i < nb; i++) {
-    const int rest = nb - 1 - i;
+  for (int i = 0; i < nbx; i++) {
+    const int rest = nbx - 1 - i;
     wait_copies<CP, NST - 1>(rest < NST - 1 ? rest : NST - 1);
-    process(pstage + st * SB, pb0 + (int64_t)NS * i, i);
-    if (i + NST < nb) copy_block(st, pb0 + (int64_t)NS * (i + NST));
+    process(pstage + st * SB, pb0 + (int64_t)NS * (MODE == kGated ? blist.pop() : i), i);
+    if (i + NST < nbx)
+      copy_block(st, pb0 + (int64_t)NS * (MODE == kGated ? bcopy.pop() : i + NST));
     st = st + 1 == NST ? 0 : st + 1;
   }
 
   // ---- epilogue: merge the four pairs, inverse rotation, store ----
   l_run = xor16_sum(l_run);
   l_run = xor32_sum(l_run);
+  if constexpr (MODE == kStats) {
+    // the split's softmax statistics per head: max and sum over the pairs
+    if (hi && col_valid && half == 0 && j == 0) {
+      ml_s[stream][head][0] = m_run;
+      ml_s[stream][head][1] = l_run;
+    }
+    __syncthreads();
+    if (wave == 0 && lane < G) {
+      float M = ml_s[0][lane][0];
+#pragma unroll
+      for (int q = 1; q < NS; q++) M = fmaxf(M, ml_s[q][lane][0]);
+      float Lsum = 0.0f;
+#pragma unroll
+      for (int q = 0; q < NS; q++)
+        Lsum = fmaf(__builtin_amdgcn_exp2f(ml_s[q][lane][0] - M), ml_s[q][lane][1], Lsum);
+      const int64_t r = ((int64_t)seq * a.part_stride + split) * a.n_q_heads + (int64_t)kvh * G + lane;
+      a.part_ml[r * 2 + 0] = M;
+      a.part_ml[r * 2 + 1] = Lsum;
+    }
+    return;
+  }
   // fold the residual columns (c >= 8) into the high-part columns (c < 8)
 #pragma unroll
   for (int n = 0; n < NTW; n++)
@@ -669,15 +753,39 @@ void cb_decode_kernel(AttnArgs a) {
   }
 }
 
+template <int D, int BITS, int MODE>
+hipError_t launch_cb_mode(const AttnArgs& a, dim3 grid, hipStream_t s, hipEvent_t ev0,
+                          hipEvent_t ev1) {
+  if (ev0 && ev1)
+    hipExtLaunchKernelGGL((cb_decode_kernel<D, BITS, MODE>), grid, dim3(kCbWaves * 64), 0, s, ev0,
+                          ev1, 0, a);
+  else
+    hipLaunchKernelGGL((cb_decode_kernel<D, BITS, MODE>), grid, dim3(kCbWaves * 64), 0, s, a);
+  return hipGetLastError();
+}
+
 template <int D, int BITS>
 hipError_t launch_cb_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s, hipEvent_t ev0,
                        hipEvent_t ev1) {
   dim3 grid(n_kv_heads, n_seqs, a.max_splits + a.new_col);
-  if (ev0 && ev1)
-    hipExtLaunchKernelGGL((cb_decode_kernel<D, BITS>), grid, dim3(kCbWaves * 64), 0, s, ev0, ev1, 0, a);
-  else
-    hipLaunchKernelGGL((cb_decode_kernel<D, BITS>), grid, dim3(kCbWaves * 64), 0, s, a);
-  hipError_t e = hipGetLastError();
+  hipError_t e;
+  if (a.tau > 0.0f) {
+    // sparse-V as the affine kernel runs it: the stats pass (its statistics
+    // in stat_ml; with a decode step's new-token column, which appends the
+    // token), the gated pass over every stored token, the combine
+    AttnArgs st = a;
+    st.part_ml = a.stat_ml;
+    if (!st.part_ml) return hipErrorInvalidValue;
+    if ((e = launch_cb_mode<D, BITS, kStats>(st, grid, s, nullptr, nullptr)) != hipSuccess) return e;
+    AttnArgs g = a;
+    g.new_col = 0;
+    g.stats_new_col = a.new_col;
+    if ((e = launch_cb_mode<D, BITS, kGated>(g, dim3(n_kv_heads, n_seqs, a.max_splits), s, ev0,
+                                             ev1)) != hipSuccess)
+      return e;
+    return a.direct ? hipSuccess : launch_combine(g, n_seqs, s);
+  }
+  e = launch_cb_mode<D, BITS, kDense>(a, grid, s, ev0, ev1);
   if (e != hipSuccess || a.direct) return e;
   return launch_combine(a, n_seqs, s);
 }

@@ -25,6 +25,7 @@
 
 #include "fmkv_device.h"
 #include "fmkv_internal.h"
+#include "fmkv_prologue.h"
 #include "fmkv_attn_common.h"
 
 namespace fmkv {
@@ -61,12 +62,26 @@ __device__ inline float bf16_value(float a) { return __uint_as_float((uint32_t)f
 // stores the step's K row, wave 1 its V row, at slot T - 1 (the rows as
 // given: a plain cache stores them unchanged), and the token's attention
 // goes out as one more partial: m = its base-2 score, l = 1, O = its V row.
-// The split columns leave that slot out.
+// The split columns leave that slot out. With a.k_norm_w the layer's
+// prologue runs on the raw projections first, as the append kernel runs it
+// (K = RoPE(k_norm(k)), V = v_norm(v) rounded to bf16 for the store); the
+// RoPE (cos, sin) table of position T - 1 is built by every thread into
+// `rope` (LDS, rope_dims / 2 float2) behind one barrier. Every thread of
+// the work-group calls it.
 template <int D>
-__device__ void plain_new_token_column(const AttnArgs& a, int64_t T, int n_splits, int kvh,
-                                       int seq, int wave, int lane) {
+__device__ void plain_new_token_column(const AttnArgs& a, float2* rope, int64_t T, int n_splits,
+                                       int kvh, int seq, int wave, int lane) {
+#pragma clang fp contract(off)
   constexpr BlockLayout L = make_layout(D, 16, kPlain);
   constexpr int E = D / 64;
+  const bool pro = a.k_norm_w != nullptr;
+  if (pro) {
+    if (T >= 1) {
+      for (int j = wave * 64 + lane; j < (a.rope_dims >> 1); j += kPlThreads)
+        rope[j] = rope_cos_sin(T - 1, rope_inv_freq(j, a.rope_dims, a.rope_theta));
+    }
+    __syncthreads();
+  }
   if (wave >= 2) return;
   const bool isv = wave == 1;
   const int G = a.group, d0 = lane * E;
@@ -86,6 +101,24 @@ __device__ void plain_new_token_column(const AttnArgs& a, int64_t T, int n_split
   const uint16_t* row = (isv ? a.v_new : a.k_new) + ((int64_t)seq * a.st.n_kv_heads + kvh) * D + d0;
   float x[E];
   load_row<E>(row, x);
+  if (pro) {
+    if (!isv) {
+      float w[E];
+      load_row<E>(a.k_norm_w + d0, w);
+      k_norm_row<E>(x, w, a.eps, lane);
+      rope_row<E>(x, a.rope_dims, lane, [&](int j) { return rope[j]; });
+    } else {
+      v_norm_row<E>(x, a.eps, lane);
+    }
+  }
+  // the stored bf16 values (the rows as given, or the prologue's output
+  // rounded to bf16: K is already, V is rounded here)
+  uint16_t xb[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) {
+    xb[i] = pro ? f32_to_bf16(x[i]) : row[i];
+    x[i] = bf16_to_f32(xb[i]);
+  }
   // slot write (a bad block-table entry skips it; the token still attends)
   const int64_t pos = T - 1;
   const int64_t slot = a.window > 0 ? pos % a.window : pos;
@@ -103,7 +136,7 @@ __device__ void plain_new_token_column(const AttnArgs& a, int64_t T, int n_split
 #pragma unroll
     for (int i = 0; i < E; i++)
       *reinterpret_cast<uint16_t*>(blk + (isv ? L.v_codes + plain_v_pos(t, d0 + i)
-                                              : L.k_codes + plain_k_pos(D, t, d0 + i))) = row[i];
+                                              : L.k_codes + plain_k_pos(D, t, d0 + i))) = xb[i];
   }
   if (!isv) {
     for (int h = 0; h < G; h++) {
@@ -125,7 +158,10 @@ __device__ void plain_new_token_column(const AttnArgs& a, int64_t T, int n_split
   }
 }
 
-template <int D>
+// MODE: kDense, or the statistics (kStats: keys only, split (m, l) and block
+// maxima) and gated (kGated) passes of sparse-V, as the affine kernel runs
+// them.
+template <int D, int MODE>
 __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
   using P = PlainPlan<D>;
   constexpr BlockLayout L = P::L;
@@ -134,6 +170,7 @@ __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
   __shared__ __align__(16) float4_t xch[2][kPlWaves][64];
   __shared__ __align__(16) float rows[8][D];
   __shared__ float ml_s[8][2];
+  __shared__ float th_s[8];  // sparse-V gated pass: the group's thresholds
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -146,14 +183,32 @@ __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
   const SeqGeom geo =
       seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
   const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits, a.skew_p);
-  if (a.new_col && split == (int)gridDim.z - 1) {
-    plain_new_token_column<D>(a, T, n_splits, kvh, seq, wave, lane);
-    return;
+  if constexpr (MODE != kGated) {
+    if (a.new_col && split == (int)gridDim.z - 1) {
+      static_assert(sizeof(rows) >= D / 2 * sizeof(float2), "rope table fits the row area");
+      plain_new_token_column<D>(a, reinterpret_cast<float2*>(rows), T, n_splits, kvh, seq, wave,
+                                lane);
+      return;
+    }
   }
   if (split >= n_splits) return;
   int64_t b_begin, b_end;
   split_range(geo, split, a.bps0, a.bps, a.skew_p, a.skew_extra, &b_begin, &b_end);
   const int nb = (int)(b_end - b_begin);
+  // sparse-V: this (sequence, KV head)'s row of block maxima; the gated pass
+  // visits only the blocks holding a score at or above a head's threshold
+  const int64_t blk_row =
+      MODE == kDense ? 0 : ((int64_t)seq * a.st.n_kv_heads + kvh) * a.blk_stride;
+  BlockList blist{0ull, 0, nb};
+  int nbx = nb;  // blocks visited
+  if constexpr (MODE == kGated) {
+    gated_thresholds(a, n_splits, seq, kvh, G, split, wave, lane, th_s, kPlWaves);
+    float thk[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) thk[k] = k < G ? th_s[k] : INFINITY;
+    blist = gated_block_list(a, thk, blk_row, geo.blk_lo, b_begin, 1, nb, T, lane, &nbx);
+  }
+  BlockList bcopy = blist;  // the loads run one block ahead on the same list
 
   const int32_t* table =
       a.st.block_table ? a.st.block_table + (int64_t)seq * a.st.table_stride : nullptr;
@@ -171,12 +226,14 @@ __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
     const uint8_t* p = blk_ptr(lb);
 #pragma unroll
     for (int s = 0; s < SW; s++) o.k[s] = *reinterpret_cast<const u32x4*>(p + k_off + s * 64);
+    if constexpr (MODE != kStats) {
 #pragma unroll
-    for (int t = 0; t < TW; t++)
-      o.v[t] = *reinterpret_cast<const uint2*>(p + v_off + t * 16 * kBlockTokens * 2);
+      for (int t = 0; t < TW; t++)
+        o.v[t] = *reinterpret_cast<const uint2*>(p + v_off + t * 16 * kBlockTokens * 2);
+    }
   };
   PlainOps<D> nxt;
-  if (nb > 0) load_ops(b_begin, nxt);
+  if (nbx > 0) load_ops(b_begin + (MODE == kGated ? bcopy.pop() : 0), nxt);
 
   // B operands: q of head c & 7 as stored, dims 32k + 8j .. + 7 of this
   // wave's slices (zero past the group)
@@ -198,15 +255,19 @@ __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
   int64_t ex_slot = -1;
   if (a.new_col && T > 0) ex_slot = a.window > 0 ? (T - 1) % a.window : T - 1;
 
+  // sparse-V: this column's score threshold
+  float theta = -INFINITY;
+  if constexpr (MODE == kGated) theta = head < G ? th_s[head] : -INFINITY;
+
   float4_t o[TW];
 #pragma unroll
   for (int t = 0; t < TW; t++) o[t] = (float4_t){0.f, 0.f, 0.f, 0.f};
   float m_run = -1e30f, l_run = 0.0f;
 
-  for (int i = 0; i < nb; i++) {
-    const int64_t b = b_begin + i;
+  for (int i = 0; i < nbx; i++) {
+    const int64_t b = b_begin + (MODE == kGated ? blist.pop() : i);
     const PlainOps<D> cur = nxt;
-    if (i + 1 < nb) load_ops(b + 1, nxt);
+    if (i + 1 < nbx) load_ops(b_begin + (MODE == kGated ? bcopy.pop() : i + 1), nxt);
 
     // -- this wave's quarter of S^T, summed over the waves in wave order --
     float4_t acc = (float4_t){0.f, 0.f, 0.f, 0.f};
@@ -237,10 +298,21 @@ __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
         if (!vis) s4[r] = -INFINITY;
       }
     }
+    if constexpr (MODE == kGated) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) s4[r] = s4[r] >= theta ? s4[r] : -INFINITY;
+    }
     // -- online softmax in base 2 (as the affine kernel) --
     float mb = fmaxf(fmaxf(s4[0], s4[1]), fmaxf(s4[2], s4[3]));
     mb = xor16_max(mb);
     mb = xor32_max(mb);
+    if constexpr (MODE == kStats) {
+      // the block's largest score per head, for the gated pass's block skip
+      // (every wave holds the same scores; wave 0 writes them)
+      const int64_t rb = b - geo.blk_lo;
+      if (wave == 0 && j == 0 && hi_col && rb < a.blk_stride)
+        a.blk_max[(blk_row + rb) * 8 + head] = head < G ? mb : -INFINITY;
+    }
     const float m_new = fmaxf(m_run, mb);
     if (__any(m_new > m_run + kRescaleSlack)) {
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -255,6 +327,12 @@ __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; r++) p[r] = __builtin_amdgcn_exp2f(s4[r] - m_run);
     l_run += (p[0] + p[1]) + (p[2] + p[3]);
+    if constexpr (MODE == kStats) continue;
+    // sparse-V: a block whose weights are all below tau adds nothing to O
+    // (every wave holds the same scores: a uniform branch)
+    if constexpr (MODE == kGated) {
+      if (!__any((p[0] + p[1]) + (p[2] + p[3]) > 0.0f)) continue;
+    }
 
     // -- O^T += V^T . P^T, P as bf16 high (c < 8) / residual (c >= 8) --
     float x[4];
@@ -271,6 +349,15 @@ __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
   // ---- epilogue: rows [head][D] in LDS, then store ----
   l_run = xor16_sum(l_run);
   l_run = xor32_sum(l_run);
+  if constexpr (MODE == kStats) {
+    // the split's softmax statistics per head (every wave holds them)
+    if (wave == 0 && j == 0 && hi_col && head < G) {
+      const int64_t r = ((int64_t)seq * a.part_stride + split) * a.n_q_heads + (int64_t)kvh * G + head;
+      a.part_ml[r * 2 + 0] = m_run;
+      a.part_ml[r * 2 + 1] = l_run;
+    }
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < TW; t++)
 #pragma unroll
@@ -314,15 +401,39 @@ __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
   }
 }
 
+template <int D, int MODE>
+hipError_t launch_plain_mode(const AttnArgs& a, dim3 grid, hipStream_t s, hipEvent_t ev0,
+                             hipEvent_t ev1) {
+  if (ev0 && ev1)
+    hipExtLaunchKernelGGL((plain_decode_kernel<D, MODE>), grid, dim3(kPlThreads), 0, s, ev0, ev1,
+                          0, a);
+  else
+    hipLaunchKernelGGL((plain_decode_kernel<D, MODE>), grid, dim3(kPlThreads), 0, s, a);
+  return hipGetLastError();
+}
+
 template <int D>
 hipError_t launch_plain_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                           hipEvent_t ev0, hipEvent_t ev1) {
   dim3 grid(n_kv_heads, n_seqs, a.max_splits + a.new_col);
-  if (ev0 && ev1)
-    hipExtLaunchKernelGGL((plain_decode_kernel<D>), grid, dim3(kPlThreads), 0, s, ev0, ev1, 0, a);
-  else
-    hipLaunchKernelGGL((plain_decode_kernel<D>), grid, dim3(kPlThreads), 0, s, a);
-  hipError_t e = hipGetLastError();
+  hipError_t e;
+  if (a.tau > 0.0f) {
+    // sparse-V as the affine kernel runs it: the stats pass (its statistics
+    // in stat_ml; with a decode step's new-token column, which stores the
+    // token), the gated pass over every stored token, the combine
+    AttnArgs st = a;
+    st.part_ml = a.stat_ml;
+    if (!st.part_ml) return hipErrorInvalidValue;
+    if ((e = launch_plain_mode<D, kStats>(st, grid, s, nullptr, nullptr)) != hipSuccess) return e;
+    AttnArgs g = a;
+    g.new_col = 0;
+    g.stats_new_col = a.new_col;
+    if ((e = launch_plain_mode<D, kGated>(g, dim3(n_kv_heads, n_seqs, a.max_splits), s, ev0,
+                                          ev1)) != hipSuccess)
+      return e;
+    return a.direct ? hipSuccess : launch_combine(g, n_seqs, s);
+  }
+  e = launch_plain_mode<D, kDense>(a, grid, s, ev0, ev1);
   if (e != hipSuccess || a.direct) return e;
   return launch_combine(a, n_seqs, s);
 }
@@ -331,8 +442,7 @@ hipError_t launch_plain_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStre
 
 hipError_t launch_plain_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads,
                                          hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
-  if (a.tau > 0.0f || (a.new_col && (a.k_norm_w || !a.k_new || !a.v_new)))
-    return hipErrorInvalidValue;
+  if (a.new_col && (!a.k_new || !a.v_new)) return hipErrorInvalidValue;
   switch (a.st.layout.head_dim) {
     case 128: return launch_plain_t<128>(a, n_seqs, n_kv_heads, s, e0, e1);
     case 256: return launch_plain_t<256>(a, n_seqs, n_kv_heads, s, e0, e1);

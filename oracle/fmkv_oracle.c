@@ -428,9 +428,12 @@ static float canonical_sumsq(const float* x, int d) {
 /* Canonical form of src/cache.rs:104-118:
  *   norm = sqrt(sumsq) ; u = x / (norm + 1e-8)
  *   z_j = (((FWHT(u)_j * c) * s_j) * sqrt_d)     (= (u . R) * sqrt(d))
- *   idx_j = #{b : z_j >= b}; stored: packed idx (LE bit stream), f16 norm. */
-void ora_codebook_quantize(const uint16_t* x_bf16, int64_t rows, int d, int bits,
-                           const float* signs, uint32_t* packed, uint16_t* norms) {
+ *   idx_j = #{b : z_j >= b}; stored: packed idx (LE bit stream), f16 norm.
+ * x_f32 / x_bf16: exactly one of them holds the rows (f32 rows are what the
+ * layer prologue leaves for V, bf16 rows what the layer stores). */
+static void codebook_quantize_rows(const float* x_f32, const uint16_t* x_bf16, int64_t rows, int d,
+                                   int bits, const float* signs, uint32_t* packed,
+                                   uint16_t* norms) {
   float bnd[15];
   int nc = ora_lloyd_max_codebook(bits, NULL, bnd);
   if (nc == 0) return;
@@ -447,7 +450,8 @@ void ora_codebook_quantize(const uint16_t* x_bf16, int64_t rows, int d, int bits
 #pragma omp for schedule(static)
 #endif
     for (int64_t r = 0; r < rows; r++) {
-      for (int j = 0; j < d; j++) x[j] = ora_bf16_to_f32(x_bf16[r * d + j]);
+      for (int j = 0; j < d; j++)
+        x[j] = x_f32 ? x_f32[r * d + j] : ora_bf16_to_f32(x_bf16[r * d + j]);
       float norm = sqrtf(canonical_sumsq(x, d));
       float den = norm + 1e-8f;
       for (int j = 0; j < d; j++) x[j] = x[j] / den;
@@ -462,6 +466,16 @@ void ora_codebook_quantize(const uint16_t* x_bf16, int64_t rows, int d, int bits
     }
     free(x);
   }
+}
+
+void ora_codebook_quantize(const uint16_t* x_bf16, int64_t rows, int d, int bits,
+                           const float* signs, uint32_t* packed, uint16_t* norms) {
+  codebook_quantize_rows(NULL, x_bf16, rows, d, bits, signs, packed, norms);
+}
+
+void ora_codebook_quantize_f32(const float* x, int64_t rows, int d, int bits, const float* signs,
+                               uint32_t* packed, uint16_t* norms) {
+  codebook_quantize_rows(x, NULL, rows, d, bits, signs, packed, norms);
 }
 
 /* Rotated-domain value of a codebook row: y_j = centroid[idx_j] * norm / sqrt(d). */

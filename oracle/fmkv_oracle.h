@@ -67,6 +67,8 @@ void ora_affine_dequantize(const uint32_t* packed, const uint16_t* scales, const
 /* TurboQuant codebook mode in canonical order */
 void ora_codebook_quantize(const uint16_t* x_bf16, int64_t rows, int d, int bits,
                            const float* signs, uint32_t* packed, uint16_t* norms);
+void ora_codebook_quantize_f32(const float* x, int64_t rows, int d, int bits, const float* signs,
+                               uint32_t* packed, uint16_t* norms);
 void ora_codebook_dequant_rotated(const uint32_t* packed, const uint16_t* norms, int64_t rows,
                                   int d, int bits, double* y);
 void ora_codebook_round_trip(const uint32_t* packed, const uint16_t* norms, int64_t rows, int d,

@@ -57,6 +57,7 @@ def lib() -> ctypes.CDLL:
             "ora_affine_quantize": ([_vp, i64, i32, i32, i32, _vp, _vp, _vp], None),
             "ora_affine_dequantize": ([_vp, _vp, _vp, i64, i32, i32, i32, _vp], None),
             "ora_codebook_quantize": ([_vp, i64, i32, i32, _vp, _vp, _vp], None),
+            "ora_codebook_quantize_f32": ([_vp, i64, i32, i32, _vp, _vp, _vp], None),
             "ora_codebook_dequant_rotated": ([_vp, _vp, i64, i32, i32, _vp], None),
             "ora_codebook_round_trip": ([_vp, _vp, i64, i32, i32, _vp, _vp], None),
             "ora_rope_inv_freq": ([i32, i32, f32], f32),
@@ -265,6 +266,19 @@ def codebook_quantize(x_bf16, bits: int, sgn):
     return packed, norms
 
 
+def codebook_quantize_f32(x, bits: int, sgn):
+    """codebook_quantize of f32 rows (a V row after v_norm)."""
+    x = _c(x, np.float32)
+    d = x.shape[-1]
+    rows = x.size // d
+    words = (d * bits + 31) // 32
+    packed = np.empty(x.shape[:-1] + (words,), np.uint32)
+    norms = np.empty(x.shape[:-1], np.uint16)
+    lib().ora_codebook_quantize_f32(_p(x), rows, d, bits, _p(_c(sgn, np.float32)), _p(packed),
+                                    _p(norms))
+    return packed, norms
+
+
 def codebook_dequant_rotated(packed, norms, d: int, bits: int) -> np.ndarray:
     packed = _c(packed, np.uint32)
     norms = _c(norms, np.uint16)
@@ -392,7 +406,14 @@ class OracleCache:
         return packed, norms[..., None]
 
     def quantize_rows_f32(self, x):
-        """[..., D] f32 rows (a V row after v_norm) -> (packed, meta); affine mode."""
+        """[..., D] f32 rows (a V row after v_norm) -> (packed, meta): affine
+        and codebook modes quantize the f32 values; a plain cache stores them
+        rounded to bf16 (RNE)."""
+        if self.mode == 2:
+            return self.quantize_rows(f32_to_bf16(x))
+        if self.mode == 1:
+            packed, norms = codebook_quantize_f32(x, self.bits, self.sgn)
+            return packed, norms[..., None]
         y = rotate_rows_f32(x, self.sgn)
         packed, sc, bi = affine_quantize(y, self.bits)
         meta = np.empty(sc.shape[:-1] + (2 * sc.shape[-1],), np.uint16)
@@ -409,9 +430,9 @@ class OracleCache:
     def append_projected(self, k_bf16, v_bf16, w_bf16, eps: float, rope_dims: int,
                          theta: float) -> None:
         """append() of raw k_proj / v_proj rows through the layer's prologue
-        (kv_prologue at the cache offset); v_bf16 None: a K==V layer."""
-        if self.mode != 0:
-            raise ValueError("the fused prologue is modelled for affine caches")
+        (kv_prologue at the cache offset); v_bf16 None: a K==V layer. K
+        leaves the prologue in bf16 and is stored as any K row; V leaves it in
+        f32 (quantize_rows_f32)."""
         k, v = kv_prologue(k_bf16, v_bf16, self.offset, w_bf16, eps, rope_dims, theta)
         kp, km = self.quantize_rows(k)
         vp, vm = self.quantize_rows_f32(v)

@@ -186,15 +186,3 @@ def test_codebook_paged_batch(gpu, ora, D, bits, Hkv, Hq):
     for s in range(n_seqs):
         ocs[s].append(k1[s:s + 1], v1[s:s + 1])
         check_attention(out[s], ocs[s].attention(q[s], 0.02), f"paged seq {s} (T={lens[s] + 1})")
-
-
-def test_codebook_rejects_sparse_v(gpu):
-    import torch
-
-    cache = gpu.KVCache.new_quantized(256, 3, 2, capacity=64, mode=CB)
-    k = torch.zeros((4, 2, 256), dtype=torch.bfloat16, device="cuda")
-    cache.append(k, k)
-    q = torch.zeros((4, 256), dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(gpu.Exception_) as e:
-        cache.attention(q, 1.0, sparse_v_tau=1e-3)
-    assert e.value.code == gpu.FMKV_ERR_UNSUPPORTED

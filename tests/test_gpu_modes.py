@@ -1,0 +1,362 @@
+"""Sparse-V and the layer prologue over codebook (TurboQuant) and plain
+caches, on the GPU against the oracle.
+
+The reference gates at decode whatever the cache kind
+(src/model/gemma4_attention.rs:91-93, :196-234) -- its published sparse-V
+numbers are on 3-bit TurboQuant caches, its default (src/main.rs:84) -- and
+runs k_norm, v_norm and RoPE before every cache kind (:50-81). Here the
+codebook and plain kernels take the same statistics and gated passes as the
+affine one, and their decode steps' new-token columns run the same prologue
+helpers as the append kernel.
+
+  * sparse-V attention within the path tolerance (max-abs 2e-2, mean-abs
+    2e-3; bf16 outputs also allow one bf16 ulp) of the oracle's gated f64
+    attention over the stored rows: several shapes, lengths, (scale, tau)
+    pairs, forced split sizes (the gated pass's block skip), fused decode
+    steps through ring wraps, 32K steps on the default 3-bit cache, a paged
+    batch;
+  * the prologue: codes / norms / bf16 rows bit-exact with
+    OracleCache.append_projected for appends and fused decode steps, with and
+    without K==V, through ring wraps, in a paged pool at large positions."""
+import numpy as np
+import pytest
+
+import synth
+from gpu_util import check_attention, check_codes, dev_bf16, fast_kv, fast_q, host_u16, host_u32, kv_batch
+
+pytestmark = pytest.mark.gpu
+
+CB, PLAIN = 1, 2
+
+SHAPES = [  # mode, D, bits, Hkv, Hq
+    (CB, 512, 3, 2, 16),
+    (CB, 256, 2, 8, 16),
+    (CB, 128, 4, 4, 8),
+    (PLAIN, 512, 16, 2, 16),
+    (PLAIN, 256, 16, 8, 16),
+]
+
+
+def make_cache(gpu, ora, mode, D, bits, Hkv, window=0, cap=0):
+    cache = gpu.KVCache(gpu.make_desc(Hkv, D, bits, window, cap, mode))
+    oc = ora.OracleCache(Hkv, D, bits, window, cap, mode=mode)
+    return cache, oc
+
+
+def q_batch(seed, Hq, Hkv, D):
+    return synth.q_rows(seed + 100, Hq, Hkv, D, synth.outlier_channels(seed, Hkv, D))
+
+
+@pytest.mark.parametrize("mode,D,bits,Hkv,Hq", SHAPES)
+@pytest.mark.parametrize("T", [1, 33, 700, 1500])
+def test_sparse_v_modes_match_oracle(gpu, ora, mode, D, bits, Hkv, Hq, T):
+    import torch
+
+    cache, oc = make_cache(gpu, ora, mode, D, bits, Hkv, cap=T + 16)
+    k, v = kv_batch(T + mode, T, Hkv, D), kv_batch(T + mode + 1, T, Hkv, D)
+    cache.append(dev_bf16(k), dev_bf16(v))
+    oc.append(k, v)
+    q = q_batch(T, Hq, Hkv, D)
+    for scale, tau in ((1.0, 1e-3), (0.05, 1.0 / (2 * T)), (0.003, 1e-3)):
+        ref = oc.attention(q, scale, tau)
+        out32 = cache.attention(dev_bf16(q), scale, sparse_v_tau=tau, dtype=torch.float32)
+        out16 = cache.attention(dev_bf16(q), scale, sparse_v_tau=tau, dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        check_attention(out32, ref, f"mode {mode} f32 scale={scale} tau={tau}")
+        check_attention(out16, ref, f"mode {mode} bf16 scale={scale} tau={tau}")
+
+
+@pytest.mark.parametrize("mode,bits", [(CB, 3), (PLAIN, 16)])
+def test_sparse_v_modes_gate_is_exercised(gpu, ora, mode, bits):
+    """tau at the weights' 99th percentile of a soft softmax: about 1% of the
+    weights kept, the result far from dense attention, within tolerance of
+    the gated oracle."""
+    import torch
+
+    D, Hkv, Hq, T = 512, 2, 16, 1500
+    cache, oc = make_cache(gpu, ora, mode, D, bits, Hkv, cap=T)
+    k, v = kv_batch(5, T, Hkv, D), kv_batch(6, T, Hkv, D)
+    cache.append(dev_bf16(k), dev_bf16(v))
+    oc.append(k, v)
+    q = q_batch(5, Hq, Hkv, D)
+    scale = 0.003
+    w = oc.attention_weights(q, scale)
+    tau = float(np.quantile(w, 0.99))
+    assert 0.005 < float(np.mean(w >= tau)) < 0.05
+    ref = oc.attention(q, scale, tau)
+    assert np.abs(oc.attention(q, scale) - ref).max() > 0.1
+    out = cache.attention(dev_bf16(q), scale, sparse_v_tau=tau, dtype=torch.float32)
+    torch.cuda.synchronize()
+    check_attention(out, ref, f"mode {mode} gated")
+
+
+@pytest.mark.parametrize("mode,D,bits,Hkv,Hq", [SHAPES[0], SHAPES[3], SHAPES[4]])
+@pytest.mark.parametrize("bps", [1, 40, 300])
+def test_sparse_v_modes_split_sizes(gpu, ora, mode, D, bits, Hkv, Hq, bps):
+    """Forced split sizes: one block per work-group (thousands of gated
+    work-groups, several waves per CU) and long splits whose streams carry
+    more than the 64 blocks one ballot tests, at a peaked and a soft scale."""
+    import torch
+
+    T = 6000
+    cache, oc = make_cache(gpu, ora, mode, D, bits, Hkv, cap=T)
+    k, v = fast_kv(12 + mode, T, Hkv, D), fast_kv(13 + mode, T, Hkv, D)
+    cache.append(dev_bf16(k), dev_bf16(v))
+    oc.append(k, v)
+    q = fast_q(12 + mode, 1, Hq, Hkv, D)[0]
+    gpu.set_blocks_per_split(bps)
+    try:
+        outs = [(s, t, cache.attention(dev_bf16(q), s, sparse_v_tau=t, dtype=torch.float32))
+                for s, t in ((1.0, 1e-3), (0.05, 1.0 / 12000))]
+        torch.cuda.synchronize()
+    finally:
+        gpu.set_blocks_per_split(0)
+    for scale, tau, out in outs:
+        check_attention(out, oc.attention(q, scale, tau), f"mode {mode} bps={bps} scale={scale}")
+
+
+@pytest.mark.parametrize("mode,D,bits", [(CB, 256, 3), (CB, 256, 4), (PLAIN, 256, 16)])
+def test_sparse_v_modes_ring_steps(gpu, ora, mode, D, bits):
+    """Sliding layer W = 64: decode steps through wraps with tau > 0 (the
+    statistics pass's new-token column stores the token, the gated pass
+    reads it back); outputs within tolerance, stored rows bit-exact."""
+    import torch
+
+    Hkv, Hq, W = 8, 16, 64
+    cache, oc = make_cache(gpu, ora, mode, D, bits, Hkv, window=W)
+    k0, v0 = kv_batch(1, 40, Hkv, D), kv_batch(2, 40, Hkv, D)
+    cache.append(dev_bf16(k0), dev_bf16(v0))
+    oc.append(k0, v0)
+    for step in range(100):
+        k = kv_batch(100 + 2 * step, 1, Hkv, D, special=False)
+        v = kv_batch(101 + 2 * step, 1, Hkv, D, special=False)
+        q = q_batch(300 + step, Hq, Hkv, D)
+        out = cache.decode_step(dev_bf16(k), dev_bf16(v), dev_bf16(q), 0.05, sparse_v_tau=0.01,
+                                dtype=torch.float32)
+        oc.append(k, v)
+        torch.cuda.synchronize()
+        if step % 9 == 0 or step > 90:
+            check_attention(out, oc.attention(q, 0.05, 0.01), f"mode {mode} step {step}")
+    codes, meta = cache.read_codes()
+    torch.cuda.synchronize()
+    assert np.array_equal(host_u32(codes), oc.codes), "rows written by sparse-V steps"
+    assert np.array_equal(host_u16(meta), oc.meta), "norms written by sparse-V steps"
+
+
+def test_sparse_v_codebook3_32k_steps(gpu, ora):
+    """The reference's sparse-V setting: its default 3-bit TurboQuant cache
+    at long context. Global-layer shape at 32K (Hq 16, Hkv 2, head_dim 512):
+    decode steps at tau 1e-4 (the reference's recommended threshold,
+    FUTURE_OPTIMIZATIONS.md) and at the 99.9th-percentile weight of a soft
+    scale, against the oracle; the stored indices bit-exact."""
+    import torch
+
+    Hq, Hkv, D, bits, T0, L, steps = 16, 2, 512, 3, 32768, 2048, 4
+    cap = T0 + 16
+    cache, oc = make_cache(gpu, ora, CB, D, bits, Hkv, cap=cap)
+    for c0 in range(0, T0, L):
+        k = fast_kv(900 + c0, L, Hkv, D, dist="t3", outliers=False)
+        v = fast_kv(100900 + c0, L, Hkv, D, outliers=False)
+        cache.append(dev_bf16(k), dev_bf16(v))
+        oc.append(k, v)
+    k1 = fast_kv(991, steps, Hkv, D, dist="t3", outliers=False)
+    v1 = fast_kv(992, steps, Hkv, D, outliers=False)
+    q = fast_q(993, steps, Hq, Hkv, D, outliers=False)
+    soft = 0.01
+    outs = []
+    for i in range(steps):
+        oc.append(k1[i:i + 1], v1[i:i + 1])
+        scale = 1.0 if i % 2 == 0 else soft
+        tau = 1e-4 if i % 2 == 0 else float(np.quantile(oc.attention_weights(q[i], soft), 0.999))
+        out = cache.decode_step(dev_bf16(k1[i:i + 1]), dev_bf16(v1[i:i + 1]), dev_bf16(q[i]),
+                                scale, sparse_v_tau=tau, dtype=torch.float32)
+        outs.append((out, oc.attention(q[i], scale, tau), scale, tau))
+    codes, meta = cache.read_codes()
+    torch.cuda.synchronize()
+    for i, (out, ref, scale, tau) in enumerate(outs):
+        check_attention(out, ref, f"step {i} scale {scale} tau {tau:.3g}")
+    check_codes(codes, meta, oc, slots=np.arange(T0 - 16, T0 + steps), what="32K codebook sparse-V")
+
+
+@pytest.mark.parametrize("mode,bits", [(CB, 3), (PLAIN, 16)])
+def test_sparse_v_modes_paged(gpu, ora, mode, bits):
+    """Paged pool, ragged sequences on shuffled blocks: gated decode steps,
+    each sequence against its own oracle."""
+    import torch
+
+    D, Hkv, Hq = 256, 8, 16
+    lens = [37, 300, 16, 901, 2500]
+    n_seqs = len(lens)
+    need = [(n + 2 + 15) // 16 for n in lens]
+    max_blocks, n_blocks = max(need), sum(need)
+    perm = np.argsort(synth.splitmix64(77 + mode, n_blocks)).astype(np.int32)
+    tables = np.zeros((n_seqs, max_blocks), np.int32)
+    o = 0
+    for s, nb in enumerate(need):
+        tables[s, :nb] = perm[o:o + nb]
+        o += nb
+    pool = gpu.PagedPool(gpu.make_desc(Hkv, D, bits, mode=mode), n_blocks)
+    dtab = torch.from_numpy(tables).cuda()
+    oracles = []
+    for s, n in enumerate(lens):
+        oc = ora.OracleCache(Hkv, D, bits, 0, n + 2, mode=mode)
+        k, v = kv_batch(20 * s, n, Hkv, D), kv_batch(20 * s + 1, n, Hkv, D)
+        oc.append(k, v)
+        oracles.append(oc)
+        pool.append(dev_bf16(k[None]), dev_bf16(v[None]), dtab[s:s + 1].contiguous(),
+                    torch.zeros(1, dtype=torch.int32, device="cuda"))
+    k1 = np.stack([kv_batch(700 + s, 1, Hkv, D, special=False) for s in range(n_seqs)])
+    v1 = np.stack([kv_batch(800 + s, 1, Hkv, D, special=False) for s in range(n_seqs)])
+    start = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    q = np.stack([q_batch(950 + s, Hq, Hkv, D) for s in range(n_seqs)])
+    tau = 2e-3
+    out = pool.decode_step(dev_bf16(k1), dev_bf16(v1), dtab, start, start + 1, max(lens) + 1,
+                           dev_bf16(q), 0.05, sparse_v_tau=tau, dtype=torch.float32)
+    torch.cuda.synchronize()
+    for s in range(n_seqs):
+        oracles[s].append(k1[s], v1[s])
+        check_attention(out[s], oracles[s].attention(q[s], 0.05, tau), f"mode {mode} seq {s}")
+
+
+# --------------------------------------------------------------------------
+# the layer prologue over codebook and plain caches
+# --------------------------------------------------------------------------
+def weight(seed, D):
+    rng = np.random.default_rng(seed)
+    return synth.f32_to_bf16_bits((1.0 + 0.5 * rng.standard_normal(D)).astype(np.float32))
+
+
+PRO_CONFIGS = [  # mode, D, bits, rope_dims, theta
+    (CB, 512, 3, 128, 1e6),
+    (CB, 256, 2, 256, 10000.0),
+    (CB, 128, 4, 8, 500.0),
+    (PLAIN, 512, 16, 512, 1e6),
+    (PLAIN, 256, 16, 64, 10000.0),
+]
+
+
+@pytest.mark.parametrize("mode,D,bits,rope_dims,theta", PRO_CONFIGS)
+@pytest.mark.parametrize("k_eq_v", [False, True])
+def test_projected_append_modes_bit_exact(gpu, ora, mode, D, bits, rope_dims, theta, k_eq_v):
+    import torch
+
+    Hkv, eps = 2, 1e-6
+    w = weight(D + rope_dims + mode, D)
+    pro = gpu.make_prologue(dev_bf16(w), eps, rope_dims, theta, v_from_k=k_eq_v)
+    cache, oc = make_cache(gpu, ora, mode, D, bits, Hkv, cap=200)
+    for i, n in enumerate((37, 1, 20, 16)):
+        k = kv_batch(3 * i + D, n, Hkv, D)
+        v = kv_batch(3 * i + D + 1, n, Hkv, D)
+        cache.append_projected(dev_bf16(k), None if k_eq_v else dev_bf16(v), pro)
+        oc.append_projected(k, None if k_eq_v else v, w, eps, rope_dims, theta)
+    codes, meta = cache.read_codes()
+    torch.cuda.synchronize()
+    n = oc.offset
+    assert np.array_equal(host_u32(codes)[:n], oc.codes[:n])
+    assert np.array_equal(host_u16(meta)[:n], oc.meta[:n])
+    q = synth.q_rows(D + 5, 16, Hkv, D, None)
+    out = cache.attention(dev_bf16(q), 1.0, dtype=torch.float32)
+    torch.cuda.synchronize()
+    check_attention(out, oc.attention(q, 1.0), "attention over projected rows")
+
+
+@pytest.mark.parametrize("mode,D,bits,rope_dims,theta", PRO_CONFIGS)
+@pytest.mark.parametrize("k_eq_v", [False, True])
+def test_projected_step_modes(gpu, ora, mode, D, bits, rope_dims, theta, k_eq_v):
+    """Fused projected decode steps (the prologue in the attention launch's
+    new-token column) on a linear cache, dense and with sparse-V: the stored
+    rows bit-exact after every step, each step's output within tolerance."""
+    import torch
+
+    Hkv, Hq, eps = 2, 8, 1e-6
+    w = weight(7 * D + rope_dims + mode, D)
+    pro = gpu.make_prologue(dev_bf16(w), eps, rope_dims, theta, v_from_k=k_eq_v)
+    cache, oc = make_cache(gpu, ora, mode, D, bits, Hkv, cap=64)
+    k0, v0 = kv_batch(D, 30, Hkv, D), kv_batch(D + 1, 30, Hkv, D)
+    cache.append_projected(dev_bf16(k0), None if k_eq_v else dev_bf16(v0), pro)
+    oc.append_projected(k0, None if k_eq_v else v0, w, eps, rope_dims, theta)
+    for step in range(6):
+        k = kv_batch(500 + 2 * step, 1, Hkv, D, special=False)
+        v = kv_batch(501 + 2 * step, 1, Hkv, D, special=False)
+        q = synth.q_rows(600 + step, Hq, Hkv, D, None)
+        tau = 0.0 if step % 2 == 0 else 0.02
+        out = cache.decode_step_projected(dev_bf16(k), None if k_eq_v else dev_bf16(v), pro,
+                                          dev_bf16(q), 0.1, sparse_v_tau=tau, dtype=torch.float32)
+        oc.append_projected(k, None if k_eq_v else v, w, eps, rope_dims, theta)
+        codes, meta = cache.read_codes()
+        torch.cuda.synchronize()
+        n = oc.offset
+        assert np.array_equal(host_u32(codes)[:n], oc.codes[:n]), f"step {step} rows"
+        assert np.array_equal(host_u16(meta)[:n], oc.meta[:n]), f"step {step} norms"
+        check_attention(out, oc.attention(q, 0.1, tau), f"step {step} tau {tau}")
+
+
+@pytest.mark.parametrize("mode,bits", [(CB, 3), (PLAIN, 16)])
+def test_projected_steps_modes_ring(gpu, ora, mode, bits):
+    """Sliding ring W = 64: fused projected decode steps through wraps."""
+    import torch
+
+    D, Hkv, Hq, W, eps, rope_dims, theta = 256, 8, 16, 64, 1e-6, 256, 10000.0
+    w = weight(19 + mode, D)
+    pro = gpu.make_prologue(dev_bf16(w), eps, rope_dims, theta)
+    cache, oc = make_cache(gpu, ora, mode, D, bits, Hkv, window=W)
+    k0, v0 = kv_batch(31, 50, Hkv, D), kv_batch(32, 50, Hkv, D)
+    cache.append_projected(dev_bf16(k0), dev_bf16(v0), pro)
+    oc.append_projected(k0, v0, w, eps, rope_dims, theta)
+    for step in range(90):
+        k = kv_batch(1000 + 2 * step, 1, Hkv, D, special=False)
+        v = kv_batch(1001 + 2 * step, 1, Hkv, D, special=False)
+        q = synth.q_rows(2000 + step, Hq, Hkv, D, None)
+        out = cache.decode_step_projected(dev_bf16(k), dev_bf16(v), pro, dev_bf16(q), 0.1,
+                                          dtype=torch.float32)
+        oc.append_projected(k, v, w, eps, rope_dims, theta)
+        if step % 11 == 0 or step == 89:
+            torch.cuda.synchronize()
+            check_attention(out, oc.attention(q, 0.1), f"ring step {step}")
+    codes, meta = cache.read_codes()
+    torch.cuda.synchronize()
+    assert np.array_equal(host_u32(codes), oc.codes)
+    assert np.array_equal(host_u16(meta), oc.meta)
+
+
+@pytest.mark.parametrize("mode,bits", [(CB, 3), (PLAIN, 16)])
+def test_projected_paged_modes_large_positions(gpu, ora, mode, bits):
+    """Paged pool, sequences starting at positions 100003 and 7: appends and a
+    fused decode step through the prologue, rows bit-exact with the oracle."""
+    import torch
+
+    D, Hkv, Hq, eps, rope_dims, theta = 512, 2, 16, 1e-6, 128, 1e6
+    w = weight(11 + mode, D)
+    pro = gpu.make_prologue(dev_bf16(w), eps, rope_dims, theta)
+    starts, n = [100003, 7], 21
+    width = (max(starts) + n + 1) // 16 + 1
+    tables = np.full((2, width), -1, np.int32)
+    phys = 0
+    for s, p0 in enumerate(starts):
+        for lb in range(p0 // 16, (p0 + n) // 16 + 1):
+            tables[s, lb] = phys
+            phys += 1
+    pool = gpu.PagedPool(gpu.make_desc(Hkv, D, bits, mode=mode), phys)
+    dtab = torch.from_numpy(tables).cuda()
+    k = np.stack([kv_batch(60 + s, n + 1, Hkv, D, special=False) for s in range(2)])
+    v = np.stack([kv_batch(70 + s, n + 1, Hkv, D, special=False) for s in range(2)])
+    st = torch.tensor(starts, dtype=torch.int32, device="cuda")
+    pool.append_projected(dev_bf16(k[:, :n].copy()), dev_bf16(v[:, :n].copy()), dtab, st, pro)
+    q = np.stack([synth.q_rows(80 + s, Hq, Hkv, D, None) for s in range(2)])
+    out = pool.decode_step_projected(dev_bf16(k[:, n:].copy()), dev_bf16(v[:, n:].copy()), dtab,
+                                     st + n, st + n + 1, max(starts) + n + 1, pro, dev_bf16(q),
+                                     0.1, dtype=torch.float32)
+    codes, meta = pool.read_codes()
+    torch.cuda.synchronize()
+    codes, meta = host_u32(codes), host_u16(meta)
+    qz = ora.OracleCache(Hkv, D, bits, 0, 1, mode=mode)
+    for s, p0 in enumerate(starts):
+        ko, vo = ora.kv_prologue(k[s], v[s], p0, w, eps, rope_dims, theta)
+        kp, km = qz.quantize_rows(ko)
+        vp, vm = qz.quantize_rows_f32(vo)
+        for t in range(n + 1):
+            p = p0 + t
+            slot = tables[s, p // 16] * 16 + p % 16
+            assert np.array_equal(codes[slot, 0], kp[t]) and np.array_equal(meta[slot, 0], km[t])
+            assert np.array_equal(codes[slot, 1], vp[t]) and np.array_equal(meta[slot, 1], vm[t])
+    assert torch.isfinite(out[1]).all()

@@ -258,24 +258,16 @@ def test_plain_linear_decode_steps(gpu, ora, bps):
     check_codes(codes, meta, oc, None, f"bps={bps} rows")
 
 
-def test_plain_rejects_quantized_only_paths(gpu):
-    """Sparse-V, prefill attention and the fused prologue read quantized
-    caches only; each fails before launching anything."""
+def test_plain_rejects_prefill(gpu):
+    """Prefill attention reads quantized caches only; it fails before
+    launching anything."""
     import torch
 
     D = 256
     cache = gpu.KVCache.new(D, 2, capacity=64)
     k = torch.zeros((4, 2, D), dtype=torch.bfloat16, device="cuda")
     cache.append(k, k)
-    q = torch.zeros((4, D), dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(gpu.Exception_) as e:
-        cache.attention(q, 1.0, sparse_v_tau=1e-3)
-    assert e.value.code == gpu.FMKV_ERR_UNSUPPORTED
     with pytest.raises(gpu.Exception_) as e:
         cache.prefill_step(k, k, torch.zeros((4, 4, D), dtype=torch.bfloat16, device="cuda"))
-    assert e.value.code == gpu.FMKV_ERR_UNSUPPORTED
-    w = torch.ones(D, dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(gpu.Exception_) as e:
-        cache.append_projected(k, k, gpu.make_prologue(w, 1e-6, 256, 1e4))
     assert e.value.code == gpu.FMKV_ERR_UNSUPPORTED
     assert cache.offset() == 4

@@ -138,7 +138,3 @@ def test_projected_append_rejects_bad_prologue(gpu):
     with pytest.raises(ValueError):  # weight length != head_dim
         cache.append_projected(k, k, gpu.make_prologue(dev_bf16(weight(1, 128)), 1e-6, 256, 1e4))
     assert cache.offset() == 0
-    cb = gpu.KVCache(gpu.make_desc(2, D, 3, mode=gpu.MODE_CODEBOOK, capacity=32))
-    with pytest.raises(gpu.Exception_) as e:
-        cb.append_projected(k, k, gpu.make_prologue(wd, 1e-6, 256, 1e4))
-    assert e.value.code == gpu.FMKV_ERR_UNSUPPORTED

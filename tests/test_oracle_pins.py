@@ -278,6 +278,32 @@ def test_codebook_canonical_vs_dense_reference(ora, bits, d):
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("d", [256, 512])
+def test_codebook_quantize_f32_rows(ora, bits, d):
+    """ora_codebook_quantize_f32 (f32 rows: V after v_norm) bins exactly as
+    ora_codebook_quantize on bf16-representable rows, and on general f32 rows
+    follows the exact binning of (x/|x|) . R . sqrt(d) (src/cache.rs:104-118,
+    f64) up to boundary flips of the f32 rounding."""
+    rng = np.random.default_rng(7 * bits + d)
+    x = rng.standard_normal((64, d)).astype(np.float32)
+    x /= np.sqrt(np.mean(x * x, axis=1, keepdims=True))
+    x[:, 3] *= 20
+    s = ora.signs(d, 42)
+    xb = synth.f32_to_bf16_bits(x)
+    pb, nb = ora.codebook_quantize(xb, bits, s)
+    pf, nf = ora.codebook_quantize_f32(ora.bf16_to_f32(xb), bits, s)
+    assert np.array_equal(pb, pf) and np.array_equal(nb, nf)
+    packed, norms = ora.codebook_quantize_f32(x, bits, s)
+    r, _ = ora.build_rht(d, 42)
+    xf = x.astype(np.float64)
+    z = (xf / np.linalg.norm(xf, axis=1, keepdims=True)) @ r.astype(np.float64) * math.sqrt(d)
+    idx_exact = np.searchsorted(ora.codebook(bits)[1].astype(np.float64), z, side="right")
+    assert np.mean(ora.unpack_codes(packed, d, bits) != idx_exact) < 1e-3
+    assert np.array_equal(norms, ora.f32_to_f16(np.sqrt(np.sum(xf * xf, axis=1)).astype(np.float32))) or \
+        np.allclose(ora.f16_to_f32(norms), np.linalg.norm(xf, axis=1), rtol=1e-3)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
 @pytest.mark.parametrize("d", [128, 256, 512])
 def test_codebook_dequant_rotated_is_reference_dequant(ora, bits, d):
     """ora_codebook_dequant_rotated (the rotated-domain row every codebook
