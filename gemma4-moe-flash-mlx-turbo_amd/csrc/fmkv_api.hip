@@ -690,8 +690,6 @@ int fmkv_prefill_step(fmkv_cache* c, const void* k, const void* v, int64_t n, co
                       int32_t n_q_heads, float scale, void* out, int32_t out_dtype, void* stream) {
   if (!c) return fail(FMKV_ERR_INVALID_ARG, "cache is null");
   if (n < 1) return fail(FMKV_ERR_INVALID_ARG, "a prefill step appends at least one token");
-  if (c->desc.mode != FMKV_MODE_AFFINE)
-    return fail(FMKV_ERR_UNSUPPORTED, "prefill attention reads affine-mode caches");
   int rc = check_attn_args(c->desc, q, n_q_heads, 0.0f, out, out_dtype);
   if (rc) return rc;
   if (!std::isfinite(scale)) return fail(FMKV_ERR_INVALID_ARG, "scale must be finite");
@@ -976,8 +974,6 @@ int fmkv_paged_prefill_step(fmkv_pool* p, const void* k, const void* v,
   if (!p) return fail(FMKV_ERR_INVALID_ARG, "pool is null");
   if (n_seqs < 1 || n_new < 1)
     return fail(FMKV_ERR_INVALID_ARG, "a prefill step needs n_seqs >= 1 and n_new >= 1");
-  if (p->desc.mode != FMKV_MODE_AFFINE)
-    return fail(FMKV_ERR_UNSUPPORTED, "prefill attention reads affine-mode caches");
   int rc = check_attn_args(p->desc, q, n_q_heads, 0.0f, out, out_dtype);
   if (rc) return rc;
   if (!std::isfinite(scale)) return fail(FMKV_ERR_INVALID_ARG, "scale must be finite");

@@ -52,20 +52,13 @@
 #include "fmkv_prologue.h"
 #include "fmkv_quant.h"
 #include "fmkv_attn_common.h"
+#include "fmkv_cb_common.h"
 
 namespace fmkv {
 namespace {
 
-// src/cache.rs:67-89 centroids (the same literals as the append's tables).
-__constant__ float kCbCent2[4] = {-1.510f, -0.453f, 0.453f, 1.510f};
-__constant__ float kCbCent3[8] = {-2.152f, -1.344f, -0.756f, -0.245f, 0.245f, 0.756f, 1.344f, 2.152f};
-__constant__ float kCbCent4[16] = {-2.733f, -2.069f, -1.618f, -1.256f, -0.942f, -0.657f,
-                                   -0.388f, -0.128f, 0.128f,  0.388f,  0.657f,  0.942f,
-                                   1.256f,  1.618f,  2.069f,  2.733f};
-
 constexpr int kCbWaves = 8;  // four wave pairs, two waves per SIMD
 constexpr int kCbStreams = kCbWaves / 2;
-constexpr int kLutCopies = 32;
 
 template <int D, int BITS>
 struct CbPlan {
@@ -80,13 +73,9 @@ struct CbPlan {
   static constexpr int kNormOff = 4 * kHalfBytes;
   static constexpr int kStageBytes = kNormOff + 2 * 64;
   static constexpr int kCopies = 2 * kHalfCopies + 1;  // per wave per block
-  // index pairs (2 and 3 bits; 16 or 64 entries, a high-part table and a
-  // residual table) or single indices (4 bits; 16 entries of {high,
-  // residual}); 4 bytes per entry and copy
-  static constexpr bool kPairs = BITS <= 3;
-  static constexpr int kLutEntries = kPairs ? (1 << (2 * BITS)) : 16;
-  static constexpr int kLutHalf = kLutEntries * kLutCopies * 4;  // one table
-  static constexpr int kLutBytes = kPairs ? 2 * kLutHalf : kLutHalf;
+  // the centroid lookup table (fmkv_cb_common.h)
+  static constexpr int kLutHalf = CbLut<BITS>::kHalf;
+  static constexpr int kLutBytes = CbLut<BITS>::kBytes;
   // q table (the QK B operands, one KiB per slice), then the score exchange
   static constexpr int kTabBytes = (D / 32) * 1024;
   static constexpr int kXBytes = kCbWaves * 2 * 64 * 16;
@@ -154,61 +143,6 @@ __device__ void cb_build_q_table(const AttnArgs& a, uint8_t* tab, int wave, int 
     store_halves<E>(ent + (jj * 16 + wave + 8) * 16, lv);
   }
   __syncthreads();
-}
-
-// Centroid i as {f16 high part, f16 residual}.
-template <int BITS>
-__device__ inline uint32_t cent_hl(int i) {
-  const float cv = BITS == 2 ? kCbCent2[i] : BITS == 3 ? kCbCent3[i] : kCbCent4[i];
-  const _Float16 h = (_Float16)cv;
-  const _Float16 r = (_Float16)(cv - (float)h);
-  return (uint32_t)__builtin_bit_cast(uint16_t, h) | ((uint32_t)__builtin_bit_cast(uint16_t, r) << 16);
-}
-
-// A lane's field: the bits from `sh` on of word `dw` of w (and of the next
-// word at 3 bits, where fields straddle words; that word lies inside the LDS
-// staging: the K halves are followed by the V halves, the V halves by the
-// norms). 2- and 4-bit fields never straddle a word.
-template <int BITS>
-__device__ inline uint32_t lds_field(const uint32_t* w, int dw, uint32_t sh) {
-  if constexpr (BITS == 3)
-    return __builtin_amdgcn_alignbit(w[dw + 1], w[dw], sh);
-  else
-    return w[dw] >> sh;
-}
-
-typedef const uint32_t __attribute__((address_space(3)))* lds_u32_ptr;
-typedef const volatile uint32_t __attribute__((address_space(3)))* lds_vu32_ptr;
-__device__ inline uint32_t lds_load(uint32_t addr) { return *(lds_u32_ptr)(size_t)addr; }
-
-// Bits [OFF, OFF + W) of x (one v_bfe_u32; written out so that the index
-// and the table address stay two instructions).
-template <int OFF, int W>
-__device__ inline uint32_t bfe(uint32_t x) {
-  uint32_t r;
-  asm("v_bfe_u32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "n"(OFF), "n"(W));
-  return r;
-}
-
-// High and residual f16 operand words of two consecutive elements of a
-// field (the field's elements 2p and 2p + 1, element e at bits e * BITS);
-// base: LDS address of this lane's copy of entry 0 of the high-part table
-// (4-bit: of the one table). The residual is read at the same address plus
-// LUT_HALF as a volatile load, so that the two lookups stay two 4-byte loads
-// into the operand registers instead of being merged into one paired load
-// whose halves then need moving.
-template <int BITS, int LUT_HALF, int P>
-__device__ inline void cb_pair(uint32_t base, uint32_t field, uint32_t& hw, uint32_t& lw) {
-  if constexpr (BITS <= 3) {
-    const uint32_t a = base + bfe<2 * P * BITS, 2 * BITS>(field) * (kLutCopies * 4);
-    hw = lds_load(a);
-    lw = *(lds_vu32_ptr)(size_t)(a + LUT_HALF);
-  } else {
-    const uint32_t e0 = lds_load(base + bfe<8 * P, 4>(field) * (kLutCopies * 4));
-    const uint32_t e1 = lds_load(base + bfe<8 * P + 4, 4>(field) * (kLutCopies * 4));
-    hw = __builtin_amdgcn_perm(e1, e0, 0x05040100u);  // the high parts
-    lw = __builtin_amdgcn_perm(e1, e0, 0x07060302u);  // the residuals
-  }
 }
 
 // The new-token column of a decode step, one work-group per (seq, kvh): the
@@ -468,16 +402,7 @@ void cb_decode_kernel(AttnArgs a) {
   };
 
   // ---- prologue: LUT, copies, q table ----
-  for (int e = tid; e < P::kLutEntries * kLutCopies; e += kCbWaves * 64) {
-    const int idx = e / kLutCopies;
-    if constexpr (P::kPairs) {
-      const uint32_t c0 = cent_hl<BITS>(idx & ((1 << BITS) - 1)), c1 = cent_hl<BITS>(idx >> BITS);
-      *reinterpret_cast<uint32_t*>(lut + e * 4) = (c0 & 0xffffu) | (c1 << 16);
-      *reinterpret_cast<uint32_t*>(lut + P::kLutHalf + e * 4) = (c0 >> 16) | (c1 & 0xffff0000u);
-    } else {
-      *reinterpret_cast<uint32_t*>(lut + e * 4) = cent_hl<BITS>(idx);
-    }
-  }
+  cb_fill_lut<BITS>(lut, tid, kCbWaves * 64);
   if (lane == 0) xflag[wave] = 0;
   constexpr int NQ = (NST + 1) / 2;
   cb_copy_q_row<D>(a, scratch, seq, kvh, wave, lane);

@@ -1,4 +1,4 @@
-// Prefill (chunked) attention over the quantized cache (affine mode).
+// Prefill (chunked) attention over the cache, every mode.
 //
 // Replaces mlx_rs::fast::scaled_dot_product_attention for L > 1
 // (src/model/gemma4_attention.rs:84-104) with the causal mask of
@@ -15,7 +15,7 @@
 // identical softmax bookkeeping, as the decode kernel's pairs do; the
 // matrix-core columns are the pair's 16 rows.
 //
-// Per block (16 keys), per 64-dim group g of the wave's half:
+// Per block (16 keys), affine caches, per 64-dim group g of the wave's half:
 //   QK^T  S^T[16 key x 16 row] += K[16 x 32] . Q^T[32 x 16] with K codes as
 //         exact f16 integers, q_rot as an f16 high part and an f16 residual
 //         (~22 bits), each in its own accumulator; then
@@ -27,6 +27,16 @@
 //   PV    O^T[16 dim x 16 row] += V^T[16 dim x 16 key] . P'^T[16 key x 16 row]
 //         with P' = p * v_scale as f16 high part + residual (two MFMAs);
 //         the bias terms are summed on the side.
+// Codebook (TurboQuant) caches, per 32-dim slice / 16-dim tile of the
+// wave's half: the indices become f16 centroid operands (high part and
+// residual) through the decode kernel's LDS lookup table (fmkv_cb_common.h),
+// S^T = C_hi . q_hi + C_lo . q_hi + C_hi . q_lo, scaled per key by
+// norm / sqrt(D); O^T likewise with P' = p * norm / sqrt(D) as f16 high part
+// and residual (three MFMAs each: the fourth product is below f32 rounding).
+// Plain (bf16) caches read K rows and V columns as bf16 operands
+// (v_mfma_f32_16x16x32_bf16 / 16x16x16_bf16) against the raw bf16 q (exact
+// products; the softmax scale applies after), P as bf16 high part and
+// residual; no rotation.
 // Blocks wholly outside a pair's rows' windows are skipped by that pair.
 //
 // A paged pool runs one sequence per grid z with its own start position and
@@ -46,6 +56,7 @@
 #include "fmkv_device.h"
 #include "fmkv_internal.h"
 #include "fmkv_attn_common.h"
+#include "fmkv_cb_common.h"
 
 namespace fmkv {
 namespace {
@@ -54,22 +65,35 @@ constexpr int kPfWaves = 8;   // four pairs
 constexpr int kPfRows = 64;   // query rows per work-group (16 per pair)
 constexpr int kPfStages = 3;
 
-template <int D, int BITS>
+template <int D, int BITS, int MODE>
 struct PfPlan {
-  static constexpr BlockLayout L = make_layout(D, BITS, kAffine);
+  static constexpr BlockLayout L = make_layout(D, BITS, MODE);
   static constexpr int NG = D / 64;
   static constexpr int GH = NG / 2;  // groups per wave
-  // a head-block's codes and scale/bias: [K codes][V codes][K meta][V meta]
-  static constexpr int kBytes = (int)(2 * L.code_bytes) + 2 * NG * 64;
+  static constexpr int NSW = D / 64;  // 32-dim QK slices per wave
+  static constexpr int NTW = D / 32;  // 16-dim PV tiles per wave
+  // the bytes of a head-block the kernel reads: affine [K codes][V codes]
+  // [K meta][V meta]; codebook [K codes][V codes][K norms, padded][V norms];
+  // plain [K rows][V columns]
+  static constexpr int kBytes = MODE == kAffine     ? (int)(2 * L.code_bytes) + 2 * NG * 64
+                                : MODE == kCodebook ? (int)L.v_meta + 2 * kBlockTokens
+                                                    : (int)(2 * L.code_bytes);
   static constexpr int kNC = (kBytes + kChunk - 1) / kChunk;
   static constexpr int CP = (kNC + kPfWaves - 1) / kPfWaves;  // copies per wave per block
   static constexpr int kStageBytes = kPfWaves * CP * kChunk;
-  static constexpr int kQStride = D + 8;  // f16 per q-table row (padding against bank conflicts)
-  static constexpr int kQTab = 2 * kPfRows * kQStride * 2 + kPfRows * NG * 4;
+  static constexpr int kQStride = D + 8;  // 16-bit values per q-table row (padding against bank conflicts)
+  // q table: high and residual parts of q_rot (affine: and group sums);
+  // plain: the raw bf16 rows
+  static constexpr int kQTab = (MODE == kPlain ? 1 : 2) * kPfRows * kQStride * 2 +
+                               (MODE == kAffine ? kPfRows * NG * 4 : 0);
   static constexpr int kRStride = D + 4;  // f32 per output row
   static constexpr int kRows = kPfRows * kRStride * 4;
-  static constexpr int kRegion = cmax(cmax(kPfStages * kStageBytes, kQTab), kRows);
-  static_assert((int)L.k_meta == (int)(2 * L.code_bytes) && (int)L.v_meta == (int)L.k_meta + NG * 64,
+  // codebook: the centroid lookup table follows the stages
+  static constexpr int kLutOff = kPfStages * kStageBytes;
+  static constexpr int kLutBytes = MODE == kCodebook ? CbLut<BITS == 16 ? 2 : BITS>::kBytes : 0;
+  static constexpr int kRegion = cmax(cmax(kLutOff + kLutBytes, kQTab), kRows);
+  static_assert(MODE != kAffine || ((int)L.k_meta == (int)(2 * L.code_bytes) &&
+                                    (int)L.v_meta == (int)L.k_meta + NG * 64),
                 "codes and scale/bias are contiguous in a head-block");
   static_assert(kPfStages * CP <= 63, "vmcnt immediates");
 };
@@ -86,14 +110,24 @@ __device__ inline half8_t k_operand_plain(const u32x4 w, int g, int s) {
   }
 }
 
-template <int D, int BITS>
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+__device__ inline uint32_t pack_bf16x2(float a, float b) {
+  return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+}
+
+template <int D, int BITS, int MODE>
 __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_attn_kernel(PrefillArgs a) {
-  using P = PfPlan<D, BITS>;
+  using P = PfPlan<D, BITS, MODE>;
   constexpr BlockLayout L = P::L;
   constexpr int NG = P::NG, GH = P::GH, E = D / 64, LPG = 64 / E;
+  constexpr int NSW = P::NSW, NTW = P::NTW;
   constexpr int CP = P::CP, NST = kPfStages, SB = P::kStageBytes;
   constexpr int QS = P::kQStride, RS = P::kRStride;
+  // codebook index width (the template's BITS; other modes never use it)
+  constexpr int CB = MODE == kCodebook ? BITS : 2;
 
   __shared__ __align__(16) uint8_t region[P::kRegion];
   __shared__ __align__(16) float4_t xs[kPfWaves * 2 * 64];
@@ -182,10 +216,11 @@ void prefill_attn_kernel(PrefillArgs a) {
     return v;
   };
 
-  // ---- q_rot of the 64 rows: rows wave + 8 k, high / residual halves ----
+  // ---- q_rot of the 64 rows: rows wave + 8 k, high / residual halves
+  // (plain: the raw bf16 rows) ----
   _Float16* const qhi = reinterpret_cast<_Float16*>(region);
   _Float16* const qlo = qhi + kPfRows * QS;
-  float* const qsum = reinterpret_cast<float*>(qlo + kPfRows * QS);  // [row][NG]
+  float* const qsum = reinterpret_cast<float*>(qlo + kPfRows * QS);  // [row][NG] (affine)
   const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
   const float cs_lane = fwht_lane_sign(lane) * a.c;
   if (lane == 0) xflag[wave] = 0;
@@ -193,6 +228,16 @@ void prefill_attn_kernel(PrefillArgs a) {
   for (int k = 0; k < kPfRows / kPfWaves; k++) {
     const int r = wave + kPfWaves * k;
     const int rq_ = r / G, rh_ = r - (r / G) * G;
+    if constexpr (MODE == kPlain) {
+      // E consecutive bf16 of the row as stored (zero past the chunk)
+      const uint16_t* src =
+          a.q + (((int64_t)seq * a.n_q + qi0 + rq_) * a.n_q_heads + (int64_t)kvh * G + rh_) * D +
+          lane * E;
+      uint16_t* dst = reinterpret_cast<uint16_t*>(qhi + r * QS + lane * E);
+#pragma unroll
+      for (int i = 0; i < E; i++) dst[i] = rq_ < nq ? src[i] : (uint16_t)0;
+      continue;
+    }
     float x[E];
 #pragma unroll
     for (int i = 0; i < E; i++) x[i] = 0.0f;
@@ -216,12 +261,15 @@ void prefill_attn_kernel(PrefillArgs a) {
     gs = group_sum<LPG>(gs, lane);
     store_halves<E>(reinterpret_cast<uint8_t*>(qhi + r * QS + lane * E), hv);
     store_halves<E>(reinterpret_cast<uint8_t*>(qlo + r * QS + lane * E), lv);
-    if ((lane & (LPG - 1)) == 0) qsum[r * NG + ((lane * E) >> 6)] = gs;
+    if constexpr (MODE == kAffine)
+      if ((lane & (LPG - 1)) == 0) qsum[r * NG + ((lane * E) >> 6)] = gs;
   }
   __syncthreads();
 
   // this wave's B operands: its pair's 16 rows, its groups; the lane (j, c)
   // holds 8 consecutive dims of row `row` at the K-code placement
+  // (codebook and plain: slice k = 2 gi + s of the wave's half, dims
+  // half * D / 2 + 32 k + 8 j ..; plain B operands are the bf16 bits)
   half8_t bqh[GH][2], bql[GH][2];
   float qs[GH];
 #pragma unroll
@@ -229,13 +277,19 @@ void prefill_attn_kernel(PrefillArgs a) {
     const int g = g0 + gi;
 #pragma unroll
     for (int s = 0; s < 2; s++) {
-      const int d0 = g * 64 + (BITS == 8 ? j * 16 + s * 8 : s * 32 + j * 8);
+      const int d0 = MODE == kAffine ? g * 64 + (BITS == 8 ? j * 16 + s * 8 : s * 32 + j * 8)
+                                     : half * (D / 2) + (2 * gi + s) * 32 + j * 8;
       bqh[gi][s] = *reinterpret_cast<const half8_t*>(qhi + row * QS + d0);
-      bql[gi][s] = *reinterpret_cast<const half8_t*>(qlo + row * QS + d0);
+      if constexpr (MODE != kPlain) bql[gi][s] = *reinterpret_cast<const half8_t*>(qlo + row * QS + d0);
     }
-    qs[gi] = qsum[row * NG + g];
+    qs[gi] = MODE == kAffine ? qsum[row * NG + g] : 0.0f;
   }
   __syncthreads();  // the table is consumed: the region becomes the stages
+  // codebook: the centroid lookup table, after the stages (written before
+  // the first block's barrier)
+  uint8_t* const lut = region + P::kLutOff;
+  const uint32_t lut_l = lds_addr(lut) + (lane & (kLutCopies - 1)) * 4;
+  if constexpr (MODE == kCodebook) cb_fill_lut<CB>(lut, tid, kPfWaves * 64);
 
   // ---- copies ----
   const uint32_t stage_lds = lds_addr(region);
@@ -275,8 +329,42 @@ void prefill_attn_kernel(PrefillArgs a) {
     return lds16(sp + (int)L.v_meta + (g0 + gi) * 64 + j * 16);
   };
 
+  // codebook: this lane's index fields in the wave's half of K (token c,
+  // dims 8 j .. of each slice) and V (dim c of each tile, tokens 4 j ..)
+  constexpr int HB = D * CB;  // bytes of one half of the K (or V) indices
+  const int kbit0 = (c * (D / 2) + 8 * j) * CB, vbit0 = (c * 16 + 4 * j) * CB;
+  const uint32_t ksh = kbit0 & 31, vsh = vbit0 & 31;
+  // plain: this lane's operand offsets (K row c, dims 8 j .. of each slice;
+  // V dim c of each tile, tokens 4 j ..)
+  const int pk_off = (int)L.k_codes + (c * D + half * (D / 2) + 8 * j) * 2;
+  const int pv_off = (int)L.v_codes + ((half * (D / 2) + c) * kBlockTokens + 4 * j) * 2;
+
   auto process = [&](const uint8_t* sp, const VB& v, int it) {
     float4_t sv = (float4_t){0.f, 0.f, 0.f, 0.f};
+    if constexpr (MODE == kCodebook) {
+      const uint32_t* kw =
+          reinterpret_cast<const uint32_t*>(sp + (int)L.k_codes + half * HB) + (kbit0 >> 5);
+#pragma unroll
+      for (int k = 0; k < NSW; k++) {
+        const uint32_t f = lds_field<CB>(kw, k * CB, ksh);
+        uint32_t h4[4], l4[4];
+        cb_pair<CB, CbLut<CB>::kHalf, 0>(lut_l, f, h4[0], l4[0]);
+        cb_pair<CB, CbLut<CB>::kHalf, 1>(lut_l, f, h4[1], l4[1]);
+        cb_pair<CB, CbLut<CB>::kHalf, 2>(lut_l, f, h4[2], l4[2]);
+        cb_pair<CB, CbLut<CB>::kHalf, 3>(lut_l, f, h4[3], l4[3]);
+        const half8_t ah = __builtin_bit_cast(half8_t, (u32x4){h4[0], h4[1], h4[2], h4[3]});
+        const half8_t al = __builtin_bit_cast(half8_t, (u32x4){l4[0], l4[1], l4[2], l4[3]});
+        sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bqh[k >> 1][k & 1], sv, 0, 0, 0);
+        sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bqh[k >> 1][k & 1], sv, 0, 0, 0);
+        sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bql[k >> 1][k & 1], sv, 0, 0, 0);
+      }
+    } else if constexpr (MODE == kPlain) {
+#pragma unroll
+      for (int k = 0; k < NSW; k++)
+        sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8_t, lds16(sp + pk_off + k * 64)),
+            __builtin_bit_cast(bf16x8_t, bqh[k >> 1][k & 1]), sv, 0, 0, 0);
+    } else {
     u32x4 kw = codes(sp, (int)L.k_codes, 0), km = kmeta(sp, 0);
 #pragma unroll
     for (int gi = 0; gi < GH; gi++) {
@@ -298,7 +386,7 @@ void prefill_attn_kernel(PrefillArgs a) {
         sv[i] = fmaf(lo16(km_g[i]), acc[i], fmaf(hi16(km_g[i]), qs[gi], sv[i]));
       __builtin_amdgcn_sched_barrier(0);
     }
-    u32x4 vw = codes(sp, (int)L.v_codes, 0), vm = vmeta(sp, 0);
+    }
 
     // exchange the half scores with the partner wave (release / acquire on
     // a per-wave counter); both waves add the halves in the same order
@@ -314,6 +402,23 @@ void prefill_attn_kernel(PrefillArgs a) {
     float s[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) s[i] = s0[i] + s1[i];
+    // codebook: the keys' norms / sqrt(D) (lane (j, c) holds keys 4 j ..);
+    // plain: the softmax scale
+    float vscale[4] = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (MODE == kCodebook) {
+      const uint2 kn = *reinterpret_cast<const uint2*>(sp + (int)L.k_meta + 8 * j);
+      const uint2 vn = *reinterpret_cast<const uint2*>(sp + (int)L.v_meta + 8 * j);
+      const float ks[4] = {lo16(kn.x), hi16(kn.x), lo16(kn.y), hi16(kn.y)};
+      const float vs[4] = {lo16(vn.x), hi16(vn.x), lo16(vn.y), hi16(vn.y)};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        s[i] = s[i] * (ks[i] * a.c);
+        vscale[i] = vs[i] * a.c;
+      }
+    } else if constexpr (MODE == kPlain) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) s[i] = s[i] * a.qscale;
+    }
 
     // masks: the whole block for all rows of the pair in the common case
     const int64_t t0 = v.b * kBlockTokens;
@@ -339,7 +444,7 @@ void prefill_attn_kernel(PrefillArgs a) {
 #pragma unroll
         for (int gi = 0; gi < GH; gi++) {
           bacc[gi] *= alpha;
-          if constexpr (kBiasedCodes<BITS>) psum[gi] *= alpha;
+          if constexpr (MODE == kAffine && kBiasedCodes<BITS>) psum[gi] *= alpha;
         }
       }
       l_run *= alpha;
@@ -349,6 +454,52 @@ void prefill_attn_kernel(PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(s[i] - m_run);
     l_run += (p[0] + p[1]) + (p[2] + p[3]);
+
+    if constexpr (MODE == kCodebook) {
+      // O^T += V^T . P'^T, P' = p * norm / sqrt D as f16 high part and
+      // residual, the centroids likewise
+      float x[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) x[i] = p[i] * vscale[i];
+      const half2_t h01 = pkrtz(x[0], x[1]);
+      const half2_t h23 = pkrtz(x[2], x[3]);
+      const half2_t r01 = pkrtz(fmaf(neg_one, (float)h01[0], x[0]), fmaf(neg_one, (float)h01[1], x[1]));
+      const half2_t r23 = pkrtz(fmaf(neg_one, (float)h23[0], x[2]), fmaf(neg_one, (float)h23[1], x[3]));
+      const half4_t bh = cat4(h01, h23), bl = cat4(r01, r23);
+      const uint32_t* vw =
+          reinterpret_cast<const uint32_t*>(sp + (int)L.v_codes + half * HB) + (vbit0 >> 5);
+#pragma unroll
+      for (int n = 0; n < NTW; n++) {
+        const uint32_t f = lds_field<CB>(vw, n * 8 * CB, vsh);
+        uint32_t h2[2], l2[2];
+        cb_pair<CB, CbLut<CB>::kHalf, 0>(lut_l, f, h2[0], l2[0]);
+        cb_pair<CB, CbLut<CB>::kHalf, 1>(lut_l, f, h2[1], l2[1]);
+        const half4_t ah = __builtin_bit_cast(half4_t, make_uint2(h2[0], h2[1]));
+        const half4_t al = __builtin_bit_cast(half4_t, make_uint2(l2[0], l2[1]));
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bh, o[n], 0, 0, 0);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bh, o[n], 0, 0, 0);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bl, o[n], 0, 0, 0);
+      }
+      return;
+    } else if constexpr (MODE == kPlain) {
+      // O^T += V^T . P^T, P as bf16 high part and residual
+      float r[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) r[i] = p[i] - bf16_to_f32(f32_to_bf16(p[i]));
+      const short4_t bh = __builtin_bit_cast(
+          short4_t, make_uint2(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])));
+      const short4_t bl = __builtin_bit_cast(
+          short4_t, make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])));
+#pragma unroll
+      for (int n = 0; n < NTW; n++) {
+        const short4_t va =
+            __builtin_bit_cast(short4_t, *reinterpret_cast<const uint2*>(sp + pv_off + n * 16 * kBlockTokens * 2));
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, bh, o[n], 0, 0, 0);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, bl, o[n], 0, 0, 0);
+      }
+      return;
+    } else {
+    u32x4 vw = codes(sp, (int)L.v_codes, 0), vm = vmeta(sp, 0);
 
     // O^T += V^T . P'^T, P' = p * v_scale as f16 high part and residual
     const half2_t one2 = (half2_t){(_Float16)1.0f, (_Float16)1.0f};
@@ -388,6 +539,7 @@ void prefill_attn_kernel(PrefillArgs a) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    }
   };
 
   int st = 0, it = 0;
@@ -415,7 +567,7 @@ void prefill_attn_kernel(PrefillArgs a) {
   for (int gi = 0; gi < GH; gi++) {
     bacc[gi] = xor16_sum(bacc[gi]);
     bacc[gi] = xor32_sum(bacc[gi]);
-    if constexpr (kBiasedCodes<BITS>) {
+    if constexpr (MODE == kAffine && kBiasedCodes<BITS>) {
       // the V codes entered the MFMAs as 1024 + code
       const float t = xor32_sum(xor16_sum(psum[gi]));
       bacc[gi] = fmaf(-1024.0f, t, bacc[gi]);
@@ -423,12 +575,15 @@ void prefill_attn_kernel(PrefillArgs a) {
   }
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // the stages are free
   float* const Rr = reinterpret_cast<float*>(region);
+  // (tile n of the wave's half: dims half * D / 2 + 16 n + 4 j .., the
+  // affine group / column-tile order being the same dims)
 #pragma unroll
   for (int gi = 0; gi < GH; gi++)
 #pragma unroll
     for (int ct = 0; ct < 4; ct++) {
       const int d = (g0 + gi) * 64 + ct * 16 + 4 * j;
-      *reinterpret_cast<float4_t*>(&Rr[row * RS + d]) = o[gi * 4 + ct] + bacc[gi];
+      *reinterpret_cast<float4_t*>(&Rr[row * RS + d]) =
+          MODE == kAffine ? o[gi * 4 + ct] + bacc[gi] : o[gi * 4 + ct];
     }
   if (half == 0 && j == 0) lrow[row] = l_run;
   __syncthreads();
@@ -441,12 +596,19 @@ void prefill_attn_kernel(PrefillArgs a) {
     float x[E];
 #pragma unroll
     for (int i = 0; i < E; i++) x[i] = apply_sign(Rr[r * RS + lane * E + i], sbits, i);
-    wave_fwht_signed<E>(x, lane);
+    float cs = cs_lane;
+    if constexpr (MODE != kPlain) {
+      wave_fwht_signed<E>(x, lane);
+    } else {  // no rotation: the row as accumulated
+#pragma unroll
+      for (int i = 0; i < E; i++) x[i] = Rr[r * RS + lane * E + i];
+      cs = 1.0f;
+    }
     const int64_t o_idx =
         (((int64_t)seq * a.n_q + qi0 + rq_) * a.n_q_heads + (int64_t)kvh * G + rh_) * D + lane * E;
 #pragma unroll
     for (int i = 0; i < E; i++) {
-      const float v = l > 0.0f ? (x[i] * cs_lane) / l : 0.0f;
+      const float v = l > 0.0f ? (x[i] * cs) / l : 0.0f;
       if (a.out_f32)
         reinterpret_cast<float*>(a.out)[o_idx + i] = v;
       else
@@ -455,11 +617,11 @@ void prefill_attn_kernel(PrefillArgs a) {
   }
 }
 
-template <int D, int BITS>
+template <int D, int BITS, int MODE>
 hipError_t launch_t(const PrefillArgs& a, hipStream_t s) {
   const int qp = kPfRows / a.group;
   dim3 grid((a.n_q + qp - 1) / qp, a.new_st.n_kv_heads, a.n_seqs);
-  hipLaunchKernelGGL((prefill_attn_kernel<D, BITS>), grid, dim3(kPfWaves * 64), 0, s, a);
+  hipLaunchKernelGGL((prefill_attn_kernel<D, BITS, MODE>), grid, dim3(kPfWaves * 64), 0, s, a);
   return hipGetLastError();
 }
 
@@ -468,13 +630,33 @@ hipError_t launch_t(const PrefillArgs& a, hipStream_t s) {
 hipError_t launch_prefill_attention(const PrefillArgs& a, hipStream_t s) {
   if (a.n_q <= 0) return hipSuccess;
   const BlockLayout& L = a.new_st.layout;
-  switch (L.head_dim * 16 + L.bits) {
-    case 128 * 16 + 4: return launch_t<128, 4>(a, s);
-    case 128 * 16 + 8: return launch_t<128, 8>(a, s);
-    case 256 * 16 + 4: return launch_t<256, 4>(a, s);
-    case 256 * 16 + 8: return launch_t<256, 8>(a, s);
-    case 512 * 16 + 4: return launch_t<512, 4>(a, s);
-    case 512 * 16 + 8: return launch_t<512, 8>(a, s);
+  if (L.mode == kAffine) {
+    switch (L.head_dim * 16 + L.bits) {
+      case 128 * 16 + 4: return launch_t<128, 4, kAffine>(a, s);
+      case 128 * 16 + 8: return launch_t<128, 8, kAffine>(a, s);
+      case 256 * 16 + 4: return launch_t<256, 4, kAffine>(a, s);
+      case 256 * 16 + 8: return launch_t<256, 8, kAffine>(a, s);
+      case 512 * 16 + 4: return launch_t<512, 4, kAffine>(a, s);
+      case 512 * 16 + 8: return launch_t<512, 8, kAffine>(a, s);
+    }
+  } else if (L.mode == kCodebook) {
+    switch (L.head_dim * 16 + L.bits) {
+      case 128 * 16 + 2: return launch_t<128, 2, kCodebook>(a, s);
+      case 128 * 16 + 3: return launch_t<128, 3, kCodebook>(a, s);
+      case 128 * 16 + 4: return launch_t<128, 4, kCodebook>(a, s);
+      case 256 * 16 + 2: return launch_t<256, 2, kCodebook>(a, s);
+      case 256 * 16 + 3: return launch_t<256, 3, kCodebook>(a, s);
+      case 256 * 16 + 4: return launch_t<256, 4, kCodebook>(a, s);
+      case 512 * 16 + 2: return launch_t<512, 2, kCodebook>(a, s);
+      case 512 * 16 + 3: return launch_t<512, 3, kCodebook>(a, s);
+      case 512 * 16 + 4: return launch_t<512, 4, kCodebook>(a, s);
+    }
+  } else if (L.mode == kPlain) {
+    switch (L.head_dim) {
+      case 128: return launch_t<128, 16, kPlain>(a, s);
+      case 256: return launch_t<256, 16, kPlain>(a, s);
+      case 512: return launch_t<512, 16, kPlain>(a, s);
+    }
   }
   return hipErrorInvalidValue;
 }

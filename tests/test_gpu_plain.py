@@ -256,18 +256,3 @@ def test_plain_linear_decode_steps(gpu, ora, bps):
     codes, meta = cache.read_codes()
     torch.cuda.synchronize()
     check_codes(codes, meta, oc, None, f"bps={bps} rows")
-
-
-def test_plain_rejects_prefill(gpu):
-    """Prefill attention reads quantized caches only; it fails before
-    launching anything."""
-    import torch
-
-    D = 256
-    cache = gpu.KVCache.new(D, 2, capacity=64)
-    k = torch.zeros((4, 2, D), dtype=torch.bfloat16, device="cuda")
-    cache.append(k, k)
-    with pytest.raises(gpu.Exception_) as e:
-        cache.prefill_step(k, k, torch.zeros((4, 4, D), dtype=torch.bfloat16, device="cuda"))
-    assert e.value.code == gpu.FMKV_ERR_UNSUPPORTED
-    assert cache.offset() == 4

@@ -123,10 +123,6 @@ def test_prefill_rejects_bad_arguments(gpu):
                                    out.data_ptr(), gpu.DTYPE_F32, None)
         assert rc == code
     assert cache.offset() == 0
-    cb = gpu.KVCache(gpu.make_desc(2, D, 3, mode=gpu.MODE_CODEBOOK, capacity=32))
-    with pytest.raises(gpu.Exception_) as e:
-        cb.prefill_step(k, k, q)
-    assert e.value.code == gpu.FMKV_ERR_UNSUPPORTED
 
 
 @pytest.mark.parametrize("D,bits,Hkv,Hq", [(512, 8, 2, 16), (256, 4, 8, 16)])
