@@ -288,7 +288,8 @@ def run_c3(args) -> dict:
         "hbm_frac_of_value": round(value / HBM_PEAK_GBS, 4),
         "append_tokens_per_s": {"chunked_prefill_2048": round(append_prefill_tps, 1),
                                 "chunked_prefill_2048_prologue_k_eq_v":
-                                    None if prologue_tps is None else round(prologue_tps, 1)},
+                                    None if prologue_tps is None else round(prologue_tps, 1),
+                                **single_token_append_rates()},
         "graph_step_us": None if graph_us is None else round(graph_us, 3),
         "projected_step_us": None if proj_us is None else round(proj_us, 3),
         "roofline": {
@@ -310,6 +311,46 @@ def run_c3(args) -> dict:
         res["cpu_baseline"] = cpu_baseline_c3(args, np.concatenate(host_k), np.concatenate(host_v),
                                               Hq, Hkv, D, per_tok)
     return res
+
+
+def single_token_append_rates() -> dict:
+    """Single-token appends at the sliding-layer shape (Hkv 8, head_dim 256,
+    4-bit group 64): 4096 one-token appends into a linear cache (the C1
+    store, the reference's decode-loop store, src/cache.rs:266-310) and 8192
+    into a ring of 1024 slots (the C2 store, 7 wraps), timed as stream time
+    between two events around the whole run (launch costs included)."""
+    import torch
+
+    import fmkv
+    import synth
+
+    Hkv, D, bits = 8, 256, 4
+    lib = fmkv.load_library()
+    stream = torch.cuda.current_stream().cuda_stream
+    out = {}
+    for name, n, window in (("single_token_linear_4096", 4096, 0),
+                            ("single_token_ring_1024_8192", 8192, 1024)):
+        k = dev_bf16(synth.kv_rows(51, n, Hkv, D, None))
+        v = dev_bf16(synth.kv_rows(52, n, Hkv, D, None))
+        row = Hkv * D * 2
+        for rep in range(2):  # the first pass warms the kernel up, untimed
+            cache = fmkv.KVCache.new_quantized_with_window(D, bits, window or None, Hkv,
+                                                           0 if window else n)
+            h = cache._h
+            torch.cuda.synchronize()
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record()
+            kp, vp = k.data_ptr(), v.data_ptr()
+            for t in range(n):
+                if lib.fmkv_cache_append(h, kp + t * row, vp + t * row, 1, stream):
+                    raise RuntimeError(lib.fmkv_last_error().decode())
+            ev1.record()
+            torch.cuda.synchronize()
+            del cache
+        us = ev0.elapsed_time(ev1) * 1e3 / n
+        out[name] = round(1e6 / us, 1)
+        log(f"append {name}: {us:.2f} us per token ({1e6 / us:.0f} tokens/s)")
+    return out
 
 
 def _step_fn(lib, fmkv, h, kd, vd, qd, Hq, Hkv, D, out, stream, pool):

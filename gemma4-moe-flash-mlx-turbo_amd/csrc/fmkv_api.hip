@@ -116,6 +116,14 @@ int attn_wg_per_cu(const fmkv_cache_desc& d) {
   return d.mode == FMKV_MODE_PLAIN ? 2 : fmkv::kAttnWgPerCu;
 }
 
+// Work-groups per CU of a paged batch's decode kernel when its splits are
+// long enough for single-wave streams (at least 8 blocks each): 3 for
+// affine head-blocks of at most 1024 code bits per token (four-wave
+// work-groups), else 1.
+int paged_solo_slots(const fmkv_cache_desc& d) {
+  return d.mode == FMKV_MODE_AFFINE && d.head_dim * d.bits <= 1024 ? 3 : 1;
+}
+
 // Split-K plan: blocks per split such that the grid has about `wg_per_cu`
 // work-groups per CU (each keeps several blocks in flight, so one per CU
 // already saturates HBM; more would only add split partials), `reserved` of
@@ -416,7 +424,24 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
                                          " bytes of split partials; the no-allocation scratch "
                                          "holds " + std::to_string(ext.bytes));
   } else {
-    rc = o->ws.ensure(need);
+    // One cache: the workspace is sized once for the largest plan the
+    // cache's capacity allows (split count at most the planned work-groups
+    // per KV head + 1, a new-token column, sparse-V statistics and block
+    // maxima), so that it does not grow as the context does and a decode
+    // step captured into a HIP graph stays valid. A paged batch's need
+    // depends on each call's batch and grows on demand.
+    size_t alloc = need;
+    if (n_seqs == 1 && !st.block_table) {
+      const int64_t per_head = ((int64_t)wg_per_cu * o->cus + H - 1) / H + 1;
+      const int64_t max_splits =
+          std::max<int64_t>(g_bps_override > 0 ? blk_cap : std::min<int64_t>(blk_cap, per_head),
+                            a->max_splits);
+      const size_t rows = (size_t)(max_splits + 1) * n_q_heads;
+      const size_t off = (rows * (D + 2) + 3 * (size_t)n_q_heads + 2 * rows + 3) & ~(size_t)3;
+      const size_t blks = (size_t)H * std::max<int64_t>(std::max<int64_t>(blk_cap, nblk), 1) * 8;
+      alloc = std::max(need, (off + blks) * sizeof(float));
+    }
+    rc = o->ws.ensure(alloc);
     if (rc) return rc;
     ws = o->ws.ptr;
   }
@@ -499,15 +524,26 @@ int prepare_paged_attention(fmkv_pool* p, const void* q, const int32_t* block_ta
   // ones fill the tail (32 sequences of 512..16384 tokens: bps 171, 197 us;
   // equal splits at four per CU: 207 us). A grid of fewer work-groups has
   // no tail to fill, and a larger first split would only end last.
+  //
+  // Affine head-blocks of at most 1024 code bits per token (head_dim 128,
+  // head_dim 256 at 4 bits) run as work-groups of four single-wave streams,
+  // three to a CU (slots = 3): the plan counts slots instead of CUs, six
+  // work-groups per slot, and the floor is at most one slot's share (one
+  // sequence of 65536 tokens, Hkv 8, head_dim 256, 4 bits: bps 43, one
+  // work-group per slot, 40.7 us; bps 22 or 128: 47.6 / 52.5 us; the 32
+  // ragged sequences above at bps 57..96: 173-178 us, against 202 us with
+  // twelve-wave work-groups, one per CU).
   const int n_s = n_seqs > 0 ? n_seqs : 1;
   const int64_t total = nblk * p->desc.n_kv_heads * n_s;
-  const int64_t share = (total + p->cus - 1) / p->cus;
+  const int slots = paged_solo_slots(p->desc);
+  const int64_t n_slots = (int64_t)slots * p->cus;
+  const int64_t share = (total + n_slots - 1) / n_slots;
   const int min_bps = (int)std::min<int64_t>(64, std::max<int64_t>(share, 1));
-  const int64_t bps = choose_bps(total, p->cus, 6 * fmkv::kAttnWgPerCu, 0, min_bps);
-  const int first_mult = total >= 4 * (int64_t)p->cus * bps ? 4 : 1;
+  const int wg_per_cu = 6 * slots * fmkv::kAttnWgPerCu;
+  const int64_t bps = choose_bps(total, p->cus, wg_per_cu, 0, min_bps);
+  const int first_mult = total >= 4 * n_slots * bps ? 4 : 1;
   return prepare_attention_common(p, pool_store(p, block_tables, max_blocks), n_s, nblk,
-                                  max_blocks, q,
-                                  n_q_heads, scale, tau, out, out_dtype, 6 * fmkv::kAttnWgPerCu,
+                                  max_blocks, q, n_q_heads, scale, tau, out, out_dtype, wg_per_cu,
                                   min_bps, first_mult, new_col, a);
 }
 

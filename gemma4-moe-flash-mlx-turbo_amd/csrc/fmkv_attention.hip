@@ -27,9 +27,10 @@
 //
 // Per block (16 tokens), per 64-dim group g of the wave's half:
 //   QK^T  S^T[16 tok x 16 col] += K[16 x 32] . Q^T[32 x 16] on MFMA
-//         (v_mfma_f32_16x16x32_f16), K codes converted exactly to f16
-//         integers; the f16 scale/bias apply after the MFMA:
-//         s += scale * acc + bias * sum(q_group).
+//         (v_mfma_f32_16x16x32_f16), K codes entering as the exact f16
+//         values 1024 + code (8-bit) or 1 + code / 16 (4-bit), the offset
+//         cancelled by the accumulator's start (kCodeOffset); the f16
+//         scale/bias apply after the MFMA: s += scale * acc + bias * sum(q_group).
 //         Column c = q head (c & 7) of the GQA group, c < 8 carrying the f16
 //         high part of q_rot and c >= 8 the residual, so S keeps ~22 bits of
 //         q precision; DPP row_ror:8 folds the two halves.
@@ -38,9 +39,10 @@
 //         same columns; bias terms are summed on the side.
 // The QK output lane layout equals the PV B-operand layout (lane (j, c) holds
 // tokens 4j..4j+3 of column c), so no register shuffles are needed.
-// (Codes stay unbiased: an f16 1024 + code operand with the offset cancelled
-// in the accumulator is cheaper but inflates the fp32 partial sums ~64x at 4
-// bits, which outlier channels turn into visible error.)
+// (At 4 bits the 1024 + code form would inflate the f32 partial sums ~64x,
+// which outlier channels turn into visible error; 1 + code / 16 -- the code
+// in the top mantissa bits, one shift and one bit-field insert per two codes
+// against four instructions for exact small integers -- inflates them ~3x.)
 //
 // q_rot = (FWHT(q * scale * log2 e) * c) o s is computed by every work-group
 // in its prologue, while its first blocks are in flight: the raw q rows are
@@ -66,33 +68,44 @@ namespace fmkv {
 namespace {
 
 // Staging plan of one (head_dim, bits, stream kind). A block stream is a
-// wave pair (each wave owns half the 64-dim groups, SOLO false) or a single
-// wave owning every group (SOLO true). Pairs finish one block soonest; solo
-// streams, twelve per work-group and with no score exchange, finish more
+// wave pair (each wave owns half the 64-dim groups, SW = 0) or a single
+// wave owning every group (SW > 0 solo waves per work-group). Pairs finish
+// one block soonest; solo streams, with no score exchange, finish more
 // blocks per unit of time when a head-block is small (at most 1024 code
 // bits per token: head_dim 128, head_dim 256 at 4 bits), so the launch
-// picks them for work-groups of many blocks (kSoloMinBlocks).
+// picks them for work-groups of many blocks (kSoloMinBlocks). Solo
+// work-groups come in two sizes: twelve waves filling a CU's LDS (one
+// sequence), or four waves in about 46 KiB, three work-groups sharing a CU
+// (a paged batch: one work-group's prologue and epilogue then overlap the
+// others' streaming instead of leaving the CU's copies idle).
 // A stage holds one head-block as
 //   [K codes][V codes][wave 0: K meta, V meta of its groups][wave 1: ...];
 // each wave copies its groups' code chunks and, with one partial
 // instruction, its groups' scale/bias. Stages per stream: about 136 KiB of
-// staging per work-group (144 KiB for single-wave streams, which need no
-// score-exchange area), at least two, and the largest wait (stages x copies
-// per block) within the 6-bit vmcnt field.
+// staging per work-group (144 KiB for twelve single-wave streams, which need
+// no score-exchange area; 37 KiB for four), at least two, and the largest
+// wait (stages x copies per block) within the 6-bit vmcnt field.
 template <int D, int BITS>
 constexpr bool kSoloCapable = D * BITS <= 1024;
 constexpr int kSoloMinBlocks = 8;  // blocks per work-group from which solo streams pay
+#ifndef FMKV_PAGED_SOLO_WAVES
+#define FMKV_PAGED_SOLO_WAVES 4
+#endif
+// solo waves per work-group of a paged batch (4: three work-groups per CU)
+constexpr int kPagedSoloWaves = FMKV_PAGED_SOLO_WAVES;
 
-template <int D, int BITS, bool SOLO>
+template <int D, int BITS, int SW>
 struct AttnPlan {
   static constexpr BlockLayout L = make_layout(D, BITS, kAffine);
   static constexpr int NG = D / 64;
-  static constexpr bool kSolo = SOLO;
-  static_assert(!SOLO || kSoloCapable<D, BITS>, "solo streams for small head-blocks only");
+  static constexpr bool kSolo = SW > 0;
+  static_assert(!kSolo || kSoloCapable<D, BITS>, "solo streams for small head-blocks only");
+  static_assert(SW == 0 || SW == 4 || SW == 12, "pairs, or 4 or 12 solo waves");
   static constexpr int kWPS = kSolo ? 1 : 2;            // waves per stream
-  // solo work-groups run 12 waves, 3 per SIMD (<= 168 VGPRs each)
-  static constexpr int kWaves = kSolo ? 12 : kAttnWaves;
-  static constexpr int kWavesPerSimd = kWaves / 4;
+  // solo waves run three per SIMD (<= 168 VGPRs each): one work-group of 12
+  // or three of 4 per CU
+  static constexpr int kWaves = kSolo ? SW : kAttnWaves;
+  static constexpr int kWavesPerSimd = kSolo ? 3 : kWaves / 4;
   static constexpr int kStreams = kWaves / kWPS;
   static constexpr int GH = NG / kWPS;  // groups per wave
   static constexpr int kCodeChunks = (int)(L.code_bytes / kChunk);  // per K or V region
@@ -108,7 +121,7 @@ struct AttnPlan {
   static constexpr int kMetaOff = 2 * kCodeSlots * kChunk;
   static constexpr int kStageBytes = kMetaOff + 2 * kWPS * kMetaHalf;
   static constexpr int kCopies = 2 * kWaveChunks + 1;  // copy instructions per wave per block
-  static constexpr int kFit = ((kSolo ? 144 : 136) * 1024) / (kStreams * kStageBytes);
+  static constexpr int kFit = ((SW == 4 ? 37 : kSolo ? 144 : 136) * 1024) / (kStreams * kStageBytes);
   static constexpr int kStagesA = kFit < 2 ? 2 : (kFit > 8 ? 8 : kFit);
   static constexpr int kStages = kStagesA * kCopies <= 63 ? kStagesA : 63 / kCopies;
   static constexpr int kQS = D + 4;  // padded row stride (LDS banks)
@@ -126,20 +139,24 @@ struct AttnPlan {
   static_assert(8 * GH <= 64, "one partial instruction copies a wave's scale/bias");
 };
 
-// Raw bf16 q row of GQA head `wave` of (seq, kvh) (D * 2 bytes) to LDS at
-// dst + wave * D * 2, copied by that wave itself (lanes < D / 8).
-template <int D>
+// Raw bf16 q rows of the GQA heads h = wave, wave + NW, ... of (seq, kvh)
+// (D * 2 bytes each) to LDS at dst + h * D * 2, copied by that wave itself
+// (lanes < D / 8). NW: waves of the work-group.
+template <int D, int NW>
 __device__ inline void copy_q_row(const uint16_t* q, int n_q_heads, int group, uint8_t* dst,
                                   int seq, int kvh, int wave, int lane) {
-  if (wave < group && lane < D / 8) {
-    const uint16_t* qh = q + ((int64_t)seq * n_q_heads + (int64_t)kvh * group + wave) * D;
-    dma16(lds_addr(dst + wave * D * 2), lane * 16, buffer_rsrc(qh, (uint32_t)(D * 2)));
+#pragma unroll
+  for (int h = wave; h < (NW < 8 ? 8 : NW); h += NW) {
+    if (h < group && lane < D / 8) {
+      const uint16_t* qh = q + ((int64_t)seq * n_q_heads + (int64_t)kvh * group + h) * D;
+      dma16(lds_addr(dst + h * D * 2), lane * 16, buffer_rsrc(qh, (uint32_t)(D * 2)));
+    }
   }
 }
-template <int D>
+template <int D, int NW>
 __device__ inline void copy_q_row(const AttnArgs& a, uint8_t* dst, int seq, int kvh, int wave,
                                   int lane) {
-  copy_q_row<D>(a.q, a.n_q_heads, a.group, dst, seq, kvh, wave, lane);
+  copy_q_row<D, NW>(a.q, a.n_q_heads, a.group, dst, seq, kvh, wave, lane);
 }
 
 // q_rot = (FWHT(q * qscale) * c) o s of the work-group's GQA heads (q . R,
@@ -148,68 +165,81 @@ __device__ inline void copy_q_row(const AttnArgs& a, uint8_t* dst, int seq, int 
 // caller waited for its copy), written over them as the QK B operands:
 //   entry e = 2 g + s at e KiB + 16 lane, lane (j, c) = (lane / 16,
 //     lane % 16): 8 f16 of head c & 7 -- the f16 high part of q_rot for
-//     c < 8, the residual for c >= 8, zero past the group;
+//     c < 8, the residual for c >= 8, zero past the group -- times
+//     kCodeScale (the codes' operand form);
 //   float qsum[8][NG] after the 2 NG entries: per head and group, sum q_rot;
 //   float opsum[8][NG][2] after that: per head and group, the sums of the
-//     f16 high parts and of the residuals (the accumulator start of biased
-//     8-bit codes).
-// Wave w computes head w before the first barrier, so the rotation overlaps
-// the other waves' copy issue. Every thread of the work-group calls it (it
-// holds two barriers).
-template <int D, int BITS>
+//     f16 high parts and of the residuals (unscaled: the accumulator start
+//     of the offset codes).
+// Wave w computes the heads h = w, w + NW, ... (NW waves in the work-group)
+// before the first barrier, so the rotation overlaps the other waves' copy
+// issue. Every thread of the work-group calls it (it holds two barriers).
+template <int D, int BITS, int NW>
 __device__ void build_q_table(const AttnArgs& a, uint8_t* tab, int wave, int lane, uint32_t sbits) {
   constexpr int E = D / 64, NG = D / 64, LPG = 64 / E;
-  const bool hv = wave < a.group;
-  float x[E];
+  constexpr int HPW = (8 + NW - 1) / NW;  // table columns (heads) per wave
+  const QSlot<E, BITS> qs(lane);
+  _Float16 hi[HPW][E], lo[HPW][E];
+  float gsum[HPW], hsum[HPW], lsum[HPW];
 #pragma unroll
-  for (int i = 0; i < E; i++) x[i] = 0.0f;
-  if (hv) {
-    const uint32_t* raw = reinterpret_cast<const uint32_t*>(tab + (wave * D + lane * E) * 2);
+  for (int k = 0; k < HPW; k++) {
+    const int h = wave + k * NW;
+    const bool hv = h < a.group;
+    float x[E];
 #pragma unroll
-    for (int k = 0; k < E / 2; k++) {
-      const uint32_t w = raw[k];
-      x[2 * k] = __uint_as_float(w << 16) * a.qscale;
-      x[2 * k + 1] = __uint_as_float(w & 0xffff0000u) * a.qscale;
+    for (int i = 0; i < E; i++) x[i] = 0.0f;
+    if (hv) {
+      const uint32_t* raw = reinterpret_cast<const uint32_t*>(tab + (h * D + lane * E) * 2);
+#pragma unroll
+      for (int m = 0; m < E / 2; m++) {
+        const uint32_t w = raw[m];
+        x[2 * m] = __uint_as_float(w << 16) * a.qscale;
+        x[2 * m + 1] = __uint_as_float(w & 0xffff0000u) * a.qscale;
+      }
     }
-  }
-  float gsum = 0.0f;
-  if (hv) {
-    // the sign-tracking FWHT: an exact zero may come out as -0, which no
-    // score, sum or code of this kernel can tell from +0
-    wave_fwht_signed<E>(x, lane);
-    const float cs = fwht_lane_sign(lane) * a.c;
+    gsum[k] = 0.0f;
+    if (hv) {
+      // the sign-tracking FWHT: an exact zero may come out as -0, which no
+      // score, sum or code of this kernel can tell from +0
+      wave_fwht_signed<E>(x, lane);
+      const float cs = fwht_lane_sign(lane) * a.c;
+#pragma unroll
+      for (int i = 0; i < E; i++) {
+        x[i] = apply_sign(x[i] * cs, sbits, i);
+        gsum[k] += x[i];
+      }
+    }
+    gsum[k] = group_sum<LPG>(gsum[k], lane);
+    hsum[k] = lsum[k] = 0.0f;
 #pragma unroll
     for (int i = 0; i < E; i++) {
-      x[i] = apply_sign(x[i] * cs, sbits, i);
-      gsum += x[i];
+      hi[k][i] = (_Float16)x[i];
+      lo[k][i] = (_Float16)(x[i] - (float)hi[k][i]);
+      hsum[k] += (float)hi[k][i];
+      lsum[k] += (float)lo[k][i];
+      // the stored operands are scaled by kCodeScale (exact); the sums are not
+      hi[k][i] = hi[k][i] * (_Float16)kCodeScale<BITS>;
+      lo[k][i] = lo[k][i] * (_Float16)kCodeScale<BITS>;
     }
+    hsum[k] = group_sum<LPG>(hsum[k], lane);
+    lsum[k] = group_sum<LPG>(lsum[k], lane);
   }
-  gsum = group_sum<LPG>(gsum, lane);
-  const QSlot<E, BITS> qs(lane);
-  _Float16 hi[E], lo[E];
-  float hsum = 0.0f, lsum = 0.0f;
-#pragma unroll
-  for (int i = 0; i < E; i++) {
-    hi[i] = (_Float16)x[i];
-    lo[i] = (_Float16)(x[i] - (float)hi[i]);
-    hsum += (float)hi[i];
-    lsum += (float)lo[i];
-  }
-  hsum = group_sum<LPG>(hsum, lane);
-  lsum = group_sum<LPG>(lsum, lane);
   __syncthreads();  // every raw row is read before the table replaces them
-  // waves 0..7 write the 8 columns (zero past the group); more waves write
-  // nothing
+  // the 8 columns (zero past the group); heads beyond 8 write nothing
   uint8_t* ent = tab + (2 * qs.g + qs.s) * kChunk + qs.i0 * 2;
-  if (wave < 8) {
-    store_halves<E>(ent + (qs.j * 16 + wave) * 16, hi);
-    store_halves<E>(ent + (qs.j * 16 + wave + 8) * 16, lo);
-  }
-  if (wave < 8 && (lane & (LPG - 1)) == 0) {
-    reinterpret_cast<float*>(tab + 2 * NG * kChunk)[wave * NG + qs.g] = gsum;
-    float* op = reinterpret_cast<float*>(tab + 2 * NG * kChunk + 8 * NG * 4);
-    op[(wave * NG + qs.g) * 2 + 0] = hsum;
-    op[(wave * NG + qs.g) * 2 + 1] = lsum;
+#pragma unroll
+  for (int k = 0; k < HPW; k++) {
+    const int h = wave + k * NW;
+    if (h < 8) {
+      store_halves<E>(ent + (qs.j * 16 + h) * 16, hi[k]);
+      store_halves<E>(ent + (qs.j * 16 + h + 8) * 16, lo[k]);
+      if ((lane & (LPG - 1)) == 0) {
+        reinterpret_cast<float*>(tab + 2 * NG * kChunk)[h * NG + qs.g] = gsum[k];
+        float* op = reinterpret_cast<float*>(tab + 2 * NG * kChunk + 8 * NG * 4);
+        op[(h * NG + qs.g) * 2 + 0] = hsum[k];
+        op[(h * NG + qs.g) * 2 + 1] = lsum[k];
+      }
+    }
   }
   __syncthreads();
 }
@@ -294,14 +324,14 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, float2* rope, 
   constexpr int E = D / 64, LPG = 64 / E;
   const int G = a.group;
   const bool pro = a.k_norm_w != nullptr;
-  copy_q_row<D>(a, tab, seq, kvh, wave, lane);
+  copy_q_row<D, NT / 64>(a, tab, seq, kvh, wave, lane);
   if (pro && T >= 1) {
     for (int j = wave * 64 + lane; j < (a.rope_dims >> 1); j += NT)
       rope[j] = rope_cos_sin(T - 1, rope_inv_freq(j, a.rope_dims, a.rope_theta));
   }
   wait_vmcnt<0>();
   const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
-  build_q_table<D, BITS>(a, tab, wave, lane, sbits);
+  build_q_table<D, BITS, NT / 64>(a, tab, wave, lane, sbits);
   if (wave >= 2) return;  // no barrier follows
 
   const bool isv = wave == 1;
@@ -378,7 +408,8 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, float2* rope, 
       float p = 0.0f;
 #pragma unroll
       for (int i = 0; i < E; i++) p += ((float)qh[i] + (float)ql[i]) * y[i];
-      p = group_sum<64>(p, lane);
+      // the table holds q_rot * kCodeScale (a power of 2: the quotient is exact)
+      p = group_sum<64>(p, lane) * (1.0f / kCodeScale<BITS>);
       if (lane == 0) {
         a.part_ml[(pbase + h) * 2 + 0] = p;
         a.part_ml[(pbase + h) * 2 + 1] = 1.0f;
@@ -396,7 +427,7 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, float2* rope, 
 }
 
 // Pair work-groups: 8 waves, two per SIMD (register budget <= 256 each);
-// solo work-groups: 12 waves, three per SIMD (<= 168).
+// solo work-groups: 12 or 4 waves, three waves per SIMD (<= 168).
 // Arguments: what a work-group needs before its first copies comes first,
 // as 14 dwords of scalars, which the build preloads into SGPRs with the
 // dispatch (a scalar load from the argument struct waits 1.5-2 us at a
@@ -409,15 +440,15 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, float2* rope, 
 // lengths) needs the struct from the start. (Measured: C3 step 23.4 -> 23.2
 // us, 24.0 -> 23.5 us in a HIP graph; the compiler still hoists some of the
 // struct's loads above the first copies.)
-template <int D, int BITS, int MODE, bool SOLO, bool PAGED>
-__global__ __launch_bounds__((AttnPlan<D, BITS, SOLO>::kWaves * 64))
-__attribute__((amdgpu_waves_per_eu(AttnPlan<D, BITS, SOLO>::kWavesPerSimd,
-                                   AttnPlan<D, BITS, SOLO>::kWavesPerSimd)))
+template <int D, int BITS, int MODE, int SW, bool PAGED>
+__global__ __launch_bounds__((AttnPlan<D, BITS, SW>::kWaves * 64))
+__attribute__((amdgpu_waves_per_eu(AttnPlan<D, BITS, SW>::kWavesPerSimd,
+                                   AttnPlan<D, BITS, SW>::kWavesPerSimd)))
 void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
                         int32_t geo_vis_begin, int32_t window, int32_t bps0, int32_t bps,
                         int32_t max_splits, uint32_t skew, int32_t block_stride,
                         int32_t head_stride, uint32_t flags, AttnArgs a) {
-  using P = AttnPlan<D, BITS, SOLO>;
+  using P = AttnPlan<D, BITS, SW>;
   constexpr BlockLayout L = P::L;
   constexpr int NG = P::NG, GH = P::GH;
   constexpr int E = D / 64;
@@ -513,7 +544,7 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
   BlockList blist{0ull, 0, nb};
   int nbx = nb;  // blocks visited
   if constexpr (MODE == kGated) {
-    gated_thresholds(a, n_splits, seq, kvh, G, split, wave, lane, th_s);
+    gated_thresholds(a, n_splits, seq, kvh, G, split, wave, lane, th_s, P::kWaves);
     float thk[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) thk[k] = k < G ? th_s[k] : INFINITY;
@@ -555,7 +586,7 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
   // rotation's first barrier then waits for less copy issue, which stalls
   // while the whole chip's first requests queue up.
   constexpr int NQ = (NST + 1) / 2;
-  copy_q_row<D>(q, (int)(flags >> 8), G, scratch, seq, kvh, wave, lane);
+  copy_q_row<D, P::kWaves>(q, (int)(flags >> 8), G, scratch, seq, kvh, wave, lane);
 #pragma unroll
   for (int s = 0; s < NQ; s++)
     if (s < nbx) copy_block(s, pb0 + (int64_t)NS * (MODE == kGated ? bcopy.pop() : s), false);
@@ -564,37 +595,50 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
   wait_copies<CP, NQ>(nbx < NQ ? nbx : NQ);  // the q copy preceded every block
   // this lane's RHT signs, for the q rotation and the inverse rotation
   const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
-  build_q_table<D, BITS>(a, scratch, wave, lane, sbits);
+  build_q_table<D, BITS, P::kWaves>(a, scratch, wave, lane, sbits);
 #pragma unroll
   for (int s = NQ; s < NST; s++)
     if (s < nbx) copy_block(s, pb0 + (int64_t)NS * (MODE == kGated ? bcopy.pop() : s), false);
 
   // B operands of this wave's groups (hi / residual halves of q_rot) and
-  // their q sums for the bias term
-  half8_t bq[GH][2];
+  // their q sums for the bias term. Pair waves hold the operands in
+  // registers; solo waves, which own every group and run at three per SIMD
+  // (at most 168 VGPRs), read them from the q table in LDS at each use (no
+  // score exchange reuses that region in a solo work-group).
+  constexpr int GB = P::kSolo ? 1 : GH;
+  half8_t bq[GB][2];
   float qs[GH];
   const float* qsum = reinterpret_cast<const float*>(scratch + NE * kChunk);  // [head][NG]
+  auto q_operand = [&](int gi, int s) {
+    return *reinterpret_cast<const half8_t*>(scratch + ((g0 + gi) * 2 + s) * kChunk + lane * 16);
+  };
 #pragma unroll
   for (int gi = 0; gi < GH; gi++) {
+    if constexpr (!P::kSolo) {
 #pragma unroll
-    for (int s = 0; s < 2; s++)
-      bq[gi][s] = *reinterpret_cast<const half8_t*>(scratch + ((g0 + gi) * 2 + s) * kChunk + lane * 16);
+      for (int s = 0; s < 2; s++) bq[gi][s] = q_operand(gi, s);
+    }
     qs[gi] = (hi && col_valid) ? qsum[head * NG + g0 + gi] : 0.0f;
   }
-  // biased 8-bit codes: the QK accumulator of group gi starts at -1024 x this
-  // column's q operand summed over the group's 64 dims (the table's high or
-  // residual sum of the column's head)
-  float4_t kq[GH];
+  auto bq_of = [&](int gi, int s) { return P::kSolo ? q_operand(gi, s) : bq[P::kSolo ? 0 : gi][s]; };
+  // offset codes: the QK accumulator of group gi starts at -kCodeOffset x
+  // this column's q operand summed over the group's 64 dims (the table's
+  // high or residual sum of the column's head). Solo waves (three per SIMD,
+  // at most 168 VGPRs) keep the offset as one scalar per group and subtract
+  // it from the finished accumulator instead of holding four-register
+  // accumulator starts.
+  constexpr bool kKqInC = !P::kSolo;
+  float4_t kq[kKqInC ? GH : 1];
+  float kqs[GH];
   const float* opsum = reinterpret_cast<const float*>(scratch + NE * kChunk + 8 * NG * 4);
+  const U4Consts u4;
 #pragma unroll
   for (int gi = 0; gi < GH; gi++) {
-    float t = 0.0f;
-    if constexpr (kBiasedCodes<BITS>)
-      t = col_valid ? opsum[(head * NG + g0 + gi) * 2 + (hi ? 0 : 1)] : 0.0f;
-    const float k = -1024.0f * t;
-    kq[gi] = (float4_t){k, k, k, k};
+    const float t = col_valid ? opsum[(head * NG + g0 + gi) * 2 + (hi ? 0 : 1)] : 0.0f;
+    kqs[gi] = -kCodeOffset<BITS> * t;
+    if constexpr (kKqInC) kq[gi] = (float4_t){kqs[gi], kqs[gi], kqs[gi], kqs[gi]};
   }
-  __syncthreads();  // the table is consumed: the region becomes the score exchange
+  __syncthreads();  // pairs: the table is consumed, the region becomes the score exchange
   float4_t* const xs = reinterpret_cast<float4_t*>(scratch);  // [wave][parity][lane]
 
   // ---- main loop ----
@@ -602,7 +646,7 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
 #pragma unroll
   for (int i = 0; i < GH * 4; i++) o[i] = (float4_t){0.f, 0.f, 0.f, 0.f};
   float bacc[GH];
-  float psum[GH];  // biased 8-bit codes: this lane's running sum of P' per group
+  float psum[GH];  // offset codes: this lane's running sum of P' per group
 #pragma unroll
   for (int gi = 0; gi < GH; gi++) bacc[gi] = psum[gi] = 0.0f;
   // m_run starts finite (-1e30): exp2(-inf - m) is 0 for masked tokens and
@@ -653,12 +697,17 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
         km = kmeta(sp, gi + 1);
       }
       const int g = g0 + gi;
-      float4_t acc =
-          __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand<BITS>(kw_g, g, 0), bq[gi][0], kq[gi], 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand<BITS>(kw_g, g, 1), bq[gi][1], acc, 0, 0, 0);
+      const float4_t acc0 =
+          kKqInC ? kq[kKqInC ? gi : 0] : (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
+      float4_t acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand_dec<BITS>(kw_g, g, 0, u4),
+                                                            bq_of(gi, 0), acc0, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand_dec<BITS>(kw_g, g, 1, u4), bq_of(gi, 1),
+                                                   acc, 0, 0, 0);
 #pragma unroll
-      for (int i = 0; i < 4; i++)
-        sv[i] = fmaf(lo16(km_g[i]), acc[i], fmaf(hi16(km_g[i]), qs[gi], sv[i]));
+      for (int i = 0; i < 4; i++) {
+        const float ai = kKqInC ? acc[i] : acc[i] + kqs[gi];
+        sv[i] = fmaf(lo16(km_g[i]), ai, fmaf(hi16(km_g[i]), qs[gi], sv[i]));
+      }
       if constexpr (!P::kSolo) __builtin_amdgcn_sched_barrier(0);
     }
     u32x4 vw, vm;
@@ -735,7 +784,7 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
 #pragma unroll
         for (int gi = 0; gi < GH; gi++) {
           bacc[gi] *= alpha;
-          if constexpr (kBiasedCodes<BITS>) psum[gi] *= alpha;
+          psum[gi] *= alpha;
         }
       }
       l_run *= alpha;
@@ -775,14 +824,13 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
       const half2_t b01 = pkrtz(fmaf(-lo_sel, (float)h01[0], x[0]), fmaf(-lo_sel, (float)h01[1], x[1]));
       const half2_t b23 = pkrtz(fmaf(-lo_sel, (float)h23[0], x[2]), fmaf(-lo_sel, (float)h23[1], x[3]));
       const half4_t bp = cat4(b01, b23);
-      // the column's sum of P' (exact f16 values) for the 1024 offset
-      if constexpr (kBiasedCodes<BITS>)
-        psum[gi] = __builtin_amdgcn_fdot2(b23, one2, __builtin_amdgcn_fdot2(b01, one2, psum[gi], false), false);
+      // the column's sum of P' (exact f16 values) for the code offset
+      psum[gi] = __builtin_amdgcn_fdot2(b23, one2, __builtin_amdgcn_fdot2(b01, one2, psum[gi], false), false);
       const int g = g0 + gi;
 #pragma unroll
       for (int ct = 0; ct < 4; ct++)
-        o[gi * 4 + ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(v_operand<BITS>(vw_g, g, ct), bp,
-                                                               o[gi * 4 + ct], 0, 0, 0);
+        o[gi * 4 + ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(v_operand_dec<BITS>(vw_g, g, ct, u4),
+                                                               bp, o[gi * 4 + ct], 0, 0, 0);
       if constexpr (!P::kSolo) __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -834,15 +882,16 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
   for (int k = 0; k < GH * 4; k++)
 #pragma unroll
     for (int i = 0; i < 4; i++) o[k][i] = o[k][i] + row_ror8(o[k][i]);
-  if constexpr (kBiasedCodes<BITS>) {
-    // the V codes entered the MFMAs as 1024 + code: the merged row loses
-    // 1024 x the head's P' (both column halves) summed over all tokens,
-    // taken together with the bias sum of each group
+  {
+    // the V codes entered the MFMAs as (code + kCodeOffset) / kCodeScale:
+    // the merged row is kCodeScale x O less kCodeOffset x the head's P'
+    // (both column halves) summed over all tokens, the latter taken
+    // together with the bias sum of each group
 #pragma unroll
     for (int gi = 0; gi < GH; gi++) {
       float t = xor32_sum(xor16_sum(psum[gi]));
       t = t + row_ror8(t);
-      bacc[gi] = fmaf(-1024.0f, t, bacc[gi]);
+      bacc[gi] = fmaf(-kCodeOffset<BITS>, t, bacc[gi]);
     }
   }
 
@@ -862,7 +911,7 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
 #pragma unroll
       for (int ct = 0; ct < 4; ct++) {
         const int d = (g0 + gi) * 64 + ct * 16 + 4 * j;
-        *reinterpret_cast<float4_t*>(&Rp[head * QS + d]) = o[gi * 4 + ct] + bacc[gi];
+        *reinterpret_cast<float4_t*>(&Rp[head * QS + d]) = o[gi * 4 + ct] * kCodeScale<BITS> + bacc[gi];
       }
     if (half == 0 && j == 0) {
       ml_s[stream][head][0] = m_run;
@@ -871,9 +920,8 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
   }
   __syncthreads();  // every stream's rows are written
 
-  // head w on wave w
-  if (wave < G) {
-    const int hh = wave;
+  // heads w, w + kWaves, ... on wave w
+  for (int hh = wave; hh < G; hh += P::kWaves) {
     float M = ml_s[0][hh][0];
 #pragma unroll
     for (int q = 1; q < NS; q++) M = fmaxf(M, ml_s[q][hh][0]);
@@ -1018,37 +1066,33 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* part_o, const
 // The split kernel of one mode; with events, they are recorded by the
 // dispatch itself (start and end of the kernel's execution, as a kernel
 // trace times it), else a plain launch.
-template <int D, int BITS, int MODE, bool SOLO, bool PAGED>
+template <int D, int BITS, int MODE, int SW, bool PAGED>
 hipError_t launch_kind(const AttnArgs& a, dim3 grid, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   SplitPre p;
   if (!split_pre(a, &p)) return hipErrorInvalidValue;
-  const dim3 block(AttnPlan<D, BITS, SOLO>::kWaves * 64);
+  const dim3 block(AttnPlan<D, BITS, SW>::kWaves * 64);
   if (ev0 && ev1)
-    hipExtLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SOLO, PAGED>), grid, block, 0, s, ev0,
+    hipExtLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SW, PAGED>), grid, block, 0, s, ev0,
                           ev1, 0, p.base, p.q, p.geo_len, p.geo_vis_begin, p.window, p.bps0, p.bps,
                           p.max_splits, p.skew, p.block_stride, p.head_stride, p.flags, a);
   else
-    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SOLO, PAGED>), grid, block, 0, s, p.base,
+    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SW, PAGED>), grid, block, 0, s, p.base,
                        p.q, p.geo_len, p.geo_vis_begin, p.window, p.bps0, p.bps, p.max_splits,
                        p.skew, p.block_stride, p.head_stride, p.flags, a);
   return hipGetLastError();
 }
 
-template <int D, int BITS, int MODE, bool SOLO>
-hipError_t launch_paged(const AttnArgs& a, dim3 grid, hipStream_t s, hipEvent_t ev0,
-                        hipEvent_t ev1) {
-  // a paged pool has per-sequence lengths; a cache has neither
-  if ((a.st.block_table != nullptr) != (a.seq_lens != nullptr)) return hipErrorInvalidValue;
-  return a.st.block_table ? launch_kind<D, BITS, MODE, SOLO, true>(a, grid, s, ev0, ev1)
-                          : launch_kind<D, BITS, MODE, SOLO, false>(a, grid, s, ev0, ev1);
-}
-
 template <int D, int BITS, int MODE>
 hipError_t launch_split(const AttnArgs& a, dim3 grid, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
+  // a paged pool has per-sequence lengths; a cache has neither
+  if ((a.st.block_table != nullptr) != (a.seq_lens != nullptr)) return hipErrorInvalidValue;
   if constexpr (kSoloCapable<D, BITS>) {
-    if (a.bps >= kSoloMinBlocks) return launch_paged<D, BITS, MODE, true>(a, grid, s, ev0, ev1);
+    if (a.bps >= kSoloMinBlocks)
+      return a.st.block_table ? launch_kind<D, BITS, MODE, kPagedSoloWaves, true>(a, grid, s, ev0, ev1)
+                              : launch_kind<D, BITS, MODE, 12, false>(a, grid, s, ev0, ev1);
   }
-  return launch_paged<D, BITS, MODE, false>(a, grid, s, ev0, ev1);
+  return a.st.block_table ? launch_kind<D, BITS, MODE, 0, true>(a, grid, s, ev0, ev1)
+                          : launch_kind<D, BITS, MODE, 0, false>(a, grid, s, ev0, ev1);
 }
 
 template <int D, int BITS>

@@ -127,6 +127,71 @@ __device__ inline half4_t v_operand(const u32x4 w, int g, int ct) {
   }
 }
 
+// The decode kernel's operands: a code enters the matrix cores as the exact
+// f16 value (code + kCodeOffset) / kCodeScale --
+//   8-bit: 1024 + code (k_operand / v_operand: one v_perm per two codes, the
+//          code becoming the low mantissa byte of 1024);
+//   4-bit: 1 + code / 16 (the code becoming the top four mantissa bits of
+//          1.0: one shift and one bit-field insert per two codes, against
+//          four instructions for the exact small integer).
+// The q operand table is scaled by kCodeScale (exact), the QK accumulator
+// starts at -kCodeOffset * (the column's q operand summed over the group), and
+// the PV row is kCodeScale * O - kCodeOffset * (the column's P' summed over
+// the tokens): exact f16 / f32 scalings, so the products sum to sum(code * q)
+// and sum(code * P') up to the f32 rounding of partial sums that the offset
+// inflates about 9x at 8 bits and 3x at 4 bits.
+template <int BITS>
+constexpr float kCodeOffset = BITS == 8 ? 1024.0f : 16.0f;
+template <int BITS>
+constexpr float kCodeScale = BITS == 8 ? 1.0f : 16.0f;
+
+// The two register constants of the 4-bit operands, made opaque to the
+// compiler (which would otherwise rematerialise them at every use): the
+// mantissa field mask in an SGPR, 1.0 in both f16 halves in a VGPR.
+struct U4Consts {
+  uint32_t mask, one;
+  __device__ U4Consts() {
+    asm volatile("s_mov_b32 %0, 0x3c003c0" : "=s"(mask));
+    asm volatile("v_mov_b32 %0, 0x3c003c00" : "=v"(one));
+  }
+};
+
+// Nibbles k and k + 4 of w (bits 4k and 16 + 4k) as the f16 pair
+// {1 + c0 / 16, 1 + c1 / 16}: the codes moved to bits 6..9 of each 16-bit
+// half, then merged into 1.0 with one v_and_or_b32 over the register
+// constants. (Written in C, not as inline asm: the compiler must see the
+// write to insert the wait states an MFMA reading the result right after
+// needs.)
+__device__ inline half2_t u4x2_to_h2_unit(uint32_t w, int k, const U4Consts& u) {
+  const uint32_t x = k == 0 ? w << 6 : k == 1 ? w << 2 : k == 2 ? w >> 2 : w >> 6;
+  return __builtin_bit_cast(half2_t, (x & u.mask) | u.one);
+}
+
+// K operand of MFMA s of group g in the decode kernel's offset form.
+template <int BITS>
+__device__ inline half8_t k_operand_dec(const u32x4 w, int g, int s, const U4Consts& u) {
+  if constexpr (BITS == 8) {
+    return k_operand<8>(w, g, s);
+  } else {
+    const uint32_t x = w[(g & 1) * 2 + s];
+    return cat8(u4x2_to_h2_unit(x, 0, u), u4x2_to_h2_unit(x, 1, u), u4x2_to_h2_unit(x, 2, u),
+                u4x2_to_h2_unit(x, 3, u));
+  }
+}
+
+// V operand of column tile ct of group g in the decode kernel's offset form.
+template <int BITS>
+__device__ inline half4_t v_operand_dec(const u32x4 w, int g, int ct, const U4Consts& u) {
+  if constexpr (BITS == 8) {
+    return v_operand<8>(w, g, ct);
+  } else {
+    const int ctc = (g & 1) * 4 + ct;  // column tile inside the 128-dim chunk
+    const uint32_t x = w[ctc >> 1];
+    const int k0 = (ctc & 1) * 2;
+    return cat4(u4x2_to_h2_unit(x, k0, u), u4x2_to_h2_unit(x, k0 + 1, u));
+  }
+}
+
 __device__ inline float lo16(uint32_t w) { return f16_bits_to_f32(w); }
 __device__ inline float hi16(uint32_t w) { return f16_bits_to_f32(w >> 16); }
 

@@ -205,9 +205,9 @@ hipError_t launch_append(const AppendArgs& a, int n_seqs, int max_tasks, hipStre
 // kernel's dispatch: the start and end of its execution.
 hipError_t launch_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                                    hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr);
-// Decode attention over a codebook (TurboQuant) cache; one split of blocks per
-// work-group as launch_decode_attention plans it (no new-token column, no
-// sparse-V).
+// Decode attention over a codebook (TurboQuant) cache, planned as
+// launch_decode_attention plans it: a decode step's new-token column, and
+// sparse-V as a statistics pass, a gated pass and the combine.
 hipError_t launch_cb_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                                       hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr);
 // Decode attention over a plain (bf16) cache, planned as the codebook kernel.

@@ -114,8 +114,8 @@ int fmkv_cache_trim(fmkv_cache* cache, int64_t keep_last);
  * sparse_v_tau > 0 is the reference's sparse-V decode
  * (src/model/gemma4_attention.rs:196-234): softmax weights below tau are
  * zeroed without renormalisation. It reads the keys twice (a statistics
- * pass, then the gated pass); 0 is plain softmax attention; affine caches
- * only (FMKV_ERR_UNSUPPORTED for codebook and plain caches). Negative or
+ * pass, then the gated pass, which skips the blocks whose weights all fall
+ * below tau); 0 is plain softmax attention. Every cache mode. Negative or
  * non-finite tau returns FMKV_ERR_INVALID_ARG. */
 int fmkv_decode_attention(fmkv_cache* cache, const void* q_bf16, int32_t n_q_heads, float scale,
                           float sparse_v_tau, void* out, int32_t out_dtype, void* stream);
@@ -128,7 +128,9 @@ int fmkv_decode_attention(fmkv_cache* cache, const void* q_bf16, int32_t n_q_hea
  *   V = v_norm(v_proj) -- RMSNormNoScale (norm.rs:16-29), f32 -- or, with
  *       v_from_k, v_norm of the raw K (K==V global layers, :54-59).
  * rope_dims = head_dim * partial_rotary_factor (config.rs:209-225), a power
- * of 2 in [2 * head_dim / 64, head_dim]. Affine-mode caches only. */
+ * of 2 in [2 * head_dim / 64, head_dim]. Every cache mode: affine and
+ * codebook caches quantize the prologue's output (V in f32), a plain cache
+ * stores it rounded to bf16. */
 typedef struct fmkv_kv_prologue {
   const void* k_norm_weight; /* bf16 [head_dim], device */
   float eps;                 /* rms_norm_eps (k_norm and v_norm) */
@@ -161,10 +163,11 @@ int fmkv_decode_step(fmkv_cache* cache, const void* k_bf16, const void* v_bf16, 
  * offset + n_tokens - 1, their store, then the attention read -- the whole
  * of Gemma4Attention::forward after the q/k/v projections for L == n_tokens
  * (src/model/gemma4_attention.rs:50-104; q arrives normed and roped). With
- * one new token and sparse_v_tau == 0 the prologue, quantization and store
- * run inside the attention launch's new-token column (one launch plus the
- * split combine); otherwise fmkv_cache_append_projected, then
- * fmkv_decode_attention. Affine-mode caches; errors as those calls. */
+ * one new token the prologue, quantization and store run inside the
+ * attention launch's new-token column (one launch plus the split combine;
+ * with sparse_v_tau > 0 inside the statistics pass's); otherwise
+ * fmkv_cache_append_projected, then fmkv_decode_attention. Every cache mode;
+ * errors as those calls. */
 int fmkv_decode_step_projected(fmkv_cache* cache, const void* k_proj_bf16,
                                const void* v_proj_bf16, int64_t n_tokens,
                                const fmkv_kv_prologue* prologue, const void* q_bf16,
@@ -203,8 +206,9 @@ int fmkv_decode_step_noalloc(fmkv_cache* cache, const void* k_bf16, const void* 
  * slots also j > p - W. A ring attends before its slots are overwritten (the
  * chunk's rows are quantized into a handle-owned staging area first), so
  * every query sees its whole window. out: [n_tokens][n_q_heads][D] in
- * out_dtype. Affine mode; at most 8 query heads per KV head; n_tokens >= 1.
- * Nothing is launched or changed when validation fails. */
+ * out_dtype. Every cache mode (codebook caches are read as stored, plain
+ * caches as their bf16 rows); at most 8 query heads per KV head;
+ * n_tokens >= 1. Nothing is launched or changed when validation fails. */
 int fmkv_prefill_step(fmkv_cache* cache, const void* k_bf16, const void* v_bf16, int64_t n_tokens,
                       const void* q_bf16, int32_t n_q_heads, float scale, void* out,
                       int32_t out_dtype, void* stream);
@@ -266,8 +270,8 @@ int fmkv_paged_decode_attention(fmkv_pool* pool, const void* q_bf16, const int32
  * start_pos, then fmkv_paged_decode_attention with seq_lens (which the
  * caller sets to start_pos + n_new) -- the per-layer sequence of
  * src/model/gemma4_attention.rs:84-103 for a batch of requests. With one new
- * token per sequence and sparse_v_tau == 0 the attention launch appends the
- * tokens itself (at seq_lens - 1). */
+ * token per sequence the attention launch appends the tokens itself (at
+ * seq_lens - 1; with sparse_v_tau > 0 the statistics pass does). */
 int fmkv_paged_decode_step(fmkv_pool* pool, const void* k_bf16, const void* v_bf16,
                            const int32_t* block_tables, int32_t max_blocks,
                            const int32_t* start_pos, const int32_t* seq_lens, int32_t n_seqs,
@@ -292,7 +296,7 @@ int fmkv_paged_decode_step_projected(fmkv_pool* pool, const void* k_proj_bf16,
  * :84-104 with L > 1, mask of create_attention_mask, src/model/mod.rs
  * :682-704) -- fmkv_prefill_step for a batch of requests. q: bf16
  * [n_seqs][n_new][n_q_heads][head_dim]; out: the same shape in out_dtype.
- * Affine mode; at most 8 query heads per KV head. */
+ * Every cache mode; at most 8 query heads per KV head. */
 int fmkv_paged_prefill_step(fmkv_pool* pool, const void* k_bf16, const void* v_bf16,
                             const int32_t* block_tables, int32_t max_blocks,
                             const int32_t* start_pos, int32_t n_seqs, int32_t n_new,

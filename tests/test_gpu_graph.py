@@ -68,3 +68,42 @@ def test_graph_replays_match_eager(gpu, D, bits, Hkv, Hq, W, T0, tau):
     cb, mb = graphed.read_codes()
     torch.cuda.synchronize()
     assert torch.equal(ca, cb) and torch.equal(ma, mb)
+
+
+@pytest.mark.parametrize("mode,bits", [(0, 8), (1, 3), (2, 16)])
+def test_graph_steps_across_split_plans(gpu, mode, bits):
+    """A cache's workspace is sized for the largest plan its capacity allows:
+    after one eager step, a graph of 40 decode steps whose context crosses
+    three block boundaries (the split count grows with each) captures with
+    no allocation, and every replay equals the eager steps bit for bit."""
+    import torch
+
+    D, Hkv, Hq, T0, n = 512, 2, 16, 100, 40
+    caches = [gpu.KVCache(gpu.make_desc(Hkv, D, bits, 0, T0 + n + 16, mode)) for _ in range(2)]
+    k0, v0 = dev_bf16(kv_batch(3, T0, Hkv, D)), dev_bf16(kv_batch(4, T0, Hkv, D))
+    ks = [dev_bf16(kv_batch(100 + j, 1, Hkv, D, special=False)) for j in range(n + 1)]
+    vs = [dev_bf16(kv_batch(200 + j, 1, Hkv, D, special=False)) for j in range(n + 1)]
+    qs = [dev_bf16(synth.q_rows(300 + j, Hq, Hkv, D, None)) for j in range(n + 1)]
+    for c in caches:
+        c.append(k0, v0)
+        c.decode_step(ks[0], vs[0], qs[0], 1.0, dtype=torch.float32)
+    eager, graphed = caches
+    splits0 = eager.decode_splits()
+    want = [eager.decode_step(ks[j], vs[j], qs[j], 1.0, dtype=torch.float32) for j in range(1, n + 1)]
+    assert eager.decode_splits() > splits0, "the steps cross split plans"
+    torch.cuda.synchronize()
+    outs = [torch.empty((Hq, D), dtype=torch.float32, device="cuda") for _ in range(n)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for j in range(n):
+            graphed.decode_step(ks[j + 1], vs[j + 1], qs[j + 1], 1.0, out=outs[j], stream=s)
+    for rep in range(2):
+        for o in outs:
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for j in range(n):
+            assert torch.equal(outs[j], want[j]), f"mode {mode} replay {rep} step {j}"
