@@ -5,7 +5,7 @@ weights below tau are zeroed without renormalisation before the product
 with V. The oracle (ora_attention_f64) applies the same rule to the exact
 f64 weights; the kernel compares its f32 scores with the base-2 threshold
 M + log2(tau * L) of a statistics pass. Tolerance: max-abs 2e-2, mean-abs
-2e-3 (bf16 outputs also allow half a bf16 ulp of the reference)."""
+2e-3 (bf16 outputs: 2e-2 plus half a bf16 ulp of the exact value)."""
 import numpy as np
 import pytest
 

@@ -8,7 +8,7 @@ new-token column; other steps run the projected append, then attention.
 Either way the stored codes and scale/bias must equal the oracle's
 OracleCache.append_projected bit for bit, and the step's attention output
 the oracle's exact attention over the stored codes (max-abs 2e-2, mean-abs
-2e-3; bf16 outputs also allow one bf16 ulp)."""
+2e-3; bf16 outputs: 2e-2 plus half a bf16 ulp)."""
 import numpy as np
 import pytest
 
