@@ -548,15 +548,24 @@ def run_prefill(args) -> dict:
     import fmkv
     import synth
 
+    cb = args.mode == "codebook"
+    plain = args.mode == "plain"
     if args.prefill_sliding:
         Hq, Hkv, D, bits, W = 16, 8, 256, 4, 1024
     else:
         Hq, Hkv, D, bits, W = 16, 2, 512, 8, 0
+    if cb:
+        bits = args.bits or 3
+    elif plain:
+        bits = 16
+    elif args.bits:
+        bits = args.bits
+    mode = fmkv.MODE_CODEBOOK if cb else fmkv.MODE_PLAIN if plain else fmkv.MODE_AFFINE
     L, T0 = 2048, args.context
     steps = args.steps if args.steps <= 16 else 4
     warm = 1
     cap = 0 if W else T0 + (steps + warm) * L + 16
-    cache = fmkv.KVCache.new_quantized_with_window(D, bits, W, Hkv, cap)
+    cache = fmkv.KVCache.new_quantized_with_window(D, bits, W, Hkv, cap, mode=mode)
     for c0 in range(0, T0, L):
         n = min(L, T0 - c0)
         k = dev_bf16(synth.kv_rows(31, n, Hkv, D, None, dist="t3", offset=c0))
@@ -591,15 +600,17 @@ def run_prefill(args) -> dict:
     log(f"prefill chunk {L} at {t_begin}..{cache.offset()}: {ms:.3f} ms/chunk, {tps/1e6:.2f} M tokens/s, "
         f"{tflops:.1f} TFLOP/s")
     name = "sliding (ring W 1024)" if W else "global"
+    kind = (f"{bits}-bit TurboQuant codebook" if cb else "plain bf16" if plain else
+            f"{bits}-bit group-64 affine")
     return {
         "metric": "prefill attention tokens/s (2048-token chunks)",
         "value": round(tps, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
         "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "u8" if bits == 8 else "u4",
+        "dtype": "bf16" if plain else "u8" if bits == 8 else f"u{bits}",
         "data": "synthetic (seeded SplitMix64: K Student-t(3), V and q N(0,1))",
         "config": {"workload": f"{name} layer chunked prefill: Hq {Hq}, Hkv {Hkv}, head_dim {D}, "
-                               f"{bits}-bit group-64, 2048-token chunks after {T0} tokens",
-                   "context": T0, "chunk": L},
+                               f"{kind}, 2048-token chunks after {T0} tokens",
+                   "context": T0, "chunk": L, "mode": args.mode, "bits": bits},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": round(tflops / 2500.0, 4), "traffic": None,
                      "kernel": "prefill_attn_kernel (with the chunk's append)"},
@@ -932,10 +943,11 @@ def main(argv=None) -> int:
                     help="prefill workload on the sliding-layer shape (ring W 1024)")
     ap.add_argument("--c5-context", type=int, default=131072)
     ap.add_argument("--mode", choices=["affine", "codebook", "plain"], default="affine",
-                    help="c3: cache mode (codebook = the reference's TurboQuant indices + norm; "
-                         "plain = unquantized bf16 rows)")
+                    help="c3 and prefill: cache mode (codebook = the reference's TurboQuant "
+                         "indices + norm; plain = unquantized bf16 rows)")
     ap.add_argument("--bits", type=int, default=0,
-                    help="c3: code bits (0: 8 for affine, 3 for codebook, the reference's default)")
+                    help="c3 and prefill: code bits (0: the shape's affine bits, 3 for codebook, "
+                         "the reference's default)")
     ap.add_argument("--c4-seqs", type=int, default=0,
                     help="c4: a uniform batch of this many sequences of --c4-len tokens instead")
     ap.add_argument("--c4-len", type=int, default=32768)

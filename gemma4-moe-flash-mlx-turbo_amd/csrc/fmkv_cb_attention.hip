@@ -18,25 +18,26 @@
 // buffer_load_dwordx4 ... lds several stages ahead, exchanges its partial
 // scores with its partner through LDS and runs the same online softmax.
 //
-// Dequantization happens in registers on the way to the matrix cores: an LDS
+// Dequantization happens in registers on the way to the matrix cores. The 2-
+// and 3-bit centroids times 1000 are integers f16 holds exactly, so an LDS
 // table holds, for every pair of indices (two dims of a K row, or two tokens
-// of a V dim), the two centroids' f16 high parts as one word and, in a second
-// table at a fixed offset, their f16 residuals (cent - high), so two 4-byte
-// lookups at one address give the high and residual operand words of two
-// elements straight into the operand registers (4-bit codes: one lookup of
-// {high, residual} per element, paired by v_perm). Each table is replicated
-// 32 times, entry e of copy l at (e * 32 + l) * 4, so the lanes of a
-// half-wave never hit one bank twice. Per block, per 32-dim slice
-// and per 16-dim tile of the wave's half:
+// of a V dim), the two f16 integers as one word: one 4-byte lookup gives the
+// operand word of two elements straight into the operand registers, and the
+// 1/1000 joins the value scale norm / sqrt(D). 4-bit centroids need 12
+// significant bits: their table holds {f16 high part, f16 residual} per
+// index, paired by v_perm into a high and a residual operand word. Each table
+// is replicated 32 times, entry e of copy l at (e * 32 + l) * 4, so the lanes
+// of a half-wave never hit one bank twice. Per block, per 32-dim slice and per
+// 16-dim tile of the wave's half:
 //   QK   S^T[16 tok x 16 col] += K[16 x 32] . Q^T[32 x 16]
-//        (v_mfma_f32_16x16x32_f16), once with the high and once with the
-//        residual parts of the centroids (a product then keeps ~22 bits of
-//        the centroid; one f16 alone is off by up to 2^-12 of the value).
+//        (v_mfma_f32_16x16x32_f16; 4 bits: once with the high and once with
+//        the residual centroid parts, a product then keeping ~22 bits of the
+//        centroid where one f16 alone is off by up to 2^-12 of the value).
 //        Column c = q head c & 7, c < 8 the f16 high part of q_rot and
 //        c >= 8 its residual; the columns fold with DPP row_ror:8.
 //   PV   O^T[16 dim x 16 col] += V^T[16 dim x 16 tok] . P'^T[16 tok x 16 col]
-//        (v_mfma_f32_16x16x16f16, high and residual centroid parts), with
-//        P' = p * norm_t / sqrt D split hi/lo in the same columns.
+//        (v_mfma_f32_16x16x16f16; 4 bits: high and residual centroid parts),
+//        with P' = p * norm_t / sqrt D split hi/lo in the same columns.
 // Epilogue: the pairs' (m, l, O) merge in LDS, the inverse rotation
 // o . R^T = c * FWHT(o o s) follows, and the result is the final output (one
 // split) or a split partial for the shared combine kernel.
@@ -74,7 +75,6 @@ struct CbPlan {
   static constexpr int kStageBytes = kNormOff + 2 * 64;
   static constexpr int kCopies = 2 * kHalfCopies + 1;  // per wave per block
   // the centroid lookup table (fmkv_cb_common.h)
-  static constexpr int kLutHalf = CbLut<BITS>::kHalf;
   static constexpr int kLutBytes = CbLut<BITS>::kBytes;
   // q table (the QK B operands, one KiB per slice), then the score exchange
   static constexpr int kTabBytes = (D / 32) * 1024;
@@ -427,7 +427,8 @@ void cb_decode_kernel(AttnArgs a) {
   for (int i = 0; i < NTW; i++) o[i] = (float4_t){0.f, 0.f, 0.f, 0.f};
   float m_run = -1e30f, l_run = 0.0f;
   const float lo_sel = hi ? 0.0f : 1.0f;
-  const float inv_sd = a.c;  // 1 / sqrt(D): the codebook's value scale
+  // the codebook's value scale 1 / sqrt(D), in the table operands' units
+  const float inv_sd = a.c * kCbOperandScale<BITS>;
 
   // visible slots: linear [vis_lo, vis_hi); ring [0, min(T, W)), unless a
   // trim hides older positions (then each slot's position is computed)
@@ -457,20 +458,28 @@ void cb_decode_kernel(AttnArgs a) {
         reinterpret_cast<const uint32_t*>(sp + (int)L.k_codes + half * HB) + (kbit0 >> 5);
     const uint32_t* vw =
         reinterpret_cast<const uint32_t*>(sp + (int)L.v_codes + half * HB) + (vbit0 >> 5);
-    // this half's S^T = K . q_rot^T (high + residual centroid parts)
+    // this half's S^T = K . q_rot^T: exact integer centroids (2, 3 bits), or
+    // the high and residual centroid parts (4 bits)
     float4_t acc = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < NSW; s++) {
       const uint32_t f = lds_field<BITS>(kw, s * BITS, ksh);
-      uint32_t h4[4], l4[4];
-      cb_pair<BITS, P::kLutHalf, 0>(lut_l, f, h4[0], l4[0]);
-      cb_pair<BITS, P::kLutHalf, 1>(lut_l, f, h4[1], l4[1]);
-      cb_pair<BITS, P::kLutHalf, 2>(lut_l, f, h4[2], l4[2]);
-      cb_pair<BITS, P::kLutHalf, 3>(lut_l, f, h4[3], l4[3]);
-      const half8_t ah = __builtin_bit_cast(half8_t, (u32x4){h4[0], h4[1], h4[2], h4[3]});
-      const half8_t al = __builtin_bit_cast(half8_t, (u32x4){l4[0], l4[1], l4[2], l4[3]});
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[s], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq[s], acc, 0, 0, 0);
+      if constexpr (kCbExact<BITS>) {
+        const half8_t ak = __builtin_bit_cast(
+            half8_t, (u32x4){cb_pair_exact<BITS, 0>(lut_l, f), cb_pair_exact<BITS, 1>(lut_l, f),
+                             cb_pair_exact<BITS, 2>(lut_l, f), cb_pair_exact<BITS, 3>(lut_l, f)});
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bq[s], acc, 0, 0, 0);
+      } else {
+        uint32_t h4[4], l4[4];
+        cb_pair_hl4<0>(lut_l, f, h4[0], l4[0]);
+        cb_pair_hl4<1>(lut_l, f, h4[1], l4[1]);
+        cb_pair_hl4<2>(lut_l, f, h4[2], l4[2]);
+        cb_pair_hl4<3>(lut_l, f, h4[3], l4[3]);
+        const half8_t ah = __builtin_bit_cast(half8_t, (u32x4){h4[0], h4[1], h4[2], h4[3]});
+        const half8_t al = __builtin_bit_cast(half8_t, (u32x4){l4[0], l4[1], l4[2], l4[3]});
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[s], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq[s], acc, 0, 0, 0);
+      }
     }
     // the tokens' norms: lane (j, c) holds tokens 4j .. 4j + 3
     const uint2 kn = *reinterpret_cast<const uint2*>(sp + P::kNormOff + half * 64 + 8 * j);
@@ -559,13 +568,19 @@ void cb_decode_kernel(AttnArgs a) {
 #pragma unroll
     for (int n = 0; n < NTW; n++) {
       const uint32_t f = lds_field<BITS>(vw, n * 8 * BITS, vsh);
-      uint32_t h2[2], l2[2];
-      cb_pair<BITS, P::kLutHalf, 0>(lut_l, f, h2[0], l2[0]);
-      cb_pair<BITS, P::kLutHalf, 1>(lut_l, f, h2[1], l2[1]);
-      const half4_t ah = __builtin_bit_cast(half4_t, make_uint2(h2[0], h2[1]));
-      const half4_t al = __builtin_bit_cast(half4_t, make_uint2(l2[0], l2[1]));
-      o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bp, o[n], 0, 0, 0);
-      o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bp, o[n], 0, 0, 0);
+      if constexpr (kCbExact<BITS>) {
+        const half4_t av = __builtin_bit_cast(
+            half4_t, make_uint2(cb_pair_exact<BITS, 0>(lut_l, f), cb_pair_exact<BITS, 1>(lut_l, f)));
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bp, o[n], 0, 0, 0);
+      } else {
+        uint32_t h2[2], l2[2];
+        cb_pair_hl4<0>(lut_l, f, h2[0], l2[0]);
+        cb_pair_hl4<1>(lut_l, f, h2[1], l2[1]);
+        const half4_t ah = __builtin_bit_cast(half4_t, make_uint2(h2[0], h2[1]));
+        const half4_t al = __builtin_bit_cast(half4_t, make_uint2(l2[0], l2[1]));
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bp, o[n], 0, 0, 0);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bp, o[n], 0, 0, 0);
+      }
     }
   };
 

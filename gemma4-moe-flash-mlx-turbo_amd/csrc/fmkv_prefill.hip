@@ -28,11 +28,14 @@
 //         with P' = p * v_scale as f16 high part + residual (two MFMAs);
 //         the bias terms are summed on the side.
 // Codebook (TurboQuant) caches, per 32-dim slice / 16-dim tile of the
-// wave's half: the indices become f16 centroid operands (high part and
-// residual) through the decode kernel's LDS lookup table (fmkv_cb_common.h),
-// S^T = C_hi . q_hi + C_lo . q_hi + C_hi . q_lo, scaled per key by
-// norm / sqrt(D); O^T likewise with P' = p * norm / sqrt(D) as f16 high part
-// and residual (three MFMAs each: the fourth product is below f32 rounding).
+// wave's half: the indices become f16 centroid operands through the decode
+// kernel's LDS lookup table (fmkv_cb_common.h). 2 and 3 bits: the exact
+// integer operands 1000 * centroid, S^T = C . q_hi + C . q_lo, scaled per
+// key by norm / (1000 sqrt(D)); O^T likewise with P' = p * norm /
+// (1000 sqrt(D)) as f16 high part and residual (two MFMAs each). 4 bits: the
+// centroids' f16 high part and residual, S^T = C_hi . q_hi + C_lo . q_hi +
+// C_hi . q_lo and O^T likewise (three MFMAs each: the fourth product is below
+// f32 rounding).
 // Plain (bf16) caches read K rows and V columns as bf16 operands
 // (v_mfma_f32_16x16x32_bf16 / 16x16x16_bf16) against the raw bf16 q (exact
 // products; the softmax scale applies after), P as bf16 high part and
@@ -347,16 +350,24 @@ void prefill_attn_kernel(PrefillArgs a) {
 #pragma unroll
       for (int k = 0; k < NSW; k++) {
         const uint32_t f = lds_field<CB>(kw, k * CB, ksh);
-        uint32_t h4[4], l4[4];
-        cb_pair<CB, CbLut<CB>::kHalf, 0>(lut_l, f, h4[0], l4[0]);
-        cb_pair<CB, CbLut<CB>::kHalf, 1>(lut_l, f, h4[1], l4[1]);
-        cb_pair<CB, CbLut<CB>::kHalf, 2>(lut_l, f, h4[2], l4[2]);
-        cb_pair<CB, CbLut<CB>::kHalf, 3>(lut_l, f, h4[3], l4[3]);
-        const half8_t ah = __builtin_bit_cast(half8_t, (u32x4){h4[0], h4[1], h4[2], h4[3]});
-        const half8_t al = __builtin_bit_cast(half8_t, (u32x4){l4[0], l4[1], l4[2], l4[3]});
-        sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bqh[k >> 1][k & 1], sv, 0, 0, 0);
-        sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bqh[k >> 1][k & 1], sv, 0, 0, 0);
-        sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bql[k >> 1][k & 1], sv, 0, 0, 0);
+        if constexpr (kCbExact<CB>) {
+          const half8_t ak = __builtin_bit_cast(
+              half8_t, (u32x4){cb_pair_exact<CB, 0>(lut_l, f), cb_pair_exact<CB, 1>(lut_l, f),
+                               cb_pair_exact<CB, 2>(lut_l, f), cb_pair_exact<CB, 3>(lut_l, f)});
+          sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bqh[k >> 1][k & 1], sv, 0, 0, 0);
+          sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bql[k >> 1][k & 1], sv, 0, 0, 0);
+        } else {
+          uint32_t h4[4], l4[4];
+          cb_pair_hl4<0>(lut_l, f, h4[0], l4[0]);
+          cb_pair_hl4<1>(lut_l, f, h4[1], l4[1]);
+          cb_pair_hl4<2>(lut_l, f, h4[2], l4[2]);
+          cb_pair_hl4<3>(lut_l, f, h4[3], l4[3]);
+          const half8_t ah = __builtin_bit_cast(half8_t, (u32x4){h4[0], h4[1], h4[2], h4[3]});
+          const half8_t al = __builtin_bit_cast(half8_t, (u32x4){l4[0], l4[1], l4[2], l4[3]});
+          sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bqh[k >> 1][k & 1], sv, 0, 0, 0);
+          sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bqh[k >> 1][k & 1], sv, 0, 0, 0);
+          sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bql[k >> 1][k & 1], sv, 0, 0, 0);
+        }
       }
     } else if constexpr (MODE == kPlain) {
 #pragma unroll
@@ -410,10 +421,12 @@ void prefill_attn_kernel(PrefillArgs a) {
       const uint2 vn = *reinterpret_cast<const uint2*>(sp + (int)L.v_meta + 8 * j);
       const float ks[4] = {lo16(kn.x), hi16(kn.x), lo16(kn.y), hi16(kn.y)};
       const float vs[4] = {lo16(vn.x), hi16(vn.x), lo16(vn.y), hi16(vn.y)};
+      // (1 / sqrt(D) in the table operands' units)
+      const float cu = a.c * kCbOperandScale<CB>;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        s[i] = s[i] * (ks[i] * a.c);
-        vscale[i] = vs[i] * a.c;
+        s[i] = s[i] * (ks[i] * cu);
+        vscale[i] = vs[i] * cu;
       }
     } else if constexpr (MODE == kPlain) {
 #pragma unroll
@@ -471,14 +484,21 @@ void prefill_attn_kernel(PrefillArgs a) {
 #pragma unroll
       for (int n = 0; n < NTW; n++) {
         const uint32_t f = lds_field<CB>(vw, n * 8 * CB, vsh);
-        uint32_t h2[2], l2[2];
-        cb_pair<CB, CbLut<CB>::kHalf, 0>(lut_l, f, h2[0], l2[0]);
-        cb_pair<CB, CbLut<CB>::kHalf, 1>(lut_l, f, h2[1], l2[1]);
-        const half4_t ah = __builtin_bit_cast(half4_t, make_uint2(h2[0], h2[1]));
-        const half4_t al = __builtin_bit_cast(half4_t, make_uint2(l2[0], l2[1]));
-        o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bh, o[n], 0, 0, 0);
-        o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bh, o[n], 0, 0, 0);
-        o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bl, o[n], 0, 0, 0);
+        if constexpr (kCbExact<CB>) {
+          const half4_t av = __builtin_bit_cast(
+              half4_t, make_uint2(cb_pair_exact<CB, 0>(lut_l, f), cb_pair_exact<CB, 1>(lut_l, f)));
+          o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bh, o[n], 0, 0, 0);
+          o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bl, o[n], 0, 0, 0);
+        } else {
+          uint32_t h2[2], l2[2];
+          cb_pair_hl4<0>(lut_l, f, h2[0], l2[0]);
+          cb_pair_hl4<1>(lut_l, f, h2[1], l2[1]);
+          const half4_t ah = __builtin_bit_cast(half4_t, make_uint2(h2[0], h2[1]));
+          const half4_t al = __builtin_bit_cast(half4_t, make_uint2(l2[0], l2[1]));
+          o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bh, o[n], 0, 0, 0);
+          o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bh, o[n], 0, 0, 0);
+          o[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bl, o[n], 0, 0, 0);
+        }
       }
       return;
     } else if constexpr (MODE == kPlain) {
