@@ -37,7 +37,7 @@ HBM_PEAK_GBS = 8000.0
 # FETCH_SIZE / WRITE_SIZE passes scaled by a plain copy's readings
 # (profiles/decode_attn_c3_hbm_traffic.md holds the runs and the commands);
 # counters cannot be read inside the timed run itself.
-TRAFFIC_BYTES_PER_LAUNCH = 76_064_154
+TRAFFIC_BYTES_PER_LAUNCH = 76_025_037
 TRAFFIC_SOURCE = "profiles/decode_attn_c3_hbm_traffic.md"
 
 
