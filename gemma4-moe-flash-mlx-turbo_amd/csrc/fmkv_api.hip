@@ -87,8 +87,7 @@ int check_desc(const fmkv_cache_desc* d) {
   }
   if (d->window < 0) return fail(FMKV_ERR_INVALID_ARG, "window must be >= 0");
   if (d->window > 0) {
-    if (d->window % fmkv::kBlockTokens != 0)
-      return fail(FMKV_ERR_UNSUPPORTED, "window must be a multiple of 16");
+    if (d->window > (1 << 30)) return fail(FMKV_ERR_INVALID_ARG, "window must be <= 2^30");
   } else {
     if (d->capacity < 1) return fail(FMKV_ERR_INVALID_ARG, "capacity must be >= 1 for a global cache");
     if (d->capacity > ((int64_t)1 << 31) - 64)
@@ -97,8 +96,16 @@ int check_desc(const fmkv_cache_desc* d) {
   return FMKV_OK;
 }
 
+// Slots of a ring: the sliding window W rounded up to whole 16-token
+// head-blocks. Position p is stored at slot p mod ring_slots, so the ring
+// holds the last ring_slots positions; the last W of them are visible
+// (visible_begin), the others masked by position.
+int64_t ring_slots(const fmkv_cache_desc& d) {
+  return d.window > 0 ? fmkv::round_up(d.window, fmkv::kBlockTokens) : 0;
+}
+
 int64_t n_slots_of(const fmkv_cache_desc& d) {
-  return d.window > 0 ? (int64_t)d.window : fmkv::round_up(d.capacity, fmkv::kBlockTokens);
+  return d.window > 0 ? ring_slots(d) : fmkv::round_up(d.capacity, fmkv::kBlockTokens);
 }
 
 int device_cus() {
@@ -304,7 +311,7 @@ int prepare_append(const fmkv_cache* c, const void* k, const void* v, int64_t n,
   if (n == 0) return FMKV_OK;
   if (!k || !v) return fail(FMKV_ERR_INVALID_ARG, "k/v must be device pointers");
   if (n > ((int64_t)1 << 30)) return fail(FMKV_ERR_INVALID_ARG, "n_tokens too large");
-  const int64_t W = c->desc.window;
+  const int64_t W = ring_slots(c->desc);  // ring slots (0: linear)
   if (W == 0 && c->offset + n > c->desc.capacity)
     return fail(FMKV_ERR_CAPACITY, "append of " + std::to_string(n) + " tokens at offset " +
                                        std::to_string(c->offset) + " exceeds capacity " +
@@ -457,11 +464,13 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
 int prepare_attention(fmkv_cache* c, int64_t T, const void* q, int32_t n_q_heads, float scale,
                       float tau, void* out, int32_t out_dtype, int new_col, fmkv::AttnArgs* a,
                       ExtWorkspace ext = {}) {
-  const int64_t W = c->desc.window;
+  // a ring's slots; its visible positions are the last `window` of the T,
+  // which the kernels test per slot whenever that hides stored slots
+  const int64_t W = ring_slots(c->desc);
   a->seq_lens = nullptr;
   a->seq_len = T;
   a->window = W;
-  a->vis_begin = c->vis_begin;
+  a->vis_begin = W > 0 ? std::max<int64_t>(c->vis_begin, T - c->desc.window) : c->vis_begin;
   const int64_t filled = W > 0 ? std::min<int64_t>(T, W) : T;
   const int64_t vb = W > 0 ? 0 : c->vis_begin;
   const int64_t nblk =
@@ -736,7 +745,7 @@ int fmkv_prefill_step(fmkv_cache* c, const void* k, const void* v, int64_t n, co
   int64_t tasks = 0;
   rc = prepare_append(c, k, v, n, &ap, &tasks);
   if (rc) return rc;
-  const int64_t p0 = c->offset, W = c->desc.window;
+  const int64_t p0 = c->offset, W = c->desc.window;  // the sliding window (0: causal only)
   const int H = c->desc.n_kv_heads;
   const int64_t bb = c->layout.block_bytes;
   fmkv::PrefillArgs pa;
@@ -747,6 +756,7 @@ int fmkv_prefill_step(fmkv_cache* c, const void* k, const void* v, int64_t n, co
   pa.n_seqs = 1;
   pa.n_q = (int32_t)n;
   pa.window = W;
+  pa.ring_slots = ring_slots(c->desc);
   pa.vis_begin = c->vis_begin;
   pa.p_split = 0;
   pa.new_blk0 = 0;
@@ -904,7 +914,7 @@ int fmkv_decode_attention(fmkv_cache* c, const void* q, int32_t n_q_heads, float
 
 int fmkv_cache_decode_splits(const fmkv_cache* c, int32_t* n_splits) {
   if (!c || !n_splits) return fail(FMKV_ERR_INVALID_ARG, "null argument");
-  int64_t filled = c->desc.window > 0 ? std::min<int64_t>(c->offset, c->desc.window) : c->offset;
+  int64_t filled = c->desc.window > 0 ? std::min<int64_t>(c->offset, ring_slots(c->desc)) : c->offset;
   int64_t vb = c->desc.window > 0 ? 0 : c->vis_begin;
   int64_t nblk = (filled + fmkv::kBlockTokens - 1) / fmkv::kBlockTokens - vb / fmkv::kBlockTokens;
   if (nblk < 1) nblk = 1;
@@ -922,7 +932,7 @@ int fmkv_cache_fetch(const fmkv_cache* c, void* k_out, void* v_out, int32_t out_
   fmkv::FetchArgs a;
   a.st = cache_store(c);
   a.offset = c->offset;
-  a.window = c->desc.window;
+  a.window = ring_slots(c->desc);  // slot of position p: p mod the ring's slots
   a.first_pos = visible_begin(c);
   a.n_pos = c->offset - a.first_pos;
   a.signs = c->d_signs;
@@ -941,7 +951,7 @@ int fmkv_cache_read_codes(const fmkv_cache* c, void* codes, void* meta, void* st
     return fail(FMKV_ERR_INVALID_ARG, "codes/meta must be device pointers");
   fmkv::ReadArgs a;
   a.st = cache_store(c);
-  a.n_slots = c->desc.window > 0 ? c->desc.window : c->desc.capacity;
+  a.n_slots = c->desc.window > 0 ? ring_slots(c->desc) : c->desc.capacity;
   a.codes = static_cast<uint32_t*>(codes);
   a.meta = static_cast<uint16_t*>(meta);
   hipError_t e = fmkv::launch_read_codes(a, static_cast<hipStream_t>(stream));
@@ -1029,6 +1039,7 @@ int fmkv_paged_prefill_step(fmkv_pool* p, const void* k, const void* v,
   pa.n_seqs = n_seqs;
   pa.n_q = n_new;
   pa.window = 0;
+  pa.ring_slots = 0;
   pa.vis_begin = 0;
   pa.p_split = 0;
   pa.new_blk0 = 0;

@@ -117,7 +117,7 @@ struct AttnArgs {
 // Prefill (chunked) attention: n_q queries at positions p0 .. p0 + n_q - 1,
 // query p attending to key positions [lo(p), p], lo(p) = max(vis_begin,
 // p - window + 1) (window 0: vis_begin). Keys below p_split come from
-// old_st (a ring of window slots when window > 0, else linear), keys from
+// old_st (a ring of ring_slots slots when window > 0, else linear), keys from
 // p_split on from new_st, whose block 0 holds absolute block new_blk0 (a
 // staging copy of the chunk for rings; the cache itself, p_split 0, for
 // linear caches, which append before attending).
@@ -128,7 +128,8 @@ struct PrefillArgs {
   const int32_t* start_pos;  // paged: per sequence p0 (device), else null -> p0
   int32_t n_seqs;            // grid z; q and out gain a leading [n_seqs]
   int32_t n_q;
-  int64_t window;
+  int64_t window;      // the sliding window of the masks (0: causal only)
+  int64_t ring_slots;  // old_st's ring slots (the window rounded up to 16), 0: linear
   int64_t vis_begin;
   int64_t p_split;
   int64_t new_blk0;

@@ -201,7 +201,7 @@ void prefill_attn_kernel(PrefillArgs a) {
       v.vlo = v.b * kBlockTokens;
       v.vhi = (v.b + 1) * kBlockTokens < ps ? (v.b + 1) * kBlockTokens : ps;
       int64_t phys = v.b;
-      if (a.window > 0) phys = v.b % (a.window / kBlockTokens);
+      if (a.ring_slots > 0) phys = v.b % (a.ring_slots / kBlockTokens);
       v.ptr = a.old_st.base + phys * a.old_st.block_stride + (int64_t)kvh * a.old_st.head_stride;
     } else {
       v.b = new_first + (i - n_old);

@@ -404,7 +404,10 @@ class KVCache:
 
     # --- raw contents for bit-exact checks -------------------------------------
     def n_slots(self) -> int:
-        return self.desc.window if self.desc.window > 0 else self.desc.capacity
+        """Stored slots: a ring's window rounded up to whole 16-token blocks,
+        or a linear cache's capacity."""
+        w = self.desc.window
+        return (w + 15) // 16 * 16 if w > 0 else self.desc.capacity
 
     def read_codes(self, stream=None):
         """(codes uint32 [n_slots, 2, H, words], meta uint16 [n_slots, 2, H, n_meta])."""

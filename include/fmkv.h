@@ -63,7 +63,8 @@ typedef struct fmkv_cache_desc {
   int32_t bits;       /* affine: 4 or 8; codebook: 2, 3 or 4 (src/cache.rs:67-89); plain: 16 */
   int32_t group_size; /* 64 */
   int32_t mode;       /* FMKV_MODE_* */
-  int32_t window;     /* 0: global layer, linear growth; W > 0: ring of W slots (W % 16 == 0) */
+  int32_t window;     /* 0: global layer, linear growth; W > 0: sliding window of the last W
+                       * positions, kept in a ring of W rounded up to 16 slots (W <= 2^30) */
   int64_t capacity;   /* linear caches: max positions; ignored for rings */
   uint64_t sign_seed; /* seed of the RHT sign vector; the reference uses 42 (src/cache.rs:49) */
 } fmkv_cache_desc;

@@ -379,7 +379,11 @@ class OracleCache:
     def __init__(self, n_kv_heads: int, head_dim: int, bits: int, window: int = 0,
                  capacity: int = 0, mode: int = 0, seed: int = 42):
         self.H, self.D, self.bits, self.W, self.mode = n_kv_heads, head_dim, bits, window, mode
-        self.n_slots = window if window > 0 else capacity
+        # a ring stores position p at slot p mod Ws, Ws the window rounded up
+        # to whole 16-token blocks (the device layout); the last W positions
+        # are the visible ones
+        self.Ws = (window + 15) // 16 * 16 if window > 0 else 0
+        self.n_slots = self.Ws if window > 0 else capacity
         self.sgn = signs(head_dim, seed)
         self.words = (head_dim * bits + 31) // 32
         self.n_meta = 2 * (head_dim // 64) if mode == 0 else (1 if mode == 1 else 0)
@@ -442,9 +446,9 @@ class OracleCache:
         n = kp.shape[0]
         if self.W == 0 and self.offset + n > self.n_slots:
             raise ValueError("capacity exceeded")
-        first = 0 if self.W == 0 else max(0, n - self.W)
+        first = 0 if self.W == 0 else max(0, n - self.Ws)
         for i in range(first, n):
-            s = ring_slot(self.offset + i, self.W)
+            s = ring_slot(self.offset + i, self.Ws)
             self.codes[s, 0], self.meta[s, 0] = kp[i], km[i]
             self.codes[s, 1], self.meta[s, 1] = vp[i], vm[i]
         self.offset += n
@@ -508,7 +512,7 @@ class OracleCache:
         return len(self.visible_positions())
 
     def slots_of(self, pos: np.ndarray) -> np.ndarray:
-        return pos % self.W if self.W > 0 else pos
+        return pos % self.Ws if self.W > 0 else pos
 
     def rotated_kv(self, positions=None):
         """Dequantized rotated-domain K, V (f64) [n, H, D] for positions

@@ -33,8 +33,8 @@ def test_library_exports_header_symbols():
         (dict(n_kv_heads=8, head_dim=256, bits=3, capacity=16), fmkv.FMKV_ERR_UNSUPPORTED),
         (dict(n_kv_heads=8, head_dim=256, bits=5, capacity=16, mode=fmkv.MODE_CODEBOOK),
          fmkv.FMKV_ERR_UNSUPPORTED),
-        (dict(n_kv_heads=8, head_dim=256, bits=4, window=1000), fmkv.FMKV_ERR_UNSUPPORTED),
         (dict(n_kv_heads=8, head_dim=256, bits=4, window=-16), fmkv.FMKV_ERR_INVALID_ARG),
+        (dict(n_kv_heads=8, head_dim=256, bits=4, window=(1 << 30) + 1), fmkv.FMKV_ERR_INVALID_ARG),
         (dict(n_kv_heads=8, head_dim=256, bits=4, capacity=0), fmkv.FMKV_ERR_INVALID_ARG),
         (dict(n_kv_heads=8, head_dim=256, bits=4, capacity=1 << 31), fmkv.FMKV_ERR_INVALID_ARG),
         (dict(n_kv_heads=8, head_dim=256, bits=4, group_size=32, capacity=16), fmkv.FMKV_ERR_UNSUPPORTED),
@@ -82,6 +82,12 @@ def test_algorithmic_bytes_per_token_match_spec():
 def test_ring_and_global_arena_sizes():
     b, a = fmkv.layout_bytes(fmkv.make_desc(8, 256, 4, window=1024))
     assert a == b * 8 * 64
+    # any window: a ring of whole 16-token head-blocks (src/cache.rs:206 takes
+    # sliding_window from the config as it is)
+    for w, blocks in ((1000, 63), (5, 1), (17, 2), (1008, 63)):
+        fmkv.validate(fmkv.make_desc(8, 256, 4, window=w))
+        b, a = fmkv.layout_bytes(fmkv.make_desc(8, 256, 4, window=w))
+        assert a == b * 8 * blocks
     b, a = fmkv.layout_bytes(fmkv.make_desc(2, 512, 8, capacity=32768))
     assert a == 17408 * 2 * 2048 == 2 * 32768 * 1088
 

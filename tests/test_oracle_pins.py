@@ -378,6 +378,34 @@ def test_rotate_rows_f32_is_x_times_r(ora, d):
         assert np.array_equal(ora.rotate_rows_f32(e, s)[0], want)
 
 
+@pytest.mark.parametrize("W", [5, 40, 100])
+def test_ring_of_any_window_is_concat_then_tail(ora, W):
+    """A window that is not a multiple of 16: the ring holds Ws = W rounded up
+    to whole 16-token blocks, position p at slot p mod Ws, so after any
+    sequence of chunks it holds the last Ws positions, and the visible ones
+    are exactly the last W -- the rows concat-then-tail keeps
+    (src/cache.rs:132-148) -- in chronological order."""
+    rng = np.random.default_rng(W)
+    D, H = 128, 2
+    c = ora.OracleCache(H, D, 16, W, 0, mode=2)
+    assert c.n_slots == c.Ws == (W + 15) // 16 * 16
+    rows = []
+    for n in (3, W + 17, 1, 2 * W + 5, 7):
+        k = synth.f32_to_bf16_bits(rng.standard_normal((n, H, D)).astype(np.float32))
+        v = synth.f32_to_bf16_bits(rng.standard_normal((n, H, D)).astype(np.float32))
+        c.append(k, v)
+        rows += list(zip(k, v))
+        T = len(rows)
+        assert list(c.visible_positions()) == list(range(max(0, T - W), T))
+        for p in range(max(0, T - c.Ws), T):  # every slot holds its latest position
+            assert np.array_equal(c.codes[p % c.Ws, 0].view(np.uint16), rows[p][0])
+            assert np.array_equal(c.codes[p % c.Ws, 1].view(np.uint16), rows[p][1])
+        kf, vf = c.dequant_kv()
+        tail = rows[-W:]
+        assert np.array_equal(kf, ora.bf16_to_f32(np.stack([r[0] for r in tail])).astype(np.float64))
+        assert np.array_equal(vf, ora.bf16_to_f32(np.stack([r[1] for r in tail])).astype(np.float64))
+
+
 # --------------------------------------------------------------------------
 # cache index semantics (A8, A9, A14)
 # --------------------------------------------------------------------------
