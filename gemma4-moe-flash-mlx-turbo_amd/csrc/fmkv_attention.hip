@@ -174,7 +174,11 @@ __device__ inline void copy_q_row(const AttnArgs& a, uint8_t* dst, int seq, int 
 // Wave w computes the heads h = w, w + NW, ... (NW waves in the work-group)
 // before the first barrier, so the rotation overlaps the other waves' copy
 // issue. Every thread of the work-group calls it (it holds two barriers).
-template <int D, int BITS, int NW>
+// PACK (head_dim 256, at most 2 q heads per KV head): column c of entry
+// 2 g + s is (group c >> 2, head (c >> 1) & 1, high part if c is even,
+// residual if odd), zero unless c >> 2 == g -- each lane of the packed
+// kernel then serves one group of one head.
+template <int D, int BITS, int NW, bool PACK = false>
 __device__ void build_q_table(const AttnArgs& a, uint8_t* tab, int wave, int lane, uint32_t sbits) {
   constexpr int E = D / 64, NG = D / 64, LPG = 64 / E;
   constexpr int HPW = (8 + NW - 1) / NW;  // table columns (heads) per wave
@@ -230,9 +234,21 @@ __device__ void build_q_table(const AttnArgs& a, uint8_t* tab, int wave, int lan
 #pragma unroll
   for (int k = 0; k < HPW; k++) {
     const int h = wave + k * NW;
-    if (h < 8) {
-      store_halves<E>(ent + (qs.j * 16 + h) * 16, hi[k]);
-      store_halves<E>(ent + (qs.j * 16 + h + 8) * 16, lo[k]);
+    if (PACK ? h < 2 : h < 8) {
+      if constexpr (PACK) {
+        _Float16 zero[E];
+#pragma unroll
+        for (int i = 0; i < E; i++) zero[i] = (_Float16)0.0f;
+#pragma unroll
+        for (int gg = 0; gg < NG; gg++) {
+          uint8_t* col = ent + (qs.j * 16 + gg * 4 + h * 2) * 16;
+          store_halves<E>(col, gg == qs.g ? hi[k] : zero);
+          store_halves<E>(col + 16, gg == qs.g ? lo[k] : zero);
+        }
+      } else {
+        store_halves<E>(ent + (qs.j * 16 + h) * 16, hi[k]);
+        store_halves<E>(ent + (qs.j * 16 + h + 8) * 16, lo[k]);
+      }
       if ((lane & (LPG - 1)) == 0) {
         reinterpret_cast<float*>(tab + 2 * NG * kChunk)[h * NG + qs.g] = gsum[k];
         float* op = reinterpret_cast<float*>(tab + 2 * NG * kChunk + 8 * NG * 4);
@@ -316,7 +332,7 @@ __device__ inline void store_v_codes(uint8_t* vbase, int t, int d0, const uint32
 // the RoPE (cos, sin) table of position T - 1 is built by every thread of the
 // work-group into `rope` (LDS, rope_dims / 2 float2) before the q table's
 // barriers. NT: threads of the work-group.
-template <int D, int BITS, int NT>
+template <int D, int BITS, int NT, bool PACK = false>
 __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, float2* rope, int64_t T,
                                  int n_splits, int kvh, int seq, int wave, int lane) {
 #pragma clang fp contract(off)
@@ -331,7 +347,7 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, float2* rope, 
   }
   wait_vmcnt<0>();
   const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
-  build_q_table<D, BITS, NT / 64>(a, tab, wave, lane, sbits);
+  build_q_table<D, BITS, NT / 64, PACK>(a, tab, wave, lane, sbits);
   if (wave >= 2) return;  // no barrier follows
 
   const bool isv = wave == 1;
@@ -403,8 +419,10 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, float2* rope, 
     const QSlot<E, BITS> qs(lane);
     const uint8_t* ent = tab + (2 * qs.g + qs.s) * kChunk + qs.i0 * 2;
     for (int h = 0; h < G; h++) {
-      const _Float16* qh = reinterpret_cast<const _Float16*>(ent + (qs.j * 16 + h) * 16);
-      const _Float16* ql = reinterpret_cast<const _Float16*>(ent + (qs.j * 16 + h + 8) * 16);
+      // the head's high and residual columns (PACK: those of this lane's group)
+      const int ch = PACK ? qs.g * 4 + h * 2 : h, cl = PACK ? ch + 1 : h + 8;
+      const _Float16* qh = reinterpret_cast<const _Float16*>(ent + (qs.j * 16 + ch) * 16);
+      const _Float16* ql = reinterpret_cast<const _Float16*>(ent + (qs.j * 16 + cl) * 16);
       float p = 0.0f;
 #pragma unroll
       for (int i = 0; i < E; i++) p += ((float)qh[i] + (float)ql[i]) * y[i];
@@ -440,7 +458,7 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, float2* rope, 
 // lengths) needs the struct from the start. (Measured: C3 step 23.4 -> 23.2
 // us, 24.0 -> 23.5 us in a HIP graph; the compiler still hoists some of the
 // struct's loads above the first copies.)
-template <int D, int BITS, int MODE, int SW, bool PAGED>
+template <int D, int BITS, int MODE, int SW, bool PAGED, bool PACK>
 __global__ __launch_bounds__((AttnPlan<D, BITS, SW>::kWaves * 64))
 __attribute__((amdgpu_waves_per_eu(AttnPlan<D, BITS, SW>::kWavesPerSimd,
                                    AttnPlan<D, BITS, SW>::kWavesPerSimd)))
@@ -451,6 +469,12 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
   using P = AttnPlan<D, BITS, SW>;
   constexpr BlockLayout L = P::L;
   constexpr int NG = P::NG, GH = P::GH;
+  // PACK: dense solo streams of head_dim 256 at 4 bits with at most 2 q heads
+  // per KV head -- the 16 matrix-core columns carry (group, head, high /
+  // residual) instead of (head, high / residual), so each lane forms the
+  // scores and P' of one group only (build_q_table)
+  static_assert(!PACK || (MODE == kDense && P::kSolo && D == 256 && BITS == 4),
+                "packed columns: dense solo streams, head_dim 256, 4 bits");
   constexpr int E = D / 64;
   constexpr int QS = P::kQS;
   // copy instructions per wave per block (the stats pass copies no V codes)
@@ -469,8 +493,9 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
   constexpr int NS = P::kStreams;
   const int stream = P::kSolo ? wave : wave >> 1, half = P::kSolo ? 0 : wave & 1;
   const int j = lane >> 4, c = lane & 15;
-  const int head = c & 7;
-  const bool hi = c < 8;
+  const int head = PACK ? (c >> 1) & 1 : c & 7;
+  const bool hi = PACK ? (c & 1) == 0 : c < 8;
+  const int grp = c >> 2;  // PACK: this lane's 64-dim group
   const int G = (int)((flags >> 4) & 15u);
   const bool col_valid = head < G;
   const int skew_p = (int)(skew & 255u), skew_extra = (int)(skew >> 8);
@@ -499,7 +524,7 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
   // grid's last split column
   if constexpr (MODE != kGated) {
     if ((flags & 4u) && split == max_splits) {
-      new_token_column<D, BITS, P::kWaves * 64>(a, scratch, reinterpret_cast<float2*>(stage),
+      new_token_column<D, BITS, P::kWaves * 64, PACK>(a, scratch, reinterpret_cast<float2*>(stage),
                                                 PAGED ? Tg : a.seq_len, n_splits, kvh, seq, wave,
                                                 lane);
       return;
@@ -595,7 +620,7 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
   wait_copies<CP, NQ>(nbx < NQ ? nbx : NQ);  // the q copy preceded every block
   // this lane's RHT signs, for the q rotation and the inverse rotation
   const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
-  build_q_table<D, BITS, P::kWaves>(a, scratch, wave, lane, sbits);
+  build_q_table<D, BITS, P::kWaves, PACK>(a, scratch, wave, lane, sbits);
 #pragma unroll
   for (int s = NQ; s < NST; s++)
     if (s < nbx) copy_block(s, pb0 + (int64_t)NS * (MODE == kGated ? bcopy.pop() : s), false);
@@ -637,6 +662,13 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
     const float t = col_valid ? opsum[(head * NG + g0 + gi) * 2 + (hi ? 0 : 1)] : 0.0f;
     kqs[gi] = -kCodeOffset<BITS> * t;
     if constexpr (kKqInC) kq[gi] = (float4_t){kqs[gi], kqs[gi], kqs[gi], kqs[gi]};
+  }
+  // PACK: this lane's column is one group's: its q sum for the bias term
+  // and its offset-code accumulator start
+  float qsP = 0.0f, kqP = 0.0f;
+  if constexpr (PACK) {
+    qsP = (hi && col_valid) ? qsum[head * NG + grp] : 0.0f;
+    kqP = col_valid ? -kCodeOffset<BITS> * opsum[(head * NG + grp) * 2 + (hi ? 0 : 1)] : 0.0f;
   }
   __syncthreads();  // pairs: the table is consumed, the region becomes the score exchange
   float4_t* const xs = reinterpret_cast<float4_t*>(scratch);  // [wave][parity][lane]
@@ -684,6 +716,36 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
   };
 
   auto process = [&](const uint8_t* sp, int64_t b, int it) {
+    float s[4];
+    u32x4 vw, vm;
+    if constexpr (PACK) {
+      // all groups' QK products into one accumulator (each column sees only
+      // its own group's dims: the other groups' q operands are zero there);
+      // then the lane's group's scale and bias, and the sum over the four
+      // groups and the high / residual columns of the head (commutative at
+      // every step: the eight lanes of a head hold the same bits)
+      float4_t acc = (float4_t){kqP, kqP, kqP, kqP};
+      u32x4 kw = codes(sp, 0, 0);
+      const u32x4 km = lds16(sp + P::kMetaOff + grp * 64 + j * 16);
+#pragma unroll
+      for (int gi = 0; gi < GH; gi++) {
+        const u32x4 kw_g = kw;
+        if (gi + 1 < GH && (BITS == 8 || ((gi + 1) & 1) == 0)) kw = codes(sp, 0, gi + 1);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand_dec<BITS>(kw_g, gi, 0, u4),
+                                                     q_operand(gi, 0), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand_dec<BITS>(kw_g, gi, 1, u4),
+                                                     q_operand(gi, 1), acc, 0, 0, 0);
+      }
+      vw = codes(sp, 1, 0);  // in flight during the softmax
+      vm = lds16(sp + P::kMetaOff + MH + grp * 64 + j * 16);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float t0 = fmaf(lo16(km[i]), acc[i], hi16(km[i]) * qsP);
+        const float t1 = t0 + row_ror8(t0);
+        const float t2 = t1 + row_ror4(t1);
+        s[i] = t2 + quad_xor1(t2);
+      }
+    } else {
     // this half's S^T = K . q_rot^T, * scale + bias * sum(q), per group
     float4_t sv = (float4_t){0.f, 0.f, 0.f, 0.f};
     // (pair waves keep each group's MFMA chain in program order; a solo
@@ -710,7 +772,6 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
       }
       if constexpr (!P::kSolo) __builtin_amdgcn_sched_barrier(0);
     }
-    u32x4 vw, vm;
     if constexpr (MODE != kStats) {
       vw = codes(sp, 1, 0);  // in flight during the softmax
       vm = vmeta(sp, 0);
@@ -720,7 +781,6 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
     // release orders the data before the flag), then wait for the partner's;
     // both waves add the halves in the same order, so they hold identical
     // scores
-    float s[4];
     if constexpr (P::kSolo) {
 #pragma unroll
       for (int i = 0; i < 4; i++) s[i] = sv[i] + row_ror8(sv[i]);
@@ -739,6 +799,7 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
         const float t = s0[i] + s1[i];
         s[i] = t + row_ror8(t);
       }
+    }
     }
 
     // visibility: whole block in the common case (uniform test), per token
@@ -806,6 +867,34 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
     // (c >= 8): x = p * v_scale in f32, hi = f16(x), residual = f16(x - hi),
     // one mixed-precision FMA per element for each
     const half2_t one2 = (half2_t){(_Float16)1.0f, (_Float16)1.0f};
+    if constexpr (PACK) {
+      // P' of this lane's group (high or residual by column); every group's
+      // V tiles against all the columns, of which each lane keeps its own
+      // group's at the end
+      float x[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        x[i] = fmaf(p[i], lo16(vm[i]), 0.0f);
+        bacc[0] = fmaf(p[i], hi16(vm[i]), bacc[0]);
+      }
+      const half2_t h01 = pkrtz(x[0], x[1]);
+      const half2_t h23 = pkrtz(x[2], x[3]);
+      const half2_t b01 = pkrtz(fmaf(-lo_sel, (float)h01[0], x[0]), fmaf(-lo_sel, (float)h01[1], x[1]));
+      const half2_t b23 = pkrtz(fmaf(-lo_sel, (float)h23[0], x[2]), fmaf(-lo_sel, (float)h23[1], x[3]));
+      const half4_t bp = cat4(b01, b23);
+      psum[0] = __builtin_amdgcn_fdot2(b23, one2, __builtin_amdgcn_fdot2(b01, one2, psum[0], false), false);
+      u32x4 vwn = vw;
+#pragma unroll
+      for (int gi = 0; gi < GH; gi++) {
+        const u32x4 vw_g = vwn;
+        if (gi + 1 < GH && (BITS == 8 || ((gi + 1) & 1) == 0)) vwn = codes(sp, 1, gi + 1);
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++)
+          o[gi * 4 + ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(v_operand_dec<BITS>(vw_g, gi, ct, u4),
+                                                                 bp, o[gi * 4 + ct], 0, 0, 0);
+      }
+      return;
+    }
 #pragma unroll
     for (int gi = 0; gi < GH; gi++) {
       const u32x4 vw_g = vw, vm_g = vm;
@@ -877,12 +966,18 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
     bacc[gi] = xor16_sum(bacc[gi]);
     bacc[gi] = xor32_sum(bacc[gi]);
   }
-  // fold the residual columns (c >= 8) into the high-part columns (c < 8)
+  // fold the residual columns (c >= 8; PACK: odd c) into the high-part
+  // columns (c < 8; PACK: even c)
 #pragma unroll
   for (int k = 0; k < GH * 4; k++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) o[k][i] = o[k][i] + row_ror8(o[k][i]);
-  {
+    for (int i = 0; i < 4; i++) o[k][i] = o[k][i] + (PACK ? quad_xor1(o[k][i]) : row_ror8(o[k][i]));
+  if constexpr (PACK) {
+    // the lane's group's code-offset term, both columns of its head
+    float t = xor32_sum(xor16_sum(psum[0]));
+    t = t + quad_xor1(t);
+    bacc[0] = fmaf(-kCodeOffset<BITS>, t, bacc[0]);
+  } else {
     // the V codes entered the MFMAs as (code + kCodeOffset) / kCodeScale:
     // the merged row is kCodeScale x O less kCodeOffset x the head's P'
     // (both column halves) summed over all tokens, the latter taken
@@ -905,7 +1000,22 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
       __builtin_amdgcn_s_sleep(1);
   }
   float* const Rp = reinterpret_cast<float*>(pstage);
-  if (hi && col_valid) {
+  if constexpr (PACK) {
+    if (hi && col_valid) {
+#pragma unroll
+      for (int ct = 0; ct < 4; ct++) {
+        float4_t oc = o[ct];
+#pragma unroll
+        for (int gg = 1; gg < GH; gg++) oc = grp == gg ? o[gg * 4 + ct] : oc;
+        const int d = grp * 64 + ct * 16 + 4 * j;
+        *reinterpret_cast<float4_t*>(&Rp[head * QS + d]) = oc * kCodeScale<BITS> + bacc[0];
+      }
+      if (j == 0 && grp == 0) {
+        ml_s[stream][head][0] = m_run;
+        ml_s[stream][head][1] = l_run;
+      }
+    }
+  } else if (hi && col_valid) {
 #pragma unroll
     for (int gi = 0; gi < GH; gi++)
 #pragma unroll
@@ -1066,19 +1176,20 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* part_o, const
 // The split kernel of one mode; with events, they are recorded by the
 // dispatch itself (start and end of the kernel's execution, as a kernel
 // trace times it), else a plain launch.
-template <int D, int BITS, int MODE, int SW, bool PAGED>
+template <int D, int BITS, int MODE, int SW, bool PAGED, bool PACK = false>
 hipError_t launch_kind(const AttnArgs& a, dim3 grid, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   SplitPre p;
   if (!split_pre(a, &p)) return hipErrorInvalidValue;
   const dim3 block(AttnPlan<D, BITS, SW>::kWaves * 64);
+  const auto kern = decode_attn_kernel<D, BITS, MODE, SW, PAGED, PACK>;
   if (ev0 && ev1)
-    hipExtLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SW, PAGED>), grid, block, 0, s, ev0,
-                          ev1, 0, p.base, p.q, p.geo_len, p.geo_vis_begin, p.window, p.bps0, p.bps,
-                          p.max_splits, p.skew, p.block_stride, p.head_stride, p.flags, a);
+    hipExtLaunchKernelGGL(kern, grid, block, 0, s, ev0, ev1, 0, p.base, p.q, p.geo_len,
+                          p.geo_vis_begin, p.window, p.bps0, p.bps, p.max_splits, p.skew,
+                          p.block_stride, p.head_stride, p.flags, a);
   else
-    hipLaunchKernelGGL((decode_attn_kernel<D, BITS, MODE, SW, PAGED>), grid, block, 0, s, p.base,
-                       p.q, p.geo_len, p.geo_vis_begin, p.window, p.bps0, p.bps, p.max_splits,
-                       p.skew, p.block_stride, p.head_stride, p.flags, a);
+    hipLaunchKernelGGL(kern, grid, block, 0, s, p.base, p.q, p.geo_len, p.geo_vis_begin, p.window,
+                       p.bps0, p.bps, p.max_splits, p.skew, p.block_stride, p.head_stride, p.flags,
+                       a);
   return hipGetLastError();
 }
 
@@ -1087,9 +1198,18 @@ hipError_t launch_split(const AttnArgs& a, dim3 grid, hipStream_t s, hipEvent_t 
   // a paged pool has per-sequence lengths; a cache has neither
   if ((a.st.block_table != nullptr) != (a.seq_lens != nullptr)) return hipErrorInvalidValue;
   if constexpr (kSoloCapable<D, BITS>) {
-    if (a.bps >= kSoloMinBlocks)
+    if (a.bps >= kSoloMinBlocks) {
+      // head_dim 256 at 4 bits with at most 2 q heads per KV head (Gemma-4's
+      // sliding layers): the packed-column form of the solo streams
+      if constexpr (MODE == kDense && D == 256 && BITS == 4) {
+        if (a.group <= 2)
+          return a.st.block_table
+                     ? launch_kind<D, BITS, MODE, kPagedSoloWaves, true, true>(a, grid, s, ev0, ev1)
+                     : launch_kind<D, BITS, MODE, 12, false, true>(a, grid, s, ev0, ev1);
+      }
       return a.st.block_table ? launch_kind<D, BITS, MODE, kPagedSoloWaves, true>(a, grid, s, ev0, ev1)
                               : launch_kind<D, BITS, MODE, 12, false>(a, grid, s, ev0, ev1);
+    }
   }
   return a.st.block_table ? launch_kind<D, BITS, MODE, 0, true>(a, grid, s, ev0, ev1)
                           : launch_kind<D, BITS, MODE, 0, false>(a, grid, s, ev0, ev1);

@@ -38,6 +38,19 @@ __device__ inline float row_ror8(float v) {
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
 }
 
+// Lane l receives the value of lane (l & ~15) | ((l + 4) & 15) (DPP
+// row_ror:4).
+__device__ inline float row_ror4(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
+}
+
+// Lane l receives the value of lane l ^ 1 (DPP quad_perm [1, 0, 3, 2]).
+__device__ inline float quad_xor1(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));
+}
+
 // Sum / max with the lane 16 (resp. 32) apart: permlane swaps return the
 // pair {own, partner} in some order, so a commutative op gives both lanes the
 // same bits.
