@@ -487,6 +487,10 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
   __shared__ float ml_s[P::kStreams][8][2];
   __shared__ int xflag[P::kWaves];
   __shared__ float th_s[8];  // sparse-V gated pass: the group's thresholds
+  // paged: the work-group's range of its sequence's block table, for the
+  // loop's refills (kTblCap entries; blocks beyond read the table directly)
+  constexpr int kTblCap = PAGED ? 1024 : 4;
+  __shared__ __align__(16) int32_t tbl_s[kTblCap];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -552,6 +556,30 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
       return hbase + phys * block_stride;
     }
   };
+  // The loop's refills take the entry from the work-group's copy of its
+  // table range in LDS: a scalar load per refill would hold the stream for a
+  // memory round trip at every block (the scalar loads' counter is shared
+  // with LDS reads, so no later LDS access could go ahead of it either).
+  // (the copy starts at the 16-byte boundary at or below the range's first
+  // entry, tsh entries before it, in the same page)
+  int64_t n_tbl = 0;
+  int tsh = 0;
+  if constexpr (PAGED) {
+    tsh = (int)(((uintptr_t)(a.st.block_table + (int64_t)seq * a.st.table_stride + b_begin) & 15) >> 2);
+    n_tbl = b_end - b_begin;
+    n_tbl = n_tbl < 0 ? 0 : (n_tbl > kTblCap - tsh ? kTblCap - tsh : n_tbl);
+  }
+  auto blk_ptr_loop = [&](int64_t lb) -> const uint8_t* {
+    if constexpr (!PAGED) {
+      return blk_ptr(lb);
+    } else {
+      const int64_t r = lb - b_begin;
+      int64_t phys = (r >= 0 && r < n_tbl) ? (int64_t)__builtin_amdgcn_readfirstlane(tbl_s[tsh + r])
+                                           : (int64_t)table[lb];
+      phys = phys < 0 ? 0 : (phys >= a.st.n_blocks ? a.st.n_blocks - 1 : phys);
+      return hbase + phys * block_stride;
+    }
+  };
 
   // this stream's blocks: pb0 + NS i, i < nb
   const int64_t pb0 = b_begin + stream;
@@ -590,7 +618,7 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
   // (a stage's first fill follows no reads of it: no wait, so that the
   // first copies do not wait for the argument struct's scalar loads)
   auto copy_block = [&](int st, int64_t lb, bool refill) {
-    const u32x4 rs = buffer_rsrc(blk_ptr(lb), (uint32_t)L.block_bytes);
+    const u32x4 rs = buffer_rsrc(refill ? blk_ptr_loop(lb) : blk_ptr(lb), (uint32_t)L.block_bytes);
     const uint32_t sl = pstage_lds + st * SB;
     if (refill) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of this stage are done
 #pragma unroll
@@ -611,6 +639,17 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
   // rotation's first barrier then waits for less copy issue, which stalls
   // while the whole chip's first requests queue up.
   constexpr int NQ = (NST + 1) / 2;
+  // paged: wave 0 copies the table range first; its q copy and first stages
+  // follow, so its wait for the q row covers the table too, and the q
+  // table's barrier publishes it to the other waves before any refill
+  if constexpr (PAGED) {
+    if (wave == 0 && n_tbl > 0) {
+      const u32x4 trs = buffer_rsrc(a.st.block_table + (int64_t)seq * a.st.table_stride + b_begin - tsh,
+                                    (uint32_t)((n_tbl + tsh) * 4));
+      const int nk = (int)((n_tbl + tsh + 255) / 256);
+      for (int k = 0; k < nk; k++) dma16(lds_addr(tbl_s) + k * kChunk, k * kChunk + lane * 16, trs);
+    }
+  }
   copy_q_row<D, P::kWaves>(q, (int)(flags >> 8), G, scratch, seq, kvh, wave, lane);
 #pragma unroll
   for (int s = 0; s < NQ; s++)
