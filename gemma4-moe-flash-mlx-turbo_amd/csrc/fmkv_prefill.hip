@@ -189,10 +189,32 @@ void prefill_attn_kernel(PrefillArgs a) {
   if (new_first < b_lo) new_first = b_lo;
   const int64_t n_new = b_hi >= new_first ? b_hi - new_first + 1 : 0;
   const int nvb = (int)(n_old + n_new);
-  // virtual block i: absolute block, valid key range [vlo, vhi), store
+  // Per-block tests in 32-bit scalar form (the scalar unit has no 64-bit
+  // signed compares, and the vector unit's would cost every block): block
+  // rb = b - b_lo. A block that p_split cuts (cut_rb, visited once per
+  // store with its own part) takes the 64-bit tests; any other holds keys
+  // t0 .. t0 + 15, so the pair sees it when sees_lo <= rb <= sees_hi (a key
+  // at or past the pair's smallest lower bound, one at or before its last
+  // position) and it is whole for every row of the pair when full_lo <= rb
+  // <= full_hi (every key at or past the largest lower bound, at or before
+  // the first position). (When the pair has rows, its bounds are at or past
+  // b_lo's first key.)
+  const int64_t bl16 = b_lo * kBlockTokens;
+  auto rel_blk = [&](int64_t x) -> int {  // floor(x / 16) for x >= 0, clamped; -1 below
+    if (x < 0) return -1;
+    const int64_t q = x / kBlockTokens;
+    return (int)(q < INT32_MAX - 1 ? q : INT32_MAX - 1);
+  };
+  const int sees_lo = pair_any ? rel_blk(pair_lo_min - bl16) : INT32_MAX;
+  const int sees_hi = pair_any ? rel_blk(pB - bl16) : -1;
+  const int full_lo = pair_any && pair_full_rows ? rel_blk(pair_lo_max - bl16 + kBlockTokens - 1)
+                                                  : INT32_MAX;
+  const int full_hi = pair_any ? rel_blk(pA - (kBlockTokens - 1) - bl16) : -1;
+  const int cut_rb = ps % kBlockTokens != 0 ? rel_blk(ps - bl16) : -1;
+  const int new_rb0 = (int)(new_first - b_lo);  // rb of virtual block n_old
+  // virtual block i's absolute block and valid key range [vlo, vhi)
   struct VB {
     int64_t b, vlo, vhi;
-    const uint8_t* ptr;
   };
   auto vb_of = [&](int i) -> VB {
     VB v;
@@ -200,23 +222,40 @@ void prefill_attn_kernel(PrefillArgs a) {
       v.b = b_lo + i;
       v.vlo = v.b * kBlockTokens;
       v.vhi = (v.b + 1) * kBlockTokens < ps ? (v.b + 1) * kBlockTokens : ps;
-      int64_t phys = v.b;
-      if (a.ring_slots > 0) phys = v.b % (a.ring_slots / kBlockTokens);
-      v.ptr = a.old_st.base + phys * a.old_st.block_stride + (int64_t)kvh * a.old_st.head_stride;
     } else {
       v.b = new_first + (i - n_old);
       v.vlo = v.b * kBlockTokens > ps ? v.b * kBlockTokens : ps;
       v.vhi = (v.b + 1) * kBlockTokens;
-      int64_t phys = v.b - a.new_blk0;
-      if (table) {
-        // a table entry outside the pool (or a position past the table's
-        // width) reads a valid block rather than faulting
-        phys = v.b < a.new_st.table_stride ? (int64_t)table[v.b] : 0;
-        phys = phys < 0 ? 0 : (phys >= a.new_st.n_blocks ? a.new_st.n_blocks - 1 : phys);
-      }
-      v.ptr = a.new_st.base + phys * a.new_st.block_stride + (int64_t)kvh * a.new_st.head_stride;
     }
     return v;
+  };
+  // its head-block. A ring's slot block of virtual block i is ring0 + i
+  // modulo its nrb blocks (the old keys lie in the last W positions before
+  // p_split: n_old <= nrb + 1, so two conditional subtractions reduce it).
+  const int nrb = a.ring_slots > 0 ? (int)(a.ring_slots / kBlockTokens) : 0;
+  const int ring0 = nrb > 0 ? (int)(b_lo % nrb) : 0;
+  const int32_t n_pool = (int32_t)(a.new_st.n_blocks < INT32_MAX ? a.new_st.n_blocks : INT32_MAX);
+  auto blk_ptr = [&](int i) -> const uint8_t* {
+    if (i < n_old) {
+      int64_t phys = b_lo + i;
+      if (nrb > 0) {
+        int r = ring0 + i;
+        r -= r >= nrb ? nrb : 0;
+        r -= r >= nrb ? nrb : 0;
+        phys = r;
+      }
+      return a.old_st.base + phys * a.old_st.block_stride + (int64_t)kvh * a.old_st.head_stride;
+    }
+    const int64_t b = new_first + (i - n_old);
+    int64_t phys = b - a.new_blk0;
+    if (table) {
+      // a table entry outside the pool (or a position past the table's
+      // width) reads a valid block rather than faulting
+      int32_t e = 0;
+      if ((b >> 31) == 0 && (uint32_t)b < (uint32_t)a.new_st.table_stride) e = table[(uint32_t)b];
+      phys = e < 0 ? 0 : (e >= n_pool ? n_pool - 1 : e);
+    }
+    return a.new_st.base + phys * a.new_st.block_stride + (int64_t)kvh * a.new_st.head_stride;
   };
 
   // ---- q_rot of the 64 rows: rows wave + 8 k, high / residual halves
@@ -297,8 +336,7 @@ void prefill_attn_kernel(PrefillArgs a) {
   // ---- copies ----
   const uint32_t stage_lds = lds_addr(region);
   auto copy_vb = [&](int st, int i) {
-    const VB v = vb_of(i);
-    const u32x4 rs = buffer_rsrc(v.ptr, (uint32_t)P::kBytes);
+    const u32x4 rs = buffer_rsrc(blk_ptr(i), (uint32_t)P::kBytes);
     const uint32_t sl = stage_lds + st * SB;
 #pragma unroll
     for (int k = 0; k < CP; k++) {
@@ -342,7 +380,7 @@ void prefill_attn_kernel(PrefillArgs a) {
   const int pk_off = (int)L.k_codes + (c * D + half * (D / 2) + 8 * j) * 2;
   const int pv_off = (int)L.v_codes + ((half * (D / 2) + c) * kBlockTokens + 4 * j) * 2;
 
-  auto process = [&](const uint8_t* sp, const VB& v, int it) {
+  auto process = [&](const uint8_t* sp, int vi, int it, bool full) {
     float4_t sv = (float4_t){0.f, 0.f, 0.f, 0.f};
     if constexpr (MODE == kCodebook) {
       const uint32_t* kw =
@@ -434,10 +472,9 @@ void prefill_attn_kernel(PrefillArgs a) {
     }
 
     // masks: the whole block for all rows of the pair in the common case
-    const int64_t t0 = v.b * kBlockTokens;
-    const bool full = pair_full_rows && v.vlo == t0 && v.vhi == t0 + kBlockTokens &&
-                      t0 >= pair_lo_max && t0 + kBlockTokens - 1 <= pA;
     if (!full) {
+      const VB v = vb_of(vi);
+      const int64_t t0 = v.b * kBlockTokens;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int64_t kp = t0 + 4 * j + i;
@@ -557,7 +594,6 @@ void prefill_attn_kernel(PrefillArgs a) {
         o[gi * 4 + ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, bh, o[gi * 4 + ct], 0, 0, 0);
         o[gi * 4 + ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, bl, o[gi * 4 + ct], 0, 0, 0);
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
     }
   };
@@ -571,10 +607,16 @@ void prefill_attn_kernel(PrefillArgs a) {
     wait_copies<CP, NST - 2>(rest < NST - 2 ? rest : NST - 2);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     if (i + NST - 1 < nvb) copy_vb((i + NST - 1) % NST, i + NST - 1);
-    const VB v = vb_of(i);
     // the pair's rows see this block at all (pair-uniform)
-    if (pair_any && v.vhi - 1 >= pair_lo_min && v.vlo <= pB) {
-      process(region + st * SB, v, it);
+    const int rb = i < n_old ? i : new_rb0 + (i - (int)n_old);
+    bool sees = rb >= sees_lo && rb <= sees_hi;
+    if (rb == cut_rb) {
+      const VB v = vb_of(i);
+      sees = pair_any && v.vhi - 1 >= pair_lo_min && v.vlo <= pB;
+    }
+    if (sees) {
+      const bool full = rb >= full_lo && rb <= full_hi && rb != cut_rb;
+      process(region + st * SB, i, it, full);
       it++;
     }
     st = st + 1 == NST ? 0 : st + 1;
