@@ -263,6 +263,8 @@ def run_c3(args) -> dict:
         proj_us = (time.perf_counter() - t0) / args.steps * 1e6
         log(f"projected step (prologue in the new-token column): {proj_us:.1f} us")
 
+    copy_gbs = device_copy_gbs()
+    log(f"device copy (256 MiB, read + write): {copy_gbs:.0f} GB/s")
     res = {
         "metric": "decode-attn GB/s & % HBM peak over quantized KV at 32K ctx; append tokens/s",
         "value": round(value, 2),
@@ -303,6 +305,9 @@ def run_c3(args) -> dict:
             "kernel": (f"cb_decode_kernel<512, {bits}>" if cb else "plain_decode_kernel<512>" if plain
                        else f"decode_attn_kernel<512, {bits}, 0>"),
             "avg_kernel_us": round(kern_s * 1e6, 3),
+            # the same kernel against a plain device copy measured in this run
+            "device_copy_gbs": round(copy_gbs, 1),
+            "frac_of_device_copy": round(achieved / copy_gbs, 4),
             "kernel_us_p10_p50_p90": [kern_pct[10], kern_pct[50], kern_pct[90]],
             "bytes_per_launch": int(launch_bytes),
         },
@@ -890,6 +895,28 @@ def cpu_baseline_c1(oracle, synth, threads) -> dict:
     return {"append_tokens_per_s": round(T / (t1 - t0), 1), "appends": T,
             "decode_step_ms": round((t2 - t1) * 1e3, 3), "threads": threads,
             "workload": "Hq 16, Hkv 8, head_dim 256, 4-bit TurboQuant round trip, bf16 cache"}
+
+
+def device_copy_gbs(mib: int = 256, reps: int = 8) -> float:
+    """A plain device-to-device copy of `mib` MiB, timed with events: bytes
+    read plus bytes written per second, in GB/s (the reference point for
+    what this GPU's HBM delivers to a simple streaming kernel)."""
+    import torch
+
+    n = mib * (1 << 20)
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    ev0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / reps
+    del src, dst
+    return 2 * n / ms / 1e6
 
 
 def copy_calibration(mib: int) -> int:
