@@ -18,8 +18,8 @@
 // Per block (16 keys), affine caches, per 64-dim group g of the wave's half:
 //   QK^T  S^T[16 key x 16 row] += K[16 x 32] . Q^T[32 x 16] with K codes as
 //         exact f16 integers, q_rot as an f16 high part and an f16 residual
-//         (~22 bits), each in its own accumulator; then
-//         s += scale * (acc_hi + acc_lo) + bias * sum(q_group). (The decode
+//         (~22 bits), the residual's products first, then the high part's,
+//         in one accumulator; then s += scale * acc + bias * sum(q_group). (The decode
 //         kernel's 1024 + code operands, one v_perm per two codes, left the
 //         residual's contribution on top of a large partial sum here: the
 //         worst output error of a 1500-key test rose ~4x; the plain codes
@@ -425,11 +425,11 @@ void prefill_attn_kernel(PrefillArgs a) {
       const int g = g0 + gi;
       const half8_t k0 = k_operand_plain<BITS>(kw_g, g, 0), k1 = k_operand_plain<BITS>(kw_g, g, 1);
       const float4_t z = (float4_t){0.f, 0.f, 0.f, 0.f};
-      float4_t acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, bqh[gi][0], z, 0, 0, 0);
+      // the residual products first, then the high parts, in one accumulator
+      float4_t acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, bql[gi][0], z, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, bql[gi][1], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, bqh[gi][0], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, bqh[gi][1], acc, 0, 0, 0);
-      float4_t acl = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, bql[gi][0], z, 0, 0, 0);
-      acl = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, bql[gi][1], acl, 0, 0, 0);
-      acc = acc + acl;
 #pragma unroll
       for (int i = 0; i < 4; i++)
         sv[i] = fmaf(lo16(km_g[i]), acc[i], fmaf(hi16(km_g[i]), qs[gi], sv[i]));
