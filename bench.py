@@ -195,7 +195,11 @@ def run_c3(args) -> dict:
     kern_s = sum(each_ms) / n_rec / 1e3
     each_us = sorted(m * 1e3 for m in each_ms)
     kern_pct = {q: round(each_us[min(n_rec - 1, int(q / 100 * n_rec))], 3) for q in (10, 50, 90)}
-    launch_bytes = avg_T * Hkv * per_tok + 2 * Hq * D * 2
+    # (sparse-V: the statistics pass reads the keys, half of each token's
+    # bytes; the gated pass reads only the blocks that hold kept tokens, and
+    # its figure counts every block)
+    gather = tau > 0.0 and args.sparse_v_path == "gather"
+    launch_bytes = avg_T * Hkv * (per_tok // 2 if gather else per_tok) + 2 * Hq * D * 2
     achieved = launch_bytes / kern_s / 1e9
     log(f"step {ms_per_step*1e3:.1f} us, split kernel {kern_s*1e6:.2f} us over {n_rec} launches, "
         f"{achieved:.0f} GB/s, splits={cache.decode_splits()}; per launch p10/p50/p90 "
@@ -286,6 +290,7 @@ def run_c3(args) -> dict:
                          + ", 1 token append + attention per step"),
             "context": T0, "batch": 1, "n_q_heads": Hq, "n_kv_heads": Hkv, "head_dim": D,
             "bits": bits, "mode": args.mode, "group": 64, "sparse_v_tau": tau,
+            **({"sparse_v_path": args.sparse_v_path} if tau > 0.0 else {}),
         },
         "hbm_frac_of_value": round(value / HBM_PEAK_GBS, 4),
         "append_tokens_per_s": {"chunked_prefill_2048": round(append_prefill_tps, 1),
@@ -302,8 +307,9 @@ def run_c3(args) -> dict:
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None if (not quant or bits != 8) else TRAFFIC_BYTES_PER_LAUNCH,
             "traffic_source": None if (not quant or bits != 8) else TRAFFIC_SOURCE,
-            "kernel": (f"cb_decode_kernel<512, {bits}>" if cb else "plain_decode_kernel<512>" if plain
-                       else f"decode_attn_kernel<512, {bits}, 0>"),
+            "kernel": ((f"cb_decode_kernel<512, {bits}>" if cb else "plain_decode_kernel<512>" if plain
+                        else f"decode_attn_kernel<512, {bits}, {0 if tau == 0.0 else 1 if gather else 2}>")
+                       + ("" if tau == 0.0 else " (statistics pass)" if gather else " (gated pass)")),
             "avg_kernel_us": round(kern_s * 1e6, 3),
             # the same kernel against a plain device copy measured in this run
             "device_copy_gbs": round(copy_gbs, 1),
@@ -954,8 +960,12 @@ def main(argv=None) -> int:
     ap.add_argument("--graph-steps", type=int, default=64,
                     help="c3: also time this many steps captured in a HIP graph (0: skip)")
     ap.add_argument("--sparse-v-tau", type=float, default=0.0,
-                    help="c3: sparse-V threshold (0: dense softmax attention; > 0 adds the "
-                         "statistics pass and times the gated pass as the split kernel)")
+                    help="c3: sparse-V threshold (0: dense softmax attention; > 0: the "
+                         "statistics pass, then the second half --sparse-v-path names)")
+    ap.add_argument("--sparse-v-path", choices=["gather", "gated"], default="gather",
+                    help="sparse-V after the statistics pass: the gather of the kept V rows "
+                         "(default; the statistics pass is the timed kernel) or the gated pass "
+                         "and the split merge (the gated pass is the timed kernel)")
     ap.add_argument("--unfused", action="store_true",
                     help="time fmkv_cache_append + fmkv_decode_attention instead of fmkv_decode_step")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -992,10 +1002,11 @@ def main(argv=None) -> int:
         return 1
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
-    if args.bps:
-        import fmkv
+    import fmkv
 
+    if args.bps:
         fmkv.set_blocks_per_split(args.bps)
+    fmkv.set_sparse_v_gather(args.sparse_v_path == "gather")
     res = {"c3": run_c3, "c2": run_c2, "c4": run_c4, "c5": run_c5,
            "prefill": run_prefill, "append": run_append}[args.workload](args)
     print(json.dumps(res), flush=True)

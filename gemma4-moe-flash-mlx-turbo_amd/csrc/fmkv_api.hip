@@ -24,6 +24,9 @@ namespace {
 
 thread_local std::string g_err;
 int32_t g_bps_override = 0;
+// sparse-V after the statistics pass: 1 the gather, 0 the gated pass and the
+// combine (fmkv_set_sparse_v_gather)
+int32_t g_sparse_gather = 1;
 
 // Kernel-timing records (fmkv_profile_enable / fmkv_profile_collect).
 struct Profiler {
@@ -423,7 +426,16 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   // scratch holds the call's blocks only)
   a->blk_stride = (int32_t)std::max<int64_t>(std::max<int64_t>(nblk, ext.ptr ? 0 : blk_cap), 1);
   const size_t n_blk = tau > 0.0f ? (size_t)n_seqs * H * a->blk_stride * 8 : 0;
-  const size_t need = (n_blk ? blk_off + n_blk : stat_off + n_stat_ml) * sizeof(float);
+  // sparse-V gather: the candidate blocks' scores (16 per block row and
+  // head) after the maxima, then one arrival counter per (sequence, q head);
+  // without room for them in a caller's scratch, the gated pass
+  bool gather = tau > 0.0f && g_sparse_gather && nblk <= fmkv::kGatherMaxRows;
+  const size_t score_off = blk_off + n_blk;  // a multiple of 4 floats
+  const size_t cnt_off = score_off + 16 * n_blk;
+  const size_t need_gather = (cnt_off + (size_t)n_seqs * n_q_heads) * sizeof(float);
+  if (gather && ext.ptr && need_gather > ext.bytes) gather = false;
+  const size_t need =
+      gather ? need_gather : (n_blk ? blk_off + n_blk : stat_off + n_stat_ml) * sizeof(float);
   float* ws = ext.ptr;
   if (ws) {
     if (need > ext.bytes)
@@ -446,7 +458,7 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
       const size_t rows = (size_t)(max_splits + 1) * n_q_heads;
       const size_t off = (rows * (D + 2) + 3 * (size_t)n_q_heads + 2 * rows + 3) & ~(size_t)3;
       const size_t blks = (size_t)H * std::max<int64_t>(std::max<int64_t>(blk_cap, nblk), 1) * 8;
-      alloc = std::max(need, (off + blks) * sizeof(float));
+      alloc = std::max(need, (off + blks * (gather ? 17 : 1) + (gather ? n_q_heads : 0)) * sizeof(float));
     }
     rc = o->ws.ensure(alloc);
     if (rc) return rc;
@@ -457,6 +469,18 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   a->tau_stats = n_stats ? ws + n_rows * (D + 2) : nullptr;
   a->stat_ml = n_stat_ml ? ws + stat_off : nullptr;
   a->blk_max = n_blk ? ws + blk_off : nullptr;
+  a->blk_scores = gather ? ws + score_off : nullptr;
+  a->sv_count = gather ? reinterpret_cast<int32_t*>(ws + cnt_off) : nullptr;
+  if (gather) {
+    // parts per (sequence, q head): a part's kept tokens are at most
+    // min(visible tokens, 1 / tau) / parts when they spread evenly over the
+    // candidate blocks; 512 a part, at most 16 parts
+    const double inv_tau = std::ceil(1.0 / (double)tau);
+    const int64_t bound = std::min<int64_t>(nblk * fmkv::kBlockTokens,
+                                            inv_tau < 1e15 ? (int64_t)inv_tau : INT64_MAX);
+    a->gather_parts = (int32_t)std::clamp<int64_t>((bound + 511) / 512, 1,
+                                                   std::min<int64_t>(a->part_stride, 16));
+  }
   return FMKV_OK;
 }
 
@@ -1189,6 +1213,12 @@ int fmkv_pool_read_codes(const fmkv_pool* p, void* codes, void* meta, void* stre
   a.meta = static_cast<uint16_t*>(meta);
   hipError_t e = fmkv::launch_read_codes(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "pool read_codes launch");
+  return FMKV_OK;
+}
+
+int fmkv_set_sparse_v_gather(int32_t on) {
+  if (on != 0 && on != 1) return fail(FMKV_ERR_INVALID_ARG, "sparse_v_gather must be 0 or 1");
+  g_sparse_gather = on;
   return FMKV_OK;
 }
 

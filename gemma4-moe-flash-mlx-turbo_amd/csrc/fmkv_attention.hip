@@ -725,6 +725,7 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
   // softmax needs no special cases.
   float m_run = -1e30f, l_run = 0.0f;
   const float lo_sel = hi ? 0.0f : 1.0f;  // 1 on the residual columns
+  const float log2_tau = MODE == kStats ? log2f(a.tau) : 0.0f;
 
   // visible slots: linear [vis_lo, vis_hi); ring [0, min(T, W)), unless a trim
   // hides older positions (then each slot's position is computed)
@@ -894,7 +895,11 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
 #pragma unroll
     for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(s[i] - m_run);
     l_run += (p[0] + p[1]) + (p[2] + p[3]);
-    if constexpr (MODE == kStats) return;
+    if constexpr (MODE == kStats) {
+      store_block_scores(a, blk_row, b - geo.blk_lo, head, j, s, mb, m_run, log2_tau,
+                         half == 0 && hi && col_valid);
+      return;
+    }
     // sparse-V: a block whose weights are all below tau adds nothing to O
     // (no renormalisation), so its V dequantisation and products are
     // skipped (the pair's waves hold the same scores: a uniform branch)
@@ -997,6 +1002,7 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
       const int64_t r = ((int64_t)seq * a.part_stride + split) * a.n_q_heads + (int64_t)kvh * G + lane;
       a.part_ml[r * 2 + 0] = M;
       a.part_ml[r * 2 + 1] = Lsum;
+      if (split == 0 && a.sv_count) a.sv_count[(int64_t)seq * a.n_q_heads + (int64_t)kvh * G + lane] = 0;
     }
     return;
   }
@@ -1261,14 +1267,22 @@ hipError_t launch_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s
   hipError_t e;
   if (a.tau > 0.0f) {
     // sparse-V: the stats pass (with a decode step's new-token column, which
-    // appends the token), the gated pass over every stored token (the new
-    // one included; it derives the thresholds from the stats pass's
-    // statistics, which sit in a region of their own, stat_ml, so that no
-    // gated work-group overwrites what another still reads) and the combine
-    // of its splits
+    // appends the token), then either the gather (launch_sparse_gather) or
+    // the gated pass over every stored token (the new one included; it
+    // derives the thresholds from the stats pass's statistics, which sit in
+    // a region of their own, stat_ml, so that no gated work-group
+    // overwrites what another still reads) and the combine of its splits
     AttnArgs st = a;
     st.part_ml = a.stat_ml;
     if (!st.part_ml) return hipErrorInvalidValue;
+    if (a.blk_scores) {
+      // the gather in place of the gated pass and the combine (the stats
+      // pass stored the candidate blocks' scores and zeroed the counters)
+      if ((e = launch_split<D, BITS, kStats>(st, grid, s, ev0, ev1)) != hipSuccess) return e;
+      AttnArgs g = a;
+      g.stats_new_col = a.new_col;
+      return launch_sparse_gather(g, n_seqs, s);
+    }
     if ((e = launch_split<D, BITS, kStats>(st, grid, s, nullptr, nullptr)) != hipSuccess) return e;
     AttnArgs g = a;
     g.new_col = 0;

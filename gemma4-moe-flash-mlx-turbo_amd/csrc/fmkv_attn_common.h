@@ -281,6 +281,21 @@ __device__ inline BlockList gated_block_list(const AttnArgs& a, const float (&th
   return BlockList{mask, 64, nb};
 }
 
+// Sparse-V statistics pass, for the gather: the block's scores of the
+// lane's head (tokens 4j .. 4j + 3) when the block may hold a kept token. A
+// weight 2^(s - M) / L reaches tau only if s >= M + log2(tau) (L >= 1), and a
+// split's running reference max m_run (after this block) never exceeds the
+// full max M, so a block whose largest score mb for the head is below
+// m_run + log2(tau) holds none and is not stored (the test keeps a margin of
+// 1/64 against the rounding of either side).
+__device__ inline void store_block_scores(const AttnArgs& a, int64_t blk_row, int64_t rb, int head,
+                                          int j, const float (&s)[4], float mb, float m_run,
+                                          float log2_tau, bool writer) {
+  if (a.blk_scores && writer && rb < a.blk_stride && mb + 0.015625f >= m_run + log2_tau)
+    *reinterpret_cast<float4_t*>(a.blk_scores + ((blk_row + rb) * 8 + head) * 16 + 4 * j) =
+        (float4_t){s[0], s[1], s[2], s[3]};
+}
+
 template <int E>
 __device__ inline void store_halves(uint8_t* p, const _Float16 (&h)[E]) {
   if constexpr (E == 8)

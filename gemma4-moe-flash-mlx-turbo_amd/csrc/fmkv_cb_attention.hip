@@ -548,7 +548,11 @@ void cb_decode_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(sc[i] - m_run);
     l_run += (p[0] + p[1]) + (p[2] + p[3]);
-    if constexpr (MODE == kStats) return;
+    if constexpr (MODE == kStats) {
+      store_block_scores(a, blk_row, b - geo.blk_lo, head, j, sc, mb, m_run, log2f(a.tau),
+                         half == 0 && hi && col_valid);
+      return;
+    }
     // sparse-V: a block whose weights are all below tau adds nothing to O
     // (the pair's waves hold the same scores: a uniform branch)
     if constexpr (MODE == kGated) {
@@ -618,6 +622,7 @@ void cb_decode_kernel(AttnArgs a) {
       const int64_t r = ((int64_t)seq * a.part_stride + split) * a.n_q_heads + (int64_t)kvh * G + lane;
       a.part_ml[r * 2 + 0] = M;
       a.part_ml[r * 2 + 1] = Lsum;
+      if (split == 0 && a.sv_count) a.sv_count[(int64_t)seq * a.n_q_heads + (int64_t)kvh * G + lane] = 0;
     }
     return;
   }
@@ -716,6 +721,14 @@ hipError_t launch_cb_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_
     AttnArgs st = a;
     st.part_ml = a.stat_ml;
     if (!st.part_ml) return hipErrorInvalidValue;
+    if (a.blk_scores) {
+      // the gather in place of the gated pass and the combine (the stats
+      // pass stored the candidate blocks' scores and zeroed the counters)
+      if ((e = launch_cb_mode<D, BITS, kStats>(st, grid, s, ev0, ev1)) != hipSuccess) return e;
+      AttnArgs g = a;
+      g.stats_new_col = a.new_col;
+      return launch_sparse_gather(g, n_seqs, s);
+    }
     if ((e = launch_cb_mode<D, BITS, kStats>(st, grid, s, nullptr, nullptr)) != hipSuccess) return e;
     AttnArgs g = a;
     g.new_col = 0;

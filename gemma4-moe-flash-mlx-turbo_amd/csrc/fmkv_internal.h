@@ -112,6 +112,14 @@ struct AttnArgs {
   // the gated pass only reads it (the gated work-groups write their own
   // partials to part_ml while others may still be deriving thresholds).
   float* stat_ml = nullptr;
+  // Sparse-V gather (launch_sparse_gather in place of the gated pass and the
+  // combine): the stats pass also stores the base-2 scores of every block
+  // that may hold a kept token, [n_seqs][n_kv_heads][blk_stride][8][16]
+  // (q head of the group, token of the block), and zeroes the gather's
+  // arrival counters, [n_seqs][n_q_heads]. Null: the gated pass.
+  float* blk_scores = nullptr;
+  int32_t* sv_count = nullptr;
+  int32_t gather_parts = 0;  // work-groups per (sequence, q head) of the gather
 };
 
 // Prefill (chunked) attention: n_q queries at positions p0 .. p0 + n_q - 1,
@@ -215,6 +223,11 @@ hipError_t launch_cb_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_he
 hipError_t launch_plain_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads,
                                          hipStream_t s, hipEvent_t ev_begin = nullptr,
                                          hipEvent_t ev_end = nullptr);
+// Sparse-V after the statistics pass: the kept weights of every q head and
+// the V rows they weigh, straight to out (fmkv_readback.hip).
+// At most kGatherMaxRows visible head-blocks per sequence.
+constexpr int kGatherMaxRows = 8192;
+hipError_t launch_sparse_gather(const AttnArgs& a, int n_seqs, hipStream_t s);
 // The split merge of every decode kernel: out = LSE merge of the partials.
 hipError_t launch_combine(const AttnArgs& a, int n_seqs, hipStream_t s);
 hipError_t launch_prefill_attention(const PrefillArgs& a, hipStream_t s);

@@ -327,7 +327,11 @@ __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; r++) p[r] = __builtin_amdgcn_exp2f(s4[r] - m_run);
     l_run += (p[0] + p[1]) + (p[2] + p[3]);
-    if constexpr (MODE == kStats) continue;
+    if constexpr (MODE == kStats) {
+      store_block_scores(a, blk_row, b - geo.blk_lo, head, j, s4, mb, m_run, log2f(a.tau),
+                         wave == 0 && hi_col && head < G);
+      continue;
+    }
     // sparse-V: a block whose weights are all below tau adds nothing to O
     // (every wave holds the same scores: a uniform branch)
     if constexpr (MODE == kGated) {
@@ -355,6 +359,7 @@ __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
       const int64_t r = ((int64_t)seq * a.part_stride + split) * a.n_q_heads + (int64_t)kvh * G + head;
       a.part_ml[r * 2 + 0] = m_run;
       a.part_ml[r * 2 + 1] = l_run;
+      if (split == 0 && a.sv_count) a.sv_count[(int64_t)seq * a.n_q_heads + (int64_t)kvh * G + head] = 0;
     }
     return;
   }
@@ -424,6 +429,14 @@ hipError_t launch_plain_t(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStre
     AttnArgs st = a;
     st.part_ml = a.stat_ml;
     if (!st.part_ml) return hipErrorInvalidValue;
+    if (a.blk_scores) {
+      // the gather in place of the gated pass and the combine (the stats
+      // pass stored the candidate blocks' scores and zeroed the counters)
+      if ((e = launch_plain_mode<D, kStats>(st, grid, s, ev0, ev1)) != hipSuccess) return e;
+      AttnArgs g = a;
+      g.stats_new_col = a.new_col;
+      return launch_sparse_gather(g, n_seqs, s);
+    }
     if ((e = launch_plain_mode<D, kStats>(st, grid, s, nullptr, nullptr)) != hipSuccess) return e;
     AttnArgs g = a;
     g.new_col = 0;

@@ -1,11 +1,13 @@
-// Read-side utility kernels:
+// Read-side kernels:
 //  - read_codes: stored codes/scales in a canonical per-slot layout (MLX
 //    little-endian packing), for bit-exact comparison with the oracle;
 //  - fetch: dequantized, un-rotated K/V of the visible positions in
 //    chronological order -- what KVCache::update_and_fetch returns and
 //    KVCache::peek_kv reads (src/cache.rs:247-310). In codebook mode this is
 //    the reference's round trip output (src/cache.rs:119-125) computed from
-//    the stored indices and f16 norm; in plain mode the stored bf16 rows.
+//    the stored indices and f16 norm; in plain mode the stored bf16 rows;
+//  - sparse_gather: sparse-V attention's second half, which reads the V
+//    rows of the kept tokens only.
 #include "fmkv_device.h"
 #include "fmkv_internal.h"
 
@@ -157,7 +159,313 @@ __global__ __launch_bounds__(64) void fetch_kernel(FetchArgs a) {
   }
 }
 
+// V row of the token in slot t of head-block `blk`, dim d, in the rotated
+// domain the attention kernels read (plain caches: the stored row): affine
+// code * scale + bias, codebook centroid * norm / sqrt(D), plain bf16.
+__device__ inline float v_value(const uint8_t* blk, const BlockLayout& L, int t, int d, float c) {
+  const uint32_t code = stored_code(blk, L, 1, t, d);
+  if (L.mode == kAffine) {
+    const uint32_t sb = *reinterpret_cast<const uint32_t*>(blk + L.v_meta + scale_pos(d / kGroup, t));
+    return fmaf((float)code, f16_bits_to_f32(sb), f16_bits_to_f32(sb >> 16));
+  }
+  if (L.mode == kCodebook)
+    return (centroid(L.bits, code) * c) *
+           f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + L.v_meta + t * 2));
+  return __uint_as_float(code << 16);
+}
+
+// Exclusive prefix count over the work-group: each thread holds `n` items
+// that pass; returns the number of passing items of the threads before it
+// and sets *total. Two barriers (the count array is reused by the next call).
+template <int NT>
+__device__ inline int wg_exclusive_count(int n, int* cnt, int* total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int x = n;  // inclusive scan inside the wave
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) cnt[wave] = x;
+  __syncthreads();
+  int before = x - n, tot = 0;
+#pragma unroll
+  for (int w = 0; w < NT / 64; w++) {
+    before += w < wave ? cnt[w] : 0;
+    tot += cnt[w];
+  }
+  __syncthreads();
+  *total = tot;
+  return before;
+}
+
+// Sparse-V attention after the statistics pass (src/model/gemma4_attention.rs
+// :196-234: softmax weights below tau zeroed, no renormalisation), without
+// a second pass over the cache. Work-group (q head h, sequence, part p of
+// n_parts):
+//  1. M and L of the head from the statistics pass's split (m, l), the
+//     decode step's new-token column included, and theta = M + log2(tau L);
+//  2. the candidate blocks: those whose largest score for h reaches theta
+//     (every part builds the whole list);
+//  3. the kept tokens of the part's share of the candidates, from the
+//     scores the statistics pass stored (s >= theta), with weight
+//     w = 2^(s - M) / L; part 0 also takes the step's new token when its
+//     score (its column's m) reaches theta;
+//  4. acc[d] = sum of w * V[token][d] (rotated domain);
+//  5. out = acc R^T = c * FWHT(acc o s) (plain caches: out = acc).
+// With at most kSoloRows candidates part 0 takes them all and writes out,
+// and the other parts return. Otherwise part p takes the candidates
+// [p nc / n_parts, (p + 1) nc / n_parts), stores acc in its partial row,
+// and the last part to count itself on the (sequence, q head)'s counter
+// (zeroed by the statistics pass) sums the rows in part order and writes
+// out. Every step's loads are issued together (one memory round trip each:
+// block maxima with the statistics, scores, V rows), each a coalesced sweep
+// (thread tid takes rows and items k NT + tid); the lists are in thread-major
+// order (thread, then k), a fixed order, so the sums are deterministic.
+// Blocks: at most kGatherMaxRows visible head-blocks per sequence.
+template <int D>
+__global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
+  constexpr int NT = 256, E = D / 64, ND = (D + NT - 1) / NT;
+  constexpr int RPT = kGatherMaxRows / NT;  // block rows per thread
+  constexpr int kRound = 64;                // candidates per score round
+  constexpr int IPT = kRound * kBlockTokens / NT;  // score items per thread
+  constexpr int SPT = 2;                    // statistics per thread per load round
+  constexpr int kSoloRows = 64;
+  __shared__ int cand[kGatherMaxRows];
+  __shared__ int kept_slot[kRound * kBlockTokens + 1];
+  __shared__ float kept_w[kRound * kBlockTokens + 1];
+  __shared__ int cnt[NT / 64];
+  __shared__ float red[2][NT / 64];
+  __shared__ float xs[D];
+  __shared__ int last_s;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.x, seq = blockIdx.y, part = blockIdx.z;
+  const int n_parts = (int)gridDim.z;
+  const int G = a.group, kvh = h / G, hl = h - kvh * G;
+  const BlockLayout L = a.st.layout;
+  const int64_t nqh = a.n_q_heads;
+  const int64_t T = a.seq_lens ? (int64_t)a.seq_lens[seq] : a.seq_len;
+  const SeqGeom geo =
+      seq_geometry(T, a.window, a.vis_begin, a.st.table_stride, a.st.block_table != nullptr);
+  const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits, a.skew_p);
+  int64_t nrows = geo.blk_hi - geo.blk_lo;
+  if (nrows > a.blk_stride) nrows = a.blk_stride;  // (the host plans rows <= blk_stride)
+  const int64_t blk_row = ((int64_t)seq * a.st.n_kv_heads + kvh) * a.blk_stride;
+
+  // 1. the loads of the block maxima (rows k NT + tid), the statistics
+  // (partials i NT + tid) and the new token's score, together
+  const int kmax = (int)((nrows + NT - 1) / NT);  // <= RPT
+  float bm[RPT];
+#pragma unroll
+  for (int k = 0; k < RPT; k++) {
+    const int64_t rb = (int64_t)k * NT + tid;
+    bm[k] = -INFINITY;
+    if (k < kmax && rb < nrows) bm[k] = a.blk_max[(blk_row + rb) * 8 + hl];
+  }
+  const int n_stat = n_splits + a.stats_new_col;
+  const int64_t rbase = (int64_t)seq * a.part_stride * nqh + h;
+  float2 ml[SPT];
+#pragma unroll
+  for (int i = 0; i < SPT; i++) {
+    const int sp = i * NT + tid;
+    ml[i] = sp < n_stat ? *reinterpret_cast<const float2*>(a.stat_ml + (rbase + (int64_t)sp * nqh) * 2)
+                        : make_float2(-INFINITY, 0.0f);
+  }
+  const float m_nt = a.stats_new_col ? a.stat_ml[(rbase + (int64_t)n_splits * nqh) * 2] : -INFINITY;
+  float Mt = fmaxf(ml[0].x, ml[1].x);
+  for (int sp = SPT * NT + tid; sp < n_stat; sp += NT)
+    Mt = fmaxf(Mt, a.stat_ml[(rbase + (int64_t)sp * nqh) * 2]);
+  // the head's M: the work-group maximum
+  float v = group_max<64>(Mt, lane);
+  if (lane == 0) red[0][wave] = v;
+  __syncthreads();
+  float M = red[0][0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; w++) M = fmaxf(M, red[0][w]);
+  // the head's L at M
+  float Lt = 0.0f;
+  if (M != -INFINITY) {
+#pragma unroll
+    for (int i = 0; i < SPT; i++) Lt = fmaf(ml[i].y, exp2f(ml[i].x - M), Lt);
+    for (int sp = SPT * NT + tid; sp < n_stat; sp += NT) {
+      const float2 m2 = *reinterpret_cast<const float2*>(a.stat_ml + (rbase + (int64_t)sp * nqh) * 2);
+      Lt = fmaf(m2.y, exp2f(m2.x - M), Lt);
+    }
+  }
+  v = group_sum<64>(Lt, lane);
+  if (lane == 0) red[1][wave] = v;
+  __syncthreads();
+  float Ls = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NT / 64; w++) Ls += red[1][w];
+  const float theta = Ls > 0.0f ? M + log2f(a.tau * Ls) : INFINITY;
+  const float inv_l = Ls > 0.0f ? 1.0f / Ls : 0.0f;
+
+  // 2. candidate rows
+  uint32_t flags = 0;
+#pragma unroll
+  for (int k = 0; k < RPT; k++) flags |= (k < kmax && bm[k] >= theta ? 1u : 0u) << k;
+  int nc;
+  int pos = wg_exclusive_count<NT>(__builtin_popcount(flags), cnt, &nc);
+  while (flags) {
+    const int k = __builtin_ctz(flags);
+    flags &= flags - 1;
+    cand[pos++] = k * NT + tid;
+  }
+  __syncthreads();
+  const bool solo = nc <= kSoloRows;
+  if (solo && part != 0) return;
+  const int c0 = solo ? 0 : (int)((int64_t)part * nc / n_parts);
+  const int c1 = solo ? nc : (int)((int64_t)(part + 1) * nc / n_parts);
+
+  // block address of logical slot block lb
+  const uint8_t* hbase = a.st.base + (int64_t)kvh * a.st.head_stride;
+  auto block_of = [&](int64_t lb) -> const uint8_t* {
+    int64_t phys = lb;
+    if (a.st.block_table) {
+      phys = lb < a.st.table_stride ? (int64_t)a.st.block_table[(int64_t)seq * a.st.table_stride + lb] : 0;
+      phys = phys < 0 ? 0 : (phys >= a.st.n_blocks ? a.st.n_blocks - 1 : phys);
+    }
+    return hbase + phys * a.st.block_stride;
+  };
+
+  float acc[ND];
+#pragma unroll
+  for (int e = 0; e < ND; e++) acc[e] = 0.0f;
+  // 3. + 4. the part's candidates, kRound at a time; part 0's first round
+  // also takes the decode step's new token (appended to its kept list)
+  bool nt_pending = part == 0 && a.stats_new_col && m_nt >= theta;
+  for (int r0 = c0; r0 < c1 || nt_pending; r0 += kRound) {
+    const int rn = c1 - r0 < kRound ? (c1 > r0 ? c1 - r0 : 0) : kRound;
+    float sv[IPT];
+    int nk = 0;
+#pragma unroll
+    for (int k = 0; k < IPT; k++) {
+      const int item = k * NT + tid, ci = item / kBlockTokens;
+      sv[k] = -INFINITY;
+      if (ci < rn) {
+        const int64_t rb = cand[r0 + ci];
+        sv[k] = a.blk_scores[((blk_row + rb) * 8 + hl) * kBlockTokens + item % kBlockTokens];
+      }
+      nk += sv[k] >= theta ? 1 : 0;
+    }
+    int total;
+    int at = wg_exclusive_count<NT>(nk, cnt, &total);
+#pragma unroll
+    for (int k = 0; k < IPT; k++) {
+      if (sv[k] >= theta) {
+        const int item = k * NT + tid;
+        kept_slot[at] =
+            (int)((geo.blk_lo + cand[r0 + item / kBlockTokens]) * kBlockTokens + item % kBlockTokens);
+        kept_w[at] = exp2f(sv[k] - M) * inv_l;
+        at++;
+      }
+    }
+    int n = total;
+    if (nt_pending) {
+      if (tid == 0) {
+        kept_slot[total] = (int)(a.window > 0 ? (T - 1) % a.window : T - 1);
+        kept_w[total] = exp2f(m_nt - M) * inv_l;
+      }
+      n = total + 1;
+      nt_pending = false;
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int k = 0; k < n; k++) {
+      const int slot = kept_slot[k];
+      const float w = kept_w[k];
+      const uint8_t* blk = block_of(slot / kBlockTokens);
+      const int t = slot % kBlockTokens;
+#pragma unroll
+      for (int e = 0; e < ND; e++) {
+        const int d = tid + e * NT;
+        if (d < D) acc[e] = fmaf(w, v_value(blk, L, t, d, a.c), acc[e]);
+      }
+    }
+    __syncthreads();
+  }
+
+  // 5. merge (several parts) and the inverse rotation
+  float* const orow = a.part_o + (((int64_t)seq * a.part_stride + part) * nqh + h) * D;
+  if (!solo) {
+#pragma unroll
+    for (int e = 0; e < ND; e++) {
+      const int d = tid + e * NT;
+      if (d < D) orow[d] = acc[e];
+    }
+    __threadfence();  // release the row (agent scope)
+    __syncthreads();
+    if (tid == 0) last_s = atomicAdd(&a.sv_count[(int64_t)seq * nqh + h], 1) == n_parts - 1;
+    __syncthreads();
+    if (!last_s) return;
+    __threadfence();  // acquire the other parts' rows
+    const float* prow0 = a.part_o + ((int64_t)seq * a.part_stride * nqh + h) * D;
+#pragma unroll
+    for (int e = 0; e < ND; e++) {
+      const int d = tid + e * NT;
+      float sum = 0.0f;
+      if (d < D)
+        for (int q = 0; q < n_parts; q++) sum += __hip_atomic_load(prow0 + (int64_t)q * nqh * D + d,
+                                                                     __ATOMIC_RELAXED,
+                                                                     __HIP_MEMORY_SCOPE_AGENT);
+      acc[e] = sum;
+    }
+  }
+  const int64_t o_idx = ((int64_t)seq * nqh + h) * D;
+  if (L.mode == kPlain) {
+#pragma unroll
+    for (int e = 0; e < ND; e++) {
+      const int d = tid + e * NT;
+      if (d < D) {
+        if (a.out_f32)
+          reinterpret_cast<float*>(a.out)[o_idx + d] = acc[e];
+        else
+          reinterpret_cast<uint16_t*>(a.out)[o_idx + d] = f32_to_bf16(acc[e]);
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < ND; e++) {
+    const int d = tid + e * NT;
+    if (d < D) xs[d] = acc[e];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const uint32_t sbits = lane_sign_bits<D>(a.sign_bits, lane);
+    float x[E];
+#pragma unroll
+    for (int i = 0; i < E; i++) x[i] = apply_sign(xs[lane * E + i], sbits, i);
+    wave_fwht_signed<E>(x, lane);
+    const float cs = fwht_lane_sign(lane) * a.c;
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      const float y = x[i] * cs;
+      if (a.out_f32)
+        reinterpret_cast<float*>(a.out)[o_idx + lane * E + i] = y;
+      else
+        reinterpret_cast<uint16_t*>(a.out)[o_idx + lane * E + i] = f32_to_bf16(y);
+    }
+  }
+}
+
 }  // namespace
+
+hipError_t launch_sparse_gather(const AttnArgs& a, int n_seqs, hipStream_t s) {
+  if (!a.blk_scores || !a.sv_count || !a.blk_max || !a.stat_ml || !a.part_o || a.group < 1 ||
+      a.group > 8 || a.gather_parts < 1 || a.gather_parts > a.part_stride)
+    return hipErrorInvalidValue;
+  dim3 grid((unsigned)a.n_q_heads, (unsigned)n_seqs, (unsigned)a.gather_parts);
+  switch (a.st.layout.head_dim) {
+    case 128: hipLaunchKernelGGL((sparse_gather_kernel<128>), grid, dim3(256), 0, s, a); break;
+    case 256: hipLaunchKernelGGL((sparse_gather_kernel<256>), grid, dim3(256), 0, s, a); break;
+    case 512: hipLaunchKernelGGL((sparse_gather_kernel<512>), grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_read_codes(const ReadArgs& a, hipStream_t s) {
   if (a.n_slots <= 0) return hipSuccess;

@@ -46,7 +46,8 @@ EXPORTED = (
     "fmkv_cache_trim", "fmkv_decode_attention", "fmkv_cache_fetch", "fmkv_cache_read_codes",
     "fmkv_pool_create", "fmkv_pool_destroy", "fmkv_paged_append", "fmkv_paged_decode_attention",
     "fmkv_cache_append_projected", "fmkv_paged_append_projected",
-    "fmkv_pool_read_codes", "fmkv_set_blocks_per_split", "fmkv_cache_decode_splits",
+    "fmkv_pool_read_codes", "fmkv_set_blocks_per_split", "fmkv_set_sparse_v_gather",
+    "fmkv_cache_decode_splits",
     "fmkv_profile_enable", "fmkv_profile_collect", "fmkv_profile_collect_each",
     "fmkv_decode_step", "fmkv_paged_decode_step",
     "fmkv_prefill_step", "fmkv_paged_prefill_step", "fmkv_decode_step_noalloc",
@@ -145,6 +146,7 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
                                          ctypes.c_float, vp, i32, vp], ctypes.c_int),
         "fmkv_pool_read_codes": ([vp, vp, vp, vp], ctypes.c_int),
         "fmkv_set_blocks_per_split": ([i32], ctypes.c_int),
+        "fmkv_set_sparse_v_gather": ([i32], ctypes.c_int),
         "fmkv_cache_decode_splits": ([vp, P(i32)], ctypes.c_int),
         "fmkv_profile_enable": ([i32], ctypes.c_int),
         "fmkv_profile_collect": ([P(ctypes.c_double), P(i32)], ctypes.c_int),
@@ -214,6 +216,12 @@ def set_blocks_per_split(bps: int) -> None:
     a paged sequence's first split takes 4 x bps blocks when the grid holds
     at least four work-groups per CU."""
     _check(load_library().fmkv_set_blocks_per_split(bps))
+
+
+def set_sparse_v_gather(on: bool) -> None:
+    """Sparse-V after its statistics pass: the gather of the kept V rows
+    (True, the default) or the gated pass and the split merge (False)."""
+    _check(load_library().fmkv_set_sparse_v_gather(1 if on else 0))
 
 
 def profile_enable(max_records: int) -> None:

@@ -188,11 +188,14 @@ int fmkv_decode_step_projected(fmkv_cache* cache, const void* k_proj_bf16,
  * 12 * n_q_heads bytes of softmax statistics, P * 8 bytes of the statistics
  * pass's split (m, l), padding to 16 bytes, and 32 * n_kv_heads * blocks
  * bytes of per-block score maxima (blocks = visible 16-token blocks of the
- * call). A call needing more gets FMKV_ERR_CAPACITY and nothing is
- * launched (a 32K-token head_dim-512 layer with 16 q heads needs about
- * 4 MiB dense, 4.2 MiB with sparse-V). All calls on one GPU share that
- * scratch: calls that overlap in time on one GPU (other streams, other
- * threads) race. */
+ * call); sparse-V's gather (fmkv_set_sparse_v_gather) also takes
+ * 512 * n_kv_heads * blocks bytes of block scores and 4 * n_q_heads bytes of
+ * counters, and where those do not fit the call runs the gated pass instead.
+ * A call needing more gets FMKV_ERR_CAPACITY and nothing is launched (a
+ * 32K-token head_dim-512 layer with 16 q heads needs about 4 MiB dense,
+ * 4.2 MiB with sparse-V, 6.3 MiB with its gather). All calls on one GPU
+ * share that scratch: calls that overlap in time on one GPU (other streams,
+ * other threads) race. */
 int fmkv_decode_step_noalloc(fmkv_cache* cache, const void* k_bf16, const void* v_bf16,
                              int64_t n_tokens, const void* q_bf16, int32_t n_q_heads, float scale,
                              float sparse_v_tau, void* out, int32_t out_dtype, void* stream);
@@ -315,6 +318,16 @@ int fmkv_pool_read_codes(const fmkv_pool* pool, void* codes, void* meta, void* s
  * paged pool each sequence's first split takes 4 x that many blocks when the
  * grid holds at least four work-groups per CU. */
 int fmkv_set_blocks_per_split(int32_t blocks_per_split);
+
+/* Sparse-V (sparse_v_tau > 0) after its statistics pass: 1 (the default)
+ * reads the V rows of the kept tokens only, in one launch that writes the
+ * output; 0 runs the gated pass over the blocks that hold kept tokens and
+ * the split merge. Both give the reference's result
+ * (src/model/gemma4_attention.rs:196-234); the gather also falls back to the
+ * gated pass beyond 131072 visible tokens per sequence, or when the
+ * no-allocation scratch cannot hold its score rows. No reference
+ * counterpart (a tuning and test switch). */
+int fmkv_set_sparse_v_gather(int32_t on);
 
 /* Kernel timing (profiling aid, no reference counterpart): while enabled,
  * each decode attention call records a pair of HIP events around its split-K

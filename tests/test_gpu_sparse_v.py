@@ -3,8 +3,11 @@
 src/model/gemma4_attention.rs:196-234: at decode with tau > 0 the softmax
 weights below tau are zeroed without renormalisation before the product
 with V. The oracle (ora_attention_f64) applies the same rule to the exact
-f64 weights; the kernel compares its f32 scores with the base-2 threshold
-M + log2(tau * L) of a statistics pass. Tolerance: max-abs 2e-2, mean-abs
+f64 weights; the kernels compare their f32 scores with the base-2 threshold
+M + log2(tau * L) of a statistics pass. Each test runs on both second
+halves: the gather (one work-group per q head reads the kept tokens' V rows;
+with more than 64 candidate blocks a head's parts merge through a counter)
+and the gated pass with the split merge. Tolerance: max-abs 2e-2, mean-abs
 2e-3 (bf16 outputs: 2e-2 plus half a bf16 ulp of the exact value)."""
 import numpy as np
 import pytest
@@ -13,6 +16,15 @@ import synth
 from gpu_util import check_attention, dev_bf16, host_u16, host_u32, kv_batch
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(params=["gather", "gated"], autouse=True)
+def sparse_path(request, gpu):
+    """Every test on both second halves of sparse-V: the gather of the kept V
+    rows (the default) and the gated pass with the split merge."""
+    gpu.set_sparse_v_gather(request.param == "gather")
+    yield request.param
+    gpu.set_sparse_v_gather(True)
 
 
 def q_batch(seed, Hq, Hkv, D):
