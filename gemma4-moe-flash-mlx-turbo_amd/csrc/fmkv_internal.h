@@ -106,7 +106,7 @@ struct AttnArgs {
   // score at or above its theta.
   float* blk_max = nullptr;
   int32_t blk_stride = 0;
-  int32_t stats_new_col = 0;  // gated pass: the stats pass had a new-token column
+  int32_t stats_new_col = 0;  // gated pass, gather: the stats pass had a new-token column
   // Sparse-V: the stats pass's split (m, l), [n_seqs][part_stride][n_q_heads][2],
   // a region of its own: the stats launch writes it in place of part_ml and
   // the gated pass only reads it (the gated work-groups write their own
@@ -216,7 +216,8 @@ hipError_t launch_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads
                                    hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr);
 // Decode attention over a codebook (TurboQuant) cache, planned as
 // launch_decode_attention plans it: a decode step's new-token column, and
-// sparse-V as a statistics pass, a gated pass and the combine.
+// sparse-V as a statistics pass and the gather (or the gated pass and the
+// combine).
 hipError_t launch_cb_decode_attention(const AttnArgs& a, int n_seqs, int n_kv_heads, hipStream_t s,
                                       hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr);
 // Decode attention over a plain (bf16) cache, planned as the codebook kernel.

@@ -153,7 +153,8 @@ int fmkv_cache_append_projected(fmkv_cache* cache, const void* k_proj_bf16,
  * and sparse_v_tau == 0 this is, in every mode, a single attention launch
  * (plus the split combine) whose new-token column also appends the token;
  * with sparse_v_tau > 0 the statistics pass's new-token column appends it
- * (then the gated pass and the combine). Arguments and errors as those two
+ * (then the gather, or the gated pass and the combine: see
+ * fmkv_set_sparse_v_gather). Arguments and errors as those two
  * calls; nothing is launched or changed when validation fails. */
 int fmkv_decode_step(fmkv_cache* cache, const void* k_bf16, const void* v_bf16, int64_t n_tokens,
                      const void* q_bf16, int32_t n_q_heads, float scale, float sparse_v_tau,
