@@ -333,3 +333,47 @@ def test_sparse_v_rejects_bad_tau(gpu):
         with pytest.raises(gpu.Exception_) as e:
             cache.attention(q, 1.0, sparse_v_tau=bad)
         assert e.value.code == gpu.FMKV_ERR_INVALID_ARG
+
+
+def test_sparse_v_many_candidates_with_new_token(gpu, ora):
+    """Soft weights and tau at the median weight, so that about half the
+    weights are kept and almost every block holds one: the gather splits
+    each head's candidate blocks over several parts that merge through the
+    head's counter, and part 0 also takes the decode step's new token, whose
+    K row is a q of its group scaled so that its weight is kept. Three
+    decode steps against the oracle's gated attention."""
+    import torch
+
+    from gpu_util import fast_kv, fast_q
+
+    D, bits, Hkv, Hq, T0, steps = 256, 4, 2, 16, 4000, 3
+    cap = T0 + 16
+    cache = gpu.KVCache.new_quantized(D, bits, Hkv, capacity=cap)
+    oc = ora.OracleCache(Hkv, D, bits, 0, cap)
+    k, v = fast_kv(71, T0, Hkv, D), fast_kv(72, T0, Hkv, D)
+    cache.append(dev_bf16(k), dev_bf16(v))
+    oc.append(k, v)
+    q = fast_q(73, steps, Hq, Hkv, D)
+    v1 = fast_kv(74, steps, Hkv, D)
+    scale = 0.003
+    G = Hq // Hkv
+    for i in range(steps):
+        # the new K row of KV head h: q of head h G, scaled so that its score
+        # sits four standard deviations above that head's other scores
+        qf = synth.bf16_bits_to_f32(q[i]).astype(np.float64)
+        kd, _ = oc.dequant_kv()
+        kf = np.zeros((1, Hkv, D), np.float32)
+        for h in range(Hkv):
+            sc = scale * (kd[:, h] @ qf[h * G])
+            kf[0, h] = qf[h * G] * ((sc.mean() + 4 * sc.std()) / (scale * qf[h * G] @ qf[h * G]))
+        k1 = synth.f32_to_bf16_bits(kf)
+        oc.append(k1, v1[i:i + 1])
+        w = oc.attention_weights(q[i], scale)
+        tau = float(np.quantile(w, 0.5))
+        assert w[0, -1] >= tau and w[G, -1] >= tau, "the new token is kept"
+        assert 0.3 < np.mean(w >= tau) < 0.7, "about half the weights kept"
+        ref = oc.attention(q[i], scale, tau)
+        out = cache.decode_step(dev_bf16(k1), dev_bf16(v1[i:i + 1]), dev_bf16(q[i]), scale,
+                                sparse_v_tau=tau, dtype=torch.float32)
+        torch.cuda.synchronize()
+        check_attention(out, ref, f"step {i}")
