@@ -364,14 +364,14 @@ def single_token_append_rates() -> dict:
     return out
 
 
-def _step_fn(lib, fmkv, h, kd, vd, qd, Hq, Hkv, D, out, stream, pool):
+def _step_fn(lib, fmkv, h, kd, vd, qd, Hq, Hkv, D, out, stream, pool, tau=0.0):
     """fmkv_decode_step of one token; inputs cycle through `pool` resident rows."""
     row, qrow = Hkv * D * 2, Hq * D * 2
     kp, vp, qp, op = kd.data_ptr(), vd.data_ptr(), qd.data_ptr(), out.data_ptr()
 
     def step(i):
         t = i % pool
-        rc = lib.fmkv_decode_step(h, kp + t * row, vp + t * row, 1, qp + t * qrow, Hq, 1.0, 0.0, op,
+        rc = lib.fmkv_decode_step(h, kp + t * row, vp + t * row, 1, qp + t * qrow, Hq, 1.0, tau, op,
                                   fmkv.DTYPE_BF16, stream)
         if rc:
             raise RuntimeError(lib.fmkv_last_error().decode())
@@ -700,7 +700,9 @@ def run_c5(args) -> dict:
     """Decode-step cache traffic of a 30-layer Gemma-4-26B-A4B-shaped stack:
     25 sliding layers (ring of 1024, Hkv 8, head_dim 256, 4-bit) and 5 global
     layers (Hkv 2, head_dim 512, 8-bit) at i % 6 == 5; chunked-prefill appends
-    of 2048 tokens to 131072 positions, then decode steps of every layer."""
+    of 2048 tokens to 131072 positions, then decode steps of every layer
+    (with --sparse-v-tau, every layer's decode step gated, as the reference
+    gates every layer at decode: src/model/gemma4_attention.rs:91-93)."""
     import torch
 
     import fmkv
@@ -734,8 +736,9 @@ def run_c5(args) -> dict:
     lib = fmkv.load_library()
     stream = torch.cuda.current_stream().cuda_stream
     outs = {D: torch.empty((Hq, D), dtype=torch.bfloat16, device="cuda") for D in inputs}
+    tau = float(args.sparse_v_tau)
     fns = [_step_fn(lib, fmkv, c_._h, inputs[D][0], inputs[D][1], inputs[D][2], Hq, Hkv, D, outs[D],
-                    stream, 64) for c_, (Hkv, D, bits) in zip(caches, shapes)]
+                    stream, 64, tau) for c_, (Hkv, D, bits) in zip(caches, shapes)]
     for i in range(warm):
         for f in fns:
             f(i)
@@ -760,7 +763,8 @@ def run_c5(args) -> dict:
         "config": {"workload": "gemma4-26B-A4B-shaped 30-layer stack: 25 sliding (W 1024, Hkv 8, "
                                "head_dim 256, 4-bit) + 5 global (Hkv 2, head_dim 512, 8-bit) layers, "
                                "chunked prefill of 2048, then 1-token decode steps",
-                   "context": T0, "layers": 30, "batch": 1},
+                   "context": T0, "layers": 30, "batch": 1, "sparse_v_tau": tau,
+                   **({"sparse_v_path": args.sparse_v_path} if tau > 0.0 else {})},
         "hbm_frac_of_value": round(gbs / HBM_PEAK_GBS, 4),
         "prefill_ms": round(prefill_ms, 2),
         "prefill_tokens_per_s_per_layer": round(T0 / (prefill_ms / 1e3) * 30, 1),
@@ -960,7 +964,7 @@ def main(argv=None) -> int:
     ap.add_argument("--graph-steps", type=int, default=64,
                     help="c3: also time this many steps captured in a HIP graph (0: skip)")
     ap.add_argument("--sparse-v-tau", type=float, default=0.0,
-                    help="c3: sparse-V threshold (0: dense softmax attention; > 0: the "
+                    help="c3, c5: sparse-V threshold (0: dense softmax attention; > 0: the "
                          "statistics pass, then the second half --sparse-v-path names)")
     ap.add_argument("--sparse-v-path", choices=["gather", "gated"], default="gather",
                     help="sparse-V after the statistics pass: the gather of the kept V rows "
