@@ -867,7 +867,7 @@ void decode_attn_kernel(const uint8_t* base, const uint16_t* q, int32_t geo_len,
       // the block's largest score per head, for the gated pass's block skip
       const int64_t rb = b - geo.blk_lo;
       if (half == 0 && j == 0 && hi && rb < a.blk_stride)
-        a.blk_max[(blk_row + rb) * 8 + head] = col_valid ? mb : -INFINITY;
+        a.blk_max[blk_max_at(a, blk_row, rb, head)] = col_valid ? mb : -INFINITY;
     }
     // The reference max moves only when a score exceeds it by more than
     // kRescaleSlack (base 2): O, l and the bias sums are then rescaled, which

@@ -281,6 +281,13 @@ __device__ inline BlockList gated_block_list(const AttnArgs& a, const float (&th
   return BlockList{mask, 64, nb};
 }
 
+// Index of the block maximum of (sequence and KV head at blk_row, block rb,
+// q head of the group): block-major for the gated pass, head-major for the
+// gather.
+__device__ inline int64_t blk_max_at(const AttnArgs& a, int64_t blk_row, int64_t rb, int head) {
+  return a.blk_scores ? blk_row * 8 + (int64_t)head * a.blk_stride + rb : (blk_row + rb) * 8 + head;
+}
+
 // Sparse-V statistics pass, for the gather: the block's scores of the
 // lane's head (tokens 4j .. 4j + 3) when the block may hold a kept token. A
 // weight 2^(s - M) / L reaches tau only if s >= M + log2(tau) (L >= 1), and a

@@ -532,7 +532,7 @@ void cb_decode_kernel(AttnArgs a) {
       // the block's largest score per head, for the gated pass's block skip
       const int64_t rb = b - geo.blk_lo;
       if (half == 0 && j == 0 && hi && rb < a.blk_stride)
-        a.blk_max[(blk_row + rb) * 8 + head] = col_valid ? mb : -INFINITY;
+        a.blk_max[blk_max_at(a, blk_row, rb, head)] = col_valid ? mb : -INFINITY;
     }
     const float m_new = fmaxf(m_run, mb);
     if (__any(m_new > m_run + kRescaleSlack)) {

@@ -101,9 +101,12 @@ struct AttnArgs {
   float* tau_stats;
   // Sparse-V: the stats pass's largest base-2 score per (sequence, KV head,
   // block) and q head of the group, [n_seqs][n_kv_heads][blk_stride][8]
-  // (-inf for heads beyond the group; block index relative to the first
-  // visible block); the gated pass skips the blocks in which no head has a
-  // score at or above its theta.
+  // block-major for the gated pass, which reads a block's 8 together and
+  // skips the blocks in which no head has a score at or above its theta,
+  // and [n_seqs][n_kv_heads][8][blk_stride] head-major for the gather
+  // (blk_scores set), whose work-groups each read one head's row (-inf for
+  // heads beyond the group; block index relative to the first visible
+  // block).
   float* blk_max = nullptr;
   int32_t blk_stride = 0;
   int32_t stats_new_col = 0;  // gated pass, gather: the stats pass had a new-token column
@@ -227,7 +230,7 @@ hipError_t launch_plain_decode_attention(const AttnArgs& a, int n_seqs, int n_kv
 // Sparse-V after the statistics pass: the kept weights of every q head and
 // the V rows they weigh, straight to out (fmkv_readback.hip).
 // At most kGatherMaxRows visible head-blocks per sequence.
-constexpr int kGatherMaxRows = 8192;
+constexpr int kGatherMaxRows = 16384;
 hipError_t launch_sparse_gather(const AttnArgs& a, int n_seqs, hipStream_t s);
 // The split merge of every decode kernel: out = LSE merge of the partials.
 hipError_t launch_combine(const AttnArgs& a, int n_seqs, hipStream_t s);

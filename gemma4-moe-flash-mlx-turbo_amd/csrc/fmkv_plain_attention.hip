@@ -311,7 +311,7 @@ __global__ __launch_bounds__(kPlThreads) void plain_decode_kernel(AttnArgs a) {
       // (every wave holds the same scores; wave 0 writes them)
       const int64_t rb = b - geo.blk_lo;
       if (wave == 0 && j == 0 && hi_col && rb < a.blk_stride)
-        a.blk_max[(blk_row + rb) * 8 + head] = head < G ? mb : -INFINITY;
+        a.blk_max[blk_max_at(a, blk_row, rb, head)] = head < G ? mb : -INFINITY;
     }
     const float m_new = fmaxf(m_run, mb);
     if (__any(m_new > m_run + kRescaleSlack)) {

@@ -159,19 +159,97 @@ __global__ __launch_bounds__(64) void fetch_kernel(FetchArgs a) {
   }
 }
 
-// V row of the token in slot t of head-block `blk`, dim d, in the rotated
-// domain the attention kernels read (plain caches: the stored row): affine
-// code * scale + bias, codebook centroid * norm / sqrt(D), plain bf16.
-__device__ inline float v_value(const uint8_t* blk, const BlockLayout& L, int t, int d, float c) {
-  const uint32_t code = stored_code(blk, L, 1, t, d);
-  if (L.mode == kAffine) {
-    const uint32_t sb = *reinterpret_cast<const uint32_t*>(blk + L.v_meta + scale_pos(d / kGroup, t));
-    return fmaf((float)code, f16_bits_to_f32(sb), f16_bits_to_f32(sb >> 16));
+// acc[e] += w_k V[slot_k][tid + e NT] over the kept list (k = 0 .. n-1, in
+// list order), V in the rotated domain the attention kernels read (plain
+// caches: the stored row): affine code * scale + bias, codebook
+// centroid * c * norm (c = 1/sqrt(D), the centroids in LDS), plain bf16. One
+// instance per cache mode and width, so that the words of a batch of tokens
+// are all loaded before the first is decoded: a batch of kept rows costs one
+// memory round trip (with the mode switched per channel, every load waits
+// on its own). Batches of 16 while more than 4 tokens remain, then of 4 (a
+// short list pays for no padding). Threads past D load channel D-1 and
+// leave acc alone.
+template <int MODE, int BITS, int D, int NT, int kUnroll, typename BlockOf>
+__device__ inline void accumulate_batch(const int* kept_slot, const float* kept_w, int k0, int n,
+                                        const BlockLayout& L, const float* cent, float c,
+                                        const BlockOf& block_of, float (&acc)[(D + NT - 1) / NT]) {
+  constexpr int ND = (D + NT - 1) / NT;
+  constexpr int NW = MODE == kCodebook && BITS == 3 ? 2 : 1;  // 3-bit codes straddle words
+  constexpr uint32_t mask = MODE == kPlain ? 0xffffu : (1u << BITS) - 1u;
+  const int tid = threadIdx.x;
+  {
+    uint32_t word[kUnroll][ND][NW];
+    uint32_t meta[kUnroll][ND];
+    uint32_t nrm[kUnroll];
+    int tok[kUnroll];
+    float w[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+      const bool ok = k0 + u < n;
+      const int k = ok ? k0 + u : n - 1;
+      const int slot = kept_slot[k];
+      w[u] = ok ? kept_w[k] : 0.0f;
+      const uint8_t* blk = block_of(slot / kBlockTokens);
+      const int t = slot % kBlockTokens;
+      tok[u] = t;
+      nrm[u] = MODE == kCodebook ? *reinterpret_cast<const uint16_t*>(blk + L.v_meta + t * 2) : 0u;
+#pragma unroll
+      for (int e = 0; e < ND; e++) {
+        const int d = tid + e * NT < D ? tid + e * NT : D - 1;
+        if (MODE == kAffine) {
+          int64_t off;
+          int sh;
+          v_code_pos(BITS, t, d, &off, &sh);
+          word[u][e][0] = *reinterpret_cast<const uint32_t*>(blk + L.v_codes + off);
+          meta[u][e] = *reinterpret_cast<const uint32_t*>(blk + L.v_meta + scale_pos(d / kGroup, t));
+        } else if (MODE == kCodebook) {
+          // the word after a 3-bit code's first is in the block (the V norms
+          // follow the V codes)
+          const uint32_t* region = reinterpret_cast<const uint32_t*>(blk + L.v_codes);
+          const int64_t wi = cb_v_bit(BITS, t, d) >> 5;
+#pragma unroll
+          for (int i = 0; i < NW; i++) word[u][e][i] = region[wi + i];
+        } else {
+          word[u][e][0] = *reinterpret_cast<const uint16_t*>(blk + L.v_codes + plain_v_pos(t, d));
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+      const int t = tok[u];
+#pragma unroll
+      for (int e = 0; e < ND; e++) {
+        const int d = tid + e * NT < D ? tid + e * NT : D - 1;
+        float v;
+        if (MODE == kAffine) {
+          int64_t off;
+          int sh;
+          v_code_pos(BITS, t, d, &off, &sh);
+          v = fmaf((float)((word[u][e][0] >> sh) & mask), f16_bits_to_f32(meta[u][e]),
+                   f16_bits_to_f32(meta[u][e] >> 16));
+        } else if (MODE == kCodebook) {
+          const int sh = (int)(cb_v_bit(BITS, t, d) & 31);
+          uint32_t x = word[u][e][0] >> sh;
+          if (NW == 2 && sh + BITS > 32) x |= word[u][e][NW - 1] << (32 - sh);
+          v = (cent[x & mask] * c) * f16_bits_to_f32(nrm[u]);
+        } else {
+          v = __uint_as_float(word[u][e][0] << 16);
+        }
+        acc[e] = fmaf(w[u], k0 + u < n ? v : 0.0f, acc[e]);
+      }
+    }
   }
-  if (L.mode == kCodebook)
-    return (centroid(L.bits, code) * c) *
-           f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + L.v_meta + t * 2));
-  return __uint_as_float(code << 16);
+}
+
+template <int MODE, int BITS, int D, int NT, typename BlockOf>
+__device__ inline void accumulate_kept(const int* kept_slot, const float* kept_w, int n,
+                                       const BlockLayout& L, const float* cent, float c,
+                                       const BlockOf& block_of, float (&acc)[(D + NT - 1) / NT]) {
+  int k0 = 0;
+  for (; n - k0 > 4; k0 += 16)
+    accumulate_batch<MODE, BITS, D, NT, 16>(kept_slot, kept_w, k0, n, L, cent, c, block_of, acc);
+  for (; k0 < n; k0 += 4)
+    accumulate_batch<MODE, BITS, D, NT, 4>(kept_slot, kept_w, k0, n, L, cent, c, block_of, acc);
 }
 
 // Exclusive prefix count over the work-group: each thread holds `n` items
@@ -237,6 +315,7 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
   __shared__ int cnt[NT / 64];
   __shared__ float red[2][NT / 64];
   __shared__ float xs[D];
+  __shared__ float cent[16];
   __shared__ int last_s;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -255,13 +334,14 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
 
   // 1. the loads of the block maxima (rows k NT + tid), the statistics
   // (partials i NT + tid) and the new token's score, together
+  if (tid < 16) cent[tid] = L.mode == kCodebook && tid < (1 << L.bits) ? centroid(L.bits, tid) : 0.0f;
   const int kmax = (int)((nrows + NT - 1) / NT);  // <= RPT
   float bm[RPT];
 #pragma unroll
   for (int k = 0; k < RPT; k++) {
     const int64_t rb = (int64_t)k * NT + tid;
     bm[k] = -INFINITY;
-    if (k < kmax && rb < nrows) bm[k] = a.blk_max[(blk_row + rb) * 8 + hl];
+    if (k < kmax && rb < nrows) bm[k] = a.blk_max[blk_row * 8 + (int64_t)hl * a.blk_stride + rb];
   }
   const int n_stat = n_splits + a.stats_new_col;
   const int64_t rbase = (int64_t)seq * a.part_stride * nqh + h;
@@ -303,13 +383,14 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
   const float inv_l = Ls > 0.0f ? 1.0f / Ls : 0.0f;
 
   // 2. candidate rows
-  uint32_t flags = 0;
+  static_assert(RPT <= 64, "one flag word per thread");
+  uint64_t flags = 0;
 #pragma unroll
-  for (int k = 0; k < RPT; k++) flags |= (k < kmax && bm[k] >= theta ? 1u : 0u) << k;
+  for (int k = 0; k < RPT; k++) flags |= (k < kmax && bm[k] >= theta ? 1ull : 0ull) << k;
   int nc;
-  int pos = wg_exclusive_count<NT>(__builtin_popcount(flags), cnt, &nc);
+  int pos = wg_exclusive_count<NT>(__builtin_popcountll(flags), cnt, &nc);
   while (flags) {
-    const int k = __builtin_ctz(flags);
+    const int k = __builtin_ctzll(flags);
     flags &= flags - 1;
     cand[pos++] = k * NT + tid;
   }
@@ -372,17 +453,20 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
       nt_pending = false;
     }
     __syncthreads();
-#pragma unroll 4
-    for (int k = 0; k < n; k++) {
-      const int slot = kept_slot[k];
-      const float w = kept_w[k];
-      const uint8_t* blk = block_of(slot / kBlockTokens);
-      const int t = slot % kBlockTokens;
-#pragma unroll
-      for (int e = 0; e < ND; e++) {
-        const int d = tid + e * NT;
-        if (d < D) acc[e] = fmaf(w, v_value(blk, L, t, d, a.c), acc[e]);
-      }
+    if (L.mode == kAffine) {
+      if (L.bits == 8)
+        accumulate_kept<kAffine, 8, D, NT>(kept_slot, kept_w, n, L, cent, a.c, block_of, acc);
+      else
+        accumulate_kept<kAffine, 4, D, NT>(kept_slot, kept_w, n, L, cent, a.c, block_of, acc);
+    } else if (L.mode == kCodebook) {
+      if (L.bits == 2)
+        accumulate_kept<kCodebook, 2, D, NT>(kept_slot, kept_w, n, L, cent, a.c, block_of, acc);
+      else if (L.bits == 3)
+        accumulate_kept<kCodebook, 3, D, NT>(kept_slot, kept_w, n, L, cent, a.c, block_of, acc);
+      else
+        accumulate_kept<kCodebook, 4, D, NT>(kept_slot, kept_w, n, L, cent, a.c, block_of, acc);
+    } else {
+      accumulate_kept<kPlain, 16, D, NT>(kept_slot, kept_w, n, L, cent, a.c, block_of, acc);
     }
     __syncthreads();
   }

@@ -325,7 +325,7 @@ int fmkv_set_blocks_per_split(int32_t blocks_per_split);
  * output; 0 runs the gated pass over the blocks that hold kept tokens and
  * the split merge. Both give the reference's result
  * (src/model/gemma4_attention.rs:196-234); the gather also falls back to the
- * gated pass beyond 131072 visible tokens per sequence, or when the
+ * gated pass beyond 262144 visible tokens per sequence, or when the
  * no-allocation scratch cannot hold its score rows. No reference
  * counterpart (a tuning and test switch). */
 int fmkv_set_sparse_v_gather(int32_t on);

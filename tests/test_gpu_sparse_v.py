@@ -377,3 +377,32 @@ def test_sparse_v_many_candidates_with_new_token(gpu, ora):
                                 sparse_v_tau=tau, dtype=torch.float32)
         torch.cuda.synchronize()
         check_attention(out, ref, f"step {i}")
+
+
+def test_sparse_v_beyond_8192_blocks(gpu, ora):
+    """140000 visible tokens (8750 blocks of 16): each gather thread scans
+    more than 32 block rows, so candidates sit in both halves of its row
+    flags. Soft weights with tau at the 99.9th percentile (kept tokens spread
+    over the whole context) and a peaked step at tau 1e-3, against the
+    oracle."""
+    import torch
+
+    from gpu_util import fast_kv, fast_q
+
+    D, bits, Hkv, Hq, T = 128, 4, 1, 4, 140000
+    cache = gpu.KVCache.new_quantized(D, bits, Hkv, capacity=T + 16)
+    oc = ora.OracleCache(Hkv, D, bits, 0, T + 16)
+    k, v = fast_kv(81, T, Hkv, D), fast_kv(82, T, Hkv, D)
+    cache.append(dev_bf16(k), dev_bf16(v))
+    oc.append(k, v)
+    q = fast_q(83, 1, Hq, Hkv, D)[0]
+    for scale in (0.003, 1.0):
+        w = oc.attention_weights(q, scale)
+        tau = float(np.quantile(w, 0.999)) if scale < 1.0 else 1e-3
+        kept = np.nonzero(w >= tau)[1]
+        if scale < 1.0:
+            assert kept.min() < 16 * 8192 <= kept.max(), "kept tokens on both sides of row 8192"
+        ref = oc.attention(q, scale, tau)
+        out = cache.attention(dev_bf16(q), scale, sparse_v_tau=tau, dtype=torch.float32)
+        torch.cuda.synchronize()
+        check_attention(out, ref, f"scale={scale} tau={tau:.3g}")
