@@ -480,6 +480,7 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
                                             inv_tau < 1e15 ? (int64_t)inv_tau : INT64_MAX);
     a->gather_parts = (int32_t)std::clamp<int64_t>((bound + 511) / 512, 1,
                                                    std::min<int64_t>(a->part_stride, 16));
+    a->gather_rows = (int32_t)std::max<int64_t>(nblk, 1);
   }
   return FMKV_OK;
 }

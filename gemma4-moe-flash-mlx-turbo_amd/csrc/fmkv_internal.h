@@ -123,6 +123,7 @@ struct AttnArgs {
   float* blk_scores = nullptr;
   int32_t* sv_count = nullptr;
   int32_t gather_parts = 0;  // work-groups per (sequence, q head) of the gather
+  int32_t gather_rows = 0;   // the most visible head-blocks of a sequence (<= kGatherMaxRows)
 };
 
 // Prefill (chunked) attention: n_q queries at positions p0 .. p0 + n_q - 1,

@@ -300,16 +300,17 @@ __device__ inline int wg_exclusive_count(int n, int* cnt, int* total) {
 // block maxima with the statistics, scores, V rows), each a coalesced sweep
 // (thread tid takes rows and items k NT + tid); the lists are in thread-major
 // order (thread, then k), a fixed order, so the sums are deterministic.
-// Blocks: at most kGatherMaxRows visible head-blocks per sequence.
-template <int D>
+// Blocks: at most RPT * 256 visible head-blocks per sequence; the launch
+// takes the smallest instance that holds the call's rows.
+template <int D, int RPT>
 __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
   constexpr int NT = 256, E = D / 64, ND = (D + NT - 1) / NT;
-  constexpr int RPT = kGatherMaxRows / NT;  // block rows per thread
+  static_assert(RPT * NT <= kGatherMaxRows, "block rows per thread");
   constexpr int kRound = 64;                // candidates per score round
   constexpr int IPT = kRound * kBlockTokens / NT;  // score items per thread
   constexpr int SPT = 2;                    // statistics per thread per load round
   constexpr int kSoloRows = 64;
-  __shared__ int cand[kGatherMaxRows];
+  __shared__ int cand[RPT * NT];
   __shared__ int kept_slot[kRound * kBlockTokens + 1];
   __shared__ float kept_w[kRound * kBlockTokens + 1];
   __shared__ int cnt[NT / 64];
@@ -330,11 +331,15 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
   const int n_splits = n_splits_for(geo, a.bps0, a.bps, a.max_splits, a.skew_p);
   int64_t nrows = geo.blk_hi - geo.blk_lo;
   if (nrows > a.blk_stride) nrows = a.blk_stride;  // (the host plans rows <= blk_stride)
+  if (nrows > RPT * NT) nrows = RPT * NT;          // (and <= gather_rows <= RPT NT)
   const int64_t blk_row = ((int64_t)seq * a.st.n_kv_heads + kvh) * a.blk_stride;
 
   // 1. the loads of the block maxima (rows k NT + tid), the statistics
   // (partials i NT + tid) and the new token's score, together
-  if (tid < 16) cent[tid] = L.mode == kCodebook && tid < (1 << L.bits) ? centroid(L.bits, tid) : 0.0f;
+  // (the centroid reaches LDS after the loads below have been waited for:
+  // written here, its load would be waited for alone, a round trip of its own)
+  const float cent_v =
+      L.mode == kCodebook && tid < 16 && tid < (1 << L.bits) ? centroid(L.bits, tid) : 0.0f;
   const int kmax = (int)((nrows + NT - 1) / NT);  // <= RPT
   float bm[RPT];
 #pragma unroll
@@ -394,6 +399,7 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
     flags &= flags - 1;
     cand[pos++] = k * NT + tid;
   }
+  if (tid < 16) cent[tid] = cent_v;
   __syncthreads();
   const bool solo = nc <= kSoloRows;
   if (solo && part != 0) return;
@@ -537,18 +543,41 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
 
 }  // namespace
 
+// The gather instance for the call's rows: RPT block maxima per thread are
+// loaded (unrolled, predicated) and held in registers and RPT * 256 list
+// entries in LDS, and each row per thread the instance holds beyond the
+// call's costs time. Measured at a 32K step (2049 rows), sparse-V tau 1e-3:
+// 64 rows per thread 20.95 us, 32 19.6 us, 16 18.3 us, 9 18.0 us; the C5
+// stack's 1024-slot rings (64 rows) gained 0.35 us a layer from 16 to 1.
+// Instances: 256 rows (a ring of up to 4096 slots), 2304 (a 36K context),
+// 4096, 8192 and 16384.
+template <int D>
+hipError_t launch_gather_rows(const AttnArgs& a, dim3 grid, hipStream_t s) {
+  if (a.gather_rows <= 1 * 256)
+    hipLaunchKernelGGL((sparse_gather_kernel<D, 1>), grid, dim3(256), 0, s, a);
+  else if (a.gather_rows <= 9 * 256)
+    hipLaunchKernelGGL((sparse_gather_kernel<D, 9>), grid, dim3(256), 0, s, a);
+  else if (a.gather_rows <= 16 * 256)
+    hipLaunchKernelGGL((sparse_gather_kernel<D, 16>), grid, dim3(256), 0, s, a);
+  else if (a.gather_rows <= 32 * 256)
+    hipLaunchKernelGGL((sparse_gather_kernel<D, 32>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((sparse_gather_kernel<D, 64>), grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_sparse_gather(const AttnArgs& a, int n_seqs, hipStream_t s) {
   if (!a.blk_scores || !a.sv_count || !a.blk_max || !a.stat_ml || !a.part_o || a.group < 1 ||
-      a.group > 8 || a.gather_parts < 1 || a.gather_parts > a.part_stride)
+      a.group > 8 || a.gather_parts < 1 || a.gather_parts > a.part_stride ||
+      a.gather_rows < 1 || a.gather_rows > kGatherMaxRows)
     return hipErrorInvalidValue;
   dim3 grid((unsigned)a.n_q_heads, (unsigned)n_seqs, (unsigned)a.gather_parts);
   switch (a.st.layout.head_dim) {
-    case 128: hipLaunchKernelGGL((sparse_gather_kernel<128>), grid, dim3(256), 0, s, a); break;
-    case 256: hipLaunchKernelGGL((sparse_gather_kernel<256>), grid, dim3(256), 0, s, a); break;
-    case 512: hipLaunchKernelGGL((sparse_gather_kernel<512>), grid, dim3(256), 0, s, a); break;
+    case 128: return launch_gather_rows<128>(a, grid, s);
+    case 256: return launch_gather_rows<256>(a, grid, s);
+    case 512: return launch_gather_rows<512>(a, grid, s);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 hipError_t launch_read_codes(const ReadArgs& a, hipStream_t s) {
