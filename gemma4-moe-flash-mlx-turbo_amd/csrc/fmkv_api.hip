@@ -472,13 +472,13 @@ int prepare_attention_common(Owner* o, const fmkv::Store& st, int32_t n_seqs, in
   a->blk_scores = gather ? ws + score_off : nullptr;
   a->sv_count = gather ? reinterpret_cast<int32_t*>(ws + cnt_off) : nullptr;
   if (gather) {
-    // parts per (sequence, q head): a part's kept tokens are at most
-    // min(visible tokens, 1 / tau) / parts when they spread evenly over the
-    // candidate blocks; 512 a part, at most 16 parts
+    // parts per (sequence, q head): the kept tokens, and so the candidate
+    // blocks, are at most min(visible tokens, 1 / tau); one part per 128 of
+    // them, at most 64 (the gather uses one per 16 candidate blocks)
     const double inv_tau = std::ceil(1.0 / (double)tau);
     const int64_t bound = std::min<int64_t>(nblk * fmkv::kBlockTokens,
                                             inv_tau < 1e15 ? (int64_t)inv_tau : INT64_MAX);
-    a->gather_parts = (int32_t)std::clamp<int64_t>((bound + 511) / 512, 1,
+    a->gather_parts = (int32_t)std::clamp<int64_t>((bound + 127) / 128, 1,
                                                    std::min<int64_t>(a->part_stride, 16));
     a->gather_rows = (int32_t)std::max<int64_t>(nblk, 1);
   }

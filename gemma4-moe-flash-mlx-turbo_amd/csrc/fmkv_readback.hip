@@ -292,11 +292,12 @@ __device__ inline int wg_exclusive_count(int n, int* cnt, int* total) {
 //  4. acc[d] = sum of w * V[token][d] (rotated domain);
 //  5. out = acc R^T = c * FWHT(acc o s) (plain caches: out = acc).
 // With at most kSoloRows candidates part 0 takes them all and writes out,
-// and the other parts return. Otherwise part p takes the candidates
-// [p nc / n_parts, (p + 1) nc / n_parts), stores acc in its partial row,
-// and the last part to count itself on the (sequence, q head)'s counter
-// (zeroed by the statistics pass) sums the rows in part order and writes
-// out. Every step's loads are issued together (one memory round trip each:
+// and the other parts return. Otherwise the candidates go to
+// n_act = min(n_parts, ceil(nc / kRowsPerPart)) parts (the rest return):
+// part p takes [p nc / n_act, (p + 1) nc / n_act), stores acc in its
+// partial row, and the last part to count itself on the (sequence, q
+// head)'s counter (zeroed by the statistics pass) sums the rows in part
+// order and writes out. Every step's loads are issued together (one memory round trip each:
 // block maxima with the statistics, scores, V rows), each a coalesced sweep
 // (thread tid takes rows and items k NT + tid); the lists are in thread-major
 // order (thread, then k), a fixed order, so the sums are deterministic.
@@ -310,6 +311,7 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
   constexpr int IPT = kRound * kBlockTokens / NT;  // score items per thread
   constexpr int SPT = 2;                    // statistics per thread per load round
   constexpr int kSoloRows = 64;
+  constexpr int kRowsPerPart = 16;
   __shared__ int cand[RPT * NT];
   __shared__ int kept_slot[kRound * kBlockTokens + 1];
   __shared__ float kept_w[kRound * kBlockTokens + 1];
@@ -402,9 +404,10 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
   if (tid < 16) cent[tid] = cent_v;
   __syncthreads();
   const bool solo = nc <= kSoloRows;
-  if (solo && part != 0) return;
-  const int c0 = solo ? 0 : (int)((int64_t)part * nc / n_parts);
-  const int c1 = solo ? nc : (int)((int64_t)(part + 1) * nc / n_parts);
+  const int n_act = solo ? 1 : min(n_parts, (nc + kRowsPerPart - 1) / kRowsPerPart);
+  if (part >= n_act) return;
+  const int c0 = solo ? 0 : (int)((int64_t)part * nc / n_act);
+  const int c1 = solo ? nc : (int)((int64_t)(part + 1) * nc / n_act);
 
   // block address of logical slot block lb
   const uint8_t* hbase = a.st.base + (int64_t)kvh * a.st.head_stride;
@@ -480,27 +483,44 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
   // 5. merge (several parts) and the inverse rotation
   float* const orow = a.part_o + (((int64_t)seq * a.part_stride + part) * nqh + h) * D;
   if (!solo) {
+    // the row through LDS, so that one wave stores it, releases it (an L2
+    // write-back at agent scope, one per work-group rather than per wave)
+    // and counts the part
 #pragma unroll
     for (int e = 0; e < ND; e++) {
       const int d = tid + e * NT;
-      if (d < D) orow[d] = acc[e];
+      if (d < D) xs[d] = acc[e];
     }
-    __threadfence();  // release the row (agent scope)
     __syncthreads();
-    if (tid == 0) last_s = atomicAdd(&a.sv_count[(int64_t)seq * nqh + h], 1) == n_parts - 1;
+    if (wave == 0) {
+      for (int d = lane; d < D; d += 64) orow[d] = xs[d];
+      __threadfence();  // release the row (agent scope)
+      if (lane == 0) last_s = atomicAdd(&a.sv_count[(int64_t)seq * nqh + h], 1) == n_act - 1;
+    }
     __syncthreads();
     if (!last_s) return;
     __threadfence();  // acquire the other parts' rows
+    // plain loads after the acquire, 16 parts' rows at a time, all issued
+    // before the first is added (atomic loads waited one by one); the sum in
+    // part order (rows past n_act read row n_act - 1 and add nothing)
     const float* prow0 = a.part_o + ((int64_t)seq * a.part_stride * nqh + h) * D;
 #pragma unroll
-    for (int e = 0; e < ND; e++) {
-      const int d = tid + e * NT;
-      float sum = 0.0f;
-      if (d < D)
-        for (int q = 0; q < n_parts; q++) sum += __hip_atomic_load(prow0 + (int64_t)q * nqh * D + d,
-                                                                     __ATOMIC_RELAXED,
-                                                                     __HIP_MEMORY_SCOPE_AGENT);
-      acc[e] = sum;
+    for (int e = 0; e < ND; e++) acc[e] = 0.0f;
+    for (int q0 = 0; q0 < n_act; q0 += 16) {
+      float v[16][ND];
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const int64_t q = q0 + i < n_act ? q0 + i : n_act - 1;
+#pragma unroll
+        for (int e = 0; e < ND; e++) {
+          const int d = tid + e * NT < D ? tid + e * NT : D - 1;
+          v[i][e] = prow0[q * nqh * D + d];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 16; i++)
+#pragma unroll
+        for (int e = 0; e < ND; e++) acc[e] += q0 + i < n_act ? v[i][e] : 0.0f;
     }
   }
   const int64_t o_idx = ((int64_t)seq * nqh + h) * D;
