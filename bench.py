@@ -76,8 +76,8 @@ def run_c3(args) -> dict:
     mode = fmkv.MODE_CODEBOOK if cb else fmkv.MODE_PLAIN if plain else fmkv.MODE_AFFINE
     per_tok = bytes_per_token_head(D, bits, cb, plain)
     # steps: warmup, timed, two event-timed passes, then warmup + timed
-    # projected steps
-    n_dec = 2 * args.warmup + 4 * args.steps + 1
+    # projected steps and warmup + timed sparse-V steps
+    n_dec = 3 * args.warmup + 5 * args.steps + 1
     cache = fmkv.KVCache.new_quantized(D, bits, Hkv, capacity=T0 + n_dec + args.graph_steps + 16,
                                        mode=mode)
 
@@ -267,6 +267,30 @@ def run_c3(args) -> dict:
         proj_us = (time.perf_counter() - t0) / args.steps * 1e6
         log(f"projected step (prologue in the new-token column): {proj_us:.1f} us")
 
+    # The same decode step with sparse-V at tau 1e-3 (the reference's gate,
+    # src/model/gemma4_attention.rs:196-234: the statistics pass over the
+    # keys, then the gather of the kept tokens' V rows) on the same cache.
+    # Informational, eager; the headline value above is the dense step.
+    sv_us = None
+    if tau == 0.0:
+        def sv_step():
+            nonlocal i
+            rc = lib.fmkv_decode_step(h, kp[i], vp[i], 1, qp[i], Hq, 1.0, 1e-3, outp,
+                                      fmkv.DTYPE_BF16, stream)
+            if rc:
+                raise RuntimeError(lib.fmkv_last_error().decode())
+            i += 1
+
+        for _ in range(args.warmup):
+            sv_step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            sv_step()
+        torch.cuda.synchronize()
+        sv_us = (time.perf_counter() - t0) / args.steps * 1e6
+        log(f"sparse-V step (tau 1e-3, gather): {sv_us:.1f} us against {ms_per_step * 1e3:.1f} us dense")
+
     copy_gbs = device_copy_gbs()
     log(f"device copy (256 MiB, read + write): {copy_gbs:.0f} GB/s")
     res = {
@@ -298,6 +322,9 @@ def run_c3(args) -> dict:
                                     None if prologue_tps is None else round(prologue_tps, 1),
                                 **single_token_append_rates()},
         "graph_step_us": None if graph_us is None else round(graph_us, 3),
+        "sparse_v_step_us": None if sv_us is None else {
+            "tau": 1e-3, "path": "gather", "us": round(sv_us, 2),
+            "dense_us": round(ms_per_step * 1e3, 2)},
         "projected_step_us": None if proj_us is None else round(proj_us, 3),
         "roofline": {
             "bound": "hbm",
