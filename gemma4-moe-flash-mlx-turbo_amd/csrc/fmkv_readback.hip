@@ -291,16 +291,17 @@ __device__ inline int wg_exclusive_count(int n, int* cnt, int* total) {
 //     score (its column's m) reaches theta;
 //  4. acc[d] = sum of w * V[token][d] (rotated domain);
 //  5. out = acc R^T = c * FWHT(acc o s) (plain caches: out = acc).
-// With at most kSoloRows candidates part 0 takes them all and writes out,
-// and the other parts return. Otherwise the candidates go to
-// n_act = min(n_parts, ceil(nc / kRowsPerPart)) parts (the rest return):
-// part p takes [p nc / n_act, (p + 1) nc / n_act), stores acc in its
-// partial row, and the last part to count itself on the (sequence, q
-// head)'s counter (zeroed by the statistics pass) sums the rows in part
-// order and writes out. Every step's loads are issued together (one memory round trip each:
-// block maxima with the statistics, scores, V rows), each a coalesced sweep
-// (thread tid takes rows and items k NT + tid); the lists are in thread-major
-// order (thread, then k), a fixed order, so the sums are deterministic.
+// With at most kSoloRows candidates (or one part launched) part 0 takes
+// them all and writes out, and the other parts return. Otherwise the
+// candidates go to n_act = min(n_parts, ceil(nc / kRowsPerPart)) parts (the
+// rest return): part p takes [p nc / n_act, (p + 1) nc / n_act), stores acc
+// in its partial row, and the last part to count itself on the (sequence,
+// q head)'s counter (zeroed by the statistics pass) sums the rows in part
+// order and writes out. Every step's loads are issued together (one memory
+// round trip each: block maxima with the statistics, scores, V rows), each
+// a coalesced sweep (thread tid takes rows and items k NT + tid); the lists
+// are in thread-major order (thread, then k), a fixed order, so the sums
+// are deterministic.
 // Blocks: at most RPT * 256 visible head-blocks per sequence; the launch
 // takes the smallest instance that holds the call's rows.
 template <int D, int RPT>
@@ -403,8 +404,8 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
   }
   if (tid < 16) cent[tid] = cent_v;
   __syncthreads();
-  const bool solo = nc <= kSoloRows;
-  const int n_act = solo ? 1 : min(n_parts, (nc + kRowsPerPart - 1) / kRowsPerPart);
+  const int n_act = nc <= kSoloRows ? 1 : min(n_parts, (nc + kRowsPerPart - 1) / kRowsPerPart);
+  const bool solo = n_act == 1;  // part 0 takes every candidate, no merge
   if (part >= n_act) return;
   const int c0 = solo ? 0 : (int)((int64_t)part * nc / n_act);
   const int c1 = solo ? nc : (int)((int64_t)(part + 1) * nc / n_act);
