@@ -406,3 +406,32 @@ def test_sparse_v_beyond_8192_blocks(gpu, ora):
         out = cache.attention(dev_bf16(q), scale, sparse_v_tau=tau, dtype=torch.float32)
         torch.cuda.synchronize()
         check_attention(out, ref, f"scale={scale} tau={tau:.3g}")
+
+
+@pytest.mark.parametrize("T", [4096, 4112, 40000, 70000])
+def test_sparse_v_gather_row_instances(gpu, ora, T):
+    """Contexts at the gather's instance boundaries (256 and 257 block rows)
+    and inside the 4096- and 8192-row instances (2500 and 4375 rows): a soft
+    step with tau at the 99.9th percentile (kept tokens spread over every
+    row) and a peaked one at tau 1e-3, against the oracle."""
+    import torch
+
+    from gpu_util import fast_kv, fast_q
+
+    D, bits, Hkv, Hq = 128, 4, 1, 4
+    cache = gpu.KVCache.new_quantized(D, bits, Hkv, capacity=T + 16)
+    oc = ora.OracleCache(Hkv, D, bits, 0, T + 16)
+    k, v = fast_kv(91 + T, T, Hkv, D), fast_kv(92 + T, T, Hkv, D)
+    cache.append(dev_bf16(k), dev_bf16(v))
+    oc.append(k, v)
+    q = fast_q(93 + T, 1, Hq, Hkv, D)[0]
+    for scale in (0.003, 1.0):
+        w = oc.attention_weights(q, scale)
+        tau = float(np.quantile(w, 0.999)) if scale < 1.0 else 1e-3
+        if scale < 1.0:
+            kept = np.nonzero(w >= tau)[1]
+            assert kept.max() >= T - T // 8, "kept tokens reach the last rows"
+        ref = oc.attention(q, scale, tau)
+        out = cache.attention(dev_bf16(q), scale, sparse_v_tau=tau, dtype=torch.float32)
+        torch.cuda.synchronize()
+        check_attention(out, ref, f"T={T} scale={scale} tau={tau:.3g}")
