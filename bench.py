@@ -535,12 +535,14 @@ def run_c4(args) -> dict:
     stream = torch.cuda.current_stream().cuda_stream
     row, qrow = n_seqs * Hkv * D * 2, n_seqs * Hq * D * 2
 
+    tau = float(args.sparse_v_tau)
+
     def step(i):
         mx = int(lens.max()) + i + 1
         rc = lib.fmkv_paged_decode_step(pool._h, kd.data_ptr() + i * row, vd.data_ptr() + i * row,
                                         dtab.data_ptr(), max_blocks, starts[i].data_ptr(),
                                         slens[i].data_ptr(), n_seqs, 1, mx, qd.data_ptr() + i * qrow,
-                                        Hq, 1.0, 0.0, out.data_ptr(), fmkv.DTYPE_BF16, stream)
+                                        Hq, 1.0, tau, out.data_ptr(), fmkv.DTYPE_BF16, stream)
         if rc:
             raise RuntimeError(lib.fmkv_last_error().decode())
 
@@ -568,7 +570,8 @@ def run_c4(args) -> dict:
                                f"{n_seqs} sequences, Hq 16, Hkv {Hkv}, head_dim {D}, {bits}-bit group-64, "
                                "1 token append + attention per sequence per step",
                    "n_seqs": n_seqs, "total_context": int(lens.sum()), "n_q_heads": Hq,
-                   "n_kv_heads": Hkv, "head_dim": D, "bits": bits},
+                   "n_kv_heads": Hkv, "head_dim": D, "bits": bits, "sparse_v_tau": tau,
+                   **({"sparse_v_path": args.sparse_v_path} if tau > 0.0 else {})},
         "hbm_frac_of_value": round(gbs / HBM_PEAK_GBS, 4),
         "bytes_per_step": int(read),
     }
@@ -991,7 +994,7 @@ def main(argv=None) -> int:
     ap.add_argument("--graph-steps", type=int, default=64,
                     help="c3: also time this many steps captured in a HIP graph (0: skip)")
     ap.add_argument("--sparse-v-tau", type=float, default=0.0,
-                    help="c3, c5: sparse-V threshold (0: dense softmax attention; > 0: the "
+                    help="c3, c4, c5: sparse-V threshold (0: dense softmax attention; > 0: the "
                          "statistics pass, then the second half --sparse-v-path names)")
     ap.add_argument("--sparse-v-path", choices=["gather", "gated"], default="gather",
                     help="sparse-V after the statistics pass: the gather of the kept V rows "
