@@ -455,9 +455,9 @@ __device__ void new_token_column(const AttnArgs& a, uint8_t* tab, float2* rope, 
 // flags: bit 2 new-token column, bits 4-7 q heads per KV head, bits 8-31 q
 // heads. A linear or ring cache's dense or stats pass needs no struct field
 // for its first copies; a paged pool's (PAGED: block table, per-sequence
-// lengths) needs the struct from the start. (Measured: C3 step 23.4 -> 23.2
-// us, 24.0 -> 23.5 us in a HIP graph; the compiler still hoists some of the
-// struct's loads above the first copies.)
+// lengths) needs the struct from the start. (Measured: 32K global-layer
+// step 23.4 -> 23.2 us, 24.0 -> 23.5 us in a HIP graph; the compiler still
+// hoists some of the struct's loads above the first copies.)
 template <int D, int BITS, int MODE, int SW, bool PAGED, bool PACK>
 __global__ __launch_bounds__((AttnPlan<D, BITS, SW>::kWaves * 64))
 __attribute__((amdgpu_waves_per_eu(AttnPlan<D, BITS, SW>::kWavesPerSimd,

@@ -568,8 +568,9 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
 // loaded (unrolled, predicated) and held in registers and RPT * 256 list
 // entries in LDS, and each row per thread the instance holds beyond the
 // call's costs time. Measured at a 32K step (2049 rows), sparse-V tau 1e-3:
-// 64 rows per thread 20.95 us, 32 19.6 us, 16 18.3 us, 9 18.0 us; the C5
-// stack's 1024-slot rings (64 rows) gained 0.35 us a layer from 16 to 1.
+// 64 rows per thread 20.95 us, 32 19.6 us, 16 18.3 us, 9 18.0 us; the
+// 1024-slot rings of a 30-layer stack's sliding layers (64 rows) gained
+// 0.35 us a layer from 16 to 1.
 // Instances: 256 rows (a ring of up to 4096 slots), 2304 (a 36K context),
 // 4096, 8192 and 16384.
 template <int D>
