@@ -435,3 +435,47 @@ def test_sparse_v_gather_row_instances(gpu, ora, T):
         out = cache.attention(dev_bf16(q), scale, sparse_v_tau=tau, dtype=torch.float32)
         torch.cuda.synchronize()
         check_attention(out, ref, f"T={T} scale={scale} tau={tau:.3g}")
+
+
+def test_sparse_v_paged_long_ragged(gpu, ora):
+    """Paged pool, shuffled block ids, ragged sequences up to 70000 tokens
+    (the gather's 8192-row instance, reading through block tables): one
+    decode step at scale 0.05 with tau 1e-3, against the oracle."""
+    import torch
+
+    from gpu_util import fast_kv, fast_q
+
+    D, bits, Hkv, Hq = 128, 4, 1, 4
+    lens = [70000, 300, 40000, 5000]
+    n_seqs = len(lens)
+    need = [(n + 2 + 15) // 16 for n in lens]
+    max_blocks, n_blocks = max(need), sum(need)
+    perm = np.argsort(synth.splitmix64(78, n_blocks)).astype(np.int32)
+    tables = np.zeros((n_seqs, max_blocks), np.int32)
+    o = 0
+    for s, nb in enumerate(need):
+        tables[s, :nb] = perm[o:o + nb]
+        o += nb
+    pool = gpu.PagedPool(gpu.make_desc(Hkv, D, bits), n_blocks)
+    dtab = torch.from_numpy(tables).cuda()
+    oracles = []
+    for s, n in enumerate(lens):
+        oc = ora.OracleCache(Hkv, D, bits, 0, n + 2)
+        k, v = fast_kv(30 * s + 5, n, Hkv, D), fast_kv(30 * s + 6, n, Hkv, D)
+        oc.append(k, v)
+        oracles.append(oc)
+        pool.append(dev_bf16(k[None]), dev_bf16(v[None]), dtab[s:s + 1].contiguous(),
+                    torch.zeros(1, dtype=torch.int32, device="cuda"))
+    k1 = np.stack([fast_kv(710 + s, 1, Hkv, D) for s in range(n_seqs)])
+    v1 = np.stack([fast_kv(810 + s, 1, Hkv, D) for s in range(n_seqs)])
+    start = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    q = np.stack([fast_q(960 + s, 1, Hq, Hkv, D)[0] for s in range(n_seqs)])
+    scale, tau = 0.05, 1e-3  # kept fractions 0.13%, 22%, 0.27%, 0.12%
+    out = pool.decode_step(dev_bf16(k1), dev_bf16(v1), dtab, start, start + 1, max(lens) + 1,
+                           dev_bf16(q), scale, sparse_v_tau=tau, dtype=torch.float32)
+    torch.cuda.synchronize()
+    for s in range(n_seqs):
+        oracles[s].append(k1[s], v1[s])
+        w = oracles[s].attention_weights(q[s], scale)
+        assert 0 < np.mean(w >= tau) < 1, f"seq {s}: the gate keeps some weights and drops some"
+        check_attention(out[s], oracles[s].attention(q[s], scale, tau), f"seq {s} (T={lens[s] + 1})")
