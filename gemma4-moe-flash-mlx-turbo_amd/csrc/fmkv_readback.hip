@@ -311,7 +311,7 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
   constexpr int kRound = 64;                // candidates per score round
   constexpr int IPT = kRound * kBlockTokens / NT;  // score items per thread
   constexpr int SPT = 2;                    // statistics per thread per load round
-  constexpr int kSoloRows = 64;
+  constexpr int kSoloRows = 32;
   constexpr int kRowsPerPart = 16;
   __shared__ int cand[RPT * NT];
   __shared__ int kept_slot[kRound * kBlockTokens + 1];
