@@ -107,3 +107,47 @@ def test_graph_steps_across_split_plans(gpu, mode, bits):
         torch.cuda.synchronize()
         for j in range(n):
             assert torch.equal(outs[j], want[j]), f"mode {mode} replay {rep} step {j}"
+
+
+def test_graph_replays_sparse_gather_merge(gpu):
+    """Sparse-V steps whose heads have more candidate blocks than one
+    work-group takes (soft weights, tau 1e-4 on a 1500-token global layer:
+    most tokens kept, about 94 candidate blocks, so several parts merge
+    through the head's counter, which the statistics pass zeroes): every
+    replay equals the eager steps bit for bit (the parts' rows are summed in
+    part order whatever order they arrive in)."""
+    import torch
+
+    D, bits, Hkv, Hq, T0, n = 512, 8, 2, 16, 1500, 6
+    scale, tau = 0.003, 1e-4
+    caches = [gpu.KVCache.new_quantized(D, bits, Hkv, capacity=T0 + 32) for _ in range(2)]
+    k0, v0 = dev_bf16(kv_batch(3, T0, Hkv, D)), dev_bf16(kv_batch(4, T0, Hkv, D))
+    ks = [dev_bf16(kv_batch(110 + j, 1, Hkv, D, special=False)) for j in range(n + 1)]
+    vs = [dev_bf16(kv_batch(140 + j, 1, Hkv, D, special=False)) for j in range(n + 1)]
+    qs = [dev_bf16(synth.q_rows(170 + j, Hq, Hkv, D, None)) for j in range(n + 1)]
+    for c in caches:
+        c.append(k0, v0)
+        c.decode_step(ks[0], vs[0], qs[0], scale, sparse_v_tau=tau, dtype=torch.float32)
+    eager, graphed = caches
+    want = [eager.decode_step(ks[j], vs[j], qs[j], scale, sparse_v_tau=tau, dtype=torch.float32)
+            for j in range(1, n + 1)]
+    torch.cuda.synchronize()
+    outs = [torch.empty((Hq, D), dtype=torch.float32, device="cuda") for _ in range(n)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for j in range(n):
+            graphed.decode_step(ks[j + 1], vs[j + 1], qs[j + 1], scale, sparse_v_tau=tau,
+                                out=outs[j], stream=s)
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        noise = torch.randn(1 << 16, device="cuda").sum()  # unrelated eager work
+        torch.cuda.synchronize()
+        assert torch.isfinite(noise)
+        for j in range(n):
+            assert torch.equal(outs[j], want[j]), f"replay {rep} step {j}"
