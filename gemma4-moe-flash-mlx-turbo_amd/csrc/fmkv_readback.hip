@@ -303,8 +303,10 @@ __device__ inline int wg_exclusive_count(int n, int* cnt, int* total) {
 // are in thread-major order (thread, then k), a fixed order, so the sums
 // are deterministic.
 // Blocks: at most RPT * 256 visible head-blocks per sequence; the launch
-// takes the smallest instance that holds the call's rows.
-template <int D, int RPT>
+// takes the smallest instance that holds the call's rows, and the one of
+// the cache's mode and width (MODE, BITS), so that each kernel holds one
+// mode's kept-row loop.
+template <int D, int RPT, int MODE, int BITS>
 __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
   constexpr int NT = 256, E = D / 64, ND = (D + NT - 1) / NT;
   static_assert(RPT * NT <= kGatherMaxRows, "block rows per thread");
@@ -342,7 +344,7 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
   // (the centroid reaches LDS after the loads below have been waited for:
   // written here, its load would be waited for alone, a round trip of its own)
   const float cent_v =
-      L.mode == kCodebook && tid < 16 && tid < (1 << L.bits) ? centroid(L.bits, tid) : 0.0f;
+      MODE == kCodebook && tid < (1 << BITS) ? centroid(BITS, tid) : 0.0f;
   const int kmax = (int)((nrows + NT - 1) / NT);  // <= RPT
   float bm[RPT];
 #pragma unroll
@@ -463,21 +465,7 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
       nt_pending = false;
     }
     __syncthreads();
-    if (L.mode == kAffine) {
-      if (L.bits == 8)
-        accumulate_kept<kAffine, 8, D, NT>(kept_slot, kept_w, n, L, cent, a.c, block_of, acc);
-      else
-        accumulate_kept<kAffine, 4, D, NT>(kept_slot, kept_w, n, L, cent, a.c, block_of, acc);
-    } else if (L.mode == kCodebook) {
-      if (L.bits == 2)
-        accumulate_kept<kCodebook, 2, D, NT>(kept_slot, kept_w, n, L, cent, a.c, block_of, acc);
-      else if (L.bits == 3)
-        accumulate_kept<kCodebook, 3, D, NT>(kept_slot, kept_w, n, L, cent, a.c, block_of, acc);
-      else
-        accumulate_kept<kCodebook, 4, D, NT>(kept_slot, kept_w, n, L, cent, a.c, block_of, acc);
-    } else {
-      accumulate_kept<kPlain, 16, D, NT>(kept_slot, kept_w, n, L, cent, a.c, block_of, acc);
-    }
+    accumulate_kept<MODE, BITS, D, NT>(kept_slot, kept_w, n, L, cent, a.c, block_of, acc);
     __syncthreads();
   }
 
@@ -525,7 +513,7 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
     }
   }
   const int64_t o_idx = ((int64_t)seq * nqh + h) * D;
-  if (L.mode == kPlain) {
+  if constexpr (MODE == kPlain) {
 #pragma unroll
     for (int e = 0; e < ND; e++) {
       const int d = tid + e * NT;
@@ -573,19 +561,31 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(AttnArgs a) {
 // 0.35 us a layer from 16 to 1.
 // Instances: 256 rows (a ring of up to 4096 slots), 2304 (a 36K context),
 // 4096, 8192 and 16384.
-template <int D>
+template <int D, int MODE, int BITS>
 hipError_t launch_gather_rows(const AttnArgs& a, dim3 grid, hipStream_t s) {
   if (a.gather_rows <= 1 * 256)
-    hipLaunchKernelGGL((sparse_gather_kernel<D, 1>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((sparse_gather_kernel<D, 1, MODE, BITS>), grid, dim3(256), 0, s, a);
   else if (a.gather_rows <= 9 * 256)
-    hipLaunchKernelGGL((sparse_gather_kernel<D, 9>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((sparse_gather_kernel<D, 9, MODE, BITS>), grid, dim3(256), 0, s, a);
   else if (a.gather_rows <= 16 * 256)
-    hipLaunchKernelGGL((sparse_gather_kernel<D, 16>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((sparse_gather_kernel<D, 16, MODE, BITS>), grid, dim3(256), 0, s, a);
   else if (a.gather_rows <= 32 * 256)
-    hipLaunchKernelGGL((sparse_gather_kernel<D, 32>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((sparse_gather_kernel<D, 32, MODE, BITS>), grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((sparse_gather_kernel<D, 64>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((sparse_gather_kernel<D, 64, MODE, BITS>), grid, dim3(256), 0, s, a);
   return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_gather_mode(const AttnArgs& a, dim3 grid, hipStream_t s) {
+  const BlockLayout& L = a.st.layout;
+  if (L.mode == kAffine && L.bits == 8) return launch_gather_rows<D, kAffine, 8>(a, grid, s);
+  if (L.mode == kAffine && L.bits == 4) return launch_gather_rows<D, kAffine, 4>(a, grid, s);
+  if (L.mode == kCodebook && L.bits == 2) return launch_gather_rows<D, kCodebook, 2>(a, grid, s);
+  if (L.mode == kCodebook && L.bits == 3) return launch_gather_rows<D, kCodebook, 3>(a, grid, s);
+  if (L.mode == kCodebook && L.bits == 4) return launch_gather_rows<D, kCodebook, 4>(a, grid, s);
+  if (L.mode == kPlain) return launch_gather_rows<D, kPlain, 16>(a, grid, s);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_sparse_gather(const AttnArgs& a, int n_seqs, hipStream_t s) {
@@ -595,9 +595,9 @@ hipError_t launch_sparse_gather(const AttnArgs& a, int n_seqs, hipStream_t s) {
     return hipErrorInvalidValue;
   dim3 grid((unsigned)a.n_q_heads, (unsigned)n_seqs, (unsigned)a.gather_parts);
   switch (a.st.layout.head_dim) {
-    case 128: return launch_gather_rows<128>(a, grid, s);
-    case 256: return launch_gather_rows<256>(a, grid, s);
-    case 512: return launch_gather_rows<512>(a, grid, s);
+    case 128: return launch_gather_mode<128>(a, grid, s);
+    case 256: return launch_gather_mode<256>(a, grid, s);
+    case 512: return launch_gather_mode<512>(a, grid, s);
     default: return hipErrorInvalidValue;
   }
 }
